@@ -1,0 +1,117 @@
+// common.h -- device-side helpers and the HBM layout of Q8_0 expert weights.
+//
+// Tiled Q8_0 layout. A matrix W[R][C] (int8, one fp16 scale per 32-column block)
+// is stored as two planes:
+//   q plane: 16-row panels; inside a panel, 64-column chunks of 1 KB. Byte 16*l + 8*h + i
+//            of chunk (p, j) is W[16p + l%16][64j + 32h + 8*(l/16) + i] (l = lane 0..63,
+//            h = 0..1, i = 0..7). One dwordx4 load per lane reads a whole chunk, and its
+//            two 8-byte halves are exactly the B operands of two v_mfma_i32_16x16x32_i8
+//            (lane l = row l%16, k = 8*(l/16)..+8), one per 32-column quantisation block.
+//   s plane: fp16 scale of (row r, block b) at ((r/16)*(C/32) + b)*16 + r%16, so the 16
+//            rows of a panel read one block's scales as 32 contiguous bytes.
+// One expert = gate, up, down q planes then their s planes, 34 bytes per 32 weights.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define GM_TILE_ROWS 16
+#define GM_QBLOCK 32
+#define GM_CHUNK_COLS 64
+#define GM_CHUNK_BYTES 1024
+#define GM_MAX_E 256
+#define GM_MAX_K 8
+#define GM_MAX_DIM 8192
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__host__ __device__ static inline size_t gm_q_offset(int r, int c, int cols) {
+    const int p = r >> 4, j = c >> 6;
+    const int lane = (r & 15) + 16 * ((c & 31) >> 3);
+    const int half = (c & 63) >> 5;
+    return ((size_t)p * (size_t)(cols >> 6) + (size_t)j) * GM_CHUNK_BYTES + (size_t)lane * 16 + (size_t)half * 8 +
+           (size_t)(c & 7);
+}
+
+__host__ __device__ static inline size_t gm_s_offset(int r, int b, int cols) {
+    return ((size_t)(r >> 4) * (size_t)(cols >> 5) + (size_t)b) * 16 + (size_t)(r & 15);
+}
+
+// ---------------------------------------------------------------- reductions
+
+__device__ static inline double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ static inline float wave_max_f(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Block-wide sum of doubles for a 256-thread block; every thread gets the total.
+// `red` must hold 4 doubles of shared memory. Summation order is fixed.
+__device__ static inline double block_sum_d(double v, double *red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    v = wave_sum_d(v);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    double t = ((red[0] + red[1]) + red[2]) + red[3];
+    return t;
+}
+
+// Block-wide exclusive prefix sum of doubles (256 threads) in thread order.
+__device__ static inline double block_exclusive_scan_d(double v, double *red, double *total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    double incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        double n = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += n;
+    }
+    __syncthreads();
+    if (lane == 63) red[w] = incl;
+    __syncthreads();
+    double base = 0.0;
+    for (int i = 0; i < w; i++) base += red[i];
+    *total = ((red[0] + red[1]) + red[2]) + red[3];
+    return base + incl - v;
+}
+
+// ---------------------------------------------------------------- int8 digit form
+//
+// A block of 32 fp32 activations is written exactly-enough as 2^e * X with X integer,
+// |X| <= 8323072 = 127*2^16 + 127*2^8 (22-23 significant bits relative to the block
+// maximum), and X is split into balanced base-256 digits d0, d1, d2 in [-128, 127]:
+// X = d0 + 256*d1 + 65536*d2. An int8 MFMA then gives each digit's dot product with a
+// weight block exactly in int32, and the block dot is rebuilt in fp32.
+
+__device__ static inline int digit_exponent(float maxabs) {
+    if (!(maxabs > 0.0f) || !isfinite(maxabs)) return 0;
+    int k;
+    float m = frexpf(maxabs, &k);  // maxabs = m * 2^k, m in [0.5, 1)
+    // m * 2^23 <= 8323072 keeps the top digit within int8; otherwise use one bit less.
+    return (m * 8388608.0f <= 8323072.0f) ? k - 23 : k - 22;
+}
+
+__device__ static inline void split_digits(float v, int e, int8_t *d0, int8_t *d1, int8_t *d2) {
+    int X = (int)rintf(ldexpf(v, -e));
+    int a0 = ((X + 128) & 255) - 128;
+    int X1 = (X - a0) >> 8;
+    int a1 = ((X1 + 128) & 255) - 128;
+    int a2 = (X1 - a1) >> 8;
+    *d0 = (int8_t)a0;
+    *d1 = (int8_t)a1;
+    *d2 = (int8_t)a2;
+}
+
+// fp32 value of D0 + 256*D1 + 65536*D2 for int32 digit dots (|Di| < 2^20).
+__device__ static inline float digits_to_float(int D0, int D1, int D2) {
+    int lo = D0 + (D1 << 8);  // |lo| < 2^29
+    return fmaf((float)D2, 65536.0f, (float)lo);
+}

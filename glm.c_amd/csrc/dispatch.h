@@ -1,0 +1,79 @@
+// dispatch.h -- per-expert token lists from the per-token top-k (the grouping that the
+// reference never materialises: its prefill routes token by token, infer.c:2190-2233).
+//
+// List e holds every token t with e in topk(t), in ascending t, with the top-k slot it
+// came from. One block per expert scans the [T][K] assignments in order and compacts
+// its matches with a ballot prefix, so the order never depends on atomics; the last
+// block to finish turns the counts into offsets and packs the lists.
+#pragma once
+
+#include "common.h"
+
+struct DispatchArgs {
+    const int *topk_idx;  // [T][K]
+    int T, K, E;
+    int *tmp_tok;         // [E][T]
+    int *tmp_slot;        // [E][T]
+    int *counts;          // [E]
+    unsigned *counter;    // zero between launches
+    int *offsets;         // [E+1]
+    int *tokens;          // [T*K]
+    int *slots;           // [T*K]
+};
+
+#define DP_BLOCK 256
+
+__global__ __launch_bounds__(DP_BLOCK) void k_dispatch(DispatchArgs a) {
+    __shared__ int wave_cnt[DP_BLOCK / 64];
+    __shared__ int s_last;
+    __shared__ int s_off[GM_MAX_E + 1];
+    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int total = a.T * a.K;
+    int base = 0;
+    for (int a0 = 0; a0 < total; a0 += DP_BLOCK) {
+        const int i = a0 + tid;
+        const bool match = i < total && a.topk_idx[i] == e;
+        const unsigned long long bal = __ballot(match);
+        const int before = __popcll(bal & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_cnt[w] = __popcll(bal);
+        __syncthreads();
+        int wbase = 0;
+        for (int q = 0; q < w; q++) wbase += wave_cnt[q];
+        const int tot = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+        if (match) {
+            const int pos = base + wbase + before;  // < T: a token selects an expert at most once
+            if (pos < a.T) {
+                a.tmp_tok[(size_t)e * a.T + pos] = i / a.K;
+                a.tmp_slot[(size_t)e * a.T + pos] = i % a.K;
+            }
+        }
+        base += tot;
+        __syncthreads();
+    }
+    if (tid == 0) a.counts[e] = base < a.T ? base : a.T;
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = (atomicAdd(a.counter, 1u) == (unsigned)(a.E - 1));
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    if (tid == 0) {
+        *a.counter = 0u;
+        int off = 0;
+        for (int q = 0; q < a.E; q++) {
+            s_off[q] = off;
+            a.offsets[q] = off;
+            off += a.counts[q];
+        }
+        s_off[a.E] = off;
+        a.offsets[a.E] = off;
+    }
+    __syncthreads();
+    for (int q = 0; q < a.E; q++) {
+        const int n = s_off[q + 1] - s_off[q];
+        for (int i = tid; i < n; i += DP_BLOCK) {
+            a.tokens[s_off[q] + i] = a.tmp_tok[(size_t)q * a.T + i];
+            a.slots[s_off[q] + i] = a.tmp_slot[(size_t)q * a.T + i];
+        }
+    }
+}

@@ -1,0 +1,220 @@
+// experts.h -- expert products for one token per block row: gate/up with SwiGLU
+// (infer.c:1184-1188, 1197-1202) and down with the weighted combine and residual
+// (infer.c:1190-1192, 1205, 1212-1214).
+//
+// Each block owns one 16-row panel of one expert matrix (or of gate and up together)
+// and one token. Its four waves split the columns; each wave streams 1 KB chunks of
+// the tiled q plane (one dwordx4 per lane) and feeds each 32-column block to
+// v_mfma_i32_16x16x32_i8 with the activation digits as the A operand (rows 0..2 =
+// digits, k = the block's 32 columns). Lanes 0..15 then rebuild that block's fp32 dot
+// for their row and apply the fp16 block scale and the digit exponent.
+#pragma once
+
+#include "common.h"
+
+struct ExpertArgs {
+    const uint8_t *experts;  // layer base: expert e at experts + e * stride, shared expert at index E
+    size_t stride;
+    size_t off_gq, off_uq, off_dq, off_gs, off_us, off_ds;
+    int D, F, E, K, S;
+    int flags;
+};
+
+#define EX_BLOCK 256
+#define EX_WAVES 4
+#define EX_NB 8  // chunks per wave kept in flight
+
+// Digit form of n activations (n a multiple of 32) into shared memory:
+// dig[j*n + i] = digit j of v[i], dexp[i/32] = block exponent.
+__device__ static inline void load_digits(const float *__restrict__ v, int n, int8_t *dig, int *dexp) {
+    for (int i0 = threadIdx.x * 8; i0 < n; i0 += EX_BLOCK * 8) {
+        float vals[8];
+        float mx = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            vals[k] = v[i0 + k];
+            mx = fmaxf(mx, fabsf(vals[k]));
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        const int e = digit_exponent(mx);
+        unsigned long long w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            int8_t a, b, c;
+            split_digits(vals[k], e, &a, &b, &c);
+            w0 |= (unsigned long long)(uint8_t)a << (8 * k);
+            w1 |= (unsigned long long)(uint8_t)b << (8 * k);
+            w2 |= (unsigned long long)(uint8_t)c << (8 * k);
+        }
+        *(unsigned long long *)(dig + i0) = w0;
+        *(unsigned long long *)(dig + n + i0) = w1;
+        *(unsigned long long *)(dig + 2 * n + i0) = w2;
+        if ((threadIdx.x & 3) == 0) dexp[i0 >> 5] = e;
+    }
+}
+
+__device__ static inline long chunk_half(const u32x4 &c, int h) {
+    return h == 0 ? (long)(((unsigned long long)c.y << 32) | c.x) : (long)(((unsigned long long)c.w << 32) | c.z);
+}
+
+// One block of 32 columns: digit dots via MFMA, then lanes 0..15 accumulate their row.
+__device__ static inline void mfma_block(long A, long B, const __half *__restrict__ s, size_t s_idx, int dexp,
+                                         int lane, float &acc) {
+    const v4i zero = {0, 0, 0, 0};
+    v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+    if (lane < 16) {
+        const float f = digits_to_float(d[0], d[1], d[2]);
+        const float sc = __half2float(s[s_idx + lane]);
+        acc = fmaf(f, ldexpf(sc, dexp), acc);
+    }
+}
+
+// Partial dot products of panel p of one or two matrices (same shape, same activations)
+// over the chunks j = w, w+4, ... ; lanes 0..15 return their row's partial sums.
+template <int NMAT>
+__device__ static inline void panel_partial(const uint8_t *__restrict__ q0, const __half *__restrict__ s0,
+                                            const uint8_t *__restrict__ q1, const __half *__restrict__ s1, int p,
+                                            int cols, const int8_t *dig, const int *dexp, float *out0, float *out1) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int nchunks = cols >> 6, nblocks = cols >> 5;
+    const int m = lane & 15, kofs = 8 * (lane >> 4);
+    const u32x4 *qa = (const u32x4 *)(q0 + (size_t)p * nchunks * GM_CHUNK_BYTES) + lane;
+    const u32x4 *qb = NMAT > 1 ? (const u32x4 *)(q1 + (size_t)p * nchunks * GM_CHUNK_BYTES) + lane : qa;
+    const size_t sbase = (size_t)p * nblocks * 16;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int j0 = w; j0 < nchunks; j0 += EX_WAVES * EX_NB) {
+        u32x4 ba[EX_NB], bb[EX_NB];
+#pragma unroll
+        for (int u = 0; u < EX_NB; u++) {
+            const int j = j0 + EX_WAVES * u;
+            if (j < nchunks) {
+                ba[u] = qa[(size_t)j * 64];
+                if (NMAT > 1) bb[u] = qb[(size_t)j * 64];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < EX_NB; u++) {
+            const int j = j0 + EX_WAVES * u;
+            if (j < nchunks) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int b = 2 * j + h;
+                    long A = 0;
+                    if (m < 3) A = *(const long *)(dig + m * cols + 32 * b + kofs);
+                    const int de = dexp[b];
+                    mfma_block(A, chunk_half(ba[u], h), s0, sbase + (size_t)b * 16, de, lane, acc0);
+                    if (NMAT > 1) mfma_block(A, chunk_half(bb[u], h), s1, sbase + (size_t)b * 16, de, lane, acc1);
+                }
+            }
+        }
+    }
+    *out0 = acc0;
+    *out1 = acc1;
+}
+
+// grid (F/16, K+S, T): h[t][slot][F] = silu(gate . xn) * (up . xn) for the slot's expert.
+__global__ __launch_bounds__(EX_BLOCK) void k_gate_up(ExpertArgs a, const float *__restrict__ xn,
+                                                      const int *__restrict__ topk_idx, float *__restrict__ h) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float part[EX_WAVES][2][16];
+    const int p = blockIdx.x, slot = blockIdx.y, t = blockIdx.z;
+    const int D = a.D, F = a.F, K = a.K, nslots = a.K + a.S;
+    int e = a.E;
+    if (slot < K) {
+        if (a.flags & 1) return;
+        e = topk_idx[(size_t)t * K + slot];
+        if (e < 0) return;
+    }
+    int8_t *dig = (int8_t *)smem;
+    int *dexp = (int *)(smem + 3 * D);
+    load_digits(xn + (size_t)t * D, D, dig, dexp);
+    __syncthreads();
+    const uint8_t *base = a.experts + (size_t)e * a.stride;
+    float g, u;
+    panel_partial<2>(base + a.off_gq, (const __half *)(base + a.off_gs), base + a.off_uq,
+                     (const __half *)(base + a.off_us), p, D, dig, dexp, &g, &u);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane < 16) {
+        part[w][0][lane] = g;
+        part[w][1][lane] = u;
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const int l = threadIdx.x;
+        const float gs = ((part[0][0][l] + part[1][0][l]) + part[2][0][l]) + part[3][0][l];
+        const float us = ((part[0][1][l] + part[1][1][l]) + part[2][1][l]) + part[3][1][l];
+        const float act = gs / (1.0f + expf(-gs));
+        h[((size_t)t * nslots + slot) * F + (size_t)p * 16 + l] = act * us;
+    }
+}
+
+struct CombineArgs {
+    const int *topk_idx;      // [T][K]
+    const float *topk_ws;     // [T][K] weights * routed_scale
+    float *y;                 // [T][K+S][D] per-slot down outputs
+    unsigned *panel_counter;  // [T][D/16], zero between launches
+    const float *x_in;        // [T][D]
+    float *x_out;             // [T][D]
+    float *shared_out;        // [T][D]
+    float *routed_out;        // [T][D]
+};
+
+// grid (D/16, K+S, T): y[t][slot] = down . h[t][slot]; the last slot block of each
+// (token, panel) forms x_out = x_in + (shared + sum_k w_k y_k) for the panel's rows.
+__global__ __launch_bounds__(EX_BLOCK) void k_down_combine(ExpertArgs a, CombineArgs c, const float *__restrict__ h) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ float part[EX_WAVES][16];
+    __shared__ int s_last;
+    const int p = blockIdx.x, slot = blockIdx.y, t = blockIdx.z;
+    const int D = a.D, F = a.F, K = a.K, nslots = a.K + a.S;
+    const int routed_on = !(a.flags & 1);
+    int e = a.E;
+    bool valid = true;
+    if (slot < K) {
+        e = c.topk_idx[(size_t)t * K + slot];
+        valid = routed_on && e >= 0;
+    }
+    if (valid) {
+        int8_t *dig = (int8_t *)smem;
+        int *dexp = (int *)(smem + 3 * F);
+        load_digits(h + ((size_t)t * nslots + slot) * F, F, dig, dexp);
+        __syncthreads();
+        const uint8_t *base = a.experts + (size_t)e * a.stride;
+        float yv, unused;
+        panel_partial<1>(base + a.off_dq, (const __half *)(base + a.off_ds), nullptr, nullptr, p, F, dig, dexp, &yv,
+                         &unused);
+        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+        if (lane < 16) part[w][lane] = yv;
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            const int l = threadIdx.x;
+            c.y[((size_t)t * nslots + slot) * D + (size_t)p * 16 + l] =
+                ((part[0][l] + part[1][l]) + part[2][l]) + part[3][l];
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = (atomicAdd(&c.panel_counter[(size_t)t * (D >> 4) + p], 1u) == (unsigned)(nslots - 1));
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    if (threadIdx.x == 0) c.panel_counter[(size_t)t * (D >> 4) + p] = 0u;
+    if (threadIdx.x < 16) {
+        const int r = p * 16 + threadIdx.x;
+        float acc = 0.0f;
+        if (routed_on) {
+            for (int k = 0; k < K; k++) {
+                if (c.topk_idx[(size_t)t * K + k] < 0) continue;
+                const float yk = c.y[((size_t)t * nslots + k) * D + r];
+                acc = __fadd_rn(acc, __fmul_rn(c.topk_ws[(size_t)t * K + k], yk));
+            }
+        }
+        const float sh = a.S ? c.y[((size_t)t * nslots + K) * D + r] : 0.0f;
+        const size_t o = (size_t)t * D + r;
+        c.routed_out[o] = acc;
+        c.shared_out[o] = sh;
+        c.x_out[o] = __fadd_rn(c.x_in[o], __fadd_rn(sh, acc));
+    }
+}

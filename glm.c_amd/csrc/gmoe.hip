@@ -1,0 +1,547 @@
+// gmoe.hip -- C ABI of the MI355X MoE FFN library (include/gmoe.h).
+//
+// One forward of a MoE layer is three kernels on the caller's stream:
+//   k_norm_router   grid (E, T)        rmsnorm, router logits, certified top-k (router.h)
+//   k_gate_up       grid (F/16, K+1, T) gate/up products and SwiGLU (experts.h)
+//   k_down_combine  grid (D/16, K+1, T) down products, weighted combine, residual (experts.h)
+// plus k_dispatch (dispatch.h) for the per-expert token lists. Expert weights are
+// uploaded once per layer into the tiled Q8_0 layout of common.h and stay resident.
+#include "gmoe.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "common.h"
+#include "dispatch.h"
+#include "experts.h"
+#include "repack.h"
+#include "router.h"
+
+static thread_local char g_err[512];
+
+static void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+#define HIP_OK(expr)                                                                     \
+    do {                                                                                 \
+        hipError_t err_ = (expr);                                                        \
+        if (err_ != hipSuccess) {                                                        \
+            set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(err_), __FILE__, __LINE__); \
+            return GMOE_ERR_HIP;                                                         \
+        }                                                                                \
+    } while (0)
+
+struct LayerDev {
+    uint8_t *experts = nullptr;  // (E+1) * stride bytes, tiled
+    float *norm = nullptr;       // [D]
+    float *gate_inp = nullptr;   // [E][D]
+    float *bias = nullptr;       // [E]
+    int has_routed = 0;
+    int uploaded = 0;
+    int last_T = 0;
+};
+
+struct gmoe_ctx {
+    int device = 0;
+    gmoe_config cfg{};
+    int D = 0, F = 0, E = 0, K = 0, S = 0, L = 0, Tmax = 0;
+    size_t stride = 0, off_gq = 0, off_uq = 0, off_dq = 0, off_gs = 0, off_us = 0, off_ds = 0;
+    LayerDev *layers = nullptr;
+
+    float *xn = nullptr, *router_prob = nullptr, *topk_w = nullptr, *topk_ws = nullptr;
+    float *h = nullptr, *y = nullptr, *shared_out = nullptr, *routed_out = nullptr;
+    double2 *stage = nullptr;
+    int *topk_idx = nullptr;
+    unsigned *tok_counter = nullptr, *panel_counter = nullptr, *disp_counter = nullptr;
+    int *disp_tmp_tok = nullptr, *disp_tmp_slot = nullptr, *disp_counts = nullptr;
+    int *offsets = nullptr, *tokens = nullptr, *slots = nullptr;
+    int *hist_idx = nullptr;
+    float *hist_w = nullptr;
+    unsigned long long *stats_dev = nullptr;
+    float *x_host_io = nullptr;  // [T][D] device copy of gmoe_forward_host's activations
+
+    uint8_t *staging = nullptr;
+    size_t staging_bytes = 0;
+
+    long long tokens_routed = 0;
+    long long scale_inexact = 0;
+    int last_layer = -1, last_T = 0, last_flags = 0, last_dispatched = 0;
+};
+
+extern "C" const char *gmoe_last_error(void) { return g_err; }
+
+template <typename T>
+static int dev_alloc(T **p, size_t count) {
+    *p = nullptr;
+    if (count == 0) count = 1;
+    hipError_t e = hipMalloc((void **)p, count * sizeof(T));
+    if (e != hipSuccess) {
+        set_err("hipMalloc of %zu bytes failed: %s", count * sizeof(T), hipGetErrorString(e));
+        *p = nullptr;
+        return GMOE_ERR_NOMEM;
+    }
+    return GMOE_OK;
+}
+
+static void dev_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+static void free_ctx(gmoe_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->layers) {
+        for (int l = 0; l < c->L; l++) {
+            dev_free(c->layers[l].experts);
+            dev_free(c->layers[l].norm);
+            dev_free(c->layers[l].gate_inp);
+            dev_free(c->layers[l].bias);
+        }
+        delete[] c->layers;
+    }
+    void *bufs[] = {c->xn, c->router_prob, c->topk_w, c->topk_ws, c->h, c->y, c->shared_out, c->routed_out,
+                    c->stage, c->topk_idx, c->tok_counter, c->panel_counter, c->disp_counter, c->disp_tmp_tok,
+                    c->disp_tmp_slot, c->disp_counts, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
+                    c->stats_dev, c->x_host_io, c->staging};
+    for (void *b : bufs) dev_free(b);
+    delete c;
+}
+
+extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
+    if (!out || !cfg) {
+        set_err("gmoe_create: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    *out = nullptr;
+    const gmoe_config &g = *cfg;
+    if (g.dim <= 0 || g.dim % 64 || g.dim > GM_MAX_DIM || g.moe_ffn_dim <= 0 || g.moe_ffn_dim % 64 ||
+        g.moe_ffn_dim > GM_MAX_DIM) {
+        set_err("gmoe_create: dim and moe_ffn_dim must be positive multiples of 64 and <= %d (got %d, %d)",
+                GM_MAX_DIM, g.dim, g.moe_ffn_dim);
+        return GMOE_ERR_INVALID;
+    }
+    if (g.n_routed_experts < 1 || g.n_routed_experts > GM_MAX_E || g.n_experts_used < 1 ||
+        g.n_experts_used > GM_MAX_K) {
+        set_err("gmoe_create: need 1 <= n_routed_experts <= %d and 1 <= n_experts_used <= %d (got %d, %d)",
+                GM_MAX_E, GM_MAX_K, g.n_routed_experts, g.n_experts_used);
+        return GMOE_ERR_INVALID;
+    }
+    if (g.n_shared_experts != 1) {
+        set_err("gmoe_create: glm.c always runs exactly one shared expert (infer.c:1197); got %d",
+                g.n_shared_experts);
+        return GMOE_ERR_INVALID;
+    }
+    if (g.group_size != GM_QBLOCK) {
+        set_err("gmoe_create: group_size must be %d (got %d)", GM_QBLOCK, g.group_size);
+        return GMOE_ERR_INVALID;
+    }
+    if (g.n_layers < 2 || g.max_tokens < 1 || g.max_tokens > 65535) {
+        set_err("gmoe_create: need n_layers >= 2 and 1 <= max_tokens <= 65535 (got %d, %d)", g.n_layers,
+                g.max_tokens);
+        return GMOE_ERR_INVALID;
+    }
+    int ndev = 0;
+    HIP_OK(hipGetDeviceCount(&ndev));
+    if (device < 0 || device >= ndev) {
+        set_err("gmoe_create: device %d out of range (%d devices)", device, ndev);
+        return GMOE_ERR_INVALID;
+    }
+    HIP_OK(hipSetDevice(device));
+
+    gmoe_ctx *c = new gmoe_ctx();
+    c->device = device;
+    c->cfg = g;
+    c->D = g.dim;
+    c->F = g.moe_ffn_dim;
+    c->E = g.n_routed_experts;
+    c->K = g.n_experts_used;
+    c->S = g.n_shared_experts;
+    c->L = g.n_layers;
+    c->Tmax = g.max_tokens;
+    const size_t qb = (size_t)c->F * c->D;  // bytes of one q plane
+    const size_t sb = qb / GM_QBLOCK * 2;   // bytes of one fp16 s plane
+    c->off_gq = 0;
+    c->off_uq = qb;
+    c->off_dq = 2 * qb;
+    c->off_gs = 3 * qb;
+    c->off_us = 3 * qb + sb;
+    c->off_ds = 3 * qb + 2 * sb;
+    c->stride = (3 * qb + 3 * sb + 255) & ~(size_t)255;
+    c->layers = new LayerDev[c->L];
+
+    const size_t T = c->Tmax, D = c->D, F = c->F, E = c->E, K = c->K, NS = c->K + c->S;
+    int rc = GMOE_OK;
+    rc |= dev_alloc(&c->xn, T * D);
+    rc |= dev_alloc(&c->router_prob, T * E);
+    rc |= dev_alloc(&c->topk_w, T * K);
+    rc |= dev_alloc(&c->topk_ws, T * K);
+    rc |= dev_alloc(&c->h, T * NS * F);
+    rc |= dev_alloc(&c->y, T * NS * D);
+    rc |= dev_alloc(&c->shared_out, T * D);
+    rc |= dev_alloc(&c->routed_out, T * D);
+    rc |= dev_alloc(&c->stage, T * E);
+    rc |= dev_alloc(&c->topk_idx, T * K);
+    rc |= dev_alloc(&c->tok_counter, T);
+    rc |= dev_alloc(&c->panel_counter, T * (D / 16));
+    rc |= dev_alloc(&c->disp_counter, 1);
+    rc |= dev_alloc(&c->disp_tmp_tok, E * T);
+    rc |= dev_alloc(&c->disp_tmp_slot, E * T);
+    rc |= dev_alloc(&c->disp_counts, E);
+    rc |= dev_alloc(&c->offsets, E + 1);
+    rc |= dev_alloc(&c->tokens, T * K);
+    rc |= dev_alloc(&c->slots, T * K);
+    rc |= dev_alloc(&c->hist_idx, (size_t)c->L * T * K);
+    rc |= dev_alloc(&c->hist_w, (size_t)c->L * T * K);
+    rc |= dev_alloc(&c->stats_dev, GM_STAT_COUNT);
+    rc |= dev_alloc(&c->x_host_io, T * D);
+    if (rc != GMOE_OK) {
+        free_ctx(c);
+        return GMOE_ERR_NOMEM;
+    }
+    // Counters start at zero; each kernel's last block puts its counter back to zero.
+    hipError_t e0 = hipMemset(c->tok_counter, 0, T * sizeof(unsigned));
+    hipError_t e1 = hipMemset(c->panel_counter, 0, T * (D / 16) * sizeof(unsigned));
+    hipError_t e2 = hipMemset(c->disp_counter, 0, sizeof(unsigned));
+    hipError_t e3 = hipMemset(c->stats_dev, 0, GM_STAT_COUNT * sizeof(unsigned long long));
+    hipError_t e4 = hipMemset(c->hist_idx, 0xff, (size_t)c->L * T * K * sizeof(int));
+    hipError_t e5 = hipDeviceSynchronize();
+    if (e0 || e1 || e2 || e3 || e4 || e5) {
+        set_err("gmoe_create: initialising device buffers failed");
+        free_ctx(c);
+        return GMOE_ERR_HIP;
+    }
+    *out = c;
+    return GMOE_OK;
+}
+
+extern "C" void gmoe_destroy(gmoe_ctx *ctx) { free_ctx(ctx); }
+
+static int copy_in(void *dst, const void *src, size_t bytes) {
+    HIP_OK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return GMOE_OK;
+}
+
+// Upload n_mat raw matrices (rows x cols int8 + fp32 scales) and repack them to
+// dst + m*dst_stride (+off_q for q, +off_s for scales).
+static int upload_matrices(gmoe_ctx *c, const int8_t *q, const float *s, int n_mat, int rows, int cols, uint8_t *dst,
+                           size_t dst_stride, size_t off_q, size_t off_s, unsigned long long *inexact_dev) {
+    const size_t qbytes = (size_t)n_mat * rows * cols;
+    const size_t sbytes = (size_t)n_mat * rows * (cols / GM_QBLOCK) * sizeof(float);
+    if (qbytes + sbytes > c->staging_bytes) {
+        dev_free(c->staging);
+        c->staging = nullptr;
+        c->staging_bytes = 0;
+        if (dev_alloc(&c->staging, qbytes + sbytes) != GMOE_OK) return GMOE_ERR_NOMEM;
+        c->staging_bytes = qbytes + sbytes;
+    }
+    int rc = copy_in(c->staging, q, qbytes);
+    if (rc) return rc;
+    rc = copy_in(c->staging + qbytes, s, sbytes);
+    if (rc) return rc;
+    const size_t units = qbytes / 16;
+    hipLaunchKernelGGL(k_repack_q, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, 0,
+                       (const int8_t *)c->staging, dst + off_q, dst_stride, rows, cols, n_mat);
+    const size_t ns = sbytes / sizeof(float);
+    hipLaunchKernelGGL(k_repack_s, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, 0,
+                       (const float *)(c->staging + qbytes), dst + off_s, dst_stride, rows, cols, n_mat, inexact_dev);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipDeviceSynchronize());
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weights *w) {
+    if (!c || !w) {
+        set_err("gmoe_upload_layer: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    if (layer < 1 || layer >= c->L) {
+        set_err("gmoe_upload_layer: layer %d outside the MoE layers 1..%d", layer, c->L - 1);
+        return GMOE_ERR_INVALID;
+    }
+    if (!w->ffn_norm || !w->gate_inp || !w->exp_probs_b || !w->gate_sh_q || !w->gate_sh_s || !w->up_sh_q ||
+        !w->up_sh_s || !w->down_sh_q || !w->down_sh_s) {
+        set_err("gmoe_upload_layer: layer %d lacks its norm, router or shared expert", layer);
+        return GMOE_ERR_INVALID;
+    }
+    const int has_routed = w->gate_q && w->gate_s && w->up_q && w->up_s && w->down_q && w->down_s;
+    HIP_OK(hipSetDevice(c->device));
+    LayerDev &L = c->layers[layer];
+    L.uploaded = 0;
+    const int D = c->D, F = c->F, E = c->E;
+    if (!L.experts && dev_alloc(&L.experts, (size_t)(E + 1) * c->stride) != GMOE_OK) return GMOE_ERR_NOMEM;
+    if (!L.norm && dev_alloc(&L.norm, (size_t)D) != GMOE_OK) return GMOE_ERR_NOMEM;
+    if (!L.gate_inp && dev_alloc(&L.gate_inp, (size_t)E * D) != GMOE_OK) return GMOE_ERR_NOMEM;
+    if (!L.bias && dev_alloc(&L.bias, (size_t)E) != GMOE_OK) return GMOE_ERR_NOMEM;
+    int rc;
+    if ((rc = copy_in(L.norm, w->ffn_norm, (size_t)D * sizeof(float)))) return rc;
+    if ((rc = copy_in(L.gate_inp, w->gate_inp, (size_t)E * D * sizeof(float)))) return rc;
+    if ((rc = copy_in(L.bias, w->exp_probs_b, (size_t)E * sizeof(float)))) return rc;
+
+    unsigned long long *inexact = nullptr;
+    if (dev_alloc(&inexact, 1) != GMOE_OK) return GMOE_ERR_NOMEM;
+    HIP_OK(hipMemset(inexact, 0, sizeof(unsigned long long)));
+    uint8_t *sh = L.experts + (size_t)E * c->stride;
+    rc = upload_matrices(c, w->gate_sh_q, w->gate_sh_s, 1, F, D, sh, c->stride, c->off_gq, c->off_gs, inexact);
+    if (!rc) rc = upload_matrices(c, w->up_sh_q, w->up_sh_s, 1, F, D, sh, c->stride, c->off_uq, c->off_us, inexact);
+    if (!rc) rc = upload_matrices(c, w->down_sh_q, w->down_sh_s, 1, D, F, sh, c->stride, c->off_dq, c->off_ds, inexact);
+    if (has_routed) {
+        if (!rc) rc = upload_matrices(c, w->gate_q, w->gate_s, E, F, D, L.experts, c->stride, c->off_gq, c->off_gs, inexact);
+        if (!rc) rc = upload_matrices(c, w->up_q, w->up_s, E, F, D, L.experts, c->stride, c->off_uq, c->off_us, inexact);
+        if (!rc) rc = upload_matrices(c, w->down_q, w->down_s, E, D, F, L.experts, c->stride, c->off_dq, c->off_ds, inexact);
+    }
+    unsigned long long n_inexact = 0;
+    if (!rc && hipMemcpy(&n_inexact, inexact, sizeof(n_inexact), hipMemcpyDeviceToHost) != hipSuccess) {
+        set_err("gmoe_upload_layer: reading the scale check failed");
+        rc = GMOE_ERR_HIP;
+    }
+    dev_free(inexact);
+    if (rc) return rc;
+    if (n_inexact) {
+        c->scale_inexact += (long long)n_inexact;
+        set_err("gmoe_upload_layer: layer %d has %llu scales that fp16 cannot hold exactly", layer, n_inexact);
+        return GMOE_ERR_SCALE;
+    }
+    L.has_routed = has_routed;
+    L.uploaded = 1;
+    return GMOE_OK;
+}
+
+static int launch_dispatch(gmoe_ctx *c, int T, hipStream_t st) {
+    DispatchArgs da;
+    da.topk_idx = c->topk_idx;
+    da.T = T;
+    da.K = c->K;
+    da.E = c->E;
+    da.tmp_tok = c->disp_tmp_tok;
+    da.tmp_slot = c->disp_tmp_slot;
+    da.counts = c->disp_counts;
+    da.counter = c->disp_counter;
+    da.offsets = c->offsets;
+    da.tokens = c->tokens;
+    da.slots = c->slots;
+    hipLaunchKernelGGL(k_dispatch, dim3(c->E), dim3(DP_BLOCK), 0, st, da);
+    HIP_OK(hipGetLastError());
+    c->last_dispatched = 1;
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, float *x_out, int flags,
+                            void *stream) {
+    if (!c || !x_in || !x_out) {
+        set_err("gmoe_forward: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    if (layer < 1 || layer >= c->L || !c->layers[layer].uploaded) {
+        set_err("gmoe_forward: layer %d is not an uploaded MoE layer", layer);
+        return GMOE_ERR_INVALID;
+    }
+    if (T < 1 || T > c->Tmax) {
+        set_err("gmoe_forward: n_tokens %d outside 1..%d", T, c->Tmax);
+        return GMOE_ERR_INVALID;
+    }
+    HIP_OK(hipSetDevice(c->device));
+    hipStream_t st = (hipStream_t)stream;
+    LayerDev &L = c->layers[layer];
+    const int fl = flags | (L.has_routed ? 0 : GMOE_FLAG_NO_ROUTED);
+    const int D = c->D, F = c->F, E = c->E, K = c->K, NS = c->K + c->S;
+
+    RouterArgs ra;
+    ra.x = x_in;
+    ra.norm_w = L.norm;
+    ra.gate_inp = L.gate_inp;
+    ra.bias = L.bias;
+    ra.xn = c->xn;
+    ra.stage = c->stage;
+    ra.tok_counter = c->tok_counter;
+    ra.router_prob = c->router_prob;
+    ra.topk_idx = c->topk_idx;
+    ra.topk_w = c->topk_w;
+    ra.topk_ws = c->topk_ws;
+    ra.hist_idx = c->hist_idx + (size_t)layer * c->Tmax * K;
+    ra.hist_w = c->hist_w + (size_t)layer * c->Tmax * K;
+    ra.stats = c->stats_dev;
+    ra.D = D;
+    ra.E = E;
+    ra.K = K;
+    ra.eps = c->cfg.norm_eps;
+    ra.routed_scale = c->cfg.routed_scale;
+    hipLaunchKernelGGL(k_norm_router, dim3(E, T), dim3(RT_BLOCK), (size_t)D * sizeof(float), st, ra);
+
+    ExpertArgs ea;
+    ea.experts = L.experts;
+    ea.stride = c->stride;
+    ea.off_gq = c->off_gq;
+    ea.off_uq = c->off_uq;
+    ea.off_dq = c->off_dq;
+    ea.off_gs = c->off_gs;
+    ea.off_us = c->off_us;
+    ea.off_ds = c->off_ds;
+    ea.D = D;
+    ea.F = F;
+    ea.E = E;
+    ea.K = K;
+    ea.S = c->S;
+    ea.flags = fl;
+    hipLaunchKernelGGL(k_gate_up, dim3(F / 16, NS, T), dim3(EX_BLOCK), (size_t)3 * D + (size_t)(D / 32) * 4, st, ea,
+                       (const float *)c->xn, (const int *)c->topk_idx, c->h);
+
+    CombineArgs ca;
+    ca.topk_idx = c->topk_idx;
+    ca.topk_ws = c->topk_ws;
+    ca.y = c->y;
+    ca.panel_counter = c->panel_counter;
+    ca.x_in = x_in;
+    ca.x_out = x_out;
+    ca.shared_out = c->shared_out;
+    ca.routed_out = c->routed_out;
+    hipLaunchKernelGGL(k_down_combine, dim3(D / 16, NS, T), dim3(EX_BLOCK), (size_t)3 * F + (size_t)(F / 32) * 4, st,
+                       ea, ca, (const float *)c->h);
+    HIP_OK(hipGetLastError());
+    c->last_dispatched = 0;
+    if (T > 1) {
+        int rc = launch_dispatch(c, T, st);
+        if (rc) return rc;
+    }
+    c->last_layer = layer;
+    c->last_T = T;
+    c->last_flags = fl;
+    L.last_T = T;
+    c->tokens_routed += T;
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_forward_layers(gmoe_ctx *c, int first, int n, int T, const float *x_in, float *x_out, int flags,
+                                   void *stream) {
+    if (!c || n < 1) {
+        set_err("gmoe_forward_layers: bad arguments");
+        return GMOE_ERR_INVALID;
+    }
+    for (int i = 0; i < n; i++) {
+        int rc = gmoe_forward(c, first + i, T, i == 0 ? x_in : x_out, x_out, flags, stream);
+        if (rc) return rc;
+    }
+    return GMOE_OK;
+}
+
+static int copy_out(void *dst, const void *src, size_t bytes) {
+    if (!dst || bytes == 0) return GMOE_OK;
+    HIP_OK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_read_layer_state(gmoe_ctx *c, gmoe_layer_state *o, void *stream);
+
+extern "C" int gmoe_forward_host(gmoe_ctx *c, int layer, int T, const float *x_in, float *x_out, int flags,
+                                 gmoe_layer_state *state) {
+    if (!c || !x_in || !x_out) {
+        set_err("gmoe_forward_host: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    if (T < 1 || T > c->Tmax) {
+        set_err("gmoe_forward_host: n_tokens %d outside 1..%d", T, c->Tmax);
+        return GMOE_ERR_INVALID;
+    }
+    HIP_OK(hipSetDevice(c->device));
+    const size_t bytes = (size_t)T * c->D * sizeof(float);
+    HIP_OK(hipMemcpy(c->x_host_io, x_in, bytes, hipMemcpyHostToDevice));
+    int rc = gmoe_forward(c, layer, T, c->x_host_io, c->x_host_io, flags, nullptr);
+    if (rc) return rc;
+    HIP_OK(hipMemcpy(x_out, c->x_host_io, bytes, hipMemcpyDeviceToHost));
+    if (state) return gmoe_read_layer_state(c, state, nullptr);
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_read_layer_state(gmoe_ctx *c, gmoe_layer_state *o, void *stream) {
+    if (!c || !o) {
+        set_err("gmoe_read_layer_state: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    if (c->last_layer < 0) {
+        set_err("gmoe_read_layer_state: no forward has run");
+        return GMOE_ERR_INVALID;
+    }
+    HIP_OK(hipSetDevice(c->device));
+    hipStream_t st = (hipStream_t)stream;
+    const size_t T = c->last_T, D = c->D, E = c->E, K = c->K;
+    if ((o->expert_offsets || o->expert_tokens) && !c->last_dispatched) {
+        int rc = launch_dispatch(c, (int)T, st);
+        if (rc) return rc;
+    }
+    HIP_OK(hipStreamSynchronize(st));
+    int rc = GMOE_OK;
+    rc |= copy_out(o->xn, c->xn, T * D * sizeof(float));
+    rc |= copy_out(o->router_prob, c->router_prob, T * E * sizeof(float));
+    rc |= copy_out(o->topk_idx, c->topk_idx, T * K * sizeof(int));
+    rc |= copy_out(o->topk_w, c->topk_w, T * K * sizeof(float));
+    rc |= copy_out(o->shared_out, c->shared_out, T * D * sizeof(float));
+    rc |= copy_out(o->routed_out, c->routed_out, T * D * sizeof(float));
+    rc |= copy_out(o->expert_offsets, c->offsets, (E + 1) * sizeof(int));
+    if (o->expert_tokens) {
+        int total = 0;
+        if (hipMemcpy(&total, c->offsets + E, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return GMOE_ERR_HIP;
+        rc |= copy_out(o->expert_tokens, c->tokens, (size_t)total * sizeof(int));
+    }
+    return rc ? GMOE_ERR_HIP : GMOE_OK;
+}
+
+extern "C" int gmoe_read_topk(gmoe_ctx *c, int layer, int32_t *idx, float *w, void *stream) {
+    if (!c || layer < 1 || layer >= c->L) {
+        set_err("gmoe_read_topk: bad arguments");
+        return GMOE_ERR_INVALID;
+    }
+    HIP_OK(hipSetDevice(c->device));
+    HIP_OK(hipStreamSynchronize((hipStream_t)stream));
+    const size_t n = (size_t)c->layers[layer].last_T * c->K;
+    const size_t off = (size_t)layer * c->Tmax * c->K;
+    int rc = copy_out(idx, c->hist_idx + off, n * sizeof(int));
+    if (!rc) rc = copy_out(w, c->hist_w + off, n * sizeof(float));
+    return rc;
+}
+
+extern "C" int gmoe_get_stats(gmoe_ctx *c, gmoe_stats *o) {
+    if (!c || !o) {
+        set_err("gmoe_get_stats: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    HIP_OK(hipSetDevice(c->device));
+    unsigned long long s[GM_STAT_COUNT] = {0};
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemcpy(s, c->stats_dev, sizeof(s), hipMemcpyDeviceToHost));
+    o->tokens_routed = c->tokens_routed;
+    o->routing_exact_path = (int64_t)s[GM_STAT_ROUTE_EXACT];
+    o->routing_unresolved = (int64_t)s[GM_STAT_UNRESOLVED];
+    o->norm_exact_path = (int64_t)s[GM_STAT_NORM_EXACT];
+    o->scale_inexact = c->scale_inexact;
+    return GMOE_OK;
+}
+
+extern "C" int64_t gmoe_expert_bytes_last(gmoe_ctx *c) {
+    if (!c || c->last_layer < 0) return 0;
+    const size_t n = (size_t)c->last_T * c->K;
+    int *idx = (int *)malloc(n * sizeof(int));
+    if (!idx) return 0;
+    if (hipSetDevice(c->device) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(idx, c->topk_idx, n * sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) {
+        free(idx);
+        return 0;
+    }
+    unsigned char used[GM_MAX_E] = {0};
+    int n_used = 0;
+    if (!(c->last_flags & GMOE_FLAG_NO_ROUTED)) {
+        for (size_t i = 0; i < n; i++) {
+            if (idx[i] >= 0 && idx[i] < c->E && !used[idx[i]]) {
+                used[idx[i]] = 1;
+                n_used++;
+            }
+        }
+    }
+    free(idx);
+    const int64_t per_expert = (int64_t)3 * c->F * c->D / GM_QBLOCK * (GM_QBLOCK + 2);
+    return (int64_t)(n_used + c->S) * per_expert;
+}

@@ -1,0 +1,410 @@
+"""ctypes bindings for the MI355X MoE FFN path.
+
+libgmoe.so      kernels behind the C ABI of include/gmoe.h
+libglm_hip.so   C host side: glm.c's backend interface with BACKEND_HIP
+                (include/glm_backend.h) and the synthetic-input generator
+
+This module is plumbing for tests and the benchmark: it allocates host arrays
+in glm.c's checkpoint layout (model.h:65-84) and hands raw pointers to the C
+ABI. It never computes a result itself, and it raises if the native libraries
+are missing: there is no fallback path.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBGMOE = os.path.join(HERE, "libgmoe.so")
+LIBHOST = os.path.join(HERE, "libglm_hip.so")
+
+GMOE_FLAG_NO_ROUTED = 1
+SYNTH_NORM_ONES, SYNTH_NORM_RANDOM = 0, 1
+SYNTH_BIAS_NORMAL, SYNTH_BIAS_ZIPF = 0, 1
+
+# Zipf-shaped router bias for the skewed-routing workload: popularity ~ rank^-1.2,
+# gain chosen so the 4 most popular experts take about 40% of top-4 assignments.
+ZIPF_S = 1.2
+ZIPF_BETA = 0.06
+
+
+class GmoeConfig(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("moe_ffn_dim", C.c_int32), ("n_routed_experts", C.c_int32),
+                ("n_experts_used", C.c_int32), ("n_shared_experts", C.c_int32), ("group_size", C.c_int32),
+                ("n_layers", C.c_int32), ("max_tokens", C.c_int32), ("routed_scale", C.c_float),
+                ("norm_eps", C.c_float)]
+
+
+_LAYER_FIELDS = ["ffn_norm", "gate_inp", "exp_probs_b", "gate_sh_q", "gate_sh_s", "up_sh_q", "up_sh_s",
+                 "down_sh_q", "down_sh_s", "gate_q", "gate_s", "up_q", "up_s", "down_q", "down_s"]
+
+
+class LayerWeights(C.Structure):
+    """gmoe_layer_weights / oracle_layer / synth_layer_buffers: 15 pointers, same order."""
+    _fields_ = [(n, C.c_void_p) for n in _LAYER_FIELDS]
+
+
+class GmoeLayerState(C.Structure):
+    _fields_ = [("xn", C.c_void_p), ("router_prob", C.c_void_p), ("topk_idx", C.c_void_p), ("topk_w", C.c_void_p),
+                ("shared_out", C.c_void_p), ("routed_out", C.c_void_p), ("expert_offsets", C.c_void_p),
+                ("expert_tokens", C.c_void_p)]
+
+
+class GmoeStats(C.Structure):
+    _fields_ = [("tokens_routed", C.c_int64), ("routing_exact_path", C.c_int64), ("routing_unresolved", C.c_int64),
+                ("norm_exact_path", C.c_int64), ("scale_inexact", C.c_int64)]
+
+
+class SynthSpec(C.Structure):
+    _fields_ = [("seed", C.c_uint64), ("dim", C.c_int32), ("moe_ffn_dim", C.c_int32),
+                ("n_routed_experts", C.c_int32), ("group_size", C.c_int32), ("norm_mode", C.c_int32),
+                ("bias_mode", C.c_int32), ("zipf_s", C.c_double), ("zipf_beta", C.c_double)]
+
+
+_libs = {}
+
+
+def _load(path, what):
+    if path in _libs:
+        return _libs[path]
+    if not os.path.exists(path):
+        raise RuntimeError(f"{what} not built: {path} is missing (run __graft_entry__.build())")
+    lib = C.CDLL(path, mode=C.RTLD_GLOBAL)
+    _libs[path] = lib
+    return lib
+
+
+def host_lib():
+    lib = _load(LIBHOST, "host library")
+    if not getattr(lib, "_typed", False):
+        lib.synth_layer.argtypes = [C.POINTER(SynthSpec), C.c_int, C.c_int, C.c_int, C.POINTER(LayerWeights)]
+        lib.synth_layer.restype = C.c_int
+        lib.synth_activations.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_void_p]
+        lib.synth_activations.restype = None
+        lib.synth_round_fp16.argtypes = [C.c_float]
+        lib.synth_round_fp16.restype = C.c_float
+        lib.synth_key.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int]
+        lib.synth_key.restype = C.c_uint64
+        lib.synth_draw.argtypes = [C.c_uint64, C.c_uint64]
+        lib.synth_draw.restype = C.c_uint64
+        lib.synth_q8_at.argtypes = [C.c_uint64, C.c_uint64]
+        lib.synth_q8_at.restype = C.c_int
+        lib.synth_normal_at.argtypes = [C.c_uint64, C.c_uint64]
+        lib.synth_normal_at.restype = C.c_double
+        lib._typed = True
+    return lib
+
+
+def gmoe_lib():
+    lib = _load(LIBGMOE, "HIP library")
+    if not getattr(lib, "_typed", False):
+        P = C.c_void_p
+        lib.gmoe_create.argtypes = [C.POINTER(P), C.c_int, C.POINTER(GmoeConfig)]
+        lib.gmoe_upload_layer.argtypes = [P, C.c_int, C.POINTER(LayerWeights)]
+        lib.gmoe_forward.argtypes = [P, C.c_int, C.c_int, P, P, C.c_int, P]
+        lib.gmoe_forward_layers.argtypes = [P, C.c_int, C.c_int, C.c_int, P, P, C.c_int, P]
+        lib.gmoe_read_layer_state.argtypes = [P, C.POINTER(GmoeLayerState), P]
+        lib.gmoe_read_topk.argtypes = [P, C.c_int, P, P, P]
+        lib.gmoe_get_stats.argtypes = [P, C.POINTER(GmoeStats)]
+        lib.gmoe_expert_bytes_last.argtypes = [P]
+        lib.gmoe_expert_bytes_last.restype = C.c_int64
+        lib.gmoe_destroy.argtypes = [P]
+        lib.gmoe_destroy.restype = None
+        lib.gmoe_last_error.argtypes = []
+        lib.gmoe_last_error.restype = C.c_char_p
+        for f in ("gmoe_create", "gmoe_upload_layer", "gmoe_forward", "gmoe_forward_layers",
+                  "gmoe_read_layer_state", "gmoe_read_topk", "gmoe_get_stats"):
+            getattr(lib, f).restype = C.c_int
+        lib._typed = True
+    return lib
+
+
+def ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class Shape:
+    """MoE layer shape (RuntimeConfig fields, model.h:7-45)."""
+
+    def __init__(self, dim=2048, moe_ffn_dim=1536, n_routed_experts=64, n_experts_used=4, group_size=32):
+        self.D, self.F, self.E, self.K, self.gs = dim, moe_ffn_dim, n_routed_experts, n_experts_used, group_size
+
+    def expert_bytes(self):
+        """Algorithmic Q8_0 bytes of one expert (three matrices, 34 bytes per 32 weights)."""
+        return 3 * self.F * self.D * 34 // 32
+
+
+GLM47_FLASH = Shape()
+
+
+class HostLayer:
+    """One MoE layer's weights in glm.c's checkpoint layout, as numpy arrays.
+
+    Arrays come from np.zeros, so routed experts that are never generated cost
+    no resident memory."""
+
+    def __init__(self, shape, seed=0, layer=1, experts=None, norm_mode=SYNTH_NORM_ONES,
+                 bias_mode=SYNTH_BIAS_NORMAL, zipf_s=ZIPF_S, zipf_beta=ZIPF_BETA, routed=True):
+        s = shape
+        self.shape, self.seed, self.layer = s, seed, layer
+        D, F, E, gs = s.D, s.F, s.E, s.gs
+        self.ffn_norm = np.zeros(D, np.float32)
+        self.gate_inp = np.zeros((E, D), np.float32)
+        self.exp_probs_b = np.zeros(E, np.float32)
+        self.gate_sh_q = np.zeros((F, D), np.int8)
+        self.gate_sh_s = np.zeros((F, D // gs), np.float32)
+        self.up_sh_q = np.zeros((F, D), np.int8)
+        self.up_sh_s = np.zeros((F, D // gs), np.float32)
+        self.down_sh_q = np.zeros((D, F), np.int8)
+        self.down_sh_s = np.zeros((D, F // gs), np.float32)
+        if routed:
+            self.gate_q = np.zeros((E, F, D), np.int8)
+            self.gate_s = np.zeros((E, F, D // gs), np.float32)
+            self.up_q = np.zeros((E, F, D), np.int8)
+            self.up_s = np.zeros((E, F, D // gs), np.float32)
+            self.down_q = np.zeros((E, D, F), np.int8)
+            self.down_s = np.zeros((E, D, F // gs), np.float32)
+        else:
+            self.gate_q = self.gate_s = self.up_q = self.up_s = self.down_q = self.down_s = None
+        spec = SynthSpec(seed, D, F, E, gs, norm_mode, bias_mode, zipf_s, zipf_beta)
+        e0, e1 = (0, E) if experts is None else experts
+        if not routed:
+            e0 = e1 = 0
+        rc = host_lib().synth_layer(C.byref(spec), layer, e0, e1, C.byref(self.weights()))
+        if rc != 0:
+            raise RuntimeError("synth_layer failed")
+
+    def weights(self):
+        return LayerWeights(*[ptr(getattr(self, n)) for n in _LAYER_FIELDS])
+
+
+def activations(seed, stream, n_tokens, dim):
+    x = np.empty((n_tokens, dim), np.float32)
+    host_lib().synth_activations(seed, stream, n_tokens, dim, ptr(x))
+    return x
+
+
+def last_error():
+    e = gmoe_lib().gmoe_last_error()
+    return e.decode() if e else ""
+
+
+def check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
+
+
+class Context:
+    """A gmoe_ctx: weights resident on one device, forward calls on device pointers."""
+
+    def __init__(self, shape, n_layers, max_tokens, device=0, routed_scale=1.8, norm_eps=1e-5, n_shared=1):
+        self.lib = gmoe_lib()
+        self.shape = shape
+        self.max_tokens = max_tokens
+        cfg = GmoeConfig(shape.D, shape.F, shape.E, shape.K, n_shared, shape.gs, n_layers, max_tokens,
+                         routed_scale, norm_eps)
+        h = C.c_void_p()
+        check(self.lib.gmoe_create(C.byref(h), device, C.byref(cfg)), "gmoe_create")
+        self.h = h
+
+    def upload(self, layer, host_layer):
+        check(self.lib.gmoe_upload_layer(self.h, layer, C.byref(host_layer.weights())), "gmoe_upload_layer")
+
+    def forward(self, layer, n_tokens, x_in_dev, x_out_dev, flags=0, stream=None):
+        check(self.lib.gmoe_forward(self.h, layer, n_tokens, x_in_dev, x_out_dev, flags, stream), "gmoe_forward")
+
+    def forward_layers(self, first, n_layers, n_tokens, x_in_dev, x_out_dev, flags=0, stream=None):
+        check(self.lib.gmoe_forward_layers(self.h, first, n_layers, n_tokens, x_in_dev, x_out_dev, flags, stream),
+              "gmoe_forward_layers")
+
+    def read_state(self, n_tokens, stream=None):
+        s = self.shape
+        out = {
+            "xn": np.zeros((n_tokens, s.D), np.float32),
+            "router_prob": np.zeros((n_tokens, s.E), np.float32),
+            "topk_idx": np.zeros((n_tokens, s.K), np.int32),
+            "topk_w": np.zeros((n_tokens, s.K), np.float32),
+            "shared_out": np.zeros((n_tokens, s.D), np.float32),
+            "routed_out": np.zeros((n_tokens, s.D), np.float32),
+            "expert_offsets": np.zeros(s.E + 1, np.int32),
+            "expert_tokens": np.zeros(max(1, n_tokens * s.K), np.int32),
+        }
+        st = GmoeLayerState(*[ptr(out[n]) for n, _ in GmoeLayerState._fields_])
+        check(self.lib.gmoe_read_layer_state(self.h, C.byref(st), stream), "gmoe_read_layer_state")
+        return out
+
+    def read_topk(self, layer, n_tokens, stream=None):
+        idx = np.zeros((n_tokens, self.shape.K), np.int32)
+        w = np.zeros((n_tokens, self.shape.K), np.float32)
+        check(self.lib.gmoe_read_topk(self.h, layer, ptr(idx), ptr(w), stream), "gmoe_read_topk")
+        return idx, w
+
+    def stats(self):
+        st = GmoeStats()
+        check(self.lib.gmoe_get_stats(self.h, C.byref(st)), "gmoe_get_stats")
+        return {n: getattr(st, n) for n, _ in GmoeStats._fields_}
+
+    def expert_bytes_last(self):
+        return int(self.lib.gmoe_expert_bytes_last(self.h))
+
+    def close(self):
+        if self.h:
+            self.lib.gmoe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- HIP runtime (ctypes)
+_hip = None
+HIP_H2D, HIP_D2H, HIP_D2D = 1, 2, 3
+
+
+def hip():
+    """libamdhip64 with the few entry points the tests and the benchmark need."""
+    global _hip
+    if _hip is not None:
+        return _hip
+    lib = C.CDLL("libamdhip64.so", mode=C.RTLD_GLOBAL)
+    P = C.c_void_p
+    sig = {
+        "hipGetDeviceCount": [C.POINTER(C.c_int)],
+        "hipSetDevice": [C.c_int],
+        "hipMalloc": [C.POINTER(P), C.c_size_t],
+        "hipFree": [P],
+        "hipMemcpy": [P, P, C.c_size_t, C.c_int],
+        "hipMemset": [P, C.c_int, C.c_size_t],
+        "hipDeviceSynchronize": [],
+        "hipStreamCreate": [C.POINTER(P)],
+        "hipStreamDestroy": [P],
+        "hipStreamSynchronize": [P],
+        "hipEventCreate": [C.POINTER(P)],
+        "hipEventDestroy": [P],
+        "hipEventRecord": [P, P],
+        "hipEventSynchronize": [P],
+        "hipEventElapsedTime": [C.POINTER(C.c_float), P, P],
+        "hipStreamBeginCapture": [P, C.c_int],
+        "hipStreamEndCapture": [P, C.POINTER(P)],
+        "hipGraphInstantiate": [C.POINTER(P), P, P, P, C.c_size_t],
+        "hipGraphLaunch": [P, P],
+        "hipGraphExecDestroy": [P],
+        "hipGraphDestroy": [P],
+    }
+    for name, args in sig.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = C.c_int
+    lib.hipGetErrorString.argtypes = [C.c_int]
+    lib.hipGetErrorString.restype = C.c_char_p
+    _hip = lib
+    return lib
+
+
+def hip_check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {hip().hipGetErrorString(rc).decode()}")
+
+
+def device_count():
+    n = C.c_int(0)
+    rc = hip().hipGetDeviceCount(C.byref(n))
+    return n.value if rc == 0 else 0
+
+
+class DeviceArray:
+    """A hipMalloc'd buffer with numpy copy in/out."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        hip_check(hip().hipMalloc(C.byref(p), max(1, self.nbytes)), "hipMalloc")
+        self.ptr = p
+
+    @classmethod
+    def from_numpy(cls, a):
+        a = np.ascontiguousarray(a)
+        d = cls(a.nbytes)
+        d.upload(a)
+        return d
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        hip_check(hip().hipMemcpy(self.ptr, a.ctypes.data_as(C.c_void_p), a.nbytes, HIP_H2D), "hipMemcpy H2D")
+
+    def download(self, shape, dtype):
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        hip_check(hip().hipMemcpy(out.ctypes.data_as(C.c_void_p), self.ptr, out.nbytes, HIP_D2H), "hipMemcpy D2H")
+        return out
+
+    def free(self):
+        if self.ptr:
+            hip().hipFree(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        s = C.c_void_p()
+        hip_check(hip().hipStreamCreate(C.byref(s)), "hipStreamCreate")
+        self.h = s
+
+    def sync(self):
+        hip_check(hip().hipStreamSynchronize(self.h), "hipStreamSynchronize")
+
+
+class Event:
+    def __init__(self):
+        e = C.c_void_p()
+        hip_check(hip().hipEventCreate(C.byref(e)), "hipEventCreate")
+        self.h = e
+
+    def record(self, stream=None):
+        hip_check(hip().hipEventRecord(self.h, stream.h if stream else None), "hipEventRecord")
+
+    def elapsed_ms(self, end):
+        hip_check(hip().hipEventSynchronize(end.h), "hipEventSynchronize")
+        ms = C.c_float()
+        hip_check(hip().hipEventElapsedTime(C.byref(ms), self.h, end.h), "hipEventElapsedTime")
+        return ms.value
+
+
+def forward_host(ctx, layer, x, flags=0, with_state=True):
+    """Run one layer on host activations through gmoe_forward_host; returns (x_out, state)."""
+    lib = ctx.lib
+    x = np.ascontiguousarray(x, np.float32)
+    T = x.shape[0]
+    s = ctx.shape
+    out = np.empty_like(x)
+    st = None
+    state_p = None
+    if with_state:
+        st = {
+            "xn": np.zeros((T, s.D), np.float32),
+            "router_prob": np.zeros((T, s.E), np.float32),
+            "topk_idx": np.zeros((T, s.K), np.int32),
+            "topk_w": np.zeros((T, s.K), np.float32),
+            "shared_out": np.zeros((T, s.D), np.float32),
+            "routed_out": np.zeros((T, s.D), np.float32),
+            "expert_offsets": np.zeros(s.E + 1, np.int32),
+            "expert_tokens": np.zeros(max(1, T * s.K), np.int32),
+        }
+        state_p = C.byref(GmoeLayerState(*[ptr(st[n]) for n, _ in GmoeLayerState._fields_]))
+    lib.gmoe_forward_host.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+    lib.gmoe_forward_host.restype = C.c_int
+    check(lib.gmoe_forward_host(ctx.h, layer, T, ptr(x), ptr(out), flags, state_p), "gmoe_forward_host")
+    if st is not None:
+        n = int(st["expert_offsets"][-1])
+        st["expert_tokens"] = st["expert_tokens"][:n]
+    return out, st

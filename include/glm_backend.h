@@ -1,0 +1,53 @@
+/*
+ * glm_backend.h -- glm.c's backend interface (backend.h:1-15) with a HIP backend.
+ *
+ * The first three functions keep the signatures and contracts of backend.h:7-9:
+ *   glm_backend_init     returns the "use gpu" handle (0 = CPU, BACKEND_HIP = HIP) and
+ *                        exits the process when the requested backend cannot start,
+ *                        as backend.c:73-86 does for Metal;
+ *   glm_backend_forward_token  0 on success, nonzero on failure (backend.c:88-91);
+ *   glm_backend_free.
+ * glm_backend_try_hip_moe is the HIP counterpart of the per-op offload hook
+ * glm_backend_try_metal_matvec (backend.h:13, called at infer.c:793): it runs one
+ * whole MoE FFN layer (infer.c:1087-1216) on the GPU and returns 0, or returns -1 so
+ * that the caller runs apply_moe_shared_ffn_layer on the CPU.
+ * The glm_hip_* functions follow the backend-private pattern of backend.c:9-14.
+ */
+#ifndef GLM_BACKEND_H
+#define GLM_BACKEND_H
+
+#include <stdint.h>
+
+#include "glm_model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int glm_backend_init(BackendType backend, const Runtime *rt, RunState *st);
+int glm_backend_forward_token(int use_gpu, const Runtime *rt, RunState *st, int token, int pos, int debug_mode);
+void glm_backend_free(int use_gpu);
+
+/* backend.h:11-13. There is no Metal device here: matvec offload always declines (-1),
+ * so infer.c:792-797 keeps its CPU matvec. Kept so this file can stand in for backend.c. */
+void glm_set_metal_matvec_mode(int enabled);
+int glm_backend_metal_matvec_enabled(void);
+int glm_backend_try_metal_matvec(const int8_t *qmat, const float *smat, const float *x, float *y, int rows, int dim,
+                                 int gs);
+
+/* 0 if the HIP backend ran MoE layer `layer_idx` on `st` (filling x, xn, xb,
+ * moe_router, moe_topk_idx, moe_topk_w, moe_out_acc as infer.c:1087-1216 does);
+ * -1 if the HIP backend is not active or failed, so the CPU path must run it. */
+int glm_backend_try_hip_moe(const Runtime *rt, RunState *st, int layer_idx, int debug_mode);
+
+/* HIP backend private API (mirrors glm_metal_* in backend.c:9-14). */
+int glm_hip_init(const Runtime *rt, RunState *st);      /* 0 ok, -1 failure; idempotent */
+int glm_hip_prepare(const Runtime *rt, RunState *st);   /* uploads MoE layers 1..n_layers-1; 0 ok */
+int glm_hip_moe_layer(const Runtime *rt, RunState *st, int layer_idx, int debug_mode); /* 0 ok, -1 error */
+void glm_hip_free(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,148 @@
+/*
+ * gmoe.h -- C ABI of the MI355X MoE FFN library (libgmoe.so, built by hipcc for gfx950).
+ *
+ * One call of gmoe_forward() replaces one call of glm.c's
+ *   apply_moe_shared_ffn_layer(rt, st, gs, layer_idx, debug_mode, pos)   (infer.c:1087-1216)
+ * for a batch of T tokens whose activations already sit in device memory:
+ *   xn   = rmsnorm(x, ffn_norm)                                 infer.c:1098, 746-752
+ *   p    = sigmoid(gate_inp . xn)                               infer.c:1103-1107, 927-938
+ *   top-k of p + exp_probs_b, weights p / sum(p)                infer.c:1110-1145
+ *   acc  = sum_k 1.8 * w_k * down_k(silu(gate_k xn) * up_k xn)  infer.c:1166-1195
+ *   xb   = down_sh(silu(gate_sh xn) * up_sh xn)                 infer.c:1197-1206
+ *   x   += xb + acc                                             infer.c:1212-1214
+ * Router top-k indices, and for T > 1 the per-expert token lists, equal the CPU
+ * path's exactly; the float outputs match it to fp32-accumulation accuracy.
+ *
+ * The ABI uses plain pointers and sizes only. Device pointers are HIP device
+ * addresses; `stream` is a hipStream_t passed as void* (NULL = default stream).
+ * Every function returns 0 on success and a negative GMOE_ERR_* code on failure,
+ * with a message available from gmoe_last_error(). No function calls exit().
+ * A context is single-threaded: calls on one context must not overlap.
+ */
+#ifndef GMOE_H
+#define GMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GMOE_OK 0
+#define GMOE_ERR_INVALID (-1)   /* bad argument, shape or state */
+#define GMOE_ERR_HIP (-2)       /* a HIP runtime call failed */
+#define GMOE_ERR_NOMEM (-3)     /* device or host allocation failed */
+#define GMOE_ERR_SCALE (-4)     /* a weight scale is not representable in the device format */
+
+/* forward() flags */
+#define GMOE_FLAG_NO_ROUTED 1   /* skip routed experts, as GLM_DISABLE_MOE_ROUTED=1 does (infer.c:1161-1166) */
+
+typedef struct gmoe_ctx gmoe_ctx;
+
+/* Model shape. Field meanings follow RuntimeConfig (model.h:7-45). */
+typedef struct gmoe_config {
+    int32_t dim;               /* hidden size D (model.h:9); multiple of 64 */
+    int32_t moe_ffn_dim;       /* expert intermediate F (model.h:44); multiple of 64 */
+    int32_t n_routed_experts;  /* E (model.h:21); 1..256 */
+    int32_t n_experts_used;    /* K (model.h:22); 1..8 */
+    int32_t n_shared_experts;  /* S (model.h:23); 0 or 1 */
+    int32_t group_size;        /* quantisation group (model.h:26); must be 32 */
+    int32_t n_layers;          /* total layers; MoE layers are 1..n_layers-1 (infer.c:1844-1845) */
+    int32_t max_tokens;        /* largest n_tokens passed to the forward calls */
+    float routed_scale;        /* routed expert scale, hard-coded 1.8f at infer.c:1171 */
+    float norm_eps;            /* rmsnorm epsilon, 1e-5f at infer.c:750 */
+} gmoe_config;
+
+/* Host-side weights of one MoE layer in glm.c's checkpoint layout:
+ * LayerMoeShared (model.h:65-75) followed by LayerMoeRouted (model.h:77-84).
+ * Q8 matrices are int8 [rows][cols] with fp32 scales [rows][cols/group_size];
+ * routed tensors hold all E experts back to back (infer.c:707-739, 1177-1182). */
+typedef struct gmoe_layer_weights {
+    const float *ffn_norm;     /* [D] */
+    const float *gate_inp;     /* [E][D] fp32 router */
+    const float *exp_probs_b;  /* [E] selection bias */
+    const int8_t *gate_sh_q;   /* [F][D] */
+    const float *gate_sh_s;    /* [F][D/gs] */
+    const int8_t *up_sh_q;     /* [F][D] */
+    const float *up_sh_s;      /* [F][D/gs] */
+    const int8_t *down_sh_q;   /* [D][F] */
+    const float *down_sh_s;    /* [D][F/gs] */
+    const int8_t *gate_q;      /* [E][F][D] */
+    const float *gate_s;       /* [E][F][D/gs] */
+    const int8_t *up_q;        /* [E][F][D] */
+    const float *up_s;         /* [E][F][D/gs] */
+    const int8_t *down_q;      /* [E][D][F] */
+    const float *down_s;       /* [E][D][F/gs] */
+} gmoe_layer_weights;
+
+/* Host copies of one layer's observable intermediates, the RunState MoE fields
+ * of infer.c:855-862 widened to T tokens. Any pointer may be NULL. */
+typedef struct gmoe_layer_state {
+    float *xn;                 /* [T][D]   rmsnorm output (RunState.xn) */
+    float *router_prob;        /* [T][E]   sigmoid router probabilities (RunState.moe_router) */
+    int32_t *topk_idx;         /* [T][K]   selected experts, best first (RunState.moe_topk_idx) */
+    float *topk_w;             /* [T][K]   normalised weights before routed_scale (RunState.moe_topk_w) */
+    float *shared_out;         /* [T][D]   shared expert output (RunState.xb after the layer) */
+    float *routed_out;         /* [T][D]   weighted routed sum (RunState.moe_out_acc) */
+    int32_t *expert_offsets;   /* [E+1]    per-expert token list offsets */
+    int32_t *expert_tokens;    /* [T*K]    token ids per expert, ascending within each expert */
+} gmoe_layer_state;
+
+/* Counters over the life of a context. */
+typedef struct gmoe_stats {
+    int64_t tokens_routed;       /* token-layer routings performed */
+    int64_t routing_exact_path;  /* routings that needed the exact sequential-fp32 router replay */
+    int64_t routing_unresolved;  /* routings whose order still hinged on the last bit of libm expf */
+    int64_t norm_exact_path;     /* rmsnorms that needed the exact sequential-fp64 sum replay */
+    int64_t scale_inexact;       /* weight scales that were not fp16-exact at upload */
+} gmoe_stats;
+
+/* Create a context on HIP device `device` and reserve device memory for
+ * cfg->n_layers - 1 MoE layers and cfg->max_tokens tokens. */
+int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg);
+
+/* Upload and repack one MoE layer (1 <= layer < n_layers) from host memory into
+ * the device layout. Scales must be fp16-representable (checked; GMOE_ERR_SCALE). */
+int gmoe_upload_layer(gmoe_ctx *ctx, int layer, const gmoe_layer_weights *w);
+
+/* One MoE layer for n_tokens tokens: x_out = x_in + shared + routed.
+ * x_in and x_out are device pointers to [n_tokens][D] fp32 and may alias. */
+int gmoe_forward(gmoe_ctx *ctx, int layer, int n_tokens, const float *x_in, float *x_out,
+                 int flags, void *stream);
+
+/* Layers first_layer .. first_layer+n_layers-1 in sequence, the MoE part of the
+ * decode loop at infer.c:1818-1860. Device pointers; may alias. */
+int gmoe_forward_layers(gmoe_ctx *ctx, int first_layer, int n_layers, int n_tokens,
+                        const float *x_in, float *x_out, int flags, void *stream);
+
+/* Host-memory form of gmoe_forward for callers that make no HIP calls themselves,
+ * such as glm.c's C host: copies x_in ([n_tokens][D] fp32, host) to the device, runs
+ * the layer on the default stream, copies the result to x_out (host, may alias x_in)
+ * and, when `state` is not NULL, the layer's intermediates. Synchronous. */
+int gmoe_forward_host(gmoe_ctx *ctx, int layer, int n_tokens, const float *x_in, float *x_out, int flags,
+                      gmoe_layer_state *state);
+
+/* Copy the intermediates of the most recent gmoe_forward() call to host memory
+ * (synchronises `stream`). expert_offsets/expert_tokens are filled for every T. */
+int gmoe_read_layer_state(gmoe_ctx *ctx, gmoe_layer_state *out, void *stream);
+
+/* Copy the top-k routing of `layer` from its most recent forward to host memory
+ * ([n_tokens][K] each; either pointer may be NULL). Synchronises `stream`. */
+int gmoe_read_topk(gmoe_ctx *ctx, int layer, int32_t *topk_idx, float *topk_w, void *stream);
+
+int gmoe_get_stats(gmoe_ctx *ctx, gmoe_stats *out);
+
+/* Algorithmic Q8_0 bytes (34 per 32 weights) that one forward of n_tokens reads
+ * for its experts, given the routing of its most recent call; used for GB/s. */
+int64_t gmoe_expert_bytes_last(gmoe_ctx *ctx);
+
+void gmoe_destroy(gmoe_ctx *ctx);
+
+const char *gmoe_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

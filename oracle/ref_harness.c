@@ -1,0 +1,119 @@
+/*
+ * ORACLE (reference build) -- test infrastructure only (see oracle.h).
+ *
+ * Compiles glm.c's own infer.c into this translation unit, so that its static
+ * apply_moe_shared_ffn_layer (infer.c:1087-1216) can be driven on synthetic
+ * weights. The include path to the reference sources is supplied by
+ * oracle/Makefile; nothing from the reference is copied into this repository.
+ * The result, oracle/_ref/libref_moe.so, is built with the reference Makefile's
+ * compiler flags (Makefile:1-2, 89) and serves as the bitwise check of the
+ * restatement in moe_oracle.c and as the CPU baseline in bench.py.
+ */
+#include "infer.c"
+
+#include "oracle.h"
+
+/* A Runtime that holds only MoE layers 1..n_moe (layer 0 is the dense layer,
+ * never touched here), shaped like runtime_open leaves it (infer.c:640-743). */
+static void make_runtime(Runtime *rt, LayerMoeShared *sh, LayerMoeRouted *ro, const oracle_dims *d,
+                         const oracle_layer *layers, int n_moe) {
+    memset(rt, 0, sizeof(*rt));
+    rt->cfg.dim = d->dim;
+    rt->cfg.hidden_dim = d->group_size;
+    rt->cfg.n_layers = n_moe + 1;
+    rt->cfg.vocab_size = 1;
+    rt->cfg.seq_len = 1;
+    rt->cfg.n_routed_experts = d->n_routed_experts;
+    rt->cfg.n_experts_used = d->n_experts_used;
+    rt->cfg.n_shared_experts = 1;
+    rt->cfg.group_size = (uint64_t)d->group_size;
+    rt->cfg.moe_ffn_dim = d->moe_ffn_dim;
+    memset(&sh[0], 0, sizeof(sh[0]));
+    memset(&ro[0], 0, sizeof(ro[0]));
+    int routed = 1;
+    for (int l = 0; l < n_moe; l++) {
+        const oracle_layer *w = &layers[l];
+        LayerMoeShared *s = &sh[l + 1];
+        LayerMoeRouted *r = &ro[l + 1];
+        s->ffn_norm = w->ffn_norm;
+        s->gate_inp = w->gate_inp;
+        s->exp_probs_b = w->exp_probs_b;
+        s->gate_sh_q = w->gate_sh_q;
+        s->gate_sh_s = w->gate_sh_s;
+        s->up_sh_q = w->up_sh_q;
+        s->up_sh_s = w->up_sh_s;
+        s->down_sh_q = w->down_sh_q;
+        s->down_sh_s = w->down_sh_s;
+        r->gate_q = w->gate_q;
+        r->gate_s = w->gate_s;
+        r->up_q = w->up_q;
+        r->up_s = w->up_s;
+        r->down_q = w->down_q;
+        r->down_s = w->down_s;
+        if (!w->gate_q) routed = 0;
+    }
+    rt->has_moe_shared = 1;
+    rt->moe_layers = sh;
+    rt->has_moe_routed = routed;
+    rt->moe_routed_layers = ro;
+}
+
+int ref_moe_layer(const oracle_dims *d, const oracle_layer *w, int T, const float *x_in, const oracle_out *out,
+                  int disable_routed) {
+    if (!d || !w || !x_in || !out || T < 0) return -1;
+    Runtime rt;
+    LayerMoeShared sh[2];
+    LayerMoeRouted ro[2];
+    make_runtime(&rt, sh, ro, d, w, 1);
+    RunState st;
+    runstate_build(&st, &rt, 1);
+    if (disable_routed) setenv("GLM_DISABLE_MOE_ROUTED", "1", 1);
+    else unsetenv("GLM_DISABLE_MOE_ROUTED");
+    const int D = d->dim, E = d->n_routed_experts, K = d->n_experts_used;
+    const int gs = d->group_size;
+    for (int t = 0; t < T; t++) {
+        memcpy(st.x, x_in + (size_t)t * D, (size_t)D * sizeof(float));
+        apply_moe_shared_ffn_layer(&rt, &st, gs, 1, 0, 0);
+        if (out->x_out) memcpy(out->x_out + (size_t)t * D, st.x, (size_t)D * sizeof(float));
+        if (out->xn) memcpy(out->xn + (size_t)t * D, st.xn, (size_t)D * sizeof(float));
+        if (out->router_prob) memcpy(out->router_prob + (size_t)t * E, st.moe_router, (size_t)E * sizeof(float));
+        if (out->topk_idx)
+            for (int k = 0; k < K; k++) out->topk_idx[(size_t)t * K + k] = (int32_t)st.moe_topk_idx[k];
+        if (out->topk_w) memcpy(out->topk_w + (size_t)t * K, st.moe_topk_w, (size_t)K * sizeof(float));
+        if (out->shared_out) memcpy(out->shared_out + (size_t)t * D, st.xb, (size_t)D * sizeof(float));
+        if (out->routed_out) memcpy(out->routed_out + (size_t)t * D, st.moe_out_acc, (size_t)D * sizeof(float));
+    }
+    unsetenv("GLM_DISABLE_MOE_ROUTED");
+    runstate_free(&st);
+    return 0;
+}
+
+int ref_moe_stack(const oracle_dims *d, const oracle_layer *layers, int n_layers, int T, float *x, int32_t *topk_idx) {
+    if (!d || !layers || !x || n_layers < 0 || T < 0) return -1;
+    Runtime rt;
+    LayerMoeShared *sh = (LayerMoeShared *)calloc((size_t)n_layers + 1, sizeof(LayerMoeShared));
+    LayerMoeRouted *ro = (LayerMoeRouted *)calloc((size_t)n_layers + 1, sizeof(LayerMoeRouted));
+    if (!sh || !ro) {
+        free(sh);
+        free(ro);
+        return -1;
+    }
+    make_runtime(&rt, sh, ro, d, layers, n_layers);
+    RunState st;
+    runstate_build(&st, &rt, 1);
+    unsetenv("GLM_DISABLE_MOE_ROUTED");
+    const int D = d->dim, K = d->n_experts_used, gs = d->group_size;
+    for (int t = 0; t < T; t++) {
+        memcpy(st.x, x + (size_t)t * D, (size_t)D * sizeof(float));
+        for (int l = 1; l <= n_layers; l++) {
+            apply_moe_shared_ffn_layer(&rt, &st, gs, l, 0, 0);
+            if (topk_idx)
+                for (int k = 0; k < K; k++) topk_idx[((size_t)(l - 1) * T + t) * K + k] = (int32_t)st.moe_topk_idx[k];
+        }
+        memcpy(x + (size_t)t * D, st.x, (size_t)D * sizeof(float));
+    }
+    runstate_free(&st);
+    free(sh);
+    free(ro);
+    return 0;
+}

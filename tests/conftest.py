@@ -1,0 +1,55 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for sub in ("glm.c_amd", "oracle"):
+    p = os.path.join(ROOT, sub)
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (run with -m gpu)")
+
+
+# Parity bar for floating-point outputs (max-abs 1e-2 and rel-L2 1e-3, fp32 accumulation).
+MAX_ABS = 1e-2
+REL_L2 = 1e-3
+
+
+def assert_close(got, want, what, max_abs=MAX_ABS, rel_l2=REL_L2):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
+    assert np.all(np.isfinite(got)), f"{what}: non-finite values"
+    err = np.abs(got - want)
+    denom = np.linalg.norm(want)
+    rel = np.linalg.norm(got - want) / denom if denom > 0 else np.linalg.norm(got - want)
+    assert err.max() <= max_abs, f"{what}: max-abs {err.max():.3e} > {max_abs} (at {np.unravel_index(err.argmax(), err.shape)})"
+    assert rel <= rel_l2, f"{what}: rel-L2 {rel:.3e} > {rel_l2}"
+    return err.max(), rel
+
+
+@pytest.fixture(scope="session")
+def gpu_available():
+    import gmoe
+    try:
+        return gmoe.device_count() > 0
+    except OSError:
+        return False
+
+
+@pytest.fixture(autouse=True)
+def _require_gpu_for_gpu_tests(request):
+    if request.node.get_closest_marker("gpu") is not None:
+        import gmoe
+        n = 0
+        try:
+            n = gmoe.device_count()
+        except OSError:
+            pass
+        if n == 0:
+            pytest.fail("gpu test but no HIP device is visible")

@@ -1,0 +1,65 @@
+"""Decode (T=1 and small T) parity of the HIP MoE layer against the oracle.
+
+Each token of a batch is an independent decode step (infer.c:2190-2233), so a
+batch of T tokens checks T decode cases at once; T=1 is checked on its own too.
+Bar: top-k indices exact, xn bitwise (both pinned to glm.c's arithmetic), float
+outputs within max-abs 1e-2 and rel-L2 1e-3."""
+import numpy as np
+import pytest
+
+import gmoe
+import oracle
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+SMALL = gmoe.Shape(dim=256, moe_ffn_dim=128, n_routed_experts=16, n_experts_used=4)
+
+
+def run_case(shape, seed, T, norm_mode=gmoe.SYNTH_NORM_ONES, flags=0, layer=1):
+    print(f"[case] D={shape.D} F={shape.F} E={shape.E} K={shape.K} seed={seed} T={T} norm={norm_mode} flags={flags}",
+          flush=True)
+    L = gmoe.HostLayer(shape, seed=seed, layer=layer, norm_mode=norm_mode)
+    x = gmoe.activations(seed, 100 + layer, T, shape.D)
+    want = oracle.Oracle("port").layer(shape, L, x, disable_routed=bool(flags & gmoe.GMOE_FLAG_NO_ROUTED))
+    ctx = gmoe.Context(shape, n_layers=layer + 1, max_tokens=T)
+    try:
+        ctx.upload(layer, L)
+        got, st = gmoe.forward_host(ctx, layer, x, flags=flags)
+        stats = ctx.stats()
+    finally:
+        ctx.close()
+    return want, got, st, stats
+
+
+def check(want, got, st, stats):
+    np.testing.assert_array_equal(st["topk_idx"], want["topk_idx"], err_msg="top-k indices")
+    assert np.array_equal(st["xn"].view(np.uint32), want["xn"].view(np.uint32)), "xn not bit-identical"
+    assert_close(st["router_prob"], want["router_prob"], "router_prob", max_abs=1e-5, rel_l2=1e-5)
+    assert_close(st["topk_w"], want["topk_w"], "topk_w", max_abs=1e-5, rel_l2=1e-5)
+    assert_close(st["shared_out"], want["shared_out"], "shared_out")
+    assert_close(st["routed_out"], want["routed_out"], "routed_out")
+    assert_close(got, want["x_out"], "x_out")
+    assert stats["routing_unresolved"] == 0
+
+
+def test_small_t1():
+    check(*run_case(SMALL, seed=1, T=1))
+
+
+def test_small_batch_random_norm():
+    check(*run_case(SMALL, seed=2, T=16, norm_mode=gmoe.SYNTH_NORM_RANDOM))
+
+
+def test_small_no_routed():
+    want, got, st, stats = run_case(SMALL, seed=3, T=4, flags=gmoe.GMOE_FLAG_NO_ROUTED)
+    check(want, got, st, stats)
+    assert np.all(st["routed_out"] == 0)
+
+
+def test_glm_shape_t1():
+    check(*run_case(gmoe.GLM47_FLASH, seed=0, T=1))
+
+
+def test_glm_shape_batch8():
+    check(*run_case(gmoe.GLM47_FLASH, seed=5, T=8, norm_mode=gmoe.SYNTH_NORM_RANDOM))
