@@ -39,6 +39,11 @@ __host__ __device__ static inline size_t gm_s_offset(int r, int b, int cols) {
     return ((size_t)(r >> 4) * (size_t)(cols >> 5) + (size_t)b) * 16 + (size_t)(r & 15);
 }
 
+// Correctly rounded fp32 square root. The fp32 intrinsic lowers to v_sqrt_f32, which is
+// not always correctly rounded; the fp64 lowering is (Newton-refined), and rounding a
+// correctly rounded fp64 root to fp32 is exact-rounding since 53 >= 2*24 + 2.
+__device__ static inline float sqrt_rn_f32(float a) { return (float)sqrt((double)a); }
+
 // ---------------------------------------------------------------- reductions
 
 __device__ static inline double wave_sum_d(double v) {

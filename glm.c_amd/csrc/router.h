@@ -108,7 +108,7 @@ __global__ __launch_bounds__(RT_BLOCK) void k_norm_router(RouterArgs a) {
 
     // ---- RMSNorm, bit-identical to infer.c:746-752
     const float mean = certified_mean_sq(xt, D, red, &s_mean, e == 0, a.stats);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, a.eps)));
+    const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
     for (int i = tid; i < D; i += RT_BLOCK) {
         float v = __fmul_rn(__fmul_rn(xt[i], inv), a.norm_w[i]);
         s_xn[i] = v;
