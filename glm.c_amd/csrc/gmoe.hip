@@ -10,6 +10,8 @@
 
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <vector>
 #include <stdlib.h>
 #include <string.h>
 
@@ -18,6 +20,7 @@
 #include "experts.h"
 #include "repack.h"
 #include "router.h"
+#include "stack.h"
 
 static thread_local char g_err[512];
 
@@ -37,6 +40,8 @@ static void set_err(const char *fmt, ...) {
         }                                                                                \
     } while (0)
 
+#define GM_STACK_COUNTERS 256
+
 struct LayerDev {
     uint8_t *experts = nullptr;  // (E+1) * stride bytes, tiled
     float *norm = nullptr;       // [D]
@@ -47,8 +52,16 @@ struct LayerDev {
     int last_T = 0;
 };
 
+struct ProfRecord {
+    hipEvent_t start = nullptr, stop = nullptr;
+    int kernel = 0;
+};
+
 struct gmoe_ctx {
     int device = 0;
+    int prof_on = 0;
+    size_t prof_used = 0;
+    std::vector<ProfRecord> prof;
     gmoe_config cfg{};
     int D = 0, F = 0, E = 0, K = 0, S = 0, L = 0, Tmax = 0;
     size_t stride = 0, off_gq = 0, off_uq = 0, off_dq = 0, off_gs = 0, off_us = 0, off_ds = 0;
@@ -66,12 +79,21 @@ struct gmoe_ctx {
     unsigned long long *stats_dev = nullptr;
     float *x_host_io = nullptr;  // [T][D] device copy of gmoe_forward_host's activations
 
+    // persistent decode kernel (stack.h)
+    int stack_ok = 0;            // shape fits k_moe_stack
+    int stack_grid = 0;          // co-resident blocks
+    int8_t *sk_dig = nullptr;    // [3][D]
+    int *sk_dexp = nullptr;      // [D/32]
+    unsigned *sk_ctr = nullptr;  // [GM_STACK_COUNTERS]
+    int *sk_error = nullptr;
+    StackLayer *sk_layers = nullptr;  // [L], device
+
     uint8_t *staging = nullptr;
     size_t staging_bytes = 0;
 
     long long tokens_routed = 0;
     long long scale_inexact = 0;
-    int last_layer = -1, last_T = 0, last_flags = 0, last_dispatched = 0;
+    int last_layer = -1, last_T = 0, last_flags = 0, last_dispatched = 0, stack_launched = 0;
 };
 
 extern "C" const char *gmoe_last_error(void) { return g_err; }
@@ -96,6 +118,10 @@ static void dev_free(void *p) {
 static void free_ctx(gmoe_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
+    for (ProfRecord &r : c->prof) {
+        if (r.start) (void)hipEventDestroy(r.start);
+        if (r.stop) (void)hipEventDestroy(r.stop);
+    }
     if (c->layers) {
         for (int l = 0; l < c->L; l++) {
             dev_free(c->layers[l].experts);
@@ -108,7 +134,8 @@ static void free_ctx(gmoe_ctx *c) {
     void *bufs[] = {c->xn, c->router_prob, c->topk_w, c->topk_ws, c->h, c->y, c->shared_out, c->routed_out,
                     c->stage, c->topk_idx, c->tok_counter, c->panel_counter, c->disp_counter, c->disp_tmp_tok,
                     c->disp_tmp_slot, c->disp_counts, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
-                    c->stats_dev, c->x_host_io, c->staging};
+                    c->stats_dev, c->x_host_io, c->staging, c->sk_dig, c->sk_dexp, c->sk_ctr, c->sk_error,
+                    c->sk_layers};
     for (void *b : bufs) dev_free(b);
     delete c;
 }
@@ -200,6 +227,11 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     rc |= dev_alloc(&c->hist_w, (size_t)c->L * T * K);
     rc |= dev_alloc(&c->stats_dev, GM_STAT_COUNT);
     rc |= dev_alloc(&c->x_host_io, T * D);
+    rc |= dev_alloc(&c->sk_dig, 3 * D);
+    rc |= dev_alloc(&c->sk_dexp, D / 32);
+    rc |= dev_alloc(&c->sk_ctr, GM_STACK_COUNTERS);
+    rc |= dev_alloc(&c->sk_error, 1);
+    rc |= dev_alloc(&c->sk_layers, (size_t)c->L);
     if (rc != GMOE_OK) {
         free_ctx(c);
         return GMOE_ERR_NOMEM;
@@ -210,11 +242,31 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     hipError_t e2 = hipMemset(c->disp_counter, 0, sizeof(unsigned));
     hipError_t e3 = hipMemset(c->stats_dev, 0, GM_STAT_COUNT * sizeof(unsigned long long));
     hipError_t e4 = hipMemset(c->hist_idx, 0xff, (size_t)c->L * T * K * sizeof(int));
+    hipError_t e6 = hipMemset(c->sk_error, 0, sizeof(int));
+    hipError_t e7 = hipMemset(c->sk_layers, 0, (size_t)c->L * sizeof(StackLayer));
     hipError_t e5 = hipDeviceSynchronize();
-    if (e0 || e1 || e2 || e3 || e4 || e5) {
+    if (e0 || e1 || e2 || e3 || e4 || e5 || e6 || e7) {
         set_err("gmoe_create: initialising device buffers failed");
         free_ctx(c);
         return GMOE_ERR_HIP;
+    }
+    // The persistent decode kernel holds one panel's chunks per wave in registers and
+    // xn in shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots.
+    c->stack_ok = c->D <= 2048 && c->F <= 2048 && c->D % 256 == 0 && c->K + 1 <= SK_MAX_SLOTS &&
+                  SKC_PANEL + c->D / 16 <= GM_STACK_COUNTERS;
+    const char *env = getenv("GMOE_STACK_KERNEL");
+    if (env && env[0] == '0') c->stack_ok = 0;
+    if (c->stack_ok) {
+        int per_cu = 0, cus = 0;
+        hipDeviceProp_t prop;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_stack, SK_BLOCK, 0) != hipSuccess ||
+            hipGetDeviceProperties(&prop, device) != hipSuccess || per_cu < 1) {
+            c->stack_ok = 0;
+        } else {
+            cus = prop.multiProcessorCount;
+            const int want = per_cu < 2 ? per_cu : 2;  // 2 blocks (8 waves) per CU
+            c->stack_grid = want * cus;
+        }
     }
     *out = c;
     return GMOE_OK;
@@ -308,7 +360,63 @@ extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weight
         return GMOE_ERR_SCALE;
     }
     L.has_routed = has_routed;
+    StackLayer sl;
+    sl.experts = L.experts;
+    sl.norm = L.norm;
+    sl.gate_inp = L.gate_inp;
+    sl.bias = L.bias;
+    sl.has_routed = has_routed;
+    sl.pad = 0;
+    if ((rc = copy_in(c->sk_layers + layer, &sl, sizeof(sl)))) return rc;
     L.uploaded = 1;
+    return GMOE_OK;
+}
+
+// Event pair around one launch when profiling is on; returns the record or null.
+static ProfRecord *prof_begin(gmoe_ctx *c, hipStream_t st, int kernel) {
+    if (!c->prof_on) return nullptr;
+    if (c->prof_used == c->prof.size()) {
+        ProfRecord r;
+        if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return nullptr;
+        c->prof.push_back(r);
+    }
+    ProfRecord *r = &c->prof[c->prof_used++];
+    r->kernel = kernel;
+    (void)hipEventRecord(r->start, st);
+    return r;
+}
+
+static void prof_end(ProfRecord *r, hipStream_t st) {
+    if (r) (void)hipEventRecord(r->stop, st);
+}
+
+extern "C" int gmoe_profile(gmoe_ctx *c, int enable) {
+    if (!c) {
+        set_err("gmoe_profile: null context");
+        return GMOE_ERR_INVALID;
+    }
+    if (enable) c->prof_used = 0;
+    c->prof_on = enable ? 1 : 0;
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_profile_read(gmoe_ctx *c, gmoe_kernel_times *o) {
+    if (!c || !o) {
+        set_err("gmoe_profile_read: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    memset(o, 0, sizeof(*o));
+    HIP_OK(hipSetDevice(c->device));
+    for (size_t i = 0; i < c->prof_used; i++) {
+        ProfRecord &r = c->prof[i];
+        HIP_OK(hipEventSynchronize(r.stop));
+        float ms = 0.0f;
+        HIP_OK(hipEventElapsedTime(&ms, r.start, r.stop));
+        if (r.kernel >= 0 && r.kernel < GMOE_KERNEL_COUNT) {
+            o->launches[r.kernel]++;
+            o->ms[r.kernel] += ms;
+        }
+    }
     return GMOE_OK;
 }
 
@@ -325,9 +433,83 @@ static int launch_dispatch(gmoe_ctx *c, int T, hipStream_t st) {
     da.offsets = c->offsets;
     da.tokens = c->tokens;
     da.slots = c->slots;
+    ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_DISPATCH);
     hipLaunchKernelGGL(k_dispatch, dim3(c->E), dim3(DP_BLOCK), 0, st, da);
+    prof_end(pr, st);
     HIP_OK(hipGetLastError());
     c->last_dispatched = 1;
+    return GMOE_OK;
+}
+
+// T=1 through layers first..first+n-1 with the persistent kernel.
+static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float *x_out, int flags, hipStream_t st) {
+    StackArgs a;
+    a.layers = c->sk_layers + first;
+    a.n_layers = n;
+    a.first_layer = first;
+    a.x_in = x_in;
+    a.x = x_out;
+    a.D = c->D;
+    a.F = c->F;
+    a.E = c->E;
+    a.K = c->K;
+    a.flags = flags;
+    a.eps = c->cfg.norm_eps;
+    a.routed_scale = c->cfg.routed_scale;
+    a.stride = c->stride;
+    a.off_gq = c->off_gq;
+    a.off_uq = c->off_uq;
+    a.off_dq = c->off_dq;
+    a.off_gs = c->off_gs;
+    a.off_us = c->off_us;
+    a.off_ds = c->off_ds;
+    a.stage = c->stage;
+    a.dig = c->sk_dig;
+    a.dexp = c->sk_dexp;
+    a.xn = c->xn;
+    a.topk_idx = c->topk_idx;
+    a.topk_w = c->topk_w;
+    a.topk_ws = c->topk_ws;
+    a.router_prob = c->router_prob;
+    a.hist_idx = c->hist_idx;
+    a.hist_w = c->hist_w;
+    a.hist_stride = c->Tmax * c->K;
+    a.h = c->h;
+    a.y = c->y;
+    a.shared_out = c->shared_out;
+    a.routed_out = c->routed_out;
+    a.ctr = c->sk_ctr;
+    a.stats = c->stats_dev;
+    a.error = c->sk_error;
+    const int n_ctr = SKC_PANEL + c->D / 16;
+    hipLaunchKernelGGL(k_stack_reset, dim3(1), dim3(SK_BLOCK), 0, st, c->sk_ctr, n_ctr, c->sk_error);
+    ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_STACK);
+    hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+    prof_end(pr, st);
+    HIP_OK(hipGetLastError());
+    for (int l = first; l < first + n; l++) {
+        LayerDev &L = c->layers[l];
+        L.last_T = 1;
+    }
+    c->last_layer = first + n - 1;
+    c->last_T = 1;
+    c->last_flags = flags;
+    c->last_dispatched = 0;
+    c->tokens_routed += n;
+    c->stack_launched = 1;
+    return GMOE_OK;
+}
+
+// 0, or GMOE_ERR_HIP if a persistent-kernel dependency wait timed out (synchronises).
+static int check_stack_error(gmoe_ctx *c) {
+    if (!c->stack_launched) return GMOE_OK;
+    int err = 0;
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemcpy(&err, c->sk_error, sizeof(int), hipMemcpyDeviceToHost));
+    if (err) {
+        set_err("persistent decode kernel: a dependency wait timed out (grid not co-resident?)");
+        return GMOE_ERR_HIP;
+    }
     return GMOE_OK;
 }
 
@@ -348,6 +530,7 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     HIP_OK(hipSetDevice(c->device));
     hipStream_t st = (hipStream_t)stream;
     LayerDev &L = c->layers[layer];
+    if (T == 1 && c->stack_ok) return launch_stack(c, layer, 1, x_in, x_out, flags, st);
     const int fl = flags | (L.has_routed ? 0 : GMOE_FLAG_NO_ROUTED);
     const int D = c->D, F = c->F, E = c->E, K = c->K, NS = c->K + c->S;
 
@@ -371,7 +554,9 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     ra.K = K;
     ra.eps = c->cfg.norm_eps;
     ra.routed_scale = c->cfg.routed_scale;
+    ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_ROUTER);
     hipLaunchKernelGGL(k_norm_router, dim3(E, T), dim3(RT_BLOCK), (size_t)D * sizeof(float), st, ra);
+    prof_end(pr, st);
 
     ExpertArgs ea;
     ea.experts = L.experts;
@@ -388,8 +573,10 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     ea.K = K;
     ea.S = c->S;
     ea.flags = fl;
+    pr = prof_begin(c, st, GMOE_KERNEL_GATE_UP);
     hipLaunchKernelGGL(k_gate_up, dim3(F / 16, NS, T), dim3(EX_BLOCK), (size_t)3 * D + (size_t)(D / 32) * 4, st, ea,
                        (const float *)c->xn, (const int *)c->topk_idx, c->h);
+    prof_end(pr, st);
 
     CombineArgs ca;
     ca.topk_idx = c->topk_idx;
@@ -400,8 +587,10 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     ca.x_out = x_out;
     ca.shared_out = c->shared_out;
     ca.routed_out = c->routed_out;
+    pr = prof_begin(c, st, GMOE_KERNEL_DOWN);
     hipLaunchKernelGGL(k_down_combine, dim3(D / 16, NS, T), dim3(EX_BLOCK), (size_t)3 * F + (size_t)(F / 32) * 4, st,
                        ea, ca, (const float *)c->h);
+    prof_end(pr, st);
     HIP_OK(hipGetLastError());
     c->last_dispatched = 0;
     if (T > 1) {
@@ -418,9 +607,23 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
 
 extern "C" int gmoe_forward_layers(gmoe_ctx *c, int first, int n, int T, const float *x_in, float *x_out, int flags,
                                    void *stream) {
-    if (!c || n < 1) {
+    if (!c || n < 1 || !x_in || !x_out) {
         set_err("gmoe_forward_layers: bad arguments");
         return GMOE_ERR_INVALID;
+    }
+    if (first < 1 || first + n > c->L) {
+        set_err("gmoe_forward_layers: layers %d..%d outside 1..%d", first, first + n - 1, c->L - 1);
+        return GMOE_ERR_INVALID;
+    }
+    for (int l = first; l < first + n; l++) {
+        if (!c->layers[l].uploaded) {
+            set_err("gmoe_forward_layers: layer %d is not uploaded", l);
+            return GMOE_ERR_INVALID;
+        }
+    }
+    if (T == 1 && c->stack_ok) {
+        HIP_OK(hipSetDevice(c->device));
+        return launch_stack(c, first, n, x_in, x_out, flags, (hipStream_t)stream);
     }
     for (int i = 0; i < n; i++) {
         int rc = gmoe_forward(c, first + i, T, i == 0 ? x_in : x_out, x_out, flags, stream);
@@ -469,6 +672,7 @@ extern "C" int gmoe_read_layer_state(gmoe_ctx *c, gmoe_layer_state *o, void *str
     HIP_OK(hipSetDevice(c->device));
     hipStream_t st = (hipStream_t)stream;
     const size_t T = c->last_T, D = c->D, E = c->E, K = c->K;
+    if (int erc = check_stack_error(c)) return erc;
     if ((o->expert_offsets || o->expert_tokens) && !c->last_dispatched) {
         int rc = launch_dispatch(c, (int)T, st);
         if (rc) return rc;
@@ -497,6 +701,7 @@ extern "C" int gmoe_read_topk(gmoe_ctx *c, int layer, int32_t *idx, float *w, vo
     }
     HIP_OK(hipSetDevice(c->device));
     HIP_OK(hipStreamSynchronize((hipStream_t)stream));
+    if (int erc = check_stack_error(c)) return erc;
     const size_t n = (size_t)c->layers[layer].last_T * c->K;
     const size_t off = (size_t)layer * c->Tmax * c->K;
     int rc = copy_out(idx, c->hist_idx + off, n * sizeof(int));
@@ -512,6 +717,7 @@ extern "C" int gmoe_get_stats(gmoe_ctx *c, gmoe_stats *o) {
     HIP_OK(hipSetDevice(c->device));
     unsigned long long s[GM_STAT_COUNT] = {0};
     HIP_OK(hipDeviceSynchronize());
+    if (int erc = check_stack_error(c)) return erc;
     HIP_OK(hipMemcpy(s, c->stats_dev, sizeof(s), hipMemcpyDeviceToHost));
     o->tokens_routed = c->tokens_routed;
     o->routing_exact_path = (int64_t)s[GM_STAT_ROUTE_EXACT];

@@ -50,6 +50,13 @@ class GmoeLayerState(C.Structure):
                 ("expert_tokens", C.c_void_p)]
 
 
+KERNEL_NAMES = {0: "k_norm_router", 1: "k_gate_up", 2: "k_down_combine", 3: "k_dispatch", 4: "k_moe_stack"}
+
+
+class GmoeKernelTimes(C.Structure):
+    _fields_ = [("launches", C.c_int64 * 8), ("ms", C.c_double * 8)]
+
+
 class GmoeStats(C.Structure):
     _fields_ = [("tokens_routed", C.c_int64), ("routing_exact_path", C.c_int64), ("routing_unresolved", C.c_int64),
                 ("norm_exact_path", C.c_int64), ("scale_inexact", C.c_int64)]
@@ -108,6 +115,10 @@ def gmoe_lib():
         lib.gmoe_get_stats.argtypes = [P, C.POINTER(GmoeStats)]
         lib.gmoe_expert_bytes_last.argtypes = [P]
         lib.gmoe_expert_bytes_last.restype = C.c_int64
+        lib.gmoe_profile.argtypes = [P, C.c_int]
+        lib.gmoe_profile.restype = C.c_int
+        lib.gmoe_profile_read.argtypes = [P, C.POINTER(GmoeKernelTimes)]
+        lib.gmoe_profile_read.restype = C.c_int
         lib.gmoe_destroy.argtypes = [P]
         lib.gmoe_destroy.restype = None
         lib.gmoe_last_error.argtypes = []
@@ -243,6 +254,16 @@ class Context:
         st = GmoeStats()
         check(self.lib.gmoe_get_stats(self.h, C.byref(st)), "gmoe_get_stats")
         return {n: getattr(st, n) for n, _ in GmoeStats._fields_}
+
+    def profile(self, enable):
+        check(self.lib.gmoe_profile(self.h, 1 if enable else 0), "gmoe_profile")
+
+    def profile_read(self):
+        """{kernel name: (launches, total ms)} from the HIP events of the profiled calls."""
+        kt = GmoeKernelTimes()
+        check(self.lib.gmoe_profile_read(self.h, C.byref(kt)), "gmoe_profile_read")
+        return {KERNEL_NAMES.get(i, str(i)): (int(kt.launches[i]), float(kt.ms[i])) for i in range(8)
+                if kt.launches[i] > 0}
 
     def expert_bytes_last(self):
         return int(self.lib.gmoe_expert_bytes_last(self.h))

@@ -133,6 +133,23 @@ int gmoe_read_topk(gmoe_ctx *ctx, int layer, int32_t *topk_idx, float *topk_w, v
 
 int gmoe_get_stats(gmoe_ctx *ctx, gmoe_stats *out);
 
+/* Per-kernel timing with HIP events recorded around every launch on the caller's
+ * stream. gmoe_profile(ctx, 1) resets and starts recording, (ctx, 0) stops;
+ * gmoe_profile_read synchronises and reports launches and summed milliseconds per
+ * kernel of GMOE_KERNEL_*. Intended for measurement runs, not for serving. */
+#define GMOE_KERNEL_ROUTER 0     /* rmsnorm + router + top-k */
+#define GMOE_KERNEL_GATE_UP 1    /* gate/up products + SwiGLU */
+#define GMOE_KERNEL_DOWN 2       /* down products + combine + residual */
+#define GMOE_KERNEL_DISPATCH 3   /* per-expert token lists */
+#define GMOE_KERNEL_STACK 4      /* persistent decode kernel (T=1, all requested layers) */
+#define GMOE_KERNEL_COUNT 8
+typedef struct gmoe_kernel_times {
+    int64_t launches[GMOE_KERNEL_COUNT];
+    double ms[GMOE_KERNEL_COUNT];
+} gmoe_kernel_times;
+int gmoe_profile(gmoe_ctx *ctx, int enable);
+int gmoe_profile_read(gmoe_ctx *ctx, gmoe_kernel_times *out);
+
 /* Algorithmic Q8_0 bytes (34 per 32 weights) that one forward of n_tokens reads
  * for its experts, given the routing of its most recent call; used for GB/s. */
 int64_t gmoe_expert_bytes_last(gmoe_ctx *ctx);
