@@ -7,8 +7,8 @@
 //            h = 0..1, i = 0..7). One dwordx4 load per lane reads a whole chunk, and its
 //            two 8-byte halves are exactly the B operands of two v_mfma_i32_16x16x32_i8
 //            (lane l = row l%16, k = 8*(l/16)..+8), one per 32-column quantisation block.
-//   s plane: fp16 scale of (row r, block b) at ((r/16)*(C/32) + b)*16 + r%16, so the 16
-//            rows of a panel read one block's scales as 32 contiguous bytes.
+//   s plane: fp16 scale of (row r, block b) at r*(C/32) + b (row-major), so the row a
+//            lane owns has the scales of any run of consecutive blocks side by side.
 // One expert = gate, up, down q planes then their s planes, 34 bytes per 32 weights.
 #pragma once
 
@@ -23,6 +23,16 @@
 #define GM_MAX_E 256
 #define GM_MAX_K 8
 #define GM_MAX_DIM 8192
+#define GM_MAX_COLS 2048  // widest matrix row the expert kernels hold in registers
+
+// Global-memory (address space 1) views. Pointers read from memory (the layer table)
+// are generic to the compiler, which then emits flat loads; flat loads also count
+// against lgkmcnt, so an LDS wait would stall on every outstanding weight load.
+#define GM_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ static inline const GM_GLOBAL T *gbl(const T *p) {
+    return (const GM_GLOBAL T *)p;
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -36,7 +46,7 @@ __host__ __device__ static inline size_t gm_q_offset(int r, int c, int cols) {
 }
 
 __host__ __device__ static inline size_t gm_s_offset(int r, int b, int cols) {
-    return ((size_t)(r >> 4) * (size_t)(cols >> 5) + (size_t)b) * 16 + (size_t)(r & 15);
+    return (size_t)r * (size_t)(cols >> 5) + (size_t)b;
 }
 
 // Correctly rounded fp32 square root. The fp32 intrinsic lowers to v_sqrt_f32, which is

@@ -22,7 +22,6 @@ struct ExpertArgs {
 
 #define EX_BLOCK 256
 #define EX_WAVES 4
-#define EX_NB 8  // chunks per wave kept in flight
 
 // Digit form of n activations (n a multiple of 32) into shared memory:
 // dig[j*n + i] = digit j of v[i], dexp[i/32] = block exponent.
@@ -58,60 +57,84 @@ __device__ static inline long chunk_half(const u32x4 &c, int h) {
     return h == 0 ? (long)(((unsigned long long)c.y << 32) | c.x) : (long)(((unsigned long long)c.w << 32) | c.z);
 }
 
-// One block of 32 columns: digit dots via MFMA, then lanes 0..15 accumulate their row.
-__device__ static inline void mfma_block(long A, long B, const __half *__restrict__ s, size_t s_idx, int dexp,
-                                         int lane, float &acc) {
+// One block of 32 columns: digit dots via MFMA, then lanes 0..15 accumulate their row
+// with the block's fp16 scale `sc` (already in a register) and digit exponent.
+__device__ static inline void mfma_block(long A, long B, __half sc, int dexp, int lane, float &acc) {
     const v4i zero = {0, 0, 0, 0};
     v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
     if (lane < 16) {
         const float f = digits_to_float(d[0], d[1], d[2]);
-        const float sc = __half2float(s[s_idx + lane]);
-        acc = fmaf(f, ldexpf(sc, dexp), acc);
+        acc = fmaf(f, ldexpf(__half2float(sc), dexp), acc);
     }
 }
 
-// Partial dot products of panel p of one or two matrices (same shape, same activations)
-// over the chunks j = w, w+4, ... ; lanes 0..15 return their row's partial sums.
-template <int NMAT>
-__device__ static inline void panel_partial(const uint8_t *__restrict__ q0, const __half *__restrict__ s0,
-                                            const uint8_t *__restrict__ q1, const __half *__restrict__ s1, int p,
-                                            int cols, const int8_t *dig, const int *dexp, float *out0, float *out1) {
+// A wave's share of one 16-row panel: the chunks [w*cpw, (w+1)*cpw) of one or two
+// matrices, cpw = cols/64/4 <= NB, and for lanes 0..15 (the panel's rows) the fp16
+// scales of those chunks' blocks (two per chunk, one dword). All loads are issued
+// together so a panel costs one memory latency.
+template <int NMAT, int NB>
+struct PanelRegs {
+    u32x4 q[NMAT][NB];
+    unsigned s[NMAT][NB];
+};
+
+template <int NMAT, int NB>
+__device__ static inline void panel_load(PanelRegs<NMAT, NB> &r, const uint8_t *q0, const __half *s0,
+                                         const uint8_t *q1, const __half *s1, int p, int cols) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int nchunks = cols >> 6, nblocks = cols >> 5;
-    const int m = lane & 15, kofs = 8 * (lane >> 4);
-    const u32x4 *qa = (const u32x4 *)(q0 + (size_t)p * nchunks * GM_CHUNK_BYTES) + lane;
-    const u32x4 *qb = NMAT > 1 ? (const u32x4 *)(q1 + (size_t)p * nchunks * GM_CHUNK_BYTES) + lane : qa;
-    const size_t sbase = (size_t)p * nblocks * 16;
-    float acc0 = 0.0f, acc1 = 0.0f;
-    for (int j0 = w; j0 < nchunks; j0 += EX_WAVES * EX_NB) {
-        u32x4 ba[EX_NB], bb[EX_NB];
+    const int nchunks = cols >> 6, nblocks = cols >> 5, cpw = nchunks >> 2;
+    const int j0 = w * cpw;
+    const uint8_t *qs[2] = {q0, q1};
+    const __half *ss[2] = {s0, s1};
 #pragma unroll
-        for (int u = 0; u < EX_NB; u++) {
-            const int j = j0 + EX_WAVES * u;
-            if (j < nchunks) {
-                ba[u] = qa[(size_t)j * 64];
-                if (NMAT > 1) bb[u] = qb[(size_t)j * 64];
+    for (int m = 0; m < NMAT; m++) {
+        const GM_GLOBAL u32x4 *qp = gbl((const u32x4 *)(qs[m] + ((size_t)p * nchunks + j0) * GM_CHUNK_BYTES)) + lane;
+        const GM_GLOBAL unsigned *sp = gbl((const unsigned *)(ss[m] + ((size_t)p * 16 + (lane & 15)) * nblocks + 2 * j0));
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            if (u < cpw) {
+                r.q[m][u] = __builtin_nontemporal_load(qp + (size_t)u * 64);
+                r.s[m][u] = lane < 16 ? __builtin_nontemporal_load(sp + u) : 0u;
             }
         }
+    }
+}
+
+// Partial dot products of the wave's chunks with the activation digits `dig`
+// ([3][cols] int8) and block exponents `dexp`; lanes 0..15 get their row's sums.
+template <int NMAT, int NB>
+__device__ static inline void panel_compute(const PanelRegs<NMAT, NB> &r, int cols, const int8_t *dig,
+                                            const int *dexp, float *out) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int cpw = (cols >> 6) >> 2, j0 = w * cpw;
+    const int m = lane & 15, kofs = 8 * (lane >> 4);
+    float acc[NMAT];
 #pragma unroll
-        for (int u = 0; u < EX_NB; u++) {
-            const int j = j0 + EX_WAVES * u;
-            if (j < nchunks) {
+    for (int i = 0; i < NMAT; i++) acc[i] = 0.0f;
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int b = 2 * j + h;
-                    long A = 0;
-                    if (m < 3) A = *(const long *)(dig + m * cols + 32 * b + kofs);
-                    const int de = dexp[b];
-                    mfma_block(A, chunk_half(ba[u], h), s0, sbase + (size_t)b * 16, de, lane, acc0);
-                    if (NMAT > 1) mfma_block(A, chunk_half(bb[u], h), s1, sbase + (size_t)b * 16, de, lane, acc1);
+    for (int u = 0; u < NB; u++) {
+        if (u < cpw) {
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int b = 2 * (j0 + u) + hh;
+                long A = 0;
+                if (m < 3) A = *(const long *)(dig + m * cols + 32 * b + kofs);
+                const int de = dexp[b];
+#pragma unroll
+                for (int i = 0; i < NMAT; i++) {
+                    const unsigned sw = r.s[i][u];
+                    const __half sc = __ushort_as_half((unsigned short)(hh ? (sw >> 16) : (sw & 0xffffu)));
+                    mfma_block(A, chunk_half(r.q[i][u], hh), sc, de, lane, acc[i]);
                 }
             }
         }
     }
-    *out0 = acc0;
-    *out1 = acc1;
+#pragma unroll
+    for (int i = 0; i < NMAT; i++) out[i] = acc[i];
 }
+
+// Column tiling used by the expert kernels: cols/64 chunks split evenly over 4 waves.
+#define EX_NB_MAX 8  // chunks per wave in registers: cols <= 2048
 
 // grid (F/16, K+S, T): h[t][slot][F] = silu(gate . xn) * (up . xn) for the slot's expert.
 __global__ __launch_bounds__(EX_BLOCK) void k_gate_up(ExpertArgs a, const float *__restrict__ xn,
@@ -128,12 +151,15 @@ __global__ __launch_bounds__(EX_BLOCK) void k_gate_up(ExpertArgs a, const float 
     }
     int8_t *dig = (int8_t *)smem;
     int *dexp = (int *)(smem + 3 * D);
+    const uint8_t *base = a.experts + (size_t)e * a.stride;
+    PanelRegs<2, EX_NB_MAX> pr;
+    panel_load<2, EX_NB_MAX>(pr, base + a.off_gq, (const __half *)(base + a.off_gs), base + a.off_uq,
+                             (const __half *)(base + a.off_us), p, D);
     load_digits(xn + (size_t)t * D, D, dig, dexp);
     __syncthreads();
-    const uint8_t *base = a.experts + (size_t)e * a.stride;
-    float g, u;
-    panel_partial<2>(base + a.off_gq, (const __half *)(base + a.off_gs), base + a.off_uq,
-                     (const __half *)(base + a.off_us), p, D, dig, dexp, &g, &u);
+    float gu[2];
+    panel_compute<2, EX_NB_MAX>(pr, D, dig, dexp, gu);
+    const float g = gu[0], u = gu[1];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (lane < 16) {
         part[w][0][lane] = g;
@@ -178,12 +204,13 @@ __global__ __launch_bounds__(EX_BLOCK) void k_down_combine(ExpertArgs a, Combine
     if (valid) {
         int8_t *dig = (int8_t *)smem;
         int *dexp = (int *)(smem + 3 * F);
+        const uint8_t *base = a.experts + (size_t)e * a.stride;
+        PanelRegs<1, EX_NB_MAX> pr;
+        panel_load<1, EX_NB_MAX>(pr, base + a.off_dq, (const __half *)(base + a.off_ds), nullptr, nullptr, p, F);
         load_digits(h + ((size_t)t * nslots + slot) * F, F, dig, dexp);
         __syncthreads();
-        const uint8_t *base = a.experts + (size_t)e * a.stride;
-        float yv, unused;
-        panel_partial<1>(base + a.off_dq, (const __half *)(base + a.off_ds), nullptr, nullptr, p, F, dig, dexp, &yv,
-                         &unused);
+        float yv;
+        panel_compute<1, EX_NB_MAX>(pr, F, dig, dexp, &yv);
         const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
         if (lane < 16) part[w][lane] = yv;
         __syncthreads();

@@ -40,7 +40,7 @@ static void set_err(const char *fmt, ...) {
         }                                                                                \
     } while (0)
 
-#define GM_STACK_COUNTERS 256
+#define GM_STACK_COUNTERS (SKC_PAD * 160)
 
 struct LayerDev {
     uint8_t *experts = nullptr;  // (E+1) * stride bytes, tiled
@@ -87,6 +87,10 @@ struct gmoe_ctx {
     unsigned *sk_ctr = nullptr;  // [GM_STACK_COUNTERS]
     int *sk_error = nullptr;
     StackLayer *sk_layers = nullptr;  // [L], device
+    unsigned long long *sk_trace = nullptr;  // per-item timestamps when tracing
+    size_t sk_trace_items = 0;
+    int sk_trace_on = 0;
+    long long sk_trace_last = 0;  // items of the most recent traced launch
 
     uint8_t *staging = nullptr;
     size_t staging_bytes = 0;
@@ -135,7 +139,7 @@ static void free_ctx(gmoe_ctx *c) {
                     c->stage, c->topk_idx, c->tok_counter, c->panel_counter, c->disp_counter, c->disp_tmp_tok,
                     c->disp_tmp_slot, c->disp_counts, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
                     c->stats_dev, c->x_host_io, c->staging, c->sk_dig, c->sk_dexp, c->sk_ctr, c->sk_error,
-                    c->sk_layers};
+                    c->sk_layers, c->sk_trace};
     for (void *b : bufs) dev_free(b);
     delete c;
 }
@@ -147,10 +151,12 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     }
     *out = nullptr;
     const gmoe_config &g = *cfg;
-    if (g.dim <= 0 || g.dim % 64 || g.dim > GM_MAX_DIM || g.moe_ffn_dim <= 0 || g.moe_ffn_dim % 64 ||
-        g.moe_ffn_dim > GM_MAX_DIM) {
-        set_err("gmoe_create: dim and moe_ffn_dim must be positive multiples of 64 and <= %d (got %d, %d)",
-                GM_MAX_DIM, g.dim, g.moe_ffn_dim);
+    // Each of a block's 4 waves holds an equal share of a row's 64-column chunks in
+    // registers (at most 8): dim and moe_ffn_dim are multiples of 256, at most 2048.
+    if (g.dim <= 0 || g.dim % 256 || g.dim > GM_MAX_COLS || g.moe_ffn_dim <= 0 || g.moe_ffn_dim % 256 ||
+        g.moe_ffn_dim > GM_MAX_COLS) {
+        set_err("gmoe_create: dim and moe_ffn_dim must be positive multiples of 256 and <= %d (got %d, %d)",
+                GM_MAX_COLS, g.dim, g.moe_ffn_dim);
         return GMOE_ERR_INVALID;
     }
     if (g.n_routed_experts < 1 || g.n_routed_experts > GM_MAX_E || g.n_experts_used < 1 ||
@@ -252,8 +258,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     }
     // The persistent decode kernel holds one panel's chunks per wave in registers and
     // xn in shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots.
-    c->stack_ok = c->D <= 2048 && c->F <= 2048 && c->D % 256 == 0 && c->K + 1 <= SK_MAX_SLOTS &&
-                  SKC_PANEL + c->D / 16 <= GM_STACK_COUNTERS;
+    c->stack_ok = c->K + 1 <= SK_MAX_SLOTS && SKC(SKC_PANEL + c->D / 16) <= GM_STACK_COUNTERS;
     const char *env = getenv("GMOE_STACK_KERNEL");
     if (env && env[0] == '0') c->stack_ok = 0;
     if (c->stack_ok) {
@@ -390,6 +395,27 @@ static void prof_end(ProfRecord *r, hipStream_t st) {
     if (r) (void)hipEventRecord(r->stop, st);
 }
 
+extern "C" int gmoe_trace_items(gmoe_ctx *c, int enable) {
+    if (!c) {
+        set_err("gmoe_trace_items: null context");
+        return GMOE_ERR_INVALID;
+    }
+    c->sk_trace_on = enable ? 1 : 0;
+    return GMOE_OK;
+}
+
+extern "C" int64_t gmoe_trace_items_read(gmoe_ctx *c, uint64_t *out, int64_t max_items) {
+    if (!c || !out || max_items < 0) {
+        set_err("gmoe_trace_items_read: bad arguments");
+        return GMOE_ERR_INVALID;
+    }
+    if (!c->sk_trace || c->sk_trace_last == 0) return 0;
+    const int64_t n = c->sk_trace_last < max_items ? c->sk_trace_last : max_items;
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemcpy(out, c->sk_trace, (size_t)n * 3 * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    return n;
+}
+
 extern "C" int gmoe_profile(gmoe_ctx *c, int enable) {
     if (!c) {
         set_err("gmoe_profile: null context");
@@ -481,7 +507,20 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.ctr = c->sk_ctr;
     a.stats = c->stats_dev;
     a.error = c->sk_error;
-    const int n_ctr = SKC_PANEL + c->D / 16;
+    a.trace = nullptr;
+    if (c->sk_trace_on) {
+        const size_t items = (size_t)(c->E + (c->K + 1) * (c->F / 16 + c->D / 16)) * n;
+        if (items > c->sk_trace_items) {
+            dev_free(c->sk_trace);
+            c->sk_trace = nullptr;
+            c->sk_trace_items = 0;
+            if (dev_alloc(&c->sk_trace, 3 * items) != GMOE_OK) return GMOE_ERR_NOMEM;
+            c->sk_trace_items = items;
+        }
+        a.trace = c->sk_trace;
+        c->sk_trace_last = (long long)items;
+    }
+    const int n_ctr = SKC(SKC_PANEL + c->D / 16);
     hipLaunchKernelGGL(k_stack_reset, dim3(1), dim3(SK_BLOCK), 0, st, c->sk_ctr, n_ctr, c->sk_error);
     ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_STACK);
     hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);

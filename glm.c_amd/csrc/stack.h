@@ -27,11 +27,14 @@
 #include "router.h"
 
 #define SK_BLOCK 256
-#define SK_NB 8                  // chunks per wave held in registers (D, F <= 2048)
 #define SK_MAX_SLOTS 9           // K + 1 <= 9
 #define SK_SPIN_LIMIT (1u << 22) // polls before a wait is declared dead (~seconds)
 
+// Counters sit 64 words (256 bytes) apart so that polls of one never share a cache
+// line, or a memory channel's hot spot, with another.
+#define SKC_PAD 64
 enum { SKC_ROUTER = 0, SKC_SEL = 1, SKC_DIG = 2, SKC_X = 3, SKC_GATE = 4, SKC_PANEL = 16 };
+#define SKC(i) ((i) * SKC_PAD)
 
 struct StackLayer {
     const uint8_t *experts;
@@ -68,6 +71,7 @@ struct StackArgs {
     unsigned *ctr;        // counters, zero at launch
     unsigned long long *stats;
     int *error;           // nonzero: a wait timed out
+    unsigned long long *trace;  // optional: 3 timestamps per item (picked, deps ready, done)
 };
 
 __device__ static inline float ld_f(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -92,30 +96,6 @@ __device__ static inline unsigned publish(unsigned *c, unsigned *s_old) {
     return *s_old;
 }
 
-// Block-wide wait until *c >= target. Returns false if the wait timed out or another
-// block already failed (the caller then returns from the kernel).
-__device__ static inline bool wait_ge(const unsigned *c, unsigned target, int *error, int *s_ok) {
-    if (threadIdx.x == 0) {
-        int ok = 1;
-        unsigned spins = 0;
-        while (ld_u(c) < target) {
-            if (__hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                ok = 0;
-                break;
-            }
-            if (++spins > SK_SPIN_LIMIT) {
-                __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        *s_ok = ok;
-    }
-    __syncthreads();
-    return *s_ok != 0;
-}
-
 struct SkShared {
     union {
         struct {
@@ -135,19 +115,66 @@ struct SkShared {
     int ok, last, sel_ok;
     int idx[GM_MAX_K];
     int expert;
+    long trace_item;
+    unsigned long long *trace;
 };
+
+// Block-wide wait until *c >= target. Returns false if the wait timed out or another
+// block already failed (the caller then returns from the kernel).
+__device__ static inline bool wait_ge(const unsigned *c, unsigned target, int *error, SkShared &sh) {
+    if (threadIdx.x == 0) {
+        int ok = 1;
+        unsigned spins = 0;
+        while (ld_u(c) < target) {
+            if (__hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                ok = 0;
+                break;
+            }
+            if (++spins > SK_SPIN_LIMIT) {
+                __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);  // ~512 clocks between polls
+        }
+        sh.ok = ok;
+        if (sh.trace) sh.trace[3 * sh.trace_item + 1] = wall_clock64();
+    }
+    __syncthreads();
+    return sh.ok != 0;
+}
+
 
 // ---------------------------------------------------------------- router item
 __device__ static bool sk_router_item(const StackArgs &a, const StackLayer &L, int layer, int li, int e, SkShared &sh) {
     const int D = a.D, E = a.E, K = a.K, tid = threadIdx.x;
-    if (li > 0 && !wait_ge(&a.ctr[SKC_X], (unsigned)li * (D >> 4), a.error, &sh.ok)) return false;
+    const int per = D / SK_BLOCK;  // D is a multiple of 256 here
+    // The router row and the norm weights do not depend on x: fetch them before waiting.
+    float gw[8], nw[8];
+    const GM_GLOBAL float *g = gbl(L.gate_inp + (size_t)e * D);
+    const GM_GLOBAL float *nrm = gbl(L.norm);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (j < per) {
+            gw[j] = g[tid * per + j];
+            nw[j] = nrm[tid * per + j];
+        }
+    }
+    if (li > 0 && !wait_ge(&a.ctr[SKC(SKC_X)], (unsigned)li * (D >> 4), a.error, sh)) return false;
     const float *xsrc = li == 0 ? a.x_in : a.x;
     // rmsnorm, bit-identical to infer.c:746-752, on coherent loads of x
+    float xv[8];
     double ss = 0.0;
-    for (int i = tid; i < D; i += SK_BLOCK) {
-        const float v = ld_f(xsrc + i);
-        sh.u.r.xn[i] = v;
-        ss += (double)v * (double)v;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (j < per) xv[j] = ld_f(xsrc + tid * per + j);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (j < per) {
+            sh.u.r.xn[tid * per + j] = xv[j];
+            ss += (double)xv[j] * (double)xv[j];
+        }
     }
     ss = block_sum_d(ss, sh.red);
     const double v = ss / (double)D, rho = (double)D * 0x1p-52;
@@ -165,7 +192,13 @@ __device__ static bool sk_router_item(const StackArgs &a, const StackLayer &L, i
     }
     const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
     __syncthreads();
-    for (int i = tid; i < D; i += SK_BLOCK) sh.u.r.xn[i] = __fmul_rn(__fmul_rn(sh.u.r.xn[i], inv), L.norm[i]);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        if (j < per) {
+            xv[j] = __fmul_rn(__fmul_rn(xv[j], inv), nw[j]);
+            sh.u.r.xn[tid * per + j] = xv[j];
+        }
+    }
     __syncthreads();
 
     if (e == 0) {
@@ -196,19 +229,16 @@ __device__ static bool sk_router_item(const StackArgs &a, const StackLayer &L, i
             st_u64((unsigned long long *)(a.dig + 2 * D + i0), w2);
             if ((tid & 3) == 0) st_i(a.dexp + (i0 >> 5), ex);
         }
-        publish(&a.ctr[SKC_DIG], &sh.old);
+        publish(&a.ctr[SKC(SKC_DIG)], &sh.old);
     }
 
     // logit of expert e in fp64 and the bound on glm.c's sequential fp32 chain
-    const float *g = L.gate_inp + (size_t)e * D;
-    const int per = D / SK_BLOCK;  // D is a multiple of 256 here
     double p[8];
     double seg = 0.0, seg_abs = 0.0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         if (j < per) {
-            const int i = tid * per + j;
-            p[j] = (double)g[i] * (double)sh.u.r.xn[i];
+            p[j] = (double)gw[j] * (double)xv[j];
             seg += p[j];
             seg_abs += fabs(p[j]);
         }
@@ -233,7 +263,7 @@ __device__ static bool sk_router_item(const StackArgs &a, const StackLayer &L, i
         __hip_atomic_store((double *)&a.stage[e].x, S, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store((double *)&a.stage[e].y, B, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const unsigned old = publish(&a.ctr[SKC_ROUTER], &sh.old);
+    const unsigned old = publish(&a.ctr[SKC(SKC_ROUTER)], &sh.old);
     if (old != (unsigned)((li + 1) * E - 1)) return true;
 
     // ---- this block finished the layer's last router item: select the top-k
@@ -241,7 +271,7 @@ __device__ static bool sk_router_item(const StackArgs &a, const StackLayer &L, i
         const double S_i = __hip_atomic_load((double *)&a.stage[i].x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const double B_i = __hip_atomic_load((double *)&a.stage[i].y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         double lo, hi;
-        selection_interval(S_i, B_i, L.bias[i], &lo, &hi);
+        selection_interval(S_i, B_i, gbl(L.bias)[i], &lo, &hi);
         sh.u.r.lo[i] = lo;
         sh.u.r.hi[i] = hi;
         sh.u.r.mid[i] = 0.5 * (lo + hi);
@@ -296,12 +326,12 @@ __device__ static bool sk_router_item(const StackArgs &a, const StackLayer &L, i
     __syncthreads();
     if (!sh.sel_ok) {
         for (int i = tid; i < E; i += SK_BLOCK) {
-            const float *gi = L.gate_inp + (size_t)i * D;
+            const GM_GLOBAL float *gi = gbl(L.gate_inp + (size_t)i * D);
             float chain = 0.0f;
             for (int j = 0; j < D; j++) chain = __fadd_rn(chain, __fmul_rn(gi[j], sh.u.r.xn[j]));
             const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain)));
             sh.u.r.p[i] = pr;
-            sh.u.r.sel[i] = __fadd_rn(pr, L.bias[i]);
+            sh.u.r.sel[i] = __fadd_rn(pr, gbl(L.bias)[i]);
         }
         __syncthreads();
         if (tid == 0) {
@@ -357,54 +387,8 @@ __device__ static bool sk_router_item(const StackArgs &a, const StackLayer &L, i
         }
     }
     for (int i = tid; i < E; i += SK_BLOCK) a.router_prob[i] = sh.u.r.p[i];
-    publish(&a.ctr[SKC_SEL], &sh.old);
+    publish(&a.ctr[SKC(SKC_SEL)], &sh.old);
     return true;
-}
-
-// Load one panel's chunks for this wave (j = w, w+4, ...) into registers.
-template <int NMAT>
-__device__ static inline void sk_panel_load(const uint8_t *q0, const uint8_t *q1, int p, int cols, u32x4 *ba,
-                                            u32x4 *bb) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int nchunks = cols >> 6;
-    const u32x4 *qa = (const u32x4 *)(q0 + (size_t)p * nchunks * GM_CHUNK_BYTES) + lane;
-    const u32x4 *qb = NMAT > 1 ? (const u32x4 *)(q1 + (size_t)p * nchunks * GM_CHUNK_BYTES) + lane : qa;
-#pragma unroll
-    for (int u = 0; u < SK_NB; u++) {
-        const int j = w + EX_WAVES * u;
-        if (j < nchunks) {
-            ba[u] = __builtin_nontemporal_load(qa + (size_t)j * 64);
-            if (NMAT > 1) bb[u] = __builtin_nontemporal_load(qb + (size_t)j * 64);
-        }
-    }
-}
-
-template <int NMAT>
-__device__ static inline void sk_panel_compute(const u32x4 *ba, const u32x4 *bb, const __half *s0, const __half *s1,
-                                               int p, int cols, const int8_t *dig, const int *dexp, float *out0,
-                                               float *out1) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int nchunks = cols >> 6, nblocks = cols >> 5;
-    const int m = lane & 15, kofs = 8 * (lane >> 4);
-    const size_t sbase = (size_t)p * nblocks * 16;
-    float acc0 = 0.0f, acc1 = 0.0f;
-#pragma unroll
-    for (int u = 0; u < SK_NB; u++) {
-        const int j = w + EX_WAVES * u;
-        if (j < nchunks) {
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                const int b = 2 * j + hh;
-                long A = 0;
-                if (m < 3) A = *(const long *)(dig + m * cols + 32 * b + kofs);
-                const int de = dexp[b];
-                mfma_block(A, chunk_half(ba[u], hh), s0, sbase + (size_t)b * 16, de, lane, acc0);
-                if (NMAT > 1) mfma_block(A, chunk_half(bb[u], hh), s1, sbase + (size_t)b * 16, de, lane, acc1);
-            }
-        }
-    }
-    *out0 = acc0;
-    *out1 = acc1;
 }
 
 // Expert index of `slot` for the current layer, or -1 when the slot is idle.
@@ -417,20 +401,21 @@ __device__ static inline int sk_slot_expert(const StackArgs &a, const StackLayer
 // ---------------------------------------------------------------- gate/up item
 __device__ static bool sk_gate_up_item(const StackArgs &a, const StackLayer &L, int li, int slot, int p, SkShared &sh) {
     const int D = a.D, F = a.F;
-    if (slot < a.K && !wait_ge(&a.ctr[SKC_SEL], (unsigned)(li + 1), a.error, &sh.ok)) return false;
+    if (slot < a.K && !wait_ge(&a.ctr[SKC(SKC_SEL)], (unsigned)(li + 1), a.error, sh)) return false;
     const int e = sk_slot_expert(a, L, slot);
     if (e >= 0) {
         const uint8_t *base = L.experts + (size_t)e * a.stride;
-        u32x4 ba[SK_NB], bb[SK_NB];
-        sk_panel_load<2>(base + a.off_gq, base + a.off_uq, p, D, ba, bb);
-        if (slot == a.K && !wait_ge(&a.ctr[SKC_DIG], (unsigned)(li + 1), a.error, &sh.ok)) return false;
+        PanelRegs<2, EX_NB_MAX> pr;
+        panel_load<2, EX_NB_MAX>(pr, base + a.off_gq, (const __half *)(base + a.off_gs), base + a.off_uq,
+                                 (const __half *)(base + a.off_us), p, D);
+        if (slot == a.K && !wait_ge(&a.ctr[SKC(SKC_DIG)], (unsigned)(li + 1), a.error, sh)) return false;
         for (int i = threadIdx.x; i < (3 * D) / 8; i += SK_BLOCK)
             ((unsigned long long *)sh.u.g.dig)[i] = ld_u64((const unsigned long long *)a.dig + i);
         for (int i = threadIdx.x; i < D / 32; i += SK_BLOCK) sh.u.g.dexp[i] = ld_i(a.dexp + i);
         __syncthreads();
-        float g, u;
-        sk_panel_compute<2>(ba, bb, (const __half *)(base + a.off_gs), (const __half *)(base + a.off_us), p, D,
-                            sh.u.g.dig, sh.u.g.dexp, &g, &u);
+        float gu[2];
+        panel_compute<2, EX_NB_MAX>(pr, D, sh.u.g.dig, sh.u.g.dexp, gu);
+        const float g = gu[0], u = gu[1];
         const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
         if (lane < 16) {
             sh.u.g.part[w][0][lane] = g;
@@ -444,20 +429,20 @@ __device__ static bool sk_gate_up_item(const StackArgs &a, const StackLayer &L, 
             st_f(a.h + (size_t)slot * F + (size_t)p * 16 + l, gs / (1.0f + expf(-gs)) * us);
         }
     }
-    publish(&a.ctr[SKC_GATE + slot], &sh.old);
+    publish(&a.ctr[SKC(SKC_GATE + slot)], &sh.old);
     return true;
 }
 
 // ---------------------------------------------------------------- down item (+ combine)
 __device__ static bool sk_down_item(const StackArgs &a, const StackLayer &L, int li, int slot, int p, SkShared &sh) {
     const int D = a.D, F = a.F, K = a.K, NS = a.K + 1;
-    if (slot < K && !wait_ge(&a.ctr[SKC_SEL], (unsigned)(li + 1), a.error, &sh.ok)) return false;
+    if (slot < K && !wait_ge(&a.ctr[SKC(SKC_SEL)], (unsigned)(li + 1), a.error, sh)) return false;
     const int e = sk_slot_expert(a, L, slot);
     if (e >= 0) {
         const uint8_t *base = L.experts + (size_t)e * a.stride;
-        u32x4 ba[SK_NB], bb[SK_NB];
-        sk_panel_load<1>(base + a.off_dq, nullptr, p, F, ba, bb);
-        if (!wait_ge(&a.ctr[SKC_GATE + slot], (unsigned)(li + 1) * (F >> 4), a.error, &sh.ok)) return false;
+        PanelRegs<1, EX_NB_MAX> pr;
+        panel_load<1, EX_NB_MAX>(pr, base + a.off_dq, (const __half *)(base + a.off_ds), nullptr, nullptr, p, F);
+        if (!wait_ge(&a.ctr[SKC(SKC_GATE + slot)], (unsigned)(li + 1) * (F >> 4), a.error, sh)) return false;
         // digits of h[slot] into shared memory
         const float *hs = a.h + (size_t)slot * F;
         for (int i0 = threadIdx.x * 8; i0 < F; i0 += SK_BLOCK * 8) {
@@ -486,9 +471,8 @@ __device__ static bool sk_down_item(const StackArgs &a, const StackLayer &L, int
             if ((threadIdx.x & 3) == 0) sh.u.g.dexp[i0 >> 5] = ex;
         }
         __syncthreads();
-        float yv, unused;
-        sk_panel_compute<1>(ba, bb, (const __half *)(base + a.off_ds), nullptr, p, F, sh.u.g.dig, sh.u.g.dexp, &yv,
-                            &unused);
+        float yv;
+        panel_compute<1, EX_NB_MAX>(pr, F, sh.u.g.dig, sh.u.g.dexp, &yv);
         const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
         if (lane < 16) sh.u.g.part[w][0][lane] = yv;
         __syncthreads();
@@ -498,7 +482,7 @@ __device__ static bool sk_down_item(const StackArgs &a, const StackLayer &L, int
                  ((sh.u.g.part[0][0][l] + sh.u.g.part[1][0][l]) + sh.u.g.part[2][0][l]) + sh.u.g.part[3][0][l]);
         }
     }
-    const unsigned old = publish(&a.ctr[SKC_PANEL + p], &sh.old);
+    const unsigned old = publish(&a.ctr[SKC(SKC_PANEL + p)], &sh.old);
     if (old != (unsigned)((li + 1) * NS - 1)) return true;
     // last slot of this panel: combine (infer.c:1192, 1212-1214)
     if (threadIdx.x < 16) {
@@ -516,7 +500,7 @@ __device__ static bool sk_down_item(const StackArgs &a, const StackLayer &L, int
         a.shared_out[r] = shv;
         st_f(a.x + r, __fadd_rn(xr, __fadd_rn(shv, acc)));
     }
-    publish(&a.ctr[SKC_X], &sh.old);
+    publish(&a.ctr[SKC(SKC_X)], &sh.old);
     return true;
 }
 
@@ -524,6 +508,8 @@ __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, 
     for (int i = threadIdx.x; i < n; i += blockDim.x) ctr[i] = 0u;
     if (threadIdx.x == 0) *error = 0;
 }
+
+__device__ static inline unsigned long long sk_now() { return wall_clock64(); }
 
 __global__ __launch_bounds__(SK_BLOCK) void k_moe_stack(StackArgs a) {
     __shared__ SkShared sh;
@@ -537,6 +523,9 @@ __global__ __launch_bounds__(SK_BLOCK) void k_moe_stack(StackArgs a) {
         int r = (int)(it % per_layer);
         const StackLayer L = a.layers[li];
         const int layer = a.first_layer + li;
+        if (a.trace && threadIdx.x == 0) a.trace[3 * it] = sk_now();
+        sh.trace_item = it;
+        sh.trace = a.trace;
         bool ok;
         if (r < n_router) {
             ok = sk_router_item(a, L, layer, li, r, sh);
@@ -550,6 +539,7 @@ __global__ __launch_bounds__(SK_BLOCK) void k_moe_stack(StackArgs a) {
             ok = sk_down_item(a, L, li, slot, r % NPD, sh);
         }
         if (!ok) return;
+        if (a.trace && threadIdx.x == 0) a.trace[3 * it + 2] = sk_now();
         __syncthreads();
     }
 }

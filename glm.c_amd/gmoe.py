@@ -15,7 +15,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIBGMOE = os.path.join(HERE, "libgmoe.so")
+LIBGMOE = os.environ.get("GMOE_LIBRARY", os.path.join(HERE, "libgmoe.so"))
 LIBHOST = os.path.join(HERE, "libglm_hip.so")
 
 GMOE_FLAG_NO_ROUTED = 1

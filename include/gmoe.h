@@ -42,8 +42,8 @@ typedef struct gmoe_ctx gmoe_ctx;
 
 /* Model shape. Field meanings follow RuntimeConfig (model.h:7-45). */
 typedef struct gmoe_config {
-    int32_t dim;               /* hidden size D (model.h:9); multiple of 64 */
-    int32_t moe_ffn_dim;       /* expert intermediate F (model.h:44); multiple of 64 */
+    int32_t dim;               /* hidden size D (model.h:9); multiple of 256, <= 2048 */
+    int32_t moe_ffn_dim;       /* expert intermediate F (model.h:44); multiple of 256, <= 2048 */
     int32_t n_routed_experts;  /* E (model.h:21); 1..256 */
     int32_t n_experts_used;    /* K (model.h:22); 1..8 */
     int32_t n_shared_experts;  /* S (model.h:23); 0 or 1 */
@@ -149,6 +149,15 @@ typedef struct gmoe_kernel_times {
 } gmoe_kernel_times;
 int gmoe_profile(gmoe_ctx *ctx, int enable);
 int gmoe_profile_read(gmoe_ctx *ctx, gmoe_kernel_times *out);
+
+/* Diagnostic timeline of the persistent decode kernel. While enabled, every work
+ * item of a T=1 launch records three 100 MHz wall-clock stamps: picked up, inputs
+ * ready, done. Items of one layer are numbered E router items, then (K+1)*F/16
+ * gate/up items (shared expert first), then (K+1)*D/16 down items; layer after layer.
+ * gmoe_trace_items_read copies the most recent launch's stamps ([n][3]) and returns
+ * n, or a negative error. */
+int gmoe_trace_items(gmoe_ctx *ctx, int enable);
+int64_t gmoe_trace_items_read(gmoe_ctx *ctx, uint64_t *out, int64_t max_items);
 
 /* Algorithmic Q8_0 bytes (34 per 32 weights) that one forward of n_tokens reads
  * for its experts, given the routing of its most recent call; used for GB/s. */

@@ -13,7 +13,7 @@ from conftest import assert_close
 
 pytestmark = pytest.mark.gpu
 
-SMALL = gmoe.Shape(dim=256, moe_ffn_dim=128, n_routed_experts=16, n_experts_used=4)
+SMALL = gmoe.Shape(dim=256, moe_ffn_dim=256, n_routed_experts=16, n_experts_used=4)
 
 
 def run_case(shape, seed, T, norm_mode=gmoe.SYNTH_NORM_ONES, flags=0, layer=1):
