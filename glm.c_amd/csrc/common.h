@@ -55,6 +55,81 @@ __host__ __device__ static inline size_t gm_s_offset(int r, int b, int cols) {
 __device__ static inline float sqrt_rn_f32(float a) { return (float)sqrt((double)a); }
 
 // ---------------------------------------------------------------- reductions
+//
+// Cross-lane traffic uses DPP row operations (no LDS round trip) within each 16-lane
+// row and v_readlane across the four rows; ds_bpermute-based shuffles take ~100 clocks
+// each and a six-step chain of them dominated the router's latency.
+
+#define DPP_QUAD_1032 0xB1  // quad_perm [1,0,3,2]
+#define DPP_QUAD_2301 0x4E  // quad_perm [2,3,0,1]
+#define DPP_ROW_HALF_MIRROR 0x141
+#define DPP_ROW_MIRROR 0x140
+#define DPP_ROW_SHR(n) (0x110 + (n))
+
+template <int CTRL>
+__device__ static inline double dpp_d(double v, double fill) {
+    const int2 a = *(int2 *)&v, f = *(int2 *)&fill;
+    int2 r;
+    r.x = __builtin_amdgcn_update_dpp(f.x, a.x, CTRL, 0xF, 0xF, false);
+    r.y = __builtin_amdgcn_update_dpp(f.y, a.y, CTRL, 0xF, 0xF, false);
+    return *(double *)&r;
+}
+
+__device__ static inline double readlane_d(double v, int lane) {
+    const int2 a = *(int2 *)&v;
+    int2 r;
+    r.x = __builtin_amdgcn_readlane(a.x, lane);
+    r.y = __builtin_amdgcn_readlane(a.y, lane);
+    return *(double *)&r;
+}
+
+// Sum over the 64 lanes of a wave, returned to every lane (wave-uniform).
+__device__ static inline double wave_sum_dpp(double v) {
+    v += dpp_d<DPP_QUAD_1032>(v, 0.0);
+    v += dpp_d<DPP_QUAD_2301>(v, 0.0);
+    v += dpp_d<DPP_ROW_HALF_MIRROR>(v, 0.0);
+    v += dpp_d<DPP_ROW_MIRROR>(v, 0.0);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+
+// Maximum over the 64 lanes of a wave, returned to every lane (wave-uniform). NaN
+// inputs are ignored, as fmax ignores them.
+__device__ static inline double wave_max_dpp(double v) {
+    v = fmax(v, dpp_d<DPP_QUAD_1032>(v, -INFINITY));
+    v = fmax(v, dpp_d<DPP_QUAD_2301>(v, -INFINITY));
+    v = fmax(v, dpp_d<DPP_ROW_HALF_MIRROR>(v, -INFINITY));
+    v = fmax(v, dpp_d<DPP_ROW_MIRROR>(v, -INFINITY));
+    return fmax(fmax(readlane_d(v, 0), readlane_d(v, 16)), fmax(readlane_d(v, 32), readlane_d(v, 48)));
+}
+
+__device__ static inline float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Inclusive prefix sum over the lanes of a wave, in lane order.
+__device__ static inline double wave_incl_scan_dpp(double v) {
+    v += dpp_d<DPP_ROW_SHR(1)>(v, 0.0);
+    v += dpp_d<DPP_ROW_SHR(2)>(v, 0.0);
+    v += dpp_d<DPP_ROW_SHR(4)>(v, 0.0);
+    v += dpp_d<DPP_ROW_SHR(8)>(v, 0.0);
+    const double r0 = readlane_d(v, 15), r1 = readlane_d(v, 31), r2 = readlane_d(v, 47);
+    const int row = (threadIdx.x & 63) >> 4;
+    double off = 0.0;
+    if (row >= 1) off += r0;
+    if (row >= 2) off += r1;
+    if (row >= 3) off += r2;
+    return v + off;
+}
+
+// Block-wide sum of doubles for a 256-thread block, to every thread; `red` holds 4
+// doubles of shared memory.
+__device__ static inline double block_sum_fast(double v, double *red) {
+    v = wave_sum_dpp(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
 
 __device__ static inline double wave_sum_d(double v) {
 #pragma unroll

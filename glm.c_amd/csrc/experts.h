@@ -114,17 +114,25 @@ __device__ static inline void panel_compute(const PanelRegs<NMAT, NB> &r, int co
 #pragma unroll
     for (int u = 0; u < NB; u++) {
         if (u < cpw) {
+            // Both blocks' digit rows and exponents are read before the first product, without
+            // branches, so the shared-memory reads overlap. Lanes with m >= 3 read row 0 and
+            // use zeros.
+            long A[2];
+            int de[2];
 #pragma unroll
             for (int hh = 0; hh < 2; hh++) {
                 const int b = 2 * (j0 + u) + hh;
-                long A = 0;
-                if (m < 3) A = *(const long *)(dig + m * cols + 32 * b + kofs);
-                const int de = dexp[b];
+                const long av = *(const long *)(dig + (m < 3 ? m : 0) * cols + 32 * b + kofs);
+                A[hh] = m < 3 ? av : 0;
+                de[hh] = dexp[b];
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
 #pragma unroll
                 for (int i = 0; i < NMAT; i++) {
                     const unsigned sw = r.s[i][u];
                     const __half sc = __ushort_as_half((unsigned short)(hh ? (sw >> 16) : (sw & 0xffffu)));
-                    mfma_block(A, chunk_half(r.q[i][u], hh), sc, de, lane, acc[i]);
+                    mfma_block(A[hh], chunk_half(r.q[i][u], hh), sc, de[hh], lane, acc[i]);
                 }
             }
         }

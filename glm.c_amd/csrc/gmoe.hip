@@ -40,7 +40,8 @@ static void set_err(const char *fmt, ...) {
         }                                                                                \
     } while (0)
 
-#define GM_STACK_COUNTERS (SKC_PAD * 160)
+// stack counters: 16 fixed, one per 16-row panel of D (<= 128), two per layer (<= 256)
+#define GM_STACK_COUNTERS (SKC_PAD * (16 + 128 + 2 * 256))
 
 struct LayerDev {
     uint8_t *experts = nullptr;  // (E+1) * stride bytes, tiled
@@ -82,8 +83,9 @@ struct gmoe_ctx {
     // persistent decode kernel (stack.h)
     int stack_ok = 0;            // shape fits k_moe_stack
     int stack_grid = 0;          // co-resident blocks
-    int8_t *sk_dig = nullptr;    // [3][D]
-    int *sk_dexp = nullptr;      // [D/32]
+    uint8_t *sk_ws = nullptr;    // per-layer workspace, L regions of sk_ws_layer bytes
+    size_t sk_ws_layer = 0;
+    StackWs sk_o{};
     unsigned *sk_ctr = nullptr;  // [GM_STACK_COUNTERS]
     int *sk_error = nullptr;
     StackLayer *sk_layers = nullptr;  // [L], device
@@ -138,7 +140,7 @@ static void free_ctx(gmoe_ctx *c) {
     void *bufs[] = {c->xn, c->router_prob, c->topk_w, c->topk_ws, c->h, c->y, c->shared_out, c->routed_out,
                     c->stage, c->topk_idx, c->tok_counter, c->panel_counter, c->disp_counter, c->disp_tmp_tok,
                     c->disp_tmp_slot, c->disp_counts, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
-                    c->stats_dev, c->x_host_io, c->staging, c->sk_dig, c->sk_dexp, c->sk_ctr, c->sk_error,
+                    c->stats_dev, c->x_host_io, c->staging, c->sk_ws, c->sk_ctr, c->sk_error,
                     c->sk_layers, c->sk_trace};
     for (void *b : bufs) dev_free(b);
     delete c;
@@ -233,8 +235,28 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     rc |= dev_alloc(&c->hist_w, (size_t)c->L * T * K);
     rc |= dev_alloc(&c->stats_dev, GM_STAT_COUNT);
     rc |= dev_alloc(&c->x_host_io, T * D);
-    rc |= dev_alloc(&c->sk_dig, 3 * D);
-    rc |= dev_alloc(&c->sk_dexp, D / 32);
+    {
+        // per-layer regions of the persistent kernel, each buffer on its own 256-byte lines
+        size_t off = 0;
+        auto take = [&](size_t bytes) {
+            const size_t at = off;
+            off += (bytes + 255) & ~(size_t)255;
+            return at;
+        };
+        c->sk_o.x = take(D * sizeof(float));
+        c->sk_o.xn = take(D * sizeof(float));
+        c->sk_o.dig = take(3 * D);
+        c->sk_o.dexp = take(D / 32 * sizeof(int));
+        c->sk_o.stage = take(E * sizeof(double2));
+        c->sk_o.ex_idx = take(K * sizeof(int));
+        c->sk_o.ex_w = take(K * sizeof(float));
+        c->sk_o.ex_p = take(E * sizeof(float));
+        c->sk_o.g = take(NS * F * sizeof(float));
+        c->sk_o.u = take(NS * F * sizeof(float));
+        c->sk_o.y = take(NS * D * sizeof(float));
+        c->sk_ws_layer = off;
+        rc |= dev_alloc(&c->sk_ws, (size_t)c->L * off);
+    }
     rc |= dev_alloc(&c->sk_ctr, GM_STACK_COUNTERS);
     rc |= dev_alloc(&c->sk_error, 1);
     rc |= dev_alloc(&c->sk_layers, (size_t)c->L);
@@ -258,7 +280,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     }
     // The persistent decode kernel holds one panel's chunks per wave in registers and
     // xn in shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots.
-    c->stack_ok = c->K + 1 <= SK_MAX_SLOTS && SKC(SKC_PANEL + c->D / 16) <= GM_STACK_COUNTERS;
+    c->stack_ok = c->K + 1 <= SK_MAX_SLOTS && SKC_EXACT(c->D / 16, c->L) <= GM_STACK_COUNTERS;
     const char *env = getenv("GMOE_STACK_KERNEL");
     if (env && env[0] == '0') c->stack_ok = 0;
     if (c->stack_ok) {
@@ -271,6 +293,8 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
             cus = prop.multiProcessorCount;
             const int want = per_cu < 2 ? per_cu : 2;  // 2 blocks (8 waves) per CU
             c->stack_grid = want * cus;
+            // roles need a router block per item, a shared-expert block and a routed block
+            if (c->stack_grid < (c->E + SK_RX - 1) / SK_RX + 2) c->stack_ok = 0;
         }
     }
     *out = c;
@@ -412,7 +436,7 @@ extern "C" int64_t gmoe_trace_items_read(gmoe_ctx *c, uint64_t *out, int64_t max
     if (!c->sk_trace || c->sk_trace_last == 0) return 0;
     const int64_t n = c->sk_trace_last < max_items ? c->sk_trace_last : max_items;
     HIP_OK(hipDeviceSynchronize());
-    HIP_OK(hipMemcpy(out, c->sk_trace, (size_t)n * 3 * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(out, c->sk_trace, (size_t)n * SK_TRACE_STAMPS * sizeof(uint64_t), hipMemcpyDeviceToHost));
     return n;
 }
 
@@ -474,7 +498,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.n_layers = n;
     a.first_layer = first;
     a.x_in = x_in;
-    a.x = x_out;
+    a.x_out = x_out;
     a.D = c->D;
     a.F = c->F;
     a.E = c->E;
@@ -489,38 +513,43 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.off_gs = c->off_gs;
     a.off_us = c->off_us;
     a.off_ds = c->off_ds;
-    a.stage = c->stage;
-    a.dig = c->sk_dig;
-    a.dexp = c->sk_dexp;
+    a.ws = c->sk_ws;
+    a.ws_layer_bytes = c->sk_ws_layer;
+    a.o = c->sk_o;
     a.xn = c->xn;
     a.topk_idx = c->topk_idx;
     a.topk_w = c->topk_w;
-    a.topk_ws = c->topk_ws;
     a.router_prob = c->router_prob;
     a.hist_idx = c->hist_idx;
     a.hist_w = c->hist_w;
     a.hist_stride = c->Tmax * c->K;
-    a.h = c->h;
-    a.y = c->y;
     a.shared_out = c->shared_out;
     a.routed_out = c->routed_out;
     a.ctr = c->sk_ctr;
     a.stats = c->stats_dev;
     a.error = c->sk_error;
     a.trace = nullptr;
+    {
+        // shared-expert role: about 1/(K+1) of the non-router blocks
+        const int nr = (c->E + SK_RX - 1) / SK_RX;
+        int nsb = (c->stack_grid - nr) / (c->K + 1);
+        if (nsb < 1) nsb = 1;
+        a.shared_blocks = nsb;
+    }
     if (c->sk_trace_on) {
-        const size_t items = (size_t)(c->E + (c->K + 1) * (c->F / 16 + c->D / 16)) * n;
+        const size_t items = (size_t)((c->E + SK_RX - 1) / SK_RX + (c->K + 1) * (c->F / 16 + c->D / 16)) * n;
         if (items > c->sk_trace_items) {
             dev_free(c->sk_trace);
             c->sk_trace = nullptr;
             c->sk_trace_items = 0;
-            if (dev_alloc(&c->sk_trace, 3 * items) != GMOE_OK) return GMOE_ERR_NOMEM;
+            if (dev_alloc(&c->sk_trace, SK_TRACE_STAMPS * items) != GMOE_OK) return GMOE_ERR_NOMEM;
             c->sk_trace_items = items;
         }
         a.trace = c->sk_trace;
         c->sk_trace_last = (long long)items;
+        HIP_OK(hipMemsetAsync(c->sk_trace, 0, SK_TRACE_STAMPS * items * sizeof(uint64_t), st));
     }
-    const int n_ctr = SKC(SKC_PANEL + c->D / 16);
+    const int n_ctr = SKC_EXACT(c->D / 16, n) + SKC_PAD;
     hipLaunchKernelGGL(k_stack_reset, dim3(1), dim3(SK_BLOCK), 0, st, c->sk_ctr, n_ctr, c->sk_error);
     ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_STACK);
     hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);

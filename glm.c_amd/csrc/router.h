@@ -67,16 +67,19 @@ __device__ static float certified_mean_sq(const float *xt, int D, double *red, f
 }
 
 // Interval of fl32(p + b) where p = fl32(1 / fl32(1 + expf(-s))) and s in [S-B, S+B].
+// The sigmoid bounds are evaluated in fp32 at the interval ends rounded outwards; the
+// GPU's expf and the CPU's libm expf are both within 2 ulp, the add and the divide round
+// once each, so p moves by less than 2^-20 relative -- widened to 2^-19 for margin, and
+// one more ulp for the final add.
 __device__ static inline void selection_interval(double S, double B, float bias, double *lo, double *hi) {
-    const double plo = 1.0 / (1.0 + exp(-(S - B)));
-    const double phi = 1.0 / (1.0 + exp(-(S + B)));
-    // expf within 1 ulp, then one rounding each for the add and the divide: 2^-22 relative,
-    // doubled for margin.
-    const double dp = 0x1p-21;
+    const float slo = __double2float_rd(S - B), shi = __double2float_ru(S + B);
+    const double plo = (double)(1.0f / (1.0f + expf(-slo)));
+    const double phi = (double)(1.0f / (1.0f + expf(-shi)));
+    const double dp = 0x1p-19;
     const double vlo = plo * (1.0 - dp) + (double)bias;
     const double vhi = phi * (1.0 + dp) + (double)bias;
-    *lo = vlo - fabs(vlo) * 0x1p-23 - 0x1p-148;
-    *hi = vhi + fabs(vhi) * 0x1p-23 + 0x1p-148;
+    *lo = vlo - fabs(vlo) * 0x1p-22 - 0x1p-148;
+    *hi = vhi + fabs(vhi) * 0x1p-22 + 0x1p-148;
 }
 
 // Wave-wide argmax over (key desc, index asc); lanes hold candidates in registers.

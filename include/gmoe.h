@@ -151,11 +151,12 @@ int gmoe_profile(gmoe_ctx *ctx, int enable);
 int gmoe_profile_read(gmoe_ctx *ctx, gmoe_kernel_times *out);
 
 /* Diagnostic timeline of the persistent decode kernel. While enabled, every work
- * item of a T=1 launch records three 100 MHz wall-clock stamps: picked up, inputs
- * ready, done. Items of one layer are numbered E router items, then (K+1)*F/16
- * gate/up items (shared expert first), then (K+1)*D/16 down items; layer after layer.
- * gmoe_trace_items_read copies the most recent launch's stamps ([n][3]) and returns
- * n, or a negative error. */
+ * item of a T=1 launch records eight 100 MHz wall-clock stamps (0 where a stage does
+ * not apply): picked up, inputs ready, done, top-k known, products done, results
+ * stored, activations staged, counter published. Items of one layer are numbered
+ * E/2 router items, then 2*(K+1)*F/16 gate/up items (shared expert first), then
+ * (K+1)*D/16 down items; layer after layer. gmoe_trace_items_read copies the most
+ * recent launch's stamps ([n][8]) and returns n, or a negative error. */
 int gmoe_trace_items(gmoe_ctx *ctx, int enable);
 int64_t gmoe_trace_items_read(gmoe_ctx *ctx, uint64_t *out, int64_t max_items);
 
