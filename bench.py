@@ -93,6 +93,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device 5 times (calibrates the PMC byte counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -103,6 +105,16 @@ def main():
 
     import numpy as np
     import gmoe
+
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src, dst = gmoe.DeviceArray(n), gmoe.DeviceArray(n)
+        gmoe.hip_check(gmoe.hip().hipMemset(src.ptr, 1, n), "hipMemset")
+        for _ in range(5):
+            gmoe.hip_check(gmoe.hip().hipMemcpy(dst.ptr, src.ptr, n, gmoe.HIP_D2D), "hipMemcpy D2D")
+        gmoe.hip_check(gmoe.hip().hipDeviceSynchronize(), "sync")
+        print(json.dumps({"copy_probe_bytes": n, "copies": 5}), flush=True)
+        return
 
     shape = gmoe.GLM47_FLASH
     L = args.layers
@@ -159,6 +171,8 @@ def main():
     stream.sync()
     prof = ctx.profile_read()
     ctx.profile(False)
+    if not prof:
+        raise SystemExit("--profile-steps must be at least 1: the roofline needs the kernel's launch time")
     K1 = shape.K + 1
     mat = shape.F * shape.D * 34 // 32
     kernel_bytes = {"k_gate_up": K1 * 2 * mat, "k_down_combine": K1 * mat, "k_moe_stack": bytes_per_token}

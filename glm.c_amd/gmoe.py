@@ -25,7 +25,7 @@ SYNTH_BIAS_NORMAL, SYNTH_BIAS_ZIPF = 0, 1
 # Zipf-shaped router bias for the skewed-routing workload: popularity ~ rank^-1.2,
 # gain chosen so the 4 most popular experts take about 40% of top-4 assignments.
 ZIPF_S = 1.2
-ZIPF_BETA = 0.06
+ZIPF_BETA = 0.095
 
 
 class GmoeConfig(C.Structure):

@@ -72,7 +72,7 @@ float synth_round_fp16(float f) {
         double q = ldexp(1.0, e - 11); /* 10 fraction bits */
         r = rint(a / q) * q;
     }
-    return (float)(f < 0 ? -r : r);
+    return (float)copysign(r, (double)f);
 }
 
 static void fill_q8_matrix(uint64_t kq, uint64_t ks, int rows, int cols, int gs, int8_t *q, float *s) {

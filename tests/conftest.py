@@ -53,3 +53,16 @@ def _require_gpu_for_gpu_tests(request):
             pass
         if n == 0:
             pytest.fail("gpu test but no HIP device is visible")
+
+
+@pytest.fixture(scope="session")
+def glm_layer1():
+    """GLM-4.7-Flash layer 1 weights (seed 0), as the golden fixtures used them."""
+    import gmoe
+    return gmoe.HostLayer(gmoe.GLM47_FLASH, seed=0, layer=1)
+
+
+@pytest.fixture(scope="session")
+def glm_layer1_zipf():
+    import gmoe
+    return gmoe.HostLayer(gmoe.GLM47_FLASH, seed=0, layer=1, bias_mode=gmoe.SYNTH_BIAS_ZIPF)
