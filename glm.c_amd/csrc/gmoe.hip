@@ -22,6 +22,8 @@
 #include "router.h"
 #include "stack.h"
 
+static_assert(SK_TRACE_STAMPS == GMOE_TRACE_STAMPS, "trace stamps per item: kernel and ABI disagree");
+
 static thread_local char g_err[512];
 
 static void set_err(const char *fmt, ...) {
