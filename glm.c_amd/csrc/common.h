@@ -49,6 +49,19 @@ __host__ __device__ static inline size_t gm_s_offset(int r, int b, int cols) {
     return (size_t)r * (size_t)(cols >> 5) + (size_t)b;
 }
 
+// Down matrices ([D rows][F cols]) use the column-slice layout instead: slice j holds
+// columns 16j..16j+15 of every row, 16 bytes per row, rows in order, and the fp16
+// scales are block-major [F/32][D]. A decode item that owns 16 columns of F then reads
+// its D x 16 slice as one contiguous, fully coalesced run.
+#define GM_LAYOUT_PANELS 0
+#define GM_LAYOUT_SLICES 1
+__host__ __device__ static inline size_t gm_dq_offset(int r, int c, int rows) {
+    return ((size_t)(c >> 4) * (size_t)rows + (size_t)r) * 16 + (size_t)(c & 15);
+}
+__host__ __device__ static inline size_t gm_ds_offset(int r, int b, int rows) {
+    return (size_t)b * (size_t)rows + (size_t)r;
+}
+
 // Correctly rounded fp32 square root. The fp32 intrinsic lowers to v_sqrt_f32, which is
 // not always correctly rounded; the fp64 lowering is (Newton-refined), and rounding a
 // correctly rounded fp64 root to fp32 is exact-rounding since 53 >= 2*24 + 2.

@@ -57,15 +57,23 @@ __device__ static inline long chunk_half(const u32x4 &c, int h) {
     return h == 0 ? (long)(((unsigned long long)c.y << 32) | c.x) : (long)(((unsigned long long)c.w << 32) | c.z);
 }
 
-// One block of 32 columns: digit dots via MFMA, then lanes 0..15 accumulate their row
-// with the block's fp16 scale `sc` (already in a register) and digit exponent.
-__device__ static inline void mfma_block(long A, long B, __half sc, int dexp, int lane, float &acc) {
+// One block of 32 columns: the three digit dots of every weight row via one MFMA.
+// Lanes 0..15 hold their row's dots in d[0..2]; the other lanes hold rows 4.. of the
+// product, whose A rows are zero, so their d are zero.
+__device__ static inline v4i mfma_digits(long A, long B) {
     const v4i zero = {0, 0, 0, 0};
-    v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
-    if (lane < 16) {
-        const float f = digits_to_float(d[0], d[1], d[2]);
-        acc = fmaf(f, ldexpf(__half2float(sc), dexp), acc);
-    }
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+}
+
+// acc += (block dot) * fp16 scale * 2^dexp, on every lane without branching (lanes >= 16
+// add zeros and are never read).
+__device__ static inline void mfma_accumulate(const v4i &d, __half sc, int dexp, float &acc) {
+    acc = fmaf(digits_to_float(d[0], d[1], d[2]), ldexpf(__half2float(sc), dexp), acc);
+}
+
+__device__ static inline void mfma_block(long A, long B, __half sc, int dexp, int lane, float &acc) {
+    (void)lane;
+    mfma_accumulate(mfma_digits(A, B), sc, dexp, acc);
 }
 
 // A wave's share of one 16-row panel: the chunks [w*cpw, (w+1)*cpw) of one or two
@@ -141,8 +149,117 @@ __device__ static inline void panel_compute(const PanelRegs<NMAT, NB> &r, int co
     for (int i = 0; i < NMAT; i++) out[i] = acc[i];
 }
 
+// The q chunks of panel_load without the scales, for callers that stage a panel's
+// scales in shared memory with one wide load per lane (panel_compute_sc).
+template <int NMAT, int NB>
+__device__ static inline void panel_load_q(PanelRegs<NMAT, NB> &r, const uint8_t *q0, const uint8_t *q1, int p,
+                                           int cols) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int nchunks = cols >> 6, cpw = nchunks >> 2;
+    const int j0 = w * cpw;
+    const uint8_t *qs[2] = {q0, q1};
+    const GM_GLOBAL u32x4 *qp[2];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) qp[m] = gbl((const u32x4 *)(qs[m] + ((size_t)p * nchunks + j0) * GM_CHUNK_BYTES)) + lane;
+    // chunk u of every matrix before chunk u + 1 of any: consumers can start on u early
+#pragma unroll
+    for (int u = 0; u < NB; u++)
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+            if (u < cpw) r.q[m][u] = __builtin_nontemporal_load(qp[m] + (size_t)u * 64);
+}
+
+// panel_compute with the panel's fp16 scales in shared memory: sc[m] holds matrix m's
+// [16 rows][cols/32] scales of the panel.
+template <int NMAT, int NB>
+__device__ static inline void panel_compute_sc(const PanelRegs<NMAT, NB> &r, int cols, const int8_t *dig,
+                                               const int *dexp, const unsigned short *const *sc, float *out) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int cpw = (cols >> 6) >> 2, j0 = w * cpw, nblocks = cols >> 5;
+    const int m = lane & 15, kofs = 8 * (lane >> 4);
+    float acc[NMAT];
+#pragma unroll
+    for (int i = 0; i < NMAT; i++) acc[i] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        if (u < cpw) {
+            long A[2];
+            int de[2];
+            unsigned short sv[NMAT][2];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int b = 2 * (j0 + u) + hh;
+                const long av = *(const long *)(dig + (m < 3 ? m : 0) * cols + 32 * b + kofs);
+                A[hh] = m < 3 ? av : 0;
+                de[hh] = dexp[b];
+#pragma unroll
+                for (int i = 0; i < NMAT; i++) sv[i][hh] = sc[i][m * nblocks + b];
+            }
+            v4i d[2][NMAT];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                for (int i = 0; i < NMAT; i++) d[hh][i] = mfma_digits(A[hh], chunk_half(r.q[i][u], hh));
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                for (int i = 0; i < NMAT; i++) mfma_accumulate(d[hh][i], __ushort_as_half(sv[i][hh]), de[hh], acc[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NMAT; i++) out[i] = acc[i];
+}
+
 // Column tiling used by the expert kernels: cols/64 chunks split evenly over 4 waves.
 #define EX_NB_MAX 8  // chunks per wave in registers: cols <= 2048
+
+// One 16-row panel p of a down matrix in the column-slice layout. Each wave takes the
+// 32-column blocks [w*bpw, (w+1)*bpw); for block b, lane l holds the MFMA B operand:
+// row 16p + l%16, columns 32b + 8*(l/16) .. +8, which is 8 bytes of slice 2b + (l/32).
+// Lanes 0..15 also hold their row's fp16 scale of block b.
+#define EX_BB_MAX 16  // blocks per wave: cols <= 2048
+template <int NB>
+struct SliceRegs {
+    unsigned long long q[NB];
+    unsigned short s[NB];
+};
+
+template <int NB>
+__device__ static inline void slice_panel_load(SliceRegs<NB> &r, const uint8_t *q, const __half *s, int p, int rows,
+                                               int cols) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int bpw = (cols >> 5) >> 2, b0 = w * bpw;
+    const int row = p * 16 + (lane & 15), kq = lane >> 4;
+    const GM_GLOBAL uint8_t *qg = gbl(q) + (size_t)row * 16 + 8 * (kq & 1);
+    const GM_GLOBAL unsigned short *sg = gbl((const unsigned short *)s) + row;
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        if (u < bpw) {
+            const int b = b0 + u;
+            r.q[u] = __builtin_nontemporal_load((const GM_GLOBAL unsigned long long *)(qg + (size_t)(2 * b + (kq >> 1)) * rows * 16));
+            r.s[u] = lane < 16 ? sg[(size_t)b * rows] : (unsigned short)0;
+        }
+    }
+}
+
+// Partial dots of the wave's blocks with the activation digits; lanes 0..15 get their row's sum.
+template <int NB>
+__device__ static inline float slice_panel_compute(const SliceRegs<NB> &r, int cols, const int8_t *dig,
+                                                   const int *dexp) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int bpw = (cols >> 5) >> 2, b0 = w * bpw;
+    const int m = lane & 15, kofs = 8 * (lane >> 4);
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        if (u < bpw) {
+            const int b = b0 + u;
+            const long av = *(const long *)(dig + (m < 3 ? m : 0) * cols + 32 * b + kofs);
+            mfma_block(m < 3 ? av : 0, (long)r.q[u], __ushort_as_half(r.s[u]), dexp[b], lane, acc);
+        }
+    }
+    return acc;
+}
 
 // grid (F/16, K+S, T): h[t][slot][F] = silu(gate . xn) * (up . xn) for the slot's expert.
 __global__ __launch_bounds__(EX_BLOCK) void k_gate_up(ExpertArgs a, const float *__restrict__ xn,
@@ -213,12 +330,11 @@ __global__ __launch_bounds__(EX_BLOCK) void k_down_combine(ExpertArgs a, Combine
         int8_t *dig = (int8_t *)smem;
         int *dexp = (int *)(smem + 3 * F);
         const uint8_t *base = a.experts + (size_t)e * a.stride;
-        PanelRegs<1, EX_NB_MAX> pr;
-        panel_load<1, EX_NB_MAX>(pr, base + a.off_dq, (const __half *)(base + a.off_ds), nullptr, nullptr, p, F);
+        SliceRegs<EX_BB_MAX> sr;
+        slice_panel_load<EX_BB_MAX>(sr, base + a.off_dq, (const __half *)(base + a.off_ds), p, D, F);
         load_digits(h + ((size_t)t * nslots + slot) * F, F, dig, dexp);
         __syncthreads();
-        float yv;
-        panel_compute<1, EX_NB_MAX>(pr, F, dig, dexp, &yv);
+        const float yv = slice_panel_compute<EX_BB_MAX>(sr, F, dig, dexp);
         const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
         if (lane < 16) part[w][lane] = yv;
         __syncthreads();

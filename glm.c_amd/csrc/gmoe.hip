@@ -24,6 +24,14 @@
 
 static_assert(SK_TRACE_STAMPS == GMOE_TRACE_STAMPS, "trace stamps per item: kernel and ABI disagree");
 
+// Router blocks of the persistent kernel: the largest power of two <= min(E, 64), so
+// that every block holds at most GM_MAX_E / 64 experts.
+static int stack_routers(int E) {
+    int nr = 1;
+    while (nr * 2 <= E && nr * 2 <= SK_NR_MAX) nr *= 2;
+    return nr;
+}
+
 static thread_local char g_err[512];
 
 static void set_err(const char *fmt, ...) {
@@ -42,8 +50,6 @@ static void set_err(const char *fmt, ...) {
         }                                                                                \
     } while (0)
 
-// stack counters: 16 fixed, one per 16-row panel of D (<= 128), two per layer (<= 256)
-#define GM_STACK_COUNTERS (SKC_PAD * (16 + 128 + 2 * 256))
 
 struct LayerDev {
     uint8_t *experts = nullptr;  // (E+1) * stride bytes, tiled
@@ -249,13 +255,11 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         c->sk_o.xn = take(D * sizeof(float));
         c->sk_o.dig = take(3 * D);
         c->sk_o.dexp = take(D / 32 * sizeof(int));
-        c->sk_o.stage = take(E * sizeof(double2));
+        c->sk_o.stage = take(E * sizeof(StageEnt));
         c->sk_o.ex_idx = take(K * sizeof(int));
         c->sk_o.ex_w = take(K * sizeof(float));
         c->sk_o.ex_p = take(E * sizeof(float));
-        c->sk_o.g = take(NS * F * sizeof(float));
-        c->sk_o.u = take(NS * F * sizeof(float));
-        c->sk_o.y = take(NS * D * sizeof(float));
+        c->sk_o.ypart = take(NS * (F / 16) * D * sizeof(float));
         c->sk_ws_layer = off;
         rc |= dev_alloc(&c->sk_ws, (size_t)c->L * off);
     }
@@ -282,7 +286,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     }
     // The persistent decode kernel holds one panel's chunks per wave in registers and
     // xn in shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots.
-    c->stack_ok = c->K + 1 <= SK_MAX_SLOTS && SKC_EXACT(c->D / 16, c->L) <= GM_STACK_COUNTERS;
+    c->stack_ok = c->L <= SK_MAX_LAYERS;
     const char *env = getenv("GMOE_STACK_KERNEL");
     if (env && env[0] == '0') c->stack_ok = 0;
     if (c->stack_ok) {
@@ -295,8 +299,8 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
             cus = prop.multiProcessorCount;
             const int want = per_cu < 2 ? per_cu : 2;  // 2 blocks (8 waves) per CU
             c->stack_grid = want * cus;
-            // roles need a router block per item, a shared-expert block and a routed block
-            if (c->stack_grid < (c->E + SK_RX - 1) / SK_RX + 2) c->stack_ok = 0;
+            // roles: the router blocks, at least one shared-expert and one routed block
+            if (c->stack_grid < stack_routers(c->E) + 2) c->stack_ok = 0;
         }
     }
     *out = c;
@@ -313,7 +317,7 @@ static int copy_in(void *dst, const void *src, size_t bytes) {
 // Upload n_mat raw matrices (rows x cols int8 + fp32 scales) and repack them to
 // dst + m*dst_stride (+off_q for q, +off_s for scales).
 static int upload_matrices(gmoe_ctx *c, const int8_t *q, const float *s, int n_mat, int rows, int cols, uint8_t *dst,
-                           size_t dst_stride, size_t off_q, size_t off_s, unsigned long long *inexact_dev) {
+                           size_t dst_stride, size_t off_q, size_t off_s, int layout, unsigned long long *inexact_dev) {
     const size_t qbytes = (size_t)n_mat * rows * cols;
     const size_t sbytes = (size_t)n_mat * rows * (cols / GM_QBLOCK) * sizeof(float);
     if (qbytes + sbytes > c->staging_bytes) {
@@ -329,10 +333,11 @@ static int upload_matrices(gmoe_ctx *c, const int8_t *q, const float *s, int n_m
     if (rc) return rc;
     const size_t units = qbytes / 16;
     hipLaunchKernelGGL(k_repack_q, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, 0,
-                       (const int8_t *)c->staging, dst + off_q, dst_stride, rows, cols, n_mat);
+                       (const int8_t *)c->staging, dst + off_q, dst_stride, rows, cols, n_mat, layout);
     const size_t ns = sbytes / sizeof(float);
     hipLaunchKernelGGL(k_repack_s, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, 0,
-                       (const float *)(c->staging + qbytes), dst + off_s, dst_stride, rows, cols, n_mat, inexact_dev);
+                       (const float *)(c->staging + qbytes), dst + off_s, dst_stride, rows, cols, n_mat, layout,
+                       inexact_dev);
     HIP_OK(hipGetLastError());
     HIP_OK(hipDeviceSynchronize());
     return GMOE_OK;
@@ -370,13 +375,15 @@ extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weight
     if (dev_alloc(&inexact, 1) != GMOE_OK) return GMOE_ERR_NOMEM;
     HIP_OK(hipMemset(inexact, 0, sizeof(unsigned long long)));
     uint8_t *sh = L.experts + (size_t)E * c->stride;
-    rc = upload_matrices(c, w->gate_sh_q, w->gate_sh_s, 1, F, D, sh, c->stride, c->off_gq, c->off_gs, inexact);
-    if (!rc) rc = upload_matrices(c, w->up_sh_q, w->up_sh_s, 1, F, D, sh, c->stride, c->off_uq, c->off_us, inexact);
-    if (!rc) rc = upload_matrices(c, w->down_sh_q, w->down_sh_s, 1, D, F, sh, c->stride, c->off_dq, c->off_ds, inexact);
+    const int P = GM_LAYOUT_PANELS, S = GM_LAYOUT_SLICES;  // gate/up in row panels, down in column slices
+    rc = upload_matrices(c, w->gate_sh_q, w->gate_sh_s, 1, F, D, sh, c->stride, c->off_gq, c->off_gs, P, inexact);
+    if (!rc) rc = upload_matrices(c, w->up_sh_q, w->up_sh_s, 1, F, D, sh, c->stride, c->off_uq, c->off_us, P, inexact);
+    if (!rc) rc = upload_matrices(c, w->down_sh_q, w->down_sh_s, 1, D, F, sh, c->stride, c->off_dq, c->off_ds, S, inexact);
     if (has_routed) {
-        if (!rc) rc = upload_matrices(c, w->gate_q, w->gate_s, E, F, D, L.experts, c->stride, c->off_gq, c->off_gs, inexact);
-        if (!rc) rc = upload_matrices(c, w->up_q, w->up_s, E, F, D, L.experts, c->stride, c->off_uq, c->off_us, inexact);
-        if (!rc) rc = upload_matrices(c, w->down_q, w->down_s, E, D, F, L.experts, c->stride, c->off_dq, c->off_ds, inexact);
+        uint8_t *ex = L.experts;
+        if (!rc) rc = upload_matrices(c, w->gate_q, w->gate_s, E, F, D, ex, c->stride, c->off_gq, c->off_gs, P, inexact);
+        if (!rc) rc = upload_matrices(c, w->up_q, w->up_s, E, F, D, ex, c->stride, c->off_uq, c->off_us, P, inexact);
+        if (!rc) rc = upload_matrices(c, w->down_q, w->down_s, E, D, F, ex, c->stride, c->off_dq, c->off_ds, S, inexact);
     }
     unsigned long long n_inexact = 0;
     if (!rc && hipMemcpy(&n_inexact, inexact, sizeof(n_inexact), hipMemcpyDeviceToHost) != hipSuccess) {
@@ -532,14 +539,21 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.error = c->sk_error;
     a.trace = nullptr;
     {
-        // shared-expert role: about 1/(K+1) of the non-router blocks
-        const int nr = (c->E + SK_RX - 1) / SK_RX;
-        int nsb = (c->stack_grid - nr) / (c->K + 1);
-        if (nsb < 1) nsb = 1;
+        // One routed block per routed item when the grid allows, the rest of the non-router
+        // blocks on the shared expert (at most one per item); otherwise split in proportion.
+        const int nr = stack_routers(c->E), npf = c->F / 16;
+        const int avail = c->stack_grid - nr;
+        int nwb = c->K * npf, nsb = avail - nwb;
+        if (nsb < 1) {
+            nsb = avail / (c->K + 1) > 0 ? avail / (c->K + 1) : 1;
+            nwb = avail - nsb;
+        }
+        if (nsb > npf) nsb = npf;
+        a.n_router = nr;
         a.shared_blocks = nsb;
     }
     if (c->sk_trace_on) {
-        const size_t items = (size_t)((c->E + SK_RX - 1) / SK_RX + (c->K + 1) * (c->F / 16 + c->D / 16)) * n;
+        const size_t items = (size_t)(stack_routers(c->E) + c->D / SK_CROWS + (c->K + 1) * (c->F / 16)) * n;
         if (items > c->sk_trace_items) {
             dev_free(c->sk_trace);
             c->sk_trace = nullptr;
@@ -551,8 +565,9 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         c->sk_trace_last = (long long)items;
         HIP_OK(hipMemsetAsync(c->sk_trace, 0, SK_TRACE_STAMPS * items * sizeof(uint64_t), st));
     }
-    const int n_ctr = SKC_EXACT(c->D / 16, n) + SKC_PAD;
-    hipLaunchKernelGGL(k_stack_reset, dim3(1), dim3(SK_BLOCK), 0, st, c->sk_ctr, n_ctr, c->sk_error);
+    const int n_ctr = SK_CTR_WORDS(n);
+    hipLaunchKernelGGL(k_stack_reset, dim3((n_ctr + SK_BLOCK - 1) / SK_BLOCK), dim3(SK_BLOCK), 0, st, c->sk_ctr, n_ctr,
+                       c->sk_error);
     ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_STACK);
     hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
     prof_end(pr, st);

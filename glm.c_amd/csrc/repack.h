@@ -4,15 +4,22 @@
 
 #include "common.h"
 
-// One thread per 16-byte lane unit of the tiled q plane, for n_mat matrices of
-// rows x cols laid out back to back in `raw`; matrix m goes to dst + m * dst_stride.
+// One thread per 16-byte unit of the q plane, for n_mat matrices of rows x cols laid
+// out back to back in `raw`; matrix m goes to dst + m * dst_stride, in the tiled panel
+// layout or (GM_LAYOUT_SLICES) the column-slice layout.
 __global__ void k_repack_q(const int8_t *__restrict__ raw, uint8_t *__restrict__ dst, size_t dst_stride, int rows,
-                           int cols, int n_mat) {
+                           int cols, int n_mat, int layout) {
     const size_t units = (size_t)rows * cols / 16;
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= units * (size_t)n_mat) return;
     const int m = (int)(gid / units);
     const size_t u = gid % units;
+    if (layout == GM_LAYOUT_SLICES) {
+        const int r = (int)(u % rows), j = (int)(u / rows);
+        const u32x4 v = *(const u32x4 *)(raw + (size_t)m * rows * cols + (size_t)r * cols + 16 * (size_t)j);
+        *(u32x4 *)(dst + (size_t)m * dst_stride + u * 16) = v;
+        return;
+    }
     const int lane = (int)(u & 63);
     const size_t pj = u >> 6;
     const int nch = cols >> 6;
@@ -32,7 +39,7 @@ __global__ void k_repack_q(const int8_t *__restrict__ raw, uint8_t *__restrict__
 
 // One thread per scale; counts scales whose fp16 rounding is not exact.
 __global__ void k_repack_s(const float *__restrict__ raw, uint8_t *__restrict__ dst, size_t dst_stride, int rows,
-                           int cols, int n_mat, unsigned long long *inexact) {
+                           int cols, int n_mat, int layout, unsigned long long *inexact) {
     const int nb = cols >> 5;
     const size_t per = (size_t)rows * nb;
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -44,5 +51,5 @@ __global__ void k_repack_s(const float *__restrict__ raw, uint8_t *__restrict__ 
     const __half hs = __float2half_rn(s);
     if (__half2float(hs) != s) atomicAdd(inexact, 1ull);
     __half *out = (__half *)(dst + (size_t)m * dst_stride);
-    out[gm_s_offset(r, b, cols)] = hs;
+    out[layout == GM_LAYOUT_SLICES ? gm_ds_offset(r, b, rows) : gm_s_offset(r, b, cols)] = hs;
 }

@@ -1,19 +1,25 @@
 // stack.h -- persistent decode kernel: T=1 through a run of MoE layers in one launch.
 //
 // A decode step is a chain of small, strictly dependent phases per layer
-// (infer.c:1087-1216):  x -> rmsnorm + router -> top-k -> gate/up (K+1 experts) ->
-// down (K+1 experts) + combine -> x'.  Each phase moves 1-35 MB, a few microseconds of
-// HBM time, so kernel boundaries (~2 us each on this GPU) would cost as much as the
-// work. Instead one grid of co-resident blocks walks a per-layer work list in
-// topological order:
-//   router items   2 experts each: rmsnorm (bit-exact) + fp64 logits and error bounds;
-//                  every routed item then certifies the top-k itself (see router.h)
-//   gate/up items  (slot, 16-row panel): gate and up rows of one expert panel
-//   down items     (slot, 16-row panel of D): h = silu(gate) * up, then down; the last
-//                  slot item of a panel forms x' = x + (shared + sum_k w_k y_k)
-// Blocks have roles (router, shared expert, routed experts) and walk the layers in
-// order; an item only waits for items of the same or an earlier layer that come before
-// it in their role's order, so with all blocks resident some unfinished item can always run.
+// (infer.c:1087-1216). Each phase moves 0.5-40 MB, a few microseconds of HBM time, so
+// kernel boundaries (~2 us each on this GPU) would cost as much as the work. One grid
+// of co-resident blocks walks the layers instead, with three roles:
+//
+//   router blocks (n_router, <= 64)  per layer: rmsnorm (bit-exact) and the fp64 logit
+//       of their experts with a rigorous bound on glm.c's fp32 chain, turned into a
+//       selection interval; block 0 also publishes xn in digit form. Later in the same
+//       layer they certify the top-k and run the combine: 32 rows of
+//       x' = x + (shared + sum_k w_k y_k) per chunk.
+//   shared-expert blocks   expert items of the shared expert. They need no routing, so
+//       their weights are requested while the router is still running.
+//   routed blocks          certify the top-k (wave 0), then one expert item each.
+//
+// An expert item owns 16 rows j of F for one expert: gate and up rows (int8 MFMA on the
+// digit form of xn), h = silu(g) * u for those 16 rows, and h times the matching 16
+// columns of down (dot4 on h's digit form), a partial y over all D rows. The combine
+// sums the F/16 partials of each expert in a fixed order. Every item's weights (68 KB
+// of gate/up, 36 KB of down with scales) are requested at once, as soon as the top-k is
+// known, and h never leaves the block.
 //
 // Memory ordering without cache flushes. Every activation buffer is per layer and is
 // written exactly once per launch, by write-through (agent-scope) stores; a producer
@@ -22,6 +28,10 @@
 // of a hang) before reading. Since no cache line of a per-layer buffer is touched before
 // it is produced, and caches start clean at a kernel boundary, consumers may read it with
 // ordinary cached loads: each XCD fetches it from memory once, into its own L2.
+//
+// Blocks walk the layers in order and every wait is on work of the same or an earlier
+// layer that some other role produces without waiting on the waiter, so with all blocks
+// resident the schedule cannot deadlock.
 #pragma once
 
 #include "common.h"
@@ -29,19 +39,34 @@
 #include "router.h"
 
 #define SK_BLOCK 256
-#define SK_MAX_SLOTS 9           // K + 1 <= 9
-#define SK_SPIN_LIMIT (1u << 22) // polls before a wait is declared dead (~seconds)
+#define SK_SPIN_LIMIT (1u << 22)               // polls before a wait is declared dead (~seconds)
 #define SK_TRACE_STAMPS 16
-#define SK_RX 4                  // experts per router item: one per wave
+#define SK_NR_MAX 64                           // router blocks
+#define SK_RX_MAX (GM_MAX_E / SK_NR_MAX)       // experts per router block
+#define SK_PER_MAX (GM_MAX_COLS / SK_BLOCK)    // columns (router) or rows (down) per thread
+#define SK_NPART 16                            // completion counters of the expert items
+#define SK_CROWS 8                             // rows per combine chunk
+#define SK_CGROUPS (SK_BLOCK / SK_CROWS)       // partial sums per row in the combine
+#define SK_MAX_LAYERS 256
 
-// Counters sit 64 words (256 bytes) apart: polls of one never share a cache line, or a
-// memory channel's hot spot, with another.
+// Signalling. Producers count their arrivals on counters that nobody polls; the producer
+// whose atomic returns the last count of a layer then writes that layer's flag, once, and
+// consumers poll the flag. Polling a word that is also receiving hundreds of atomics
+// slows those atomics down badly (the phase's completion then arrives microseconds
+// late); polling a word that is written once costs nothing measurable. Every counter and
+// flag sits 64 words (256 bytes) from the next. The expert items count on SK_NPART
+// counters, whose last arrivals count on a second level.
 #define SKC_PAD 64
-enum { SKC_ROUTER = 0, SKC_DIG = 2, SKC_X = 3, SKC_GATE = 4, SKC_PANEL = 16 };
+enum { SKC_ROUTER = 0, SKC_DIG = 1, SKC_X = 2, SKC_PART2 = 3, SKC_PART = 4, SKC_FIXED = SKC_PART + SK_NPART };
+enum { SKF_SEL = 0, SKF_SELW = 1, SKF_DIG = 2, SKF_PART = 3, SKF_X = 4, SKF_PER_LAYER = 5 };
 #define SKC(i) ((i) * SKC_PAD)
-// per-layer flags of the exact top-k replay, after the D/16 panel counters
-#define SKC_CLAIM(np, li) SKC(SKC_PANEL + (np) + 2 * (li))
-#define SKC_EXACT(np, li) SKC(SKC_PANEL + (np) + 2 * (li) + 1)
+#define SKF(li, f) SKC(SKC_FIXED + SKF_PER_LAYER * (li) + (f))  // per-layer flags
+// The SEL flag carries the top-k itself, so that its consumers need nothing else: one
+// 64-bit word per four slots, 16 bits per slot holding expert + 2 (never zero, so a word
+// is either unwritten or complete).
+#define SK_SEL_WORDS ((GM_MAX_K + 3) / 4)
+#define SK_CTR_WORDS(n_layers) SKF(n_layers, 0)
+#define GM_STACK_COUNTERS SK_CTR_WORDS(SK_MAX_LAYERS)
 
 struct StackLayer {
     const uint8_t *experts;
@@ -52,9 +77,16 @@ struct StackLayer {
     int pad;
 };
 
+// One expert's certified selection interval [lo, hi] of sel = p + bias, and p.
+struct StageEnt {
+    double lo, hi;
+    float p;
+    int pad[3];
+};
+
 // Per-layer workspace: one region of `ws_layer_bytes` per layer of the launch.
 struct StackWs {
-    size_t x, xn, dig, dexp, stage, ex_idx, ex_w, ex_p, g, u, y;  // byte offsets inside a layer region
+    size_t x, xn, dig, dexp, stage, ex_idx, ex_w, ex_p, ypart;  // byte offsets inside a layer region
 };
 
 struct StackArgs {
@@ -64,7 +96,7 @@ struct StackArgs {
     float *x_out;
     int D, F, E, K, flags;
     float eps, routed_scale;
-    size_t stride, off_gq, off_uq, off_dq, off_gs, off_us, off_ds;
+    size_t stride, off_gq, off_uq, off_dq, off_gs, off_us, off_ds;  // down in the column-slice layout
     uint8_t *ws;               // per-layer workspace base
     size_t ws_layer_bytes;
     StackWs o;
@@ -82,6 +114,7 @@ struct StackArgs {
     unsigned long long *stats;
     int *error;                // nonzero: a wait timed out
     unsigned long long *trace; // optional: SK_TRACE_STAMPS timestamps per item (see k_moe_stack)
+    int n_router;              // router blocks: a power of two, <= min(E, 64)
     int shared_blocks;         // blocks in the shared-expert role
 };
 
@@ -102,66 +135,78 @@ __device__ static inline unsigned ld_u(const unsigned *p) { return __hip_atomic_
 
 struct SkShared {
     union {
-        struct {  // router item: xn at padded positions, see rpad()
-            float xn[GM_MAX_COLS + GM_MAX_COLS / 32];
+        struct {  // router item
+            double wv[4][SK_RX_MAX][3];  // per wave: segment total, sum |S_k|, sum |p|
         } r;
         struct {  // top-k selection and its exact replay
-            double lo[GM_MAX_E], hi[GM_MAX_E], mid[GM_MAX_E];
             float p[GM_MAX_E], sel[GM_MAX_E];
             float xn[GM_MAX_COLS];
             float prod[64][17];  // products of 64 experts x 16 columns
         } s;
-        struct {  // expert panels
+        struct {  // expert item
             int8_t dig[3 * GM_MAX_COLS];
             int dexp[GM_MAX_COLS / 32];
-            float part[EX_WAVES][16];
-            float part2[EX_WAVES][16];
+            float part[EX_WAVES][2][16];
+            int hd[12];  // digit rows of h: 3 x 16 int8, four per word
+            int hexp;
         } g;
+        struct {  // combine
+            float acc[SK_BLOCK / 64][GM_MAX_K + 1][SK_CROWS];
+        } c;
     } u;
+    u32x4 dslice[GM_MAX_COLS];  // an expert item's down columns, D rows x 16 bytes
+    float xn_r[GM_MAX_COLS];    // a router item's xn (kept through the top-k and its replay)
+    unsigned short sc_gu[2 * GM_MAX_COLS / 2];  // its gate and up panel scales, [2][16][D/32]
+    unsigned short sc_d[GM_MAX_COLS];           // its down scales, one per row
     double red[4];
-    float mean;
+    float mean, total;
     unsigned old;
     int ok, sel_ok;
-    float total;
     int idx[GM_MAX_K];
     float wk[GM_MAX_K], ws[GM_MAX_K];
     long trace_item;
     unsigned long long *trace;
 };
 
-// All of this block's write-through stores have completed; then thread 0 bumps `c`.
-// With `need_old` the previous counter value is returned to every thread.
-__device__ static inline unsigned publish(unsigned *c, SkShared &sh, bool need_old) {
+__device__ static inline void st_u(unsigned *p, unsigned v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ static inline unsigned add_u(unsigned *p) { return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// All of this block's write-through stores have completed; then thread 0 sets `flag`.
+__device__ static inline void signal(unsigned *flag) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        if (need_old) sh.old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (!need_old) return 0;
-    __syncthreads();
-    return sh.old;
+    if (threadIdx.x == 0) st_u(flag, 1u);
 }
 
-// Block-wide wait until *c >= target. Returns false if the wait timed out or another
-// block already failed (the caller then returns from the kernel).
+// All of this block's write-through stores have completed; then thread 0 counts the
+// arrival on `c`, and if it is the `target`-th it sets `flag`. Every earlier arrival came
+// after its own stores completed, so the flag implies all of them.
+__device__ static inline void arrive(unsigned *c, unsigned target, unsigned *flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0 && add_u(c) + 1u == target) st_u(flag, 1u);
+}
+
+// Bounded spin of one thread until *c >= target; false if it timed out or another block
+// already failed.
+__device__ static inline bool spin_ge(const unsigned *c, unsigned target, int *error) {
+    unsigned spins = 0;
+    while (ld_u(c) < target) {
+        if (__hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+        if (++spins > SK_SPIN_LIMIT) {
+            __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(2);  // ~128 clocks between polls
+    }
+    return true;
+}
+
+// Block-wide wait until *c >= target (a flag: target 1). Returns false if the wait timed
+// out or another block already failed (the caller then returns from the kernel).
 __device__ static inline bool wait_ge(const unsigned *c, unsigned target, int *error, SkShared &sh) {
     if (threadIdx.x == 0) {
-        int ok = 1;
-        unsigned spins = 0;
-        while (ld_u(c) < target) {
-            if (__hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                ok = 0;
-                break;
-            }
-            if (++spins > SK_SPIN_LIMIT) {
-                __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(8);  // ~512 clocks between polls
-        }
-        sh.ok = ok;
+        sh.ok = spin_ge(c, target, error);
         if (sh.trace) sh.trace[SK_TRACE_STAMPS * sh.trace_item + 1] = wall_clock64();
     }
     __syncthreads();
@@ -173,161 +218,22 @@ __device__ static inline void sk_stamp(SkShared &sh, int k) {
     if (sh.trace && threadIdx.x == 0) sh.trace[SK_TRACE_STAMPS * sh.trace_item + k] = wall_clock64();
 }
 
-// ---------------------------------------------------------------- router item
-#define SK_RCOLS 32  // router columns per lane: D <= 64 * 32
+typedef __attribute__((address_space(3))) void lds_void;
 
-// Column i = l * cpl + j of the router's normalised activations (lane l's segment of cpl
-// columns) sits at l * (cpl + 1) + j in shared memory. cpl is a multiple of 4, so cpl + 1
-// is odd and the 64 lanes reading their own segments start on 64 different banks instead
-// of sharing two.
-__device__ static inline int rpad(int i, int cpl) { return i + i / cpl; }
-
-__device__ __attribute__((always_inline)) static bool sk_router_item(const StackArgs &a, const StackLayer &L,
-                                                                     int layer, int li, int r0, SkShared &sh) {
-    const int D = a.D, E = a.E, tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6;
-    const int per = D / SK_BLOCK;  // norm columns per thread, D a multiple of 256
-    const int cpl = D / 64;        // router columns per lane
-    const int e = r0 * SK_RX + w;  // this wave's expert
-    // The router row and the norm weights do not depend on x: fetch them before waiting.
-    // Every load is unconditional (indices past the end are clamped and the values
-    // replaced by zeros afterwards), so all of them are in flight at once.
-    float gw[SK_RCOLS], nw[8];
-    const GM_GLOBAL float *nrm = gbl(L.norm);
-#pragma unroll
-    for (int j = 0; j < 8; j++) nw[j] = nrm[tid * per + (j < per ? j : 0)];
-    {
-        const GM_GLOBAL float *g = gbl(L.gate_inp + (size_t)(e < E ? e : 0) * D + (size_t)lane * cpl);
-#pragma unroll
-        for (int j = 0; j < SK_RCOLS; j++) gw[j] = g[j < cpl ? j : 0];
-#pragma unroll
-        for (int j = 0; j < SK_RCOLS; j++) gw[j] = j < cpl ? gw[j] : 0.0f;
-    }
-    if (li > 0 && !wait_ge(&a.ctr[SKC(SKC_X)], (unsigned)li * (D >> 4), a.error, sh)) return false;
-    const float *xsrc = li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x);
-
-    // rmsnorm, bit-identical to infer.c:746-752. Thread tid holds columns tid*per..+per,
-    // inside lane tid/4's router segment (cpl = 4 * per).
-    const int xn_at = (tid >> 2) * (cpl + 1) + (tid & 3) * per;
-    float xv[8];
-    double ss = 0.0;
-#pragma unroll
-    for (int j = 0; j < 8; j++) xv[j] = xsrc[tid * per + (j < per ? j : 0)];
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-        if (j < per) ss += (double)xv[j] * (double)xv[j];
-    ss = block_sum_fast(ss, sh.red);
-    sk_stamp(sh, 11);
-    const double v = ss / (double)D, rho = (double)D * 0x1p-52;
-    const float mlo = (float)(v * (1.0 - rho)), mhi = (float)(v * (1.0 + rho));
-    float mean = mlo;
-    if (mlo != mhi) {
-#pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (j < per) sh.u.r.xn[xn_at + j] = xv[j];
-        __syncthreads();
-        if (tid == 0) {
-            double sq = 0.0;
-            for (int i = 0; i < D; i++) sq += (double)sh.u.r.xn[rpad(i, cpl)] * (double)sh.u.r.xn[rpad(i, cpl)];
-            sh.mean = (float)(sq / (double)D);
-            if (r0 == 0) atomicAdd(&a.stats[GM_STAT_NORM_EXACT], 1ull);
-        }
-        __syncthreads();
-        mean = sh.mean;
-        __syncthreads();
-    }
-    const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
-#pragma unroll
-    for (int j = 0; j < 8; j++)
-        if (j < per) {
-            xv[j] = __fmul_rn(__fmul_rn(xv[j], inv), nw[j]);
-            sh.u.r.xn[xn_at + j] = xv[j];
-        }
-    __syncthreads();
-
-    if (r0 == 0) {
-        // publish xn and its digit form for this layer's gate/up items: 8 consecutive
-        // columns per thread, four threads per 32-column block
-        int8_t *dig = ws_at<int8_t>(a, li, a.o.dig);
-        int *dexp = ws_at<int>(a, li, a.o.dexp);
-        float *wxn = ws_at<float>(a, li, a.o.xn);
-        for (int i0 = tid * 8; i0 < D; i0 += SK_BLOCK * 8) {
-            float vals[8];
-            float mx = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                vals[j] = sh.u.r.xn[rpad(i0 + j, cpl)];
-                mx = fmaxf(mx, fabsf(vals[j]));
-                st_f(a.xn + i0 + j, vals[j]);
-                st_f(wxn + i0 + j, vals[j]);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-            const int ex = digit_exponent(mx);
-            unsigned long long w0 = 0, w1 = 0, w2 = 0;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                int8_t d0, d1, d2;
-                split_digits(vals[j], ex, &d0, &d1, &d2);
-                w0 |= (unsigned long long)(uint8_t)d0 << (8 * j);
-                w1 |= (unsigned long long)(uint8_t)d1 << (8 * j);
-                w2 |= (unsigned long long)(uint8_t)d2 << (8 * j);
-            }
-            st_u64((unsigned long long *)(dig + i0), w0);
-            st_u64((unsigned long long *)(dig + D + i0), w1);
-            st_u64((unsigned long long *)(dig + 2 * D + i0), w2);
-            if ((tid & 3) == 0) st_i(dexp + (i0 >> 5), ex);
-        }
-        publish(&a.ctr[SKC(SKC_DIG)], sh, false);
-        sk_stamp(sh, 12);
-    }
-
-    // Logit of expert e in fp64, and a rigorous bound on how far glm.c's sequential fp32
-    // chain (infer.c:916-925) can be from it. Lane l owns columns [l*cpl, (l+1)*cpl), so
-    // the exact partial sums S_k run in lane order.
-    // gw[j] is 0 for j >= cpl, so those terms add exact zeros
-    float xr[SK_RCOLS];
-#pragma unroll
-    for (int j = 0; j < SK_RCOLS; j++) xr[j] = sh.u.r.xn[lane * (cpl + 1) + j];  // <= 63 * 33 + 31
-#pragma unroll
-    for (int j = 0; j < SK_RCOLS; j++) xr[j] = j < cpl ? xr[j] : 0.0f;  // neighbours' or unset words
-    double seg = 0.0, seg_abs = 0.0;
-#pragma unroll
-    for (int j = 0; j < SK_RCOLS; j++) {
-        const double pj = (double)gw[j] * (double)xr[j];
-        seg += pj;
-        seg_abs += fabs(pj);
-    }
-    const double incl = wave_incl_scan_dpp(seg);
-    double run = incl - seg, steps = 0.0;
-#pragma unroll
-    for (int j = 0; j < SK_RCOLS; j++) {
-        run += (double)gw[j] * (double)xr[j];
-        steps += fabs(run);
-    }
-    const double S = readlane_d(incl, 63);
-    const double sp = wave_sum_dpp(steps), sa = wave_sum_dpp(seg_abs);
-    sk_stamp(sh, 13);
-    if (lane == 0 && e < E) {
-        const double u = 0x1p-24, n = (double)D;
-        const double gamma = n * u / (1.0 - n * u);
-        const double emax = gamma * sa;  // a priori bound on every partial sum's error
-        // step k rounds |fl(s_{k-1}) + fl(p_k)| <= |S_k| + emax + u|p_k| by at most u times
-        // that, and each product adds u|p_k|
-        double B = u * (1.0 + u) * sa + u * (sp + n * emax + u * sa);
-        B = B * (1.0 + 0x1p-30) + 0x1p-40 * sa + n * 0x1p-149;
-        double2 *stage = ws_at<double2>(a, li, a.o.stage);
-        st_d(&stage[e].x, S);
-        st_d(&stage[e].y, B);
-    }
-    sk_stamp(sh, 5);
-    publish(&a.ctr[SKC(SKC_ROUTER)], sh, false);
-    return true;
+// Copy `nbytes` (a multiple of 16) from global memory straight into shared memory, 1 KB
+// per wave instruction. Completion is this wave's vmcnt.
+__device__ static inline void dma_copy(void *dst, const void *src, int nbytes) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int off = 1024 * w; off < nbytes; off += 1024 * (SK_BLOCK / 64))
+        if (off + 16 * lane < nbytes)
+            __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)gbl((const uint8_t *)src + off + 16 * lane),
+                                             (lds_void *)((uint8_t *)dst + off), 16, 0, 0);
 }
 
+// ---------------------------------------------------------------- top-k selection
+//
 // Top-k of layer li (infer.c:1108-1145) into sh.idx / sh.wk (normalised) / sh.ws (times
-// routed_scale) from the router items' (S, B) table, and the router probabilities of all
-// experts into sh.u.s.p.
+// routed_scale), and the router probabilities of all experts into sh.u.s.p.
 //
 // Fast path, wave 0 alone: lane l holds experts l + 64c. The K best interval midpoints are
 // taken one at a time (a wave maximum, then the lowest lane holding it), and the result is
@@ -337,42 +243,32 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
 // or when any interval is not finite, one block replays the fp32 router exactly.
 #define SK_SEL_C (GM_MAX_E / 64)
 
-__device__ __attribute__((always_inline)) static bool sk_select(const StackArgs &a, const StackLayer &L, int li, SkShared &sh) {
+__device__ __attribute__((always_inline)) static bool sk_select_topk(const StackArgs &a, const StackLayer &L, int li,
+                                                                     SkShared &sh) {
     const int D = a.D, E = a.E, K = a.K, tid = threadIdx.x;
-    const int n_items = (E + SK_RX - 1) / SK_RX;
-    if (!wait_ge(&a.ctr[SKC(SKC_ROUTER)], (unsigned)(li + 1) * n_items, a.error, sh)) return false;
     sk_stamp(sh, 8);
-    const GM_GLOBAL float *bias = gbl(L.bias);
     if (tid < 64) {
-        const double2 *stage = ws_at<double2>(a, li, a.o.stage);
-        double2 sb[SK_SEL_C];
-        float bb[SK_SEL_C];
+        const StageEnt *stage = ws_at<StageEnt>(a, li, a.o.stage);
+        double lo[SK_SEL_C], hi[SK_SEL_C], mid[SK_SEL_C];
+        float pr[SK_SEL_C];
 #pragma unroll
         for (int c = 0; c < SK_SEL_C; c++) {  // all loads in flight at once
             const int e = tid + 64 * c < E ? tid + 64 * c : E - 1;
-            sb[c] = stage[e];
-            bb[c] = bias[e];
+            lo[c] = stage[e].lo;
+            hi[c] = stage[e].hi;
+            pr[c] = stage[e].p;
         }
-        double lo[SK_SEL_C], hi[SK_SEL_C], mid[SK_SEL_C];
-        float pr[SK_SEL_C];
         bool bad = false;
 #pragma unroll
         for (int c = 0; c < SK_SEL_C; c++) {
-            lo[c] = hi[c] = mid[c] = -INFINITY;
-            pr[c] = 0.0f;
-            if (64 * c < E) {  // wave-uniform
-                const int e = tid + 64 * c;
-                double l, h;
-                selection_interval(sb[c].x, sb[c].y, bb[c], &l, &h);
-                const float pe = 1.0f / (1.0f + expf(-(float)sb[c].x));
-                if (e < E) {
-                    sh.u.s.p[e] = pe;
-                    bad |= !(isfinite(l) && isfinite(h));
-                    lo[c] = l;
-                    hi[c] = h;
-                    mid[c] = 0.5 * (l + h);
-                    pr[c] = pe;
-                }
+            const int e = tid + 64 * c;
+            if (e < E) {
+                sh.u.s.p[e] = pr[c];
+                bad |= !(isfinite(lo[c]) && isfinite(hi[c]));
+                mid[c] = 0.5 * (lo[c] + hi[c]);
+            } else {
+                lo[c] = hi[c] = mid[c] = -INFINITY;
+                pr[c] = 0.0f;
             }
         }
         bool ok = __ballot(bad) == 0;
@@ -430,10 +326,6 @@ __device__ __attribute__((always_inline)) static bool sk_select(const StackArgs 
         }
     }
     __syncthreads();
-    int *ex_idx = ws_at<int>(a, li, a.o.ex_idx);
-    float *ex_w = ws_at<float>(a, li, a.o.ex_w);
-    float *ex_p = ws_at<float>(a, li, a.o.ex_p);
-    const int NPD = D >> 4;
     if (sh.sel_ok) {
         // normalisation of infer.c:1137-1145
         if (tid < K) {
@@ -444,13 +336,10 @@ __device__ __attribute__((always_inline)) static bool sk_select(const StackArgs 
             }
         }
     } else {
-        // The proof failed: one block replays glm.c's router exactly, the others wait for it.
-        if (tid == 0)
-            sh.old = __hip_atomic_fetch_add(&a.ctr[SKC_CLAIM(NPD, li)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        if (sh.old == 0) {
-            const float *wxn = ws_at<float>(a, li, a.o.xn);
-            for (int i = tid; i < D; i += SK_BLOCK) sh.u.s.xn[i] = wxn[i];
+        // The proof failed: this block replays glm.c's router exactly (its xn is in xn_r).
+        {
+            const GM_GLOBAL float *bias = gbl(L.bias);
+            for (int i = tid; i < D; i += SK_BLOCK) sh.u.s.xn[i] = sh.xn_r[i];
             // infer.c:916-925 for every expert, 16 columns at a time: all threads form the
             // products fl(g * xn), then lane e adds its expert's 16 in order.
             float chain[GM_MAX_E / 64];
@@ -519,20 +408,7 @@ __device__ __attribute__((always_inline)) static bool sk_select(const StackArgs 
                     const float inv_d = __fdiv_rn(1.0f, denom);
                     for (int k = 0; k < K; k++) sh.wk[k] = __fmul_rn(sh.wk[k], inv_d);
                 }
-                for (int k = 0; k < K; k++) {
-                    st_i(ex_idx + k, sh.idx[k]);
-                    st_f(ex_w + k, sh.wk[k]);
-                }
             }
-            for (int i = tid; i < E; i += SK_BLOCK) st_f(ex_p + i, sh.u.s.p[i]);
-            publish(&a.ctr[SKC_EXACT(NPD, li)], sh, false);
-        } else {
-            if (!wait_ge(&a.ctr[SKC_EXACT(NPD, li)], 1u, a.error, sh)) return false;
-            if (tid < K) {
-                sh.idx[tid] = ex_idx[tid];
-                sh.wk[tid] = ex_w[tid];
-            }
-            for (int i = tid; i < E; i += SK_BLOCK) sh.u.s.p[i] = ex_p[i];
         }
     }
     __syncthreads();
@@ -543,7 +419,7 @@ __device__ __attribute__((always_inline)) static bool sk_select(const StackArgs 
 }
 
 // Observables of layer `layer` (top-k, weights, router probabilities), written through
-// right after sk_select.
+// by the block that selected the top-k.
 __device__ static void sk_write_routing(const StackArgs &a, int layer, SkShared &sh) {
     const int tid = threadIdx.x;
     if (tid < a.K) {
@@ -555,191 +431,482 @@ __device__ static void sk_write_routing(const StackArgs &a, int layer, SkShared 
     for (int i = tid; i < a.E; i += SK_BLOCK) st_f(a.router_prob + i, sh.u.s.p[i]);
 }
 
-// ---------------------------------------------------------------- gate / up item
-__device__ __attribute__((always_inline)) static bool sk_gate_up_item(const StackArgs &a, const StackLayer &L, int li,
-                                                                      int slot, int p, int e, SkShared &sh) {
-    const int D = a.D, F = a.F;
-    if (e >= 0) {
-        const uint8_t *base = L.experts + (size_t)e * a.stride;
-        PanelRegs<2, EX_NB_MAX> pr;
-        panel_load<2, EX_NB_MAX>(pr, base + a.off_gq, (const __half *)(base + a.off_gs), base + a.off_uq,
-                                 (const __half *)(base + a.off_us), p, D);
-        if (!wait_ge(&a.ctr[SKC(SKC_DIG)], (unsigned)(li + 1), a.error, sh)) return false;
-        const unsigned long long *dig = ws_at<unsigned long long>(a, li, a.o.dig);
-        const int *dexp = ws_at<int>(a, li, a.o.dexp);
-        for (int i = threadIdx.x; i < (3 * D) / 8; i += SK_BLOCK) ((unsigned long long *)sh.u.g.dig)[i] = dig[i];
-        for (int i = threadIdx.x; i < D / 32; i += SK_BLOCK) sh.u.g.dexp[i] = dexp[i];
-        __syncthreads();
-        sk_stamp(sh, 6);
-        float gu[2];
-        panel_compute<2, EX_NB_MAX>(pr, D, sh.u.g.dig, sh.u.g.dexp, gu);
-        sk_stamp(sh, 4);
-        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-        if (lane < 16) {
-            sh.u.g.part[w][lane] = gu[0];
-            sh.u.g.part2[w][lane] = gu[1];
+// ---------------------------------------------------------------- router item
+//
+// Block b: rmsnorm of x (every router block, bit-identical to infer.c:746-752) and the
+// logits of experts b, b + NR, ... (infer.c:916-938) in fp64. Thread t owns the `per`
+// consecutive columns [t*per, (t+1)*per), so the exact partial sums S_k of glm.c's
+// sequential chain run in thread order: a block-wide scan yields them, and with them
+// the bound on the chain's rounding error (router.h). Each expert's result is stored
+// as its selection interval and probability.
+__device__ __attribute__((always_inline)) static bool sk_router_item(const StackArgs &a, const StackLayer &L, int layer,
+                                                                     int li, int b, SkShared &sh) {
+    const int D = a.D, E = a.E, NR = a.n_router, tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int per = D / SK_BLOCK;
+    const int nx = (E - b + NR - 1) / NR;
+    // The norm and router weights do not depend on x: fetch them before waiting. Every
+    // load is unconditional (indices past the end are clamped, the values zeroed after),
+    // so they are all in flight at once.
+    float nw[SK_PER_MAX], gw[SK_RX_MAX][SK_PER_MAX];
+    {
+        const GM_GLOBAL float *nrm = gbl(L.norm) + tid * per;
+#pragma unroll
+        for (int j = 0; j < SK_PER_MAX; j++) nw[j] = nrm[j < per ? j : 0];
+#pragma unroll
+        for (int x = 0; x < SK_RX_MAX; x++) {
+            const int e = b + (x < nx ? x : 0) * NR;
+            const GM_GLOBAL float *g = gbl(L.gate_inp) + (size_t)e * D + tid * per;
+#pragma unroll
+            for (int j = 0; j < SK_PER_MAX; j++) gw[x][j] = g[j < per ? j : 0];
         }
-        __syncthreads();
-        if (threadIdx.x < 16) {
-            const int l = threadIdx.x;
-            float *go = ws_at<float>(a, li, a.o.g) + (size_t)slot * F;
-            float *uo = ws_at<float>(a, li, a.o.u) + (size_t)slot * F;
-            st_f(go + (size_t)p * 16 + l, ((sh.u.g.part[0][l] + sh.u.g.part[1][l]) + sh.u.g.part[2][l]) + sh.u.g.part[3][l]);
-            st_f(uo + (size_t)p * 16 + l, ((sh.u.g.part2[0][l] + sh.u.g.part2[1][l]) + sh.u.g.part2[2][l]) + sh.u.g.part2[3][l]);
-        }
+#pragma unroll
+        for (int x = 0; x < SK_RX_MAX; x++)
+#pragma unroll
+            for (int j = 0; j < SK_PER_MAX; j++) gw[x][j] = (x < nx && j < per) ? gw[x][j] : 0.0f;
     }
-    sk_stamp(sh, 5);
-    publish(&a.ctr[SKC(SKC_GATE + slot)], sh, false);
-    return true;
-}
+    if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_X)], 1u, a.error, sh)) return false;
+    const float *xsrc = (li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x)) + tid * per;
 
-// ---------------------------------------------------------------- down item (+ combine)
-// Down item of `slot` (expert e, -1 when idle) and 16-row panel p. A routed slot stores its
-// output already multiplied by its routing weight, w_e * y (infer.c:1189-1192), and an idle
-// slot stores zeros, so the combine needs no routing: adding +0.0 to the running sum,
-// which is never -0.0, leaves it unchanged, as skipping the slot does.
-__device__ __attribute__((always_inline)) static bool sk_down_item(const StackArgs &a, const StackLayer &L, int li, int slot,
-                                                                   int p, int e, bool routed_on, SkShared &sh) {
-    const int D = a.D, F = a.F, K = a.K, NS = a.K + 1;
-    if (e >= 0) {
-        const uint8_t *base = L.experts + (size_t)e * a.stride;
-        PanelRegs<1, EX_NB_MAX> pr;
-        panel_load<1, EX_NB_MAX>(pr, base + a.off_dq, (const __half *)(base + a.off_ds), nullptr, nullptr, p, F);
-        if (!wait_ge(&a.ctr[SKC(SKC_GATE + slot)], (unsigned)(li + 1) * (F >> 4), a.error, sh)) return false;
-        // h = silu(gate) * up (infer.c:1188, 1202), then its digit form in shared memory
-        const float *gs = ws_at<float>(a, li, a.o.g) + (size_t)slot * F;
-        const float *us = ws_at<float>(a, li, a.o.u) + (size_t)slot * F;
-        for (int i0 = threadIdx.x * 8; i0 < F; i0 += SK_BLOCK * 8) {
+    float xv[SK_PER_MAX];
+#pragma unroll
+    for (int j = 0; j < SK_PER_MAX; j++) xv[j] = xsrc[j < per ? j : 0];
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < SK_PER_MAX; j++)
+        if (j < per) ss += (double)xv[j] * (double)xv[j];
+    ss = block_sum_fast(ss, sh.red);
+    sk_stamp(sh, 11);
+    // mean = (float)(sum / D) of the sequential fp64 sum: certified from the parallel sum
+    // (its relative error is below D * 2^-52), else replayed in order
+    const double v = ss / (double)D, rho = (double)D * 0x1p-52;
+    const float mlo = (float)(v * (1.0 - rho)), mhi = (float)(v * (1.0 + rho));
+    float mean = mlo;
+    if (mlo != mhi) {
+#pragma unroll
+        for (int j = 0; j < SK_PER_MAX; j++)
+            if (j < per) sh.xn_r[tid * per + j] = xv[j];
+        __syncthreads();
+        if (tid == 0) {
+            double sq = 0.0;
+            for (int i = 0; i < D; i++) sq += (double)sh.xn_r[i] * (double)sh.xn_r[i];
+            sh.mean = (float)(sq / (double)D);
+            if (b == 0) atomicAdd(&a.stats[GM_STAT_NORM_EXACT], 1ull);
+        }
+        __syncthreads();
+        mean = sh.mean;
+        __syncthreads();
+    }
+    const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
+#pragma unroll
+    for (int j = 0; j < SK_PER_MAX; j++) xv[j] = j < per ? __fmul_rn(__fmul_rn(xv[j], inv), nw[j]) : 0.0f;
+
+#pragma unroll
+    for (int j = 0; j < SK_PER_MAX; j++)
+        if (j < per) sh.xn_r[tid * per + j] = xv[j];
+    __syncthreads();
+    // This block's share of xn and its digit form for the layer's expert items: 32-column
+    // blocks q = b, b + NR, ... (every router block holds all of xn). Thread t takes
+    // columns 8 (t % 4) .. +8 of block b + NR (t / 4); the four threads of a block agree
+    // on its exponent. The DIG flag covers these stores.
+    {
+        const int q = b + NR * (tid >> 2);
+        if (q < D / 32) {
+            int8_t *dig = ws_at<int8_t>(a, li, a.o.dig);
+            int *dexp = ws_at<int>(a, li, a.o.dexp);
+            float *wxn = ws_at<float>(a, li, a.o.xn);
+            const int i0 = 32 * q + 8 * (tid & 3);
             float vals[8];
             float mx = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const float gv = gs[i0 + k];
-                vals[k] = gv / (1.0f + expf(-gv)) * us[i0 + k];
-                mx = fmaxf(mx, fabsf(vals[k]));
+            for (int j = 0; j < 8; j++) {
+                vals[j] = sh.xn_r[i0 + j];
+                mx = fmaxf(mx, fabsf(vals[j]));
+                st_f(a.xn + i0 + j, vals[j]);
+                st_f(wxn + i0 + j, vals[j]);
             }
             mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
             const int ex = digit_exponent(mx);
             unsigned long long w0 = 0, w1 = 0, w2 = 0;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
+            for (int j = 0; j < 8; j++) {
                 int8_t d0, d1, d2;
-                split_digits(vals[k], ex, &d0, &d1, &d2);
-                w0 |= (unsigned long long)(uint8_t)d0 << (8 * k);
-                w1 |= (unsigned long long)(uint8_t)d1 << (8 * k);
-                w2 |= (unsigned long long)(uint8_t)d2 << (8 * k);
+                split_digits(vals[j], ex, &d0, &d1, &d2);
+                w0 |= (unsigned long long)(uint8_t)d0 << (8 * j);
+                w1 |= (unsigned long long)(uint8_t)d1 << (8 * j);
+                w2 |= (unsigned long long)(uint8_t)d2 << (8 * j);
             }
-            *(unsigned long long *)(sh.u.g.dig + i0) = w0;
-            *(unsigned long long *)(sh.u.g.dig + F + i0) = w1;
-            *(unsigned long long *)(sh.u.g.dig + 2 * F + i0) = w2;
-            if ((threadIdx.x & 3) == 0) sh.u.g.dexp[i0 >> 5] = ex;
+            st_u64((unsigned long long *)(dig + i0), w0);
+            st_u64((unsigned long long *)(dig + D + i0), w1);
+            st_u64((unsigned long long *)(dig + 2 * D + i0), w2);
+            if ((tid & 3) == 0) st_i(dexp + q, ex);
         }
-        __syncthreads();
-        sk_stamp(sh, 6);
-        float yv;
-        panel_compute<1, EX_NB_MAX>(pr, F, sh.u.g.dig, sh.u.g.dexp, &yv);
-        sk_stamp(sh, 4);
-        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-        if (lane < 16) sh.u.g.part[w][lane] = yv;
-        __syncthreads();
-        if (threadIdx.x < 16) {
-            const int l = threadIdx.x;
-            float *y = ws_at<float>(a, li, a.o.y) + (size_t)slot * D;
-            const float yv = ((sh.u.g.part[0][l] + sh.u.g.part[1][l]) + sh.u.g.part[2][l]) + sh.u.g.part[3][l];
-            st_f(y + (size_t)p * 16 + l, slot < K ? __fmul_rn(sh.ws[slot], yv) : yv);
+    }
+    sk_stamp(sh, 12);
+
+    arrive(&a.ctr[SKC(SKC_DIG)], (unsigned)(li + 1) * NR, &a.ctr[SKF(li, SKF_DIG)]);
+
+    // Products in fp64 are exact (24 + 24 bits). Pass 1: this thread's segment sums and
+    // the block-wide exclusive prefix, in column order.
+    double sabs[SK_RX_MAX] = {0.0}, pre[SK_RX_MAX] = {0.0};
+#pragma unroll
+    for (int x = 0; x < SK_RX_MAX; x++) {
+        if (x >= nx) break;  // block-uniform
+        double s = 0.0, sa = 0.0;
+#pragma unroll
+        for (int j = 0; j < SK_PER_MAX; j++) {
+            const double pj = (double)gw[x][j] * (double)xv[j];
+            s += pj;
+            sa += fabs(pj);
         }
-    } else if (routed_on && slot < K && threadIdx.x < 16) {
-        st_f(ws_at<float>(a, li, a.o.y) + (size_t)slot * D + (size_t)p * 16 + threadIdx.x, 0.0f);
+        sabs[x] = sa;
+        const double incl = wave_incl_scan_dpp(s);
+        pre[x] = incl - s;
+        if (lane == 63) sh.u.r.wv[w][x][0] = incl;
+    }
+    __syncthreads();
+    // Pass 2: |S_k| after each column, with the waves before this one added in
+#pragma unroll
+    for (int x = 0; x < SK_RX_MAX; x++) {
+        if (x >= nx) break;  // block-uniform
+        double off = 0.0;
+        for (int v2 = 0; v2 < w; v2++) off += sh.u.r.wv[v2][x][0];
+        double run = off + pre[x], steps = 0.0;
+#pragma unroll
+        for (int j = 0; j < SK_PER_MAX; j++) {
+            run += (double)gw[x][j] * (double)xv[j];
+            steps += fabs(run);
+        }
+        const double sp = wave_sum_dpp(steps), sa = wave_sum_dpp(sabs[x]);
+        if (lane == 0) {
+            sh.u.r.wv[w][x][1] = sp;
+            sh.u.r.wv[w][x][2] = sa;
+        }
+    }
+    __syncthreads();
+    sk_stamp(sh, 13);
+    if (tid < nx) {
+        const int x = tid, e = b + x * NR;
+        const double S = ((sh.u.r.wv[0][x][0] + sh.u.r.wv[1][x][0]) + sh.u.r.wv[2][x][0]) + sh.u.r.wv[3][x][0];
+        const double sp = ((sh.u.r.wv[0][x][1] + sh.u.r.wv[1][x][1]) + sh.u.r.wv[2][x][1]) + sh.u.r.wv[3][x][1];
+        const double sa = ((sh.u.r.wv[0][x][2] + sh.u.r.wv[1][x][2]) + sh.u.r.wv[2][x][2]) + sh.u.r.wv[3][x][2];
+        const double u = 0x1p-24, n = (double)D;
+        const double gamma = n * u / (1.0 - n * u);
+        const double emax = gamma * sa;  // a priori bound on every partial sum's error
+        // step k rounds |fl(s_{k-1}) + fl(p_k)| <= |S_k| + emax + u|p_k| by at most u times
+        // that, and each product adds u|p_k|
+        double B = u * (1.0 + u) * sa + u * (sp + n * emax + u * sa);
+        B = B * (1.0 + 0x1p-30) + 0x1p-40 * sa + n * 0x1p-149;
+        double lo, hi;
+        selection_interval(S, B, L.bias[e], &lo, &hi);
+        StageEnt *st = ws_at<StageEnt>(a, li, a.o.stage) + e;
+        st_d(&st->lo, lo);
+        st_d(&st->hi, hi);
+        st_f(&st->p, 1.0f / (1.0f + expf(-(float)S)));
     }
     sk_stamp(sh, 5);
-    const unsigned old = publish(&a.ctr[SKC(SKC_PANEL + p)], sh, true);
-    sk_stamp(sh, 7);
-    if (old != (unsigned)((li + 1) * NS - 1)) return true;
-    // last slot of this panel: combine (infer.c:1192, 1212-1214)
-    if (threadIdx.x < 16) {
-        const int r = p * 16 + threadIdx.x;
-        const float *y = ws_at<float>(a, li, a.o.y);
+    // Count the arrival. The layer's last router block selects the top-k for every block,
+    // then publishes it with the SEL flag.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) sh.old = add_u(&a.ctr[SKC(SKC_ROUTER)]) + 1u == (unsigned)(li + 1) * NR;
+    __syncthreads();
+    if (sh.old) {
+        if (!sk_select_topk(a, L, li, sh)) return false;
+        if (tid < SK_SEL_WORDS) {
+            unsigned long long word = 0;
+            for (int q = 0; q < 4; q++) {
+                const int k = 4 * tid + q;
+                const unsigned v = k < a.K ? (unsigned)(sh.idx[k] + 2) : 1u;
+                word |= (unsigned long long)v << (16 * q);
+            }
+            st_u64((unsigned long long *)&a.ctr[SKF(li, SKF_SEL) + 2 * tid], word);
+        }
+        sk_stamp(sh, 3);
+        // the weights (for the combine) and the observables follow under their own flag
+        float *ex_w = ws_at<float>(a, li, a.o.ex_w);
+        if (tid < a.K) st_f(ex_w + tid, sh.wk[tid]);
+        sk_write_routing(a, layer, sh);
+        signal(&a.ctr[SKF(li, SKF_SELW)]);
+    }
+    return true;
+}
+
+// The top-k of layer li from the SEL words, into sh.idx.
+__device__ static inline bool sk_read_topk(const StackArgs &a, int li, SkShared &sh) {
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        const int nw = (a.K + 3) / 4;
+        bool ok = true;
+        for (int wd = 0; wd < nw && ok; wd++) {
+            const unsigned long long *p = (const unsigned long long *)&a.ctr[SKF(li, SKF_SEL) + 2 * wd];
+            unsigned spins = 0;
+            unsigned long long v;
+            while ((v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0ull) {
+                if (__hip_atomic_load(a.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > SK_SPIN_LIMIT) {
+                    __hip_atomic_store(a.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = false;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            for (int q = 0; q < 4 && ok; q++)
+                if (4 * wd + q < a.K) sh.idx[4 * wd + q] = (int)((v >> (16 * q)) & 0xffffu) - 2;
+        }
+        sh.ok = ok;
+        if (sh.trace) sh.trace[SK_TRACE_STAMPS * sh.trace_item + 8] = wall_clock64();
+    }
+    __syncthreads();
+    return sh.ok != 0;
+}
+
+// The normalised weights of layer li's top-k (published after the SEL words), into
+// sh.wk / sh.ws.
+__device__ static inline bool sk_read_weights(const StackArgs &a, int li, SkShared &sh) {
+    if (!wait_ge(&a.ctr[SKF(li, SKF_SELW)], 1u, a.error, sh)) return false;
+    const int tid = threadIdx.x;
+    if (tid < a.K) {
+        const float wk = ws_at<float>(a, li, a.o.ex_w)[tid];
+        sh.wk[tid] = wk;
+        sh.ws[tid] = __fmul_rn(wk, a.routed_scale);
+    }
+    __syncthreads();
+    return true;
+}
+
+// ---------------------------------------------------------------- expert item
+//
+// Rows [16j, 16j+16) of F for expert e in `slot` (-1: idle slot, nothing to compute):
+// g, u = gate, up rows . xn (infer.c:1184-1185, 1199-1200), h = silu(g) * u (:1188, :1202),
+// and the partial y = down[:, 16j..16j+16) . h over all D rows (:1190, :1205), stored at
+// ypart[slot][j]. Thread t owns the down rows t + 256 i.
+__device__ __attribute__((always_inline)) static bool sk_expert_item(const StackArgs &a, const StackLayer &L, int li,
+                                                                     int slot, int j, int e, SkShared &sh) {
+    const int D = a.D, F = a.F, NPF = F >> 4, tid = threadIdx.x;
+    if (e >= 0) {
+        const uint8_t *base = L.experts + (size_t)e * a.stride;
+        // Every weight of the item is requested before anything waits: the gate/up chunks to
+        // registers, the down slice and all scales straight to shared memory, one 16-byte load
+        // per lane (row t + 256 i of the slice lands at dslice[t + 256 i]).
+        const int c = D / SK_BLOCK, wave0 = tid & ~63, lane = tid & 63, w = tid >> 6;
+        {
+            // gate then up scales of panel j (D bytes each, contiguous in their s planes),
+            // then the down scales of column block j/2 (one fp16 per row, 2D bytes)
+            const int o = 1024 * w + 16 * lane;
+            if (o < 2 * D) {
+                const uint8_t *src = o < D ? base + a.off_gs + (size_t)j * D + o : base + a.off_us + (size_t)j * D + (o - D);
+                __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)gbl(src), (lds_void *)((uint8_t *)sh.sc_gu + 1024 * w),
+                                                 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)gbl(base + a.off_ds + (size_t)(j >> 1) * D * 2 + o),
+                                                 (lds_void *)((uint8_t *)sh.sc_d + 1024 * w), 16, 0, 0);
+            }
+        }
+        PanelRegs<2, EX_NB_MAX> pr;
+        panel_load_q<2, EX_NB_MAX>(pr, base + a.off_gq, base + a.off_uq, j, D);
+        {
+            const GM_GLOBAL u32x4 *qs = gbl((const u32x4 *)(base + a.off_dq)) + (size_t)j * D + tid;
+#pragma unroll
+            for (int i = 0; i < SK_PER_MAX; i++)
+                if (i < c)
+                    __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)(qs + (size_t)i * SK_BLOCK),
+                                                     (lds_void *)(sh.dslice + i * SK_BLOCK + wave0), 16, 0, 0);
+        }
+        if (!wait_ge(&a.ctr[SKF(li, SKF_DIG)], 1u, a.error, sh)) return false;  // digits of xn ready
+        dma_copy(sh.u.g.dig, ws_at<unsigned long long>(a, li, a.o.dig), 3 * D);
+        dma_copy(sh.u.g.dexp, ws_at<int>(a, li, a.o.dexp), D / 8);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();  // every wave's digits, scales and slice rows are in shared memory
+        sk_stamp(sh, 6);
+        float gu[2];
+        const unsigned short *scs[2] = {sh.sc_gu, sh.sc_gu + D / 2};
+        panel_compute_sc<2, EX_NB_MAX>(pr, D, sh.u.g.dig, sh.u.g.dexp, scs, gu);
+        if (lane < 16) {
+            sh.u.g.part[w][0][lane] = gu[0];
+            sh.u.g.part[w][1][lane] = gu[1];
+        }
+        __syncthreads();
+        if (tid < 16) {
+            // SwiGLU of the 16 rows, then their digit form with one exponent
+            const float g = ((sh.u.g.part[0][0][tid] + sh.u.g.part[1][0][tid]) + sh.u.g.part[2][0][tid]) + sh.u.g.part[3][0][tid];
+            const float u = ((sh.u.g.part[0][1][tid] + sh.u.g.part[1][1][tid]) + sh.u.g.part[2][1][tid]) + sh.u.g.part[3][1][tid];
+            const float h = g / (1.0f + expf(-g)) * u;
+            float mx = fabsf(h);
+            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+            const int ex = digit_exponent(mx);
+            int8_t d0, d1, d2;
+            split_digits(h, ex, &d0, &d1, &d2);
+            int8_t *hb = (int8_t *)sh.u.g.hd;
+            hb[tid] = d0;
+            hb[16 + tid] = d1;
+            hb[32 + tid] = d2;
+            if (tid == 0) sh.u.g.hexp = ex;
+        }
+        __syncthreads();
+        sk_stamp(sh, 4);
+        int h4[12];
+#pragma unroll
+        for (int q = 0; q < 12; q++) h4[q] = sh.u.g.hd[q];
+        const int hexp = sh.u.g.hexp;
+        // partials in combine order: [D/8 chunks][K+1 slots][F/16][8 rows]
+        const int NS = a.K + 1;
+        float *yp = ws_at<float>(a, li, a.o.ypart) + ((size_t)slot * NPF + j) * SK_CROWS + (tid & (SK_CROWS - 1));
+#pragma unroll
+        for (int i = 0; i < SK_PER_MAX; i++) {
+            if (i < c) {
+                const u32x4 dq = sh.dslice[i * SK_BLOCK + tid];
+                const int wq[4] = {(int)dq.x, (int)dq.y, (int)dq.z, (int)dq.w};
+                int acc[3];
+#pragma unroll
+                for (int d = 0; d < 3; d++) {
+                    int s = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) s = __builtin_amdgcn_sdot4(wq[q], h4[4 * d + q], s, false);
+                    acc[d] = s;
+                }
+                const float f = digits_to_float(acc[0], acc[1], acc[2]);
+                const int r = i * SK_BLOCK + tid;
+                st_f(yp + (size_t)(r / SK_CROWS) * NS * NPF * SK_CROWS,
+                     f * ldexpf(__half2float(__ushort_as_half(sh.sc_d[r])), hexp));
+            }
+        }
+    }
+    sk_stamp(sh, 5);
+    // two-level count of the layer's (K+1) * F/16 items, then the layer's flag
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned per_ctr = (unsigned)((a.K + 1) * NPF / SK_NPART);
+        if (add_u(&a.ctr[SKC(SKC_PART + (slot * NPF + j) % SK_NPART)]) + 1u == (unsigned)(li + 1) * per_ctr &&
+            add_u(&a.ctr[SKC(SKC_PART2)]) + 1u == (unsigned)(li + 1) * SK_NPART)
+            st_u(&a.ctr[SKF(li, SKF_PART)], 1u);
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------- combine
+//
+// Rows [8c, 8c+8) of x' = x + (shared + sum_k w_e * y_k) (infer.c:1192, 1212-1214),
+// with y_k the sum of expert k's F/16 partials in a fixed order. The chunk's partials
+// are one contiguous run ([slot][j][8 rows], 32 bytes per partial), copied to shared
+// memory with wide loads (as many slots per pass as fit). Thread t then sums the
+// partials j = g, g + 32, ... (g = t/8) of row t%8 for each slot, and 8 threads add the
+// 32 group sums in order and apply glm.c's combine order.
+__device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs &a, int li, int c, bool routed_on,
+                                                                 SkShared &sh) {
+    const int D = a.D, K = a.K, NS = K + 1, NPF = a.F >> 4, tid = threadIdx.x;
+    if (!wait_ge(&a.ctr[SKF(li, SKF_PART)], 1u, a.error, sh)) return false;  // every expert item is done
+    const int rl = tid & (SK_CROWS - 1), g = tid / SK_CROWS;
+    const size_t slot_bytes = (size_t)NPF * SK_CROWS * sizeof(float);
+    const int per_pass = (int)(sizeof(sh.dslice) / slot_bytes);  // >= 2 for F <= 2048
+    const uint8_t *src = (const uint8_t *)(ws_at<float>(a, li, a.o.ypart) + (size_t)c * NS * NPF * SK_CROWS);
+    const float *buf = (const float *)sh.dslice;
+    for (int k0 = 0; k0 < NS; k0 += per_pass) {
+        const int nk = NS - k0 < per_pass ? NS - k0 : per_pass;
+        __syncthreads();  // the previous pass's reads are done
+        dma_copy(sh.dslice, src + (size_t)k0 * slot_bytes, (int)(nk * slot_bytes));
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int kk = 0; kk < nk; kk++) {
+            float s = 0.0f;
+            for (int jq = g; jq < NPF; jq += SK_CGROUPS) s += buf[((size_t)kk * NPF + jq) * SK_CROWS + rl];
+            // the wave's 8 groups of this row, in a fixed tree (lanes rl, rl + 8, ..., rl + 56)
+            s += __shfl_xor(s, 8, 64);
+            s += __shfl_xor(s, 16, 64);
+            s += __shfl_xor(s, 32, 64);
+            if ((tid & 63) < SK_CROWS) sh.u.c.acc[tid >> 6][k0 + kk][rl] = s;
+        }
+    }
+    __syncthreads();
+    if (tid < SK_CROWS) {
+        const int r = c * SK_CROWS + rl;
         float acc = 0.0f;
         if (routed_on) {
-            float yk[GM_MAX_K];
-#pragma unroll
-            for (int k = 0; k < GM_MAX_K; k++) yk[k] = y[(size_t)(k < K ? k : 0) * D + r];
-#pragma unroll
-            for (int k = 0; k < GM_MAX_K; k++)
-                if (k < K) acc = __fadd_rn(acc, yk[k]);
+            for (int k = 0; k < K; k++) {
+                if (sh.idx[k] < 0) continue;
+                const float yk = ((sh.u.c.acc[0][k][rl] + sh.u.c.acc[1][k][rl]) + sh.u.c.acc[2][k][rl]) + sh.u.c.acc[3][k][rl];
+                acc = __fadd_rn(acc, __fmul_rn(sh.ws[k], yk));
+            }
         }
-        const float shv = y[(size_t)K * D + r];
+        const float shv = ((sh.u.c.acc[0][K][rl] + sh.u.c.acc[1][K][rl]) + sh.u.c.acc[2][K][rl]) + sh.u.c.acc[3][K][rl];
         const float xr = (li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x))[r];
         st_f(a.routed_out + r, acc);
         st_f(a.shared_out + r, shv);
         float *xo = li == a.n_layers - 1 ? a.x_out : ws_at<float>(a, li + 1, a.o.x);
         st_f(xo + r, __fadd_rn(xr, __fadd_rn(shv, acc)));
     }
-    publish(&a.ctr[SKC(SKC_X)], sh, false);
+    sk_stamp(sh, 5);
+    arrive(&a.ctr[SKC(SKC_X)], (unsigned)(li + 1) * (D / SK_CROWS), &a.ctr[SKF(li, SKF_X)]);
     return true;
 }
 
+// grid (n + 255) / 256
 __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, int *error) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) ctr[i] = 0u;
-    if (threadIdx.x == 0) *error = 0;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) ctr[i] = 0u;
+    if (i == 0) *error = 0;
 }
 
-__device__ static inline unsigned long long sk_now() { return wall_clock64(); }
-
-
-// Block roles. The first n_router blocks compute the router items, the next
-// a.shared_blocks blocks the shared expert, the rest the routed experts; each role walks
-// the layers in order, so a block never holds an item that is ready later than the
-// items other blocks of its role are waiting to start.
+// Block roles: the first n_router blocks route; the next shared_blocks run the shared
+// expert's items, then wait until the layer's expert items are all done before taking the
+// next layer's (so its 10 MB of weights stream while the combine and the next router run,
+// not during the routed burst); the rest run the routed experts' items and then the
+// combine chunks. Router blocks go from one layer's router item straight to prefetching
+// the next layer's router rows. Trace items of one layer are numbered: n_router router
+// items, D/8 combine chunks, F/16 shared items, K*F/16 routed items (a block's top-k is
+// stamped on its first expert item).
 __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
     __shared__ SkShared sh;
-    sh.trace = a.trace;
+    if (threadIdx.x == 0) {
+        sh.trace = a.trace;
+        sh.ok = 1;
+    }
+    __syncthreads();
     const int K = a.K, NS = K + 1;
-    const int NPF = a.F >> 4, NPD = a.D >> 4;
-    const int NR = (a.E + SK_RX - 1) / SK_RX, NSB = a.shared_blocks, NWB = (int)gridDim.x - NR - NSB;
-    const int per_layer = NR + NS * NPF + NS * NPD;  // trace numbering of one layer's items
+    const int NPF = a.F >> 4, NCH = a.D / SK_CROWS;  // combine chunks
+    const int NR = a.n_router, NSB = a.shared_blocks, NWB = (int)gridDim.x - NR - NSB;
+    const int per_layer = NR + NCH + NS * NPF;
     const int b = blockIdx.x;
     for (int li = 0; li < a.n_layers; li++) {
         const StackLayer L = a.layers[li];
         const int layer = a.first_layer + li;
         const long base = (long)li * per_layer;
-        bool ok = true;
-#define SK_ITEM(idx, call)                                                              \
-    do {                                                                                \
-        sh.trace_item = base + (idx);                                                   \
-        if (a.trace && threadIdx.x == 0) a.trace[SK_TRACE_STAMPS * sh.trace_item] = sk_now(); \
-        ok = (call);                                                                    \
-        if (!ok) return;                                                                \
-        if (a.trace && threadIdx.x == 0) a.trace[SK_TRACE_STAMPS * sh.trace_item + 2] = sk_now(); \
-        __syncthreads();                                                                \
-    } while (0)
         const bool routed_on = !(a.flags & 1) && L.has_routed;
+#define SK_ITEM(idx, call)                                                                    \
+    do {                                                                                      \
+        sh.trace_item = base + (idx);                                                         \
+        if (a.trace && threadIdx.x == 0) a.trace[SK_TRACE_STAMPS * sh.trace_item] = wall_clock64(); \
+        if (!(call)) return;                                                                  \
+        if (a.trace && threadIdx.x == 0) a.trace[SK_TRACE_STAMPS * sh.trace_item + 2] = wall_clock64(); \
+        __syncthreads();                                                                      \
+    } while (0)
         if (b < NR) {
             SK_ITEM(b, sk_router_item(a, L, layer, li, b, sh));
         } else if (b < NR + NSB) {
             const int sb = b - NR;
-            for (int p = sb; p < NPF; p += NSB) SK_ITEM(NR + p, sk_gate_up_item(a, L, li, K, p, a.E, sh));
-            for (int p = sb; p < NPD; p += NSB) SK_ITEM(NR + NPF + p, sk_down_item(a, L, li, K, p, a.E, routed_on, sh));
+            for (int j = sb; j < NPF; j += NSB) SK_ITEM(NR + NCH + j, sk_expert_item(a, L, li, K, j, a.E, sh));
+            sh.trace_item = base + NR + NCH + sb;
+            if (!wait_ge(&a.ctr[SKF(li, SKF_PART)], 1u, a.error, sh)) return;
         } else {
             const int wb = b - NR - NSB;
-            // the first routed block records the routing, also when routed experts are off
-            if (routed_on || wb == 0) {
-                sh.trace_item = base + NR + NPF + NPD + wb;
-                if (!sk_select(a, L, li, sh)) return;
-                if (wb == 0) sk_write_routing(a, layer, sh);
+            if (wb < K * NPF && routed_on) {
+                sh.trace_item = base + NR + NCH + NPF + wb;  // stamp 8 of its first item
+                if (!sk_read_topk(a, li, sh)) return;
             }
             for (int i = wb; i < K * NPF; i += NWB) {
                 const int slot = i / NPF;
-                SK_ITEM(NR + NPF + NPD + i, sk_gate_up_item(a, L, li, slot, i % NPF, routed_on ? sh.idx[slot] : -1, sh));
+                SK_ITEM(NR + NCH + NPF + i, sk_expert_item(a, L, li, slot, i % NPF, routed_on ? sh.idx[slot] : -1, sh));
             }
-            for (int i = wb; i < K * NPD; i += NWB) {
-                const int slot = i / NPD;
-                SK_ITEM(NR + NPF + NPD + K * NPF + i,
-                        sk_down_item(a, L, li, slot, i % NPD, routed_on ? sh.idx[slot] : -1, routed_on, sh));
+            // combine chunks, by the blocks that hold this layer's routing
+            const int ncb = NWB < K * NPF ? NWB : K * NPF;
+            if (wb < ncb && wb < NCH) {
+                if (routed_on && !sk_read_weights(a, li, sh)) return;
+                for (int c = wb; c < NCH; c += ncb) SK_ITEM(NR + c, sk_combine(a, li, c, routed_on, sh));
             }
         }
 #undef SK_ITEM
-        (void)ok;
     }
 }
