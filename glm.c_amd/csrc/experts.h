@@ -165,8 +165,10 @@ __device__ static inline void panel_load_q(PanelRegs<NMAT, NB> &r, const uint8_t
 #pragma unroll
     for (int u = 0; u < NB; u++)
 #pragma unroll
-        for (int m = 0; m < NMAT; m++)
+        for (int m = 0; m < NMAT; m++) {
             if (u < cpw) r.q[m][u] = __builtin_nontemporal_load(qp[m] + (size_t)u * 64);
+            else r.q[m][u] = u32x4{0u, 0u, 0u, 0u};  // defined operands for branch-free consumers
+        }
 }
 
 // panel_compute with the panel's fp16 scales in shared memory: sc[m] holds matrix m's

@@ -256,9 +256,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         c->sk_o.dig = take(3 * D);
         c->sk_o.dexp = take(D / 32 * sizeof(int));
         c->sk_o.stage = take(E * sizeof(StageEnt));
-        c->sk_o.ex_idx = take(K * sizeof(int));
         c->sk_o.ex_w = take(K * sizeof(float));
-        c->sk_o.ex_p = take(E * sizeof(float));
         c->sk_o.ypart = take(NS * (F / 16) * D * sizeof(float));
         c->sk_ws_layer = off;
         rc |= dev_alloc(&c->sk_ws, (size_t)c->L * off);
@@ -566,8 +564,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         HIP_OK(hipMemsetAsync(c->sk_trace, 0, SK_TRACE_STAMPS * items * sizeof(uint64_t), st));
     }
     const int n_ctr = SK_CTR_WORDS(n);
-    hipLaunchKernelGGL(k_stack_reset, dim3((n_ctr + SK_BLOCK - 1) / SK_BLOCK), dim3(SK_BLOCK), 0, st, c->sk_ctr, n_ctr,
-                       c->sk_error);
+    hipLaunchKernelGGL(k_stack_reset, dim3(n + 1), dim3(SK_BLOCK), 0, st, c->sk_ctr, n_ctr, c->sk_error, a);
     ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_STACK);
     hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
     prof_end(pr, st);

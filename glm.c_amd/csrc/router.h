@@ -71,6 +71,15 @@ __device__ static float certified_mean_sq(const float *xt, int D, double *red, f
 // GPU's expf and the CPU's libm expf are both within 2 ulp, the add and the divide round
 // once each, so p moves by less than 2^-20 relative -- widened to 2^-19 for margin, and
 // one more ulp for the final add.
+// The last step of selection_interval, from the sigmoids plo, phi at the interval ends.
+__device__ static inline void selection_bounds(double plo, double phi, float bias, double *lo, double *hi) {
+    const double dp = 0x1p-19;
+    const double vlo = plo * (1.0 - dp) + (double)bias;
+    const double vhi = phi * (1.0 + dp) + (double)bias;
+    *lo = vlo - fabs(vlo) * 0x1p-22 - 0x1p-148;
+    *hi = vhi + fabs(vhi) * 0x1p-22 + 0x1p-148;
+}
+
 __device__ static inline void selection_interval(double S, double B, float bias, double *lo, double *hi) {
     const float slo = __double2float_rd(S - B), shi = __double2float_ru(S + B);
     const double plo = (double)(1.0f / (1.0f + expf(-slo)));

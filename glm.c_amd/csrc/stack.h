@@ -57,7 +57,7 @@
 // flag sits 64 words (256 bytes) from the next. The expert items count on SK_NPART
 // counters, whose last arrivals count on a second level.
 #define SKC_PAD 64
-enum { SKC_ROUTER = 0, SKC_DIG = 1, SKC_X = 2, SKC_PART2 = 3, SKC_PART = 4, SKC_FIXED = SKC_PART + SK_NPART };
+enum { SKC_DIG = 0, SKC_X2 = 1, SKC_PART2 = 2, SKC_PART = 3, SKC_X = SKC_PART + SK_NPART, SKC_FIXED = SKC_X + SK_NPART };
 enum { SKF_SEL = 0, SKF_SELW = 1, SKF_DIG = 2, SKF_PART = 3, SKF_X = 4, SKF_PER_LAYER = 5 };
 #define SKC(i) ((i) * SKC_PAD)
 #define SKF(li, f) SKC(SKC_FIXED + SKF_PER_LAYER * (li) + (f))  // per-layer flags
@@ -65,6 +65,7 @@ enum { SKF_SEL = 0, SKF_SELW = 1, SKF_DIG = 2, SKF_PART = 3, SKF_X = 4, SKF_PER_
 // 64-bit word per four slots, 16 bits per slot holding expert + 2 (never zero, so a word
 // is either unwritten or complete).
 #define SK_SEL_WORDS ((GM_MAX_K + 3) / 4)
+static_assert(2 * SK_SEL_WORDS <= SKC_PAD, "the SEL words must fit in the flag's padding");
 #define SK_CTR_WORDS(n_layers) SKF(n_layers, 0)
 #define GM_STACK_COUNTERS SK_CTR_WORDS(SK_MAX_LAYERS)
 
@@ -77,16 +78,19 @@ struct StackLayer {
     int pad;
 };
 
-// One expert's certified selection interval [lo, hi] of sel = p + bias, and p.
+// One expert's router result, written once per launch by its router block into words that
+// the launch's reset set to SK_UNSET: w0 = fp32 bits of lo | hi << 32, the certified
+// selection interval [lo, hi] of sel = p + bias rounded outward; w1 = fp32 bits of p.
+// Each word is stored and loaded whole (64-bit, single-copy atomic), so a reader that sees
+// neither word unset has the final entry, with no counter or flag in between.
 struct StageEnt {
-    double lo, hi;
-    float p;
-    int pad[3];
+    unsigned long long w0, w1;
 };
+#define SK_UNSET (~0ull)
 
 // Per-layer workspace: one region of `ws_layer_bytes` per layer of the launch.
 struct StackWs {
-    size_t x, xn, dig, dexp, stage, ex_idx, ex_w, ex_p, ypart;  // byte offsets inside a layer region
+    size_t x, xn, dig, dexp, stage, ex_w, ypart;  // byte offsets inside a layer region
 };
 
 struct StackArgs {
@@ -156,9 +160,10 @@ struct SkShared {
     } u;
     u32x4 dslice[GM_MAX_COLS];  // an expert item's down columns, D rows x 16 bytes
     float xn_r[GM_MAX_COLS];    // a router item's xn (kept through the top-k and its replay)
-    unsigned short sc_gu[2 * GM_MAX_COLS / 2];  // its gate and up panel scales, [2][16][D/32]
+    __attribute__((aligned(16))) unsigned short sc_gu[2 * GM_MAX_COLS / 2];  // its gate and up panel scales, [2][16][D/32]
     unsigned short sc_d[GM_MAX_COLS];           // its down scales, one per row
     double red[4];
+    float mxw[4];  // per-wave max |xn|
     float mean, total;
     unsigned old;
     int ok, sel_ok;
@@ -213,6 +218,15 @@ __device__ static inline bool wait_ge(const unsigned *c, unsigned target, int *e
     return sh.ok != 0;
 }
 
+// Maximum over the 64 lanes of a wave, returned to every lane (wave-uniform), by DPP.
+__device__ static inline float wave_max_dpp_f(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_QUAD_1032, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_QUAD_2301, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_ROW_HALF_MIRROR, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_ROW_MIRROR, 0xF, 0xF, false)));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
 // Diagnostic stamp k of the current item (thread 0, when tracing).
 __device__ static inline void sk_stamp(SkShared &sh, int k) {
     if (sh.trace && threadIdx.x == 0) sh.trace[SK_TRACE_STAMPS * sh.trace_item + k] = wall_clock64();
@@ -233,189 +247,229 @@ __device__ static inline void dma_copy(void *dst, const void *src, int nbytes) {
 // ---------------------------------------------------------------- top-k selection
 //
 // Top-k of layer li (infer.c:1108-1145) into sh.idx / sh.wk (normalised) / sh.ws (times
-// routed_scale), and the router probabilities of all experts into sh.u.s.p.
+// routed_scale), from the stage entries, by every block that needs it (each routed block
+// and router block 0), with no signal in between: wave 0 polls the entries until none is
+// unset, lane l holding experts l + 64c.
 //
-// Fast path, wave 0 alone: lane l holds experts l + 64c. The K best interval midpoints are
-// taken one at a time (a wave maximum, then the lowest lane holding it), and the result is
-// certified when each chosen interval lies strictly above the next chosen one and the
-// last chosen lies strictly above every expert left out. glm.c's insertion top-k orders
-// strictly by value, so it must then pick the same experts in the same order. Otherwise,
-// or when any interval is not finite, one block replays the fp32 router exactly.
+// The K best interval midpoints are taken one at a time (a wave maximum, then the lowest
+// lane holding it), and the result is certified when each chosen interval lies strictly
+// above the next chosen one and the last chosen lies strictly above every expert left
+// out. glm.c's insertion top-k orders strictly by value, so it must then pick the same
+// experts in the same order. Every block sees the same entries and so reaches the same
+// verdict; when it is "not certified" (or an interval is not finite), router block 0
+// replays the fp32 router exactly (sk_exact_select) and the others wait for its result.
+// Returns false if the wait timed out or another block failed; sh.sel_ok = certified.
 #define SK_SEL_C (GM_MAX_E / 64)
 
-__device__ __attribute__((always_inline)) static bool sk_select_topk(const StackArgs &a, const StackLayer &L, int li,
-                                                                     SkShared &sh) {
-    const int D = a.D, E = a.E, K = a.K, tid = threadIdx.x;
-    sk_stamp(sh, 8);
+// The selection proper on wave 0, over C chunks of 64 experts whose stage words w0, w1
+// are in registers (lane l: experts l + 64c): the top-k into sh.idx / sh.wk (unscaled),
+// their sum into sh.total, the verdict into sh.sel_ok, and with keep_p every probability
+// into sh.u.s.p.
+template <int C>
+__device__ __attribute__((always_inline)) static void sk_select_rounds(const StackArgs &a, const unsigned long long *w0,
+                                                                       const unsigned long long *w1, bool keep_p,
+                                                                       SkShared &sh) {
+    const int E = a.E, K = a.K, tid = threadIdx.x;
+    float lo[C], hi[C], pr[C], key[C];
+    bool bad = false;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int e = tid + 64 * c;
+        const bool valid = e < E;
+        lo[c] = valid ? __uint_as_float((unsigned)w0[c]) : -INFINITY;
+        hi[c] = valid ? __uint_as_float((unsigned)(w0[c] >> 32)) : -INFINITY;
+        pr[c] = valid ? __uint_as_float((unsigned)w1[c]) : 0.0f;
+        if (valid) bad |= !(isfinite(lo[c]) && isfinite(hi[c]));
+        key[c] = valid ? 0.5f * lo[c] + 0.5f * hi[c] : -INFINITY;
+        if (keep_p && valid) sh.u.s.p[e] = pr[c];
+    }
+    bool cert = __ballot(bad) == 0;
+    float prev_lo = 0.0f, total = 0.0f;
+    for (int k = 0; k < K; k++) {
+        float bm = key[0];
+        int bc = 0;
+#pragma unroll
+        for (int c = 1; c < C; c++)
+            if (key[c] > bm) {
+                bm = key[c];
+                bc = c;
+            }
+        const float gm = wave_max_dpp_f(bm);
+        int ek = -1;
+        float wk = -1e30f;
+        if (gm > -INFINITY) {  // fewer than K experts leave the rest at -1 (infer.c:1110-1113)
+            const int ls = __ffsll(__ballot(bm == gm)) - 1;
+            const int cs = __builtin_amdgcn_readlane(bc, ls);
+            float ml = lo[0], mh = hi[0], mp = pr[0];
+#pragma unroll
+            for (int c = 1; c < C; c++)
+                if (bc == c) {
+                    ml = lo[c];
+                    mh = hi[c];
+                    mp = pr[c];
+                }
+            const float lk = readlane_f(ml, ls), hk = readlane_f(mh, ls);
+            if (k > 0 && !(prev_lo > hk)) cert = false;
+            prev_lo = lk;
+            ek = ls + 64 * cs;
+            wk = readlane_f(mp, ls);
+            total = __fadd_rn(total, wk);
+#pragma unroll
+            for (int c = 0; c < C; c++)
+                if (tid == ls && c == cs) key[c] = -INFINITY;
+        }
+        if (tid == 0) {
+            sh.idx[k] = ek;
+            sh.wk[k] = wk;
+        }
+    }
+    // the last chosen must lie above every expert left out (chosen ones now hold -inf)
+    float rest = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < C; c++)
+        if (key[c] > -INFINITY) rest = fmaxf(rest, hi[c]);
+    rest = wave_max_dpp_f(rest);
+    if (rest > -INFINITY && !(prev_lo > rest)) cert = false;
+    if (tid == 0) {
+        sh.sel_ok = cert;
+        sh.total = total;
+    }
+}
+
+__device__ __attribute__((always_inline)) static bool sk_stage_select(const StackArgs &a, int li, bool keep_p,
+                                                                      SkShared &sh) {
+    const int E = a.E, K = a.K, tid = threadIdx.x;
     if (tid < 64) {
         const StageEnt *stage = ws_at<StageEnt>(a, li, a.o.stage);
-        double lo[SK_SEL_C], hi[SK_SEL_C], mid[SK_SEL_C];
-        float pr[SK_SEL_C];
+        const int nch = (E + 63) >> 6;
+        unsigned long long w0[SK_SEL_C], w1[SK_SEL_C];
+        unsigned spins = 0;
+        bool alive = true;
+        for (;;) {
+            bool miss = false;
 #pragma unroll
-        for (int c = 0; c < SK_SEL_C; c++) {  // all loads in flight at once
-            const int e = tid + 64 * c < E ? tid + 64 * c : E - 1;
-            lo[c] = stage[e].lo;
-            hi[c] = stage[e].hi;
-            pr[c] = stage[e].p;
-        }
-        bool bad = false;
-#pragma unroll
-        for (int c = 0; c < SK_SEL_C; c++) {
-            const int e = tid + 64 * c;
-            if (e < E) {
-                sh.u.s.p[e] = pr[c];
-                bad |= !(isfinite(lo[c]) && isfinite(hi[c]));
-                mid[c] = 0.5 * (lo[c] + hi[c]);
-            } else {
-                lo[c] = hi[c] = mid[c] = -INFINITY;
-                pr[c] = 0.0f;
-            }
-        }
-        bool ok = __ballot(bad) == 0;
-        double prev_lo = 0.0;
-        float total = 0.0f;
-        for (int k = 0; k < K; k++) {
-            double bm = mid[0];
-            int bc = 0;
-#pragma unroll
-            for (int c = 1; c < SK_SEL_C; c++)
-                if (mid[c] > bm) {
-                    bm = mid[c];
-                    bc = c;
+            for (int c = 0; c < SK_SEL_C; c++) {
+                const int e = tid + 64 * c < E ? tid + 64 * c : E - 1;
+                if (c < nch) {
+                    w0[c] = __hip_atomic_load(&stage[e].w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    w1[c] = __hip_atomic_load(&stage[e].w1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    miss |= (w0[c] == SK_UNSET) | (w1[c] == SK_UNSET);
+                } else {
+                    w0[c] = w1[c] = 0ull;
                 }
-            const double gm = wave_max_dpp(bm);
-            int ek = -1;
-            float wk = -1e30f;
-            if (gm > -INFINITY) {  // fewer than K experts leave the rest at -1 (infer.c:1110-1113)
-                const int ls = __ffsll(__ballot(bm == gm)) - 1;
-                const int cs = __builtin_amdgcn_readlane(bc, ls);
-                double ml = lo[0], mh = hi[0];
-                float mp = pr[0];
-#pragma unroll
-                for (int c = 1; c < SK_SEL_C; c++)
-                    if (bc == c) {
-                        ml = lo[c];
-                        mh = hi[c];
-                        mp = pr[c];
-                    }
-                const double lk = readlane_d(ml, ls), hk = readlane_d(mh, ls);
-                if (k > 0 && !(prev_lo > hk)) ok = false;
-                prev_lo = lk;
-                ek = ls + 64 * cs;
-                wk = readlane_f(mp, ls);
-                total = __fadd_rn(total, wk);
-#pragma unroll
-                for (int c = 0; c < SK_SEL_C; c++)
-                    if (tid == ls && c == cs) mid[c] = -INFINITY;
             }
-            if (tid == 0) {
-                sh.idx[k] = ek;
-                sh.wk[k] = wk;
+            if (__ballot(miss) == 0) break;
+            if (__hip_atomic_load(a.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > SK_SPIN_LIMIT) {
+                if (tid == 0) __hip_atomic_store(a.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                alive = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (sh.trace && tid == 0) sh.trace[SK_TRACE_STAMPS * sh.trace_item + 8] = wall_clock64();
+        if (nch == 1)
+            sk_select_rounds<1>(a, w0, w1, keep_p, sh);
+        else
+            sk_select_rounds<SK_SEL_C>(a, w0, w1, keep_p, sh);
+        if (tid == 0) sh.ok = alive;
+    }
+    __syncthreads();
+    if (!sh.ok) return false;
+    if (sh.sel_ok && tid < K) {
+        // normalisation of infer.c:1137-1145
+        const float total = sh.total;
+        float wk = sh.wk[tid];
+        if (total > 0.0f) {
+            const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
+            wk = __fmul_rn(wk, __fdiv_rn(1.0f, denom));
+        }
+        sh.wk[tid] = wk;
+        sh.ws[tid] = __fmul_rn(wk, a.routed_scale);
+    }
+    __syncthreads();
+    sk_stamp(sh, 3);
+    return true;
+}
+
+// glm.c's router replayed exactly in fp32 for layer li (infer.c:916-938, 1108-1145), by
+// the router block whose xn is in sh.xn_r, when the certified selection failed: the top-k
+// into sh.idx / sh.wk / sh.ws and every probability into sh.u.s.p.
+__device__ static void sk_exact_select(const StackArgs &a, const StackLayer &L, SkShared &sh) {
+    const int D = a.D, E = a.E, K = a.K, tid = threadIdx.x;
+    const GM_GLOBAL float *bias = gbl(L.bias);
+    for (int i = tid; i < D; i += SK_BLOCK) sh.u.s.xn[i] = sh.xn_r[i];
+    // infer.c:916-925 for every expert, 16 columns at a time: all threads form the
+    // products fl(g * xn), then lane e adds its expert's 16 in order.
+    float chain[GM_MAX_E / 64];
+    for (int c = 0; c < GM_MAX_E / 64; c++) chain[c] = 0.0f;
+    const GM_GLOBAL float *gi = gbl(L.gate_inp);
+    for (int eb = 0; eb < E; eb += 64) {
+        const int ne = E - eb < 64 ? E - eb : 64;
+        for (int c0 = 0; c0 < D; c0 += 16) {
+            __syncthreads();
+            for (int i = tid; i < ne * 16; i += SK_BLOCK) {
+                const int er = i >> 4, cc = i & 15;
+                sh.u.s.prod[er][cc] = __fmul_rn(gi[(size_t)(eb + er) * D + c0 + cc], sh.u.s.xn[c0 + cc]);
+            }
+            __syncthreads();
+            if (tid < ne) {
+                float acc = chain[eb >> 6];
+                for (int cc = 0; cc < 16; cc++) acc = __fadd_rn(acc, sh.u.s.prod[tid][cc]);
+                chain[eb >> 6] = acc;
             }
         }
-        // the last chosen must lie above every expert left out (chosen ones now hold -inf)
-        double rest = -INFINITY;
-#pragma unroll
-        for (int c = 0; c < SK_SEL_C; c++)
-            if (mid[c] > -INFINITY) rest = fmax(rest, hi[c]);
-        rest = wave_max_dpp(rest);
-        if (rest > -INFINITY && !(prev_lo > rest)) ok = false;
-        if (tid == 0) {
-            sh.sel_ok = ok;
-            sh.total = total;
+        __syncthreads();
+        if (tid < ne) {
+            const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain[eb >> 6])));
+            sh.u.s.p[eb + tid] = pr;
+            sh.u.s.sel[eb + tid] = __fadd_rn(pr, bias[eb + tid]);
         }
     }
     __syncthreads();
-    if (sh.sel_ok) {
-        // normalisation of infer.c:1137-1145
-        if (tid < K) {
-            const float total = sh.total;
-            if (total > 0.0f) {
-                const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
-                sh.wk[tid] = __fmul_rn(sh.wk[tid], __fdiv_rn(1.0f, denom));
+    if (tid == 0) {
+        atomicAdd(&a.stats[GM_STAT_ROUTE_EXACT], 1ull);
+        int idx[GM_MAX_K];
+        for (int k = 0; k < K; k++) idx[k] = -1;
+        for (int i = 0; i < E; i++) {
+            const float sc = sh.u.s.sel[i];
+            int at = -1;
+            for (int k = 0; k < K && at < 0; k++) {
+                const float held = idx[k] >= 0 ? sh.u.s.sel[idx[k]] : -INFINITY;
+                if (sc > held) at = k;
+            }
+            if (at < 0) continue;
+            for (int k = K - 1; k > at; k--) idx[k] = idx[k - 1];
+            idx[at] = i;
+        }
+        // libm's expf may differ from the GPU's by an ulp: flag orders decided that closely
+        int unresolved = 0;
+        for (int k = 0; k < K; k++) {
+            if (idx[k] < 0) continue;
+            const float a0 = sh.u.s.sel[idx[k]];
+            const float tol = 4.0f * fmaxf(fabsf(a0), 1e-30f) * 0x1p-23f + 4.0f * 0x1p-24f;
+            for (int i = 0; i < E; i++) {
+                if (i == idx[k]) continue;
+                bool above = false;
+                for (int q = 0; q < k; q++) above |= (idx[q] == i);
+                if (!above && fabsf(sh.u.s.sel[i] - a0) <= tol) unresolved = 1;
             }
         }
-    } else {
-        // The proof failed: this block replays glm.c's router exactly (its xn is in xn_r).
-        {
-            const GM_GLOBAL float *bias = gbl(L.bias);
-            for (int i = tid; i < D; i += SK_BLOCK) sh.u.s.xn[i] = sh.xn_r[i];
-            // infer.c:916-925 for every expert, 16 columns at a time: all threads form the
-            // products fl(g * xn), then lane e adds its expert's 16 in order.
-            float chain[GM_MAX_E / 64];
-            for (int c = 0; c < GM_MAX_E / 64; c++) chain[c] = 0.0f;
-            const GM_GLOBAL float *gi = gbl(L.gate_inp);
-            for (int eb = 0; eb < E; eb += 64) {
-                const int ne = E - eb < 64 ? E - eb : 64;
-                for (int c0 = 0; c0 < D; c0 += 16) {
-                    __syncthreads();
-                    for (int i = tid; i < ne * 16; i += SK_BLOCK) {
-                        const int er = i >> 4, cc = i & 15;
-                        sh.u.s.prod[er][cc] = __fmul_rn(gi[(size_t)(eb + er) * D + c0 + cc], sh.u.s.xn[c0 + cc]);
-                    }
-                    __syncthreads();
-                    if (tid < ne) {
-                        float acc = chain[eb >> 6];
-                        for (int cc = 0; cc < 16; cc++) acc = __fadd_rn(acc, sh.u.s.prod[tid][cc]);
-                        chain[eb >> 6] = acc;
-                    }
-                }
-                __syncthreads();
-                if (tid < ne) {
-                    const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain[eb >> 6])));
-                    sh.u.s.p[eb + tid] = pr;
-                    sh.u.s.sel[eb + tid] = __fadd_rn(pr, bias[eb + tid]);
-                }
-            }
-            __syncthreads();
-            if (tid == 0) {
-                atomicAdd(&a.stats[GM_STAT_ROUTE_EXACT], 1ull);
-                int idx[GM_MAX_K];
-                for (int k = 0; k < K; k++) idx[k] = -1;
-                for (int i = 0; i < E; i++) {
-                    const float sc = sh.u.s.sel[i];
-                    int at = -1;
-                    for (int k = 0; k < K && at < 0; k++) {
-                        const float held = idx[k] >= 0 ? sh.u.s.sel[idx[k]] : -INFINITY;
-                        if (sc > held) at = k;
-                    }
-                    if (at < 0) continue;
-                    for (int k = K - 1; k > at; k--) idx[k] = idx[k - 1];
-                    idx[at] = i;
-                }
-                // libm's expf may differ from the GPU's by an ulp: flag orders decided that closely
-                int unresolved = 0;
-                for (int k = 0; k < K; k++) {
-                    if (idx[k] < 0) continue;
-                    const float a0 = sh.u.s.sel[idx[k]];
-                    const float tol = 4.0f * fmaxf(fabsf(a0), 1e-30f) * 0x1p-23f + 4.0f * 0x1p-24f;
-                    for (int i = 0; i < E; i++) {
-                        if (i == idx[k]) continue;
-                        bool above = false;
-                        for (int q = 0; q < k; q++) above |= (idx[q] == i);
-                        if (!above && fabsf(sh.u.s.sel[i] - a0) <= tol) unresolved = 1;
-                    }
-                }
-                if (unresolved) atomicAdd(&a.stats[GM_STAT_UNRESOLVED], 1ull);
-                float total = 0.0f;
-                for (int k = 0; k < K; k++) {
-                    sh.idx[k] = idx[k];
-                    sh.wk[k] = idx[k] >= 0 ? sh.u.s.p[idx[k]] : -1e30f;
-                    if (idx[k] >= 0) total = __fadd_rn(total, sh.wk[k]);
-                }
-                if (total > 0.0f) {
-                    const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
-                    const float inv_d = __fdiv_rn(1.0f, denom);
-                    for (int k = 0; k < K; k++) sh.wk[k] = __fmul_rn(sh.wk[k], inv_d);
-                }
-            }
+        if (unresolved) atomicAdd(&a.stats[GM_STAT_UNRESOLVED], 1ull);
+        float total = 0.0f;
+        for (int k = 0; k < K; k++) {
+            sh.idx[k] = idx[k];
+            sh.wk[k] = idx[k] >= 0 ? sh.u.s.p[idx[k]] : -1e30f;
+            if (idx[k] >= 0) total = __fadd_rn(total, sh.wk[k]);
+        }
+        if (total > 0.0f) {
+            const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
+            const float inv_d = __fdiv_rn(1.0f, denom);
+            for (int k = 0; k < K; k++) sh.wk[k] = __fmul_rn(sh.wk[k], inv_d);
         }
     }
     __syncthreads();
     if (tid < K) sh.ws[tid] = __fmul_rn(sh.wk[tid], a.routed_scale);
     __syncthreads();
-    sk_stamp(sh, 3);
-    return true;
 }
 
 // Observables of layer `layer` (top-k, weights, router probabilities), written through
@@ -429,6 +483,25 @@ __device__ static void sk_write_routing(const StackArgs &a, int layer, SkShared 
         st_f(a.hist_w + (size_t)layer * a.hist_stride + tid, sh.wk[tid]);
     }
     for (int i = tid; i < a.E; i += SK_BLOCK) st_f(a.router_prob + i, sh.u.s.p[i]);
+}
+
+// v[0..per) = p[0..per), v[per..) = 0, with the widest loads that `per` (a power of two
+// <= SK_PER_MAX, p aligned to 4 * per bytes) allows, all issued before any is used.
+template <typename P>
+__device__ static inline void load_seg(P p, int per, float *v) {
+    static_assert(SK_PER_MAX == 8, "load_seg covers segments of up to 8 floats");
+    if (per == 8) {
+        const float4 a0 = ((const float4 *)p)[0], a1 = ((const float4 *)p)[1];
+        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+        v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+    } else if (per == 4) {
+        const float4 a0 = ((const float4 *)p)[0];
+        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+        v[4] = v[5] = v[6] = v[7] = 0.0f;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = j < per ? p[j] : 0.0f;
+    }
 }
 
 // ---------------------------------------------------------------- router item
@@ -445,32 +518,24 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     const int lane = tid & 63, w = tid >> 6;
     const int per = D / SK_BLOCK;
     const int nx = (E - b + NR - 1) / NR;
-    // The norm and router weights do not depend on x: fetch them before waiting. Every
-    // load is unconditional (indices past the end are clamped, the values zeroed after),
-    // so they are all in flight at once.
+    // The norm and router weights do not depend on x: fetch them before waiting on x, but
+    // after the previous layer's expert items are done. A CU's vector memory path is
+    // shared by its two blocks, and these requests issued during the routed weight burst
+    // would queue the other block (an expert item) behind them for microseconds.
+    if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_PART)], 1u, a.error, sh)) return false;
     float nw[SK_PER_MAX], gw[SK_RX_MAX][SK_PER_MAX];
-    {
-        const GM_GLOBAL float *nrm = gbl(L.norm) + tid * per;
+    load_seg(gbl(L.norm) + tid * per, per, nw);
 #pragma unroll
-        for (int j = 0; j < SK_PER_MAX; j++) nw[j] = nrm[j < per ? j : 0];
+    for (int x = 0; x < SK_RX_MAX; x++) {
+        if (x < nx)  // block-uniform
+            load_seg(gbl(L.gate_inp) + (size_t)(b + x * NR) * D + tid * per, per, gw[x]);
+        else
 #pragma unroll
-        for (int x = 0; x < SK_RX_MAX; x++) {
-            const int e = b + (x < nx ? x : 0) * NR;
-            const GM_GLOBAL float *g = gbl(L.gate_inp) + (size_t)e * D + tid * per;
-#pragma unroll
-            for (int j = 0; j < SK_PER_MAX; j++) gw[x][j] = g[j < per ? j : 0];
-        }
-#pragma unroll
-        for (int x = 0; x < SK_RX_MAX; x++)
-#pragma unroll
-            for (int j = 0; j < SK_PER_MAX; j++) gw[x][j] = (x < nx && j < per) ? gw[x][j] : 0.0f;
+            for (int j = 0; j < SK_PER_MAX; j++) gw[x][j] = 0.0f;
     }
     if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_X)], 1u, a.error, sh)) return false;
-    const float *xsrc = (li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x)) + tid * per;
-
     float xv[SK_PER_MAX];
-#pragma unroll
-    for (int j = 0; j < SK_PER_MAX; j++) xv[j] = xsrc[j < per ? j : 0];
+    load_seg((li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x)) + tid * per, per, xv);
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < SK_PER_MAX; j++)
@@ -501,51 +566,16 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
 #pragma unroll
     for (int j = 0; j < SK_PER_MAX; j++) xv[j] = j < per ? __fmul_rn(__fmul_rn(xv[j], inv), nw[j]) : 0.0f;
 
+    float mloc = 0.0f;
 #pragma unroll
     for (int j = 0; j < SK_PER_MAX; j++)
-        if (j < per) sh.xn_r[tid * per + j] = xv[j];
-    __syncthreads();
-    // This block's share of xn and its digit form for the layer's expert items: 32-column
-    // blocks q = b, b + NR, ... (every router block holds all of xn). Thread t takes
-    // columns 8 (t % 4) .. +8 of block b + NR (t / 4); the four threads of a block agree
-    // on its exponent. The DIG flag covers these stores.
-    {
-        const int q = b + NR * (tid >> 2);
-        if (q < D / 32) {
-            int8_t *dig = ws_at<int8_t>(a, li, a.o.dig);
-            int *dexp = ws_at<int>(a, li, a.o.dexp);
-            float *wxn = ws_at<float>(a, li, a.o.xn);
-            const int i0 = 32 * q + 8 * (tid & 3);
-            float vals[8];
-            float mx = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                vals[j] = sh.xn_r[i0 + j];
-                mx = fmaxf(mx, fabsf(vals[j]));
-                st_f(a.xn + i0 + j, vals[j]);
-                st_f(wxn + i0 + j, vals[j]);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-            const int ex = digit_exponent(mx);
-            unsigned long long w0 = 0, w1 = 0, w2 = 0;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                int8_t d0, d1, d2;
-                split_digits(vals[j], ex, &d0, &d1, &d2);
-                w0 |= (unsigned long long)(uint8_t)d0 << (8 * j);
-                w1 |= (unsigned long long)(uint8_t)d1 << (8 * j);
-                w2 |= (unsigned long long)(uint8_t)d2 << (8 * j);
-            }
-            st_u64((unsigned long long *)(dig + i0), w0);
-            st_u64((unsigned long long *)(dig + D + i0), w1);
-            st_u64((unsigned long long *)(dig + 2 * D + i0), w2);
-            if ((tid & 3) == 0) st_i(dexp + q, ex);
+        if (j < per) {
+            sh.xn_r[tid * per + j] = xv[j];
+            mloc = fmaxf(mloc, fabsf(xv[j]));
         }
-    }
-    sk_stamp(sh, 12);
-
-    arrive(&a.ctr[SKC(SKC_DIG)], (unsigned)(li + 1) * NR, &a.ctr[SKF(li, SKF_DIG)]);
+    mloc = (float)wave_max_dpp((double)mloc);
+    if (lane == 0) sh.mxw[w] = mloc;
+    __syncthreads();
 
     // Products in fp64 are exact (24 + 24 bits). Pass 1: this thread's segment sums and
     // the block-wide exclusive prefix, in column order.
@@ -586,8 +616,10 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     }
     __syncthreads();
     sk_stamp(sh, 13);
-    if (tid < nx) {
-        const int x = tid, e = b + x * NR;
+    // The bound and the three sigmoids of each expert's entry (interval ends and p) on
+    // three lanes of wave 0, lane 3x + r for expert x.
+    if (tid < 64) {
+        const int x = tid / 3 < nx ? tid / 3 : 0, r = tid % 3, e = b + x * NR;
         const double S = ((sh.u.r.wv[0][x][0] + sh.u.r.wv[1][x][0]) + sh.u.r.wv[2][x][0]) + sh.u.r.wv[3][x][0];
         const double sp = ((sh.u.r.wv[0][x][1] + sh.u.r.wv[1][x][1]) + sh.u.r.wv[2][x][1]) + sh.u.r.wv[3][x][1];
         const double sa = ((sh.u.r.wv[0][x][2] + sh.u.r.wv[1][x][2]) + sh.u.r.wv[2][x][2]) + sh.u.r.wv[3][x][2];
@@ -598,42 +630,87 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
         // that, and each product adds u|p_k|
         double B = u * (1.0 + u) * sa + u * (sp + n * emax + u * sa);
         B = B * (1.0 + 0x1p-30) + 0x1p-40 * sa + n * 0x1p-149;
-        double lo, hi;
-        selection_interval(S, B, L.bias[e], &lo, &hi);
-        StageEnt *st = ws_at<StageEnt>(a, li, a.o.stage) + e;
-        st_d(&st->lo, lo);
-        st_d(&st->hi, hi);
-        st_f(&st->p, 1.0f / (1.0f + expf(-(float)S)));
+        const float arg = r == 0 ? __double2float_rd(S - B) : r == 1 ? __double2float_ru(S + B) : (float)S;
+        const float sg = 1.0f / (1.0f + expf(-arg));
+        const float phi = __shfl_down(sg, 1, 64), p = __shfl_down(sg, 2, 64);
+        if (r == 0 && tid / 3 < nx) {
+            double lo, hi;
+            selection_bounds((double)sg, (double)phi, L.bias[e], &lo, &hi);
+            float lo_f = __double2float_rd(lo), hi_f = __double2float_ru(hi);
+            if (!(lo_f <= hi_f)) {  // NaN: an interval that is never certified
+                lo_f = -INFINITY;
+                hi_f = INFINITY;
+            }
+            StageEnt *st = ws_at<StageEnt>(a, li, a.o.stage) + e;
+            st_u64(&st->w1, (unsigned long long)__float_as_uint(p));
+            st_u64(&st->w0, (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32));
+        }
     }
     sk_stamp(sh, 5);
-    // Count the arrival. The layer's last router block selects the top-k for every block,
-    // then publishes it with the SEL flag.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) sh.old = add_u(&a.ctr[SKC(SKC_ROUTER)]) + 1u == (unsigned)(li + 1) * NR;
-    __syncthreads();
-    if (sh.old) {
-        if (!sk_select_topk(a, L, li, sh)) return false;
-        if (tid < SK_SEL_WORDS) {
-            unsigned long long word = 0;
-            for (int q = 0; q < 4; q++) {
-                const int k = 4 * tid + q;
-                const unsigned v = k < a.K ? (unsigned)(sh.idx[k] + 2) : 1u;
-                word |= (unsigned long long)v << (16 * q);
+    // This block's share of xn and its digit form for the layer's expert items: 32-column
+    // blocks q = b, b + NR, ... (every router block holds all of xn). Thread t takes
+    // columns 8 (t % 4) .. +8 of block b + NR (t / 4). All of xn shares one exponent (from
+    // its max |xn|, which every router block finds alike), so that an expert item's block
+    // dots need only their weight scales. The DIG flag covers these stores.
+    {
+        const int ex = digit_exponent(fmaxf(fmaxf(sh.mxw[0], sh.mxw[1]), fmaxf(sh.mxw[2], sh.mxw[3])));
+        const int q = b + NR * (tid >> 2);
+        if (q < D / 32) {
+            int8_t *dig = ws_at<int8_t>(a, li, a.o.dig);
+            int *dexp = ws_at<int>(a, li, a.o.dexp);
+            float *wxn = ws_at<float>(a, li, a.o.xn);
+            const int i0 = 32 * q + 8 * (tid & 3);
+            float vals[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                vals[j] = sh.xn_r[i0 + j];
+                st_f(a.xn + i0 + j, vals[j]);
+                st_f(wxn + i0 + j, vals[j]);
             }
-            st_u64((unsigned long long *)&a.ctr[SKF(li, SKF_SEL) + 2 * tid], word);
+            unsigned long long w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                int8_t d0, d1, d2;
+                split_digits(vals[j], ex, &d0, &d1, &d2);
+                w0 |= (unsigned long long)(uint8_t)d0 << (8 * j);
+                w1 |= (unsigned long long)(uint8_t)d1 << (8 * j);
+                w2 |= (unsigned long long)(uint8_t)d2 << (8 * j);
+            }
+            st_u64((unsigned long long *)(dig + i0), w0);
+            st_u64((unsigned long long *)(dig + D + i0), w1);
+            st_u64((unsigned long long *)(dig + 2 * D + i0), w2);
+            if ((tid & 3) == 0) st_i(dexp + q, ex);
         }
-        sk_stamp(sh, 3);
-        // the weights (for the combine) and the observables follow under their own flag
-        float *ex_w = ws_at<float>(a, li, a.o.ex_w);
-        if (tid < a.K) st_f(ex_w + tid, sh.wk[tid]);
+    }
+    sk_stamp(sh, 12);
+    arrive(&a.ctr[SKC(SKC_DIG)], (unsigned)(li + 1) * NR, &a.ctr[SKF(li, SKF_DIG)]);
+
+    // Router block 0 also selects the top-k, writes the layer's observables, and when the
+    // selection is not certified replays the router exactly and publishes the result: the
+    // SEL words first (the routed blocks wait on them), then the weights under SELW.
+    if (b == 0) {
+        if (!sk_stage_select(a, li, true, sh)) return false;
+        if (!sh.sel_ok) {
+            sk_exact_select(a, L, sh);
+            if (tid < SK_SEL_WORDS) {
+                unsigned long long word = 0;
+                for (int q = 0; q < 4; q++) {
+                    const int k = 4 * tid + q;
+                    const unsigned v = k < a.K ? (unsigned)(sh.idx[k] + 2) : 1u;
+                    word |= (unsigned long long)v << (16 * q);
+                }
+                st_u64((unsigned long long *)&a.ctr[SKF(li, SKF_SEL) + 2 * tid], word);
+            }
+            float *ex_w = ws_at<float>(a, li, a.o.ex_w);
+            if (tid < a.K) st_f(ex_w + tid, sh.wk[tid]);
+        }
         sk_write_routing(a, layer, sh);
-        signal(&a.ctr[SKF(li, SKF_SELW)]);
+        if (!sh.sel_ok) signal(&a.ctr[SKF(li, SKF_SELW)]);
     }
     return true;
 }
 
-// The top-k of layer li from the SEL words, into sh.idx.
+// The top-k of layer li from the SEL words (published by the exact replay), into sh.idx.
 __device__ static inline bool sk_read_topk(const StackArgs &a, int li, SkShared &sh) {
     const int tid = threadIdx.x;
     if (tid == 0) {
@@ -661,8 +738,8 @@ __device__ static inline bool sk_read_topk(const StackArgs &a, int li, SkShared 
     return sh.ok != 0;
 }
 
-// The normalised weights of layer li's top-k (published after the SEL words), into
-// sh.wk / sh.ws.
+// The normalised weights of the exact replay's top-k (published after the SEL words),
+// into sh.wk / sh.ws.
 __device__ static inline bool sk_read_weights(const StackArgs &a, int li, SkShared &sh) {
     if (!wait_ge(&a.ctr[SKF(li, SKF_SELW)], 1u, a.error, sh)) return false;
     const int tid = threadIdx.x;
@@ -677,6 +754,50 @@ __device__ static inline bool sk_read_weights(const StackArgs &a, int li, SkShar
 
 // ---------------------------------------------------------------- expert item
 //
+// Gate and up rows [16j, 16j+16) of one expert dotted with xn, in units of 2^e where e is
+// the single exponent of xn's digit form `dig` ([3][cols] int8). Wave w takes the 64-column
+// chunks [w*cpw, (w+1)*cpw) held in `r`; each 32-column block is one MFMA per matrix (A =
+// the three digit rows, B = the 16 weight rows), whose int dots lanes 0..15 turn into their
+// row's fp32 block dot and scale by the block's fp16 scale (scg, scu: [16 rows][cols/32]).
+// Every operand is read before the first product, with no branches: chunks past cpw (cols
+// below 2048) get zero digits and zero scales. Lanes 0..15 return their row's sums.
+template <int NB>
+__device__ static inline void gu_products(const PanelRegs<2, NB> &r, int cols, const int8_t *dig,
+                                          const unsigned short *scg, const unsigned short *scu, float out[2]) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int cpw = cols >> 8, j0 = w * cpw, nblocks = cols >> 5;
+    const int m = lane & 15;
+    const int8_t *drow = dig + (m < 3 ? m : 0) * cols + 64 * j0 + 8 * (lane >> 4);
+    const unsigned *pg = (const unsigned *)(scg + m * nblocks + 2 * j0);
+    const unsigned *pu = (const unsigned *)(scu + m * nblocks + 2 * j0);
+    long A[NB][2];
+    unsigned sg[NB], su[NB];
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const bool on = u < cpw;
+        const long a0 = *(const long *)(drow + 64 * u), a1 = *(const long *)(drow + 64 * u + 32);
+        A[u][0] = (on && m < 3) ? a0 : 0;
+        A[u][1] = (on && m < 3) ? a1 : 0;
+        const unsigned g = pg[u], v = pu[u];
+        sg[u] = on ? g : 0u;
+        su[u] = on ? v : 0u;
+    }
+    float ag = 0.0f, au = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const v4i g0 = mfma_digits(A[u][0], chunk_half(r.q[0][u], 0));
+        const v4i g1 = mfma_digits(A[u][1], chunk_half(r.q[0][u], 1));
+        const v4i u0 = mfma_digits(A[u][0], chunk_half(r.q[1][u], 0));
+        const v4i u1 = mfma_digits(A[u][1], chunk_half(r.q[1][u], 1));
+        ag = fmaf(digits_to_float(g0[0], g0[1], g0[2]), __half2float(__ushort_as_half((unsigned short)(sg[u] & 0xffffu))), ag);
+        ag = fmaf(digits_to_float(g1[0], g1[1], g1[2]), __half2float(__ushort_as_half((unsigned short)(sg[u] >> 16))), ag);
+        au = fmaf(digits_to_float(u0[0], u0[1], u0[2]), __half2float(__ushort_as_half((unsigned short)(su[u] & 0xffffu))), au);
+        au = fmaf(digits_to_float(u1[0], u1[1], u1[2]), __half2float(__ushort_as_half((unsigned short)(su[u] >> 16))), au);
+    }
+    out[0] = ag;
+    out[1] = au;
+}
+
 // Rows [16j, 16j+16) of F for expert e in `slot` (-1: idle slot, nothing to compute):
 // g, u = gate, up rows . xn (infer.c:1184-1185, 1199-1200), h = silu(g) * u (:1188, :1202),
 // and the partial y = down[:, 16j..16j+16) . h over all D rows (:1190, :1205), stored at
@@ -719,8 +840,7 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
         __syncthreads();  // every wave's digits, scales and slice rows are in shared memory
         sk_stamp(sh, 6);
         float gu[2];
-        const unsigned short *scs[2] = {sh.sc_gu, sh.sc_gu + D / 2};
-        panel_compute_sc<2, EX_NB_MAX>(pr, D, sh.u.g.dig, sh.u.g.dexp, scs, gu);
+        gu_products<EX_NB_MAX>(pr, D, sh.u.g.dig, sh.sc_gu, sh.sc_gu + D / 2, gu);
         if (lane < 16) {
             sh.u.g.part[w][0][lane] = gu[0];
             sh.u.g.part[w][1][lane] = gu[1];
@@ -728,8 +848,9 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
         __syncthreads();
         if (tid < 16) {
             // SwiGLU of the 16 rows, then their digit form with one exponent
-            const float g = ((sh.u.g.part[0][0][tid] + sh.u.g.part[1][0][tid]) + sh.u.g.part[2][0][tid]) + sh.u.g.part[3][0][tid];
-            const float u = ((sh.u.g.part[0][1][tid] + sh.u.g.part[1][1][tid]) + sh.u.g.part[2][1][tid]) + sh.u.g.part[3][1][tid];
+            const int xe = sh.u.g.dexp[0];  // the exponent of all of xn's digits
+            const float g = ldexpf(((sh.u.g.part[0][0][tid] + sh.u.g.part[1][0][tid]) + sh.u.g.part[2][0][tid]) + sh.u.g.part[3][0][tid], xe);
+            const float u = ldexpf(((sh.u.g.part[0][1][tid] + sh.u.g.part[1][1][tid]) + sh.u.g.part[2][1][tid]) + sh.u.g.part[3][1][tid], xe);
             const float h = g / (1.0f + expf(-g)) * u;
             float mx = fabsf(h);
             mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
@@ -839,24 +960,38 @@ __device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs
         st_f(xo + r, __fadd_rn(xr, __fadd_rn(shv, acc)));
     }
     sk_stamp(sh, 5);
-    arrive(&a.ctr[SKC(SKC_X)], (unsigned)(li + 1) * (D / SK_CROWS), &a.ctr[SKF(li, SKF_X)]);
+    // two-level count of the layer's D/8 chunks, then the layer's flag
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned per_ctr = (unsigned)(D / SK_CROWS / SK_NPART);
+        if (add_u(&a.ctr[SKC(SKC_X + c % SK_NPART)]) + 1u == (unsigned)(li + 1) * per_ctr &&
+            add_u(&a.ctr[SKC(SKC_X2)]) + 1u == (unsigned)(li + 1) * SK_NPART)
+            st_u(&a.ctr[SKF(li, SKF_X)], 1u);
+    }
     return true;
 }
 
-// grid (n + 255) / 256
-__global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, int *error) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) ctr[i] = 0u;
-    if (i == 0) *error = 0;
+// Launch set-up, one block per layer plus one: block n_layers zeroes the counters; block
+// li puts layer li's stage entries to SK_UNSET.
+__global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, int *error, StackArgs a) {
+    const int li = blockIdx.x, tid = threadIdx.x;
+    if (li == a.n_layers) {
+        for (int i = tid; i < n; i += SK_BLOCK) ctr[i] = 0u;
+        if (tid == 0) *error = 0;
+        return;
+    }
+    unsigned long long *stage = ws_at<unsigned long long>(a, li, a.o.stage);
+    for (int i = tid; i < 2 * a.E; i += SK_BLOCK) stage[i] = SK_UNSET;
 }
 
-// Block roles: the first n_router blocks route; the next shared_blocks run the shared
-// expert's items, then wait until the layer's expert items are all done before taking the
-// next layer's (so its 10 MB of weights stream while the combine and the next router run,
-// not during the routed burst); the rest run the routed experts' items and then the
-// combine chunks. Router blocks go from one layer's router item straight to prefetching
-// the next layer's router rows. Trace items of one layer are numbered: n_router router
-// items, D/8 combine chunks, F/16 shared items, K*F/16 routed items (a block's top-k is
+// Block roles: the first n_router blocks route, and router blocks 1.. then take the shared
+// expert's items beyond the shared blocks' share; the next shared_blocks run one shared
+// item each, then wait until the layer's combine is done before taking the next layer's
+// (so its 10 MB of weights stream during the next router phase, not during the routed
+// burst or the combine's reads); the rest run the routed experts' items and then the
+// combine chunks. Trace items of one layer are numbered: n_router router items, D/8
+// combine chunks, F/16 shared items, K*F/16 routed items (a routed block's top-k is
 // stamped on its first expert item).
 __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
     __shared__ SkShared sh;
@@ -885,16 +1020,24 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
     } while (0)
         if (b < NR) {
             SK_ITEM(b, sk_router_item(a, L, layer, li, b, sh));
+            // shared items past the shared blocks' share go to router blocks 1.. (block 0
+            // also selects and writes the observables)
+            if (b > 0)
+                for (int j = NSB + b - 1; j < NPF; j += NR - 1) SK_ITEM(NR + NCH + j, sk_expert_item(a, L, li, K, j, a.E, sh));
         } else if (b < NR + NSB) {
             const int sb = b - NR;
-            for (int j = sb; j < NPF; j += NSB) SK_ITEM(NR + NCH + j, sk_expert_item(a, L, li, K, j, a.E, sh));
+            for (int j = sb; j < NPF; j += NSB) {
+                if (j >= NSB && NR > 1) break;  // the router blocks' share
+                SK_ITEM(NR + NCH + j, sk_expert_item(a, L, li, K, j, a.E, sh));
+            }
             sh.trace_item = base + NR + NCH + sb;
-            if (!wait_ge(&a.ctr[SKF(li, SKF_PART)], 1u, a.error, sh)) return;
+            if (!wait_ge(&a.ctr[SKF(li, SKF_X)], 1u, a.error, sh)) return;
         } else {
             const int wb = b - NR - NSB;
             if (wb < K * NPF && routed_on) {
-                sh.trace_item = base + NR + NCH + NPF + wb;  // stamp 8 of its first item
-                if (!sk_read_topk(a, li, sh)) return;
+                sh.trace_item = base + NR + NCH + NPF + wb;  // stamps 8 and 3 of its first item
+                if (!sk_stage_select(a, li, false, sh)) return;
+                if (!sh.sel_ok && !sk_read_topk(a, li, sh)) return;
             }
             for (int i = wb; i < K * NPF; i += NWB) {
                 const int slot = i / NPF;
@@ -903,7 +1046,7 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
             // combine chunks, by the blocks that hold this layer's routing
             const int ncb = NWB < K * NPF ? NWB : K * NPF;
             if (wb < ncb && wb < NCH) {
-                if (routed_on && !sk_read_weights(a, li, sh)) return;
+                if (routed_on && !sh.sel_ok && !sk_read_weights(a, li, sh)) return;
                 for (int c = wb; c < NCH; c += ncb) SK_ITEM(NR + c, sk_combine(a, li, c, routed_on, sh));
             }
         }
