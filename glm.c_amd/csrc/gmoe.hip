@@ -284,7 +284,8 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     }
     // The persistent decode kernel holds one panel's chunks per wave in registers and
     // xn in shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots.
-    c->stack_ok = c->L <= SK_MAX_LAYERS;
+    // (the combine stages a chunk's partials, F/16 x (K+1) x 8 floats, in the slice buffer)
+    c->stack_ok = c->L <= SK_MAX_LAYERS && (size_t)(F / 16) * (K + 1) * SK_CROWS * sizeof(float) <= sizeof(SkShared::dslice);
     const char *env = getenv("GMOE_STACK_KERNEL");
     if (env && env[0] == '0') c->stack_ok = 0;
     if (c->stack_ok) {

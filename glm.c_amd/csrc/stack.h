@@ -155,7 +155,8 @@ struct SkShared {
             int hexp;
         } g;
         struct {  // combine
-            float acc[SK_BLOCK / 64][GM_MAX_K + 1][SK_CROWS];
+            float acc[SK_BLOCK / (2 * SK_CROWS)][GM_MAX_K + 1][SK_CROWS];
+            float y[GM_MAX_K + 1][SK_CROWS];
         } c;
     } u;
     u32x4 dslice[GM_MAX_COLS];  // an expert item's down columns, D rows x 16 bytes
@@ -227,6 +228,15 @@ __device__ static inline float wave_max_dpp_f(float v) {
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
+// threadIdx.x, opaque to the optimiser. The phases of the layer loop take their thread
+// index from this, so that the many addresses derived from it are computed in the phase
+// that uses them rather than hoisted out of the loop and kept live (spilled) throughout.
+__device__ static inline int phase_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // Diagnostic stamp k of the current item (thread 0, when tracing).
 __device__ static inline void sk_stamp(SkShared &sh, int k) {
     if (sh.trace && threadIdx.x == 0) sh.trace[SK_TRACE_STAMPS * sh.trace_item + k] = wall_clock64();
@@ -269,7 +279,7 @@ template <int C>
 __device__ __attribute__((always_inline)) static void sk_select_rounds(const StackArgs &a, const unsigned long long *w0,
                                                                        const unsigned long long *w1, bool keep_p,
                                                                        SkShared &sh) {
-    const int E = a.E, K = a.K, tid = threadIdx.x;
+    const int E = a.E, K = a.K, tid = phase_tid();
     float lo[C], hi[C], pr[C], key[C];
     bool bad = false;
 #pragma unroll
@@ -338,7 +348,7 @@ __device__ __attribute__((always_inline)) static void sk_select_rounds(const Sta
 
 __device__ __attribute__((always_inline)) static bool sk_stage_select(const StackArgs &a, int li, bool keep_p,
                                                                       SkShared &sh) {
-    const int E = a.E, K = a.K, tid = threadIdx.x;
+    const int E = a.E, K = a.K, tid = phase_tid();
     if (tid < 64) {
         const StageEnt *stage = ws_at<StageEnt>(a, li, a.o.stage);
         const int nch = (E + 63) >> 6;
@@ -395,7 +405,7 @@ __device__ __attribute__((always_inline)) static bool sk_stage_select(const Stac
 // the router block whose xn is in sh.xn_r, when the certified selection failed: the top-k
 // into sh.idx / sh.wk / sh.ws and every probability into sh.u.s.p.
 __device__ static void sk_exact_select(const StackArgs &a, const StackLayer &L, SkShared &sh) {
-    const int D = a.D, E = a.E, K = a.K, tid = threadIdx.x;
+    const int D = a.D, E = a.E, K = a.K, tid = phase_tid();
     const GM_GLOBAL float *bias = gbl(L.bias);
     for (int i = tid; i < D; i += SK_BLOCK) sh.u.s.xn[i] = sh.xn_r[i];
     // infer.c:916-925 for every expert, 16 columns at a time: all threads form the
@@ -485,23 +495,29 @@ __device__ static void sk_write_routing(const StackArgs &a, int layer, SkShared 
     for (int i = tid; i < a.E; i += SK_BLOCK) st_f(a.router_prob + i, sh.u.s.p[i]);
 }
 
-// v[0..per) = p[0..per), v[per..) = 0, with the widest loads that `per` (a power of two
-// <= SK_PER_MAX, p aligned to 4 * per bytes) allows, all issued before any is used.
+// p[0..per) and zeros after, with the widest loads that `per` (a power of two <=
+// SK_PER_MAX, p aligned to 4 * per bytes) allows, returned by value so that it lives in
+// registers.
+struct Seg {
+    float v[SK_PER_MAX];
+};
 template <typename P>
-__device__ static inline void load_seg(P p, int per, float *v) {
+__device__ static inline Seg load_seg(P p, int per) {
     static_assert(SK_PER_MAX == 8, "load_seg covers segments of up to 8 floats");
+    Seg r;
     if (per == 8) {
         const float4 a0 = ((const float4 *)p)[0], a1 = ((const float4 *)p)[1];
-        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-        v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+        r.v[0] = a0.x; r.v[1] = a0.y; r.v[2] = a0.z; r.v[3] = a0.w;
+        r.v[4] = a1.x; r.v[5] = a1.y; r.v[6] = a1.z; r.v[7] = a1.w;
     } else if (per == 4) {
         const float4 a0 = ((const float4 *)p)[0];
-        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-        v[4] = v[5] = v[6] = v[7] = 0.0f;
+        r.v[0] = a0.x; r.v[1] = a0.y; r.v[2] = a0.z; r.v[3] = a0.w;
+        r.v[4] = r.v[5] = r.v[6] = r.v[7] = 0.0f;
     } else {
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = j < per ? p[j] : 0.0f;
+        for (int j = 0; j < 8; j++) r.v[j] = j < per ? p[j] : 0.0f;
     }
+    return r;
 }
 
 // ---------------------------------------------------------------- router item
@@ -514,7 +530,7 @@ __device__ static inline void load_seg(P p, int per, float *v) {
 // as its selection interval and probability.
 __device__ __attribute__((always_inline)) static bool sk_router_item(const StackArgs &a, const StackLayer &L, int layer,
                                                                      int li, int b, SkShared &sh) {
-    const int D = a.D, E = a.E, NR = a.n_router, tid = threadIdx.x;
+    const int D = a.D, E = a.E, NR = a.n_router, tid = phase_tid();
     const int lane = tid & 63, w = tid >> 6;
     const int per = D / SK_BLOCK;
     const int nx = (E - b + NR - 1) / NR;
@@ -523,19 +539,20 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     // shared by its two blocks, and these requests issued during the routed weight burst
     // would queue the other block (an expert item) behind them for microseconds.
     if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_PART)], 1u, a.error, sh)) return false;
-    float nw[SK_PER_MAX], gw[SK_RX_MAX][SK_PER_MAX];
-    load_seg(gbl(L.norm) + tid * per, per, nw);
+    const Seg nw = load_seg(gbl(L.norm) + tid * per, per);
+    Seg gw[SK_RX_MAX];
 #pragma unroll
     for (int x = 0; x < SK_RX_MAX; x++) {
-        if (x < nx)  // block-uniform
-            load_seg(gbl(L.gate_inp) + (size_t)(b + x * NR) * D + tid * per, per, gw[x]);
-        else
+        if (x < nx) {  // block-uniform
+            gw[x] = load_seg(gbl(L.gate_inp) + (size_t)(b + x * NR) * D + tid * per, per);
+        } else {
 #pragma unroll
-            for (int j = 0; j < SK_PER_MAX; j++) gw[x][j] = 0.0f;
+            for (int j = 0; j < SK_PER_MAX; j++) gw[x].v[j] = 0.0f;
+        }
     }
     if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_X)], 1u, a.error, sh)) return false;
-    float xv[SK_PER_MAX];
-    load_seg((li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x)) + tid * per, per, xv);
+    Seg xs = load_seg((li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x)) + tid * per, per);
+    float *xv = xs.v;
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < SK_PER_MAX; j++)
@@ -564,7 +581,7 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     }
     const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
 #pragma unroll
-    for (int j = 0; j < SK_PER_MAX; j++) xv[j] = j < per ? __fmul_rn(__fmul_rn(xv[j], inv), nw[j]) : 0.0f;
+    for (int j = 0; j < SK_PER_MAX; j++) xv[j] = j < per ? __fmul_rn(__fmul_rn(xv[j], inv), nw.v[j]) : 0.0f;
 
     float mloc = 0.0f;
 #pragma unroll
@@ -586,7 +603,7 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
         double s = 0.0, sa = 0.0;
 #pragma unroll
         for (int j = 0; j < SK_PER_MAX; j++) {
-            const double pj = (double)gw[x][j] * (double)xv[j];
+            const double pj = (double)gw[x].v[j] * (double)xv[j];
             s += pj;
             sa += fabs(pj);
         }
@@ -605,7 +622,7 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
         double run = off + pre[x], steps = 0.0;
 #pragma unroll
         for (int j = 0; j < SK_PER_MAX; j++) {
-            run += (double)gw[x][j] * (double)xv[j];
+            run += (double)gw[x].v[j] * (double)xv[j];
             steps += fabs(run);
         }
         const double sp = wave_sum_dpp(steps), sa = wave_sum_dpp(sabs[x]);
@@ -804,7 +821,7 @@ __device__ static inline void gu_products(const PanelRegs<2, NB> &r, int cols, c
 // ypart[slot][j]. Thread t owns the down rows t + 256 i.
 __device__ __attribute__((always_inline)) static bool sk_expert_item(const StackArgs &a, const StackLayer &L, int li,
                                                                      int slot, int j, int e, SkShared &sh) {
-    const int D = a.D, F = a.F, NPF = F >> 4, tid = threadIdx.x;
+    const int D = a.D, F = a.F, NPF = F >> 4, tid = phase_tid();
     if (e >= 0) {
         const uint8_t *base = L.experts + (size_t)e * a.stride;
         // Every weight of the item is requested before anything waits: the gate/up chunks to
@@ -872,9 +889,9 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
 #pragma unroll
         for (int q = 0; q < 12; q++) h4[q] = sh.u.g.hd[q];
         const int hexp = sh.u.g.hexp;
-        // partials in combine order: [D/8 chunks][K+1 slots][F/16][8 rows]
+        // partials in combine order: [D/8 chunks][F/16][K+1 slots][8 rows]
         const int NS = a.K + 1;
-        float *yp = ws_at<float>(a, li, a.o.ypart) + ((size_t)slot * NPF + j) * SK_CROWS + (tid & (SK_CROWS - 1));
+        float *yp = ws_at<float>(a, li, a.o.ypart) + ((size_t)j * NS + slot) * SK_CROWS + (tid & (SK_CROWS - 1));
 #pragma unroll
         for (int i = 0; i < SK_PER_MAX; i++) {
             if (i < c) {
@@ -912,48 +929,66 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
 //
 // Rows [8c, 8c+8) of x' = x + (shared + sum_k w_e * y_k) (infer.c:1192, 1212-1214),
 // with y_k the sum of expert k's F/16 partials in a fixed order. The chunk's partials
-// are one contiguous run ([slot][j][8 rows], 32 bytes per partial), copied to shared
-// memory with wide loads (as many slots per pass as fit). Thread t then sums the
-// partials j = g, g + 32, ... (g = t/8) of row t%8 for each slot, and 8 threads add the
-// 32 group sums in order and apply glm.c's combine order.
+// are one contiguous run ([j][slot][8 rows]), copied to shared memory with wide loads.
+// With P = 8 (K+1) (slot, row) pairs and Q = 256 / P groups, thread q P + p adds the
+// partials j = q, q + Q, ... of pair p in order; 8 threads then add the Q group sums in
+// order and apply glm.c's combine order.
 __device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs &a, int li, int c, bool routed_on,
                                                                  SkShared &sh) {
-    const int D = a.D, K = a.K, NS = K + 1, NPF = a.F >> 4, tid = threadIdx.x;
+    const int D = a.D, K = a.K, NS = K + 1, NPF = a.F >> 4, tid = phase_tid();
+    const int P = NS * SK_CROWS, Q = SK_BLOCK / P;
+    // the residual rows, fetched while the expert items finish
+    const int r = c * SK_CROWS + (tid & (SK_CROWS - 1));
+    const float xr = tid < SK_CROWS ? (li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x))[r] : 0.0f;
     if (!wait_ge(&a.ctr[SKF(li, SKF_PART)], 1u, a.error, sh)) return false;  // every expert item is done
-    const int rl = tid & (SK_CROWS - 1), g = tid / SK_CROWS;
-    const size_t slot_bytes = (size_t)NPF * SK_CROWS * sizeof(float);
-    const int per_pass = (int)(sizeof(sh.dslice) / slot_bytes);  // >= 2 for F <= 2048
-    const uint8_t *src = (const uint8_t *)(ws_at<float>(a, li, a.o.ypart) + (size_t)c * NS * NPF * SK_CROWS);
+    const uint8_t *src = (const uint8_t *)(ws_at<float>(a, li, a.o.ypart) + (size_t)c * NPF * P);
+    const int nbytes = NPF * P * (int)sizeof(float);  // <= sizeof(sh.dslice) for F <= 2048, K <= 8
+    dma_copy(sh.dslice, src, nbytes);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     const float *buf = (const float *)sh.dslice;
-    for (int k0 = 0; k0 < NS; k0 += per_pass) {
-        const int nk = NS - k0 < per_pass ? NS - k0 : per_pass;
-        __syncthreads();  // the previous pass's reads are done
-        dma_copy(sh.dslice, src + (size_t)k0 * slot_bytes, (int)(nk * slot_bytes));
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        for (int kk = 0; kk < nk; kk++) {
-            float s = 0.0f;
-            for (int jq = g; jq < NPF; jq += SK_CGROUPS) s += buf[((size_t)kk * NPF + jq) * SK_CROWS + rl];
-            // the wave's 8 groups of this row, in a fixed tree (lanes rl, rl + 8, ..., rl + 56)
-            s += __shfl_xor(s, 8, 64);
-            s += __shfl_xor(s, 16, 64);
-            s += __shfl_xor(s, 32, 64);
-            if ((tid & 63) < SK_CROWS) sh.u.c.acc[tid >> 6][k0 + kk][rl] = s;
+    // Shared-memory reads are issued eight at a time (clamped indices, masked values), so
+    // each batch costs one latency rather than eight.
+    if (tid < P * Q) {
+        const int q = tid / P, pr = tid - q * P;
+        float s = 0.0f;
+        for (int j0 = q; j0 < NPF; j0 += 8 * Q) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int jq = j0 + u * Q;
+                v[u] = buf[(jq < NPF ? jq : q) * P + pr];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (j0 + u * Q < NPF) s += v[u];
         }
+        sh.u.c.acc[q][pr / SK_CROWS][pr % SK_CROWS] = s;
+    }
+    __syncthreads();
+    if (tid < P) {  // each pair's Q group sums, in order
+        float v[SK_BLOCK / (2 * SK_CROWS)];
+#pragma unroll
+        for (int q = 0; q < SK_BLOCK / (2 * SK_CROWS); q++) v[q] = sh.u.c.acc[q < Q ? q : 0][tid / SK_CROWS][tid % SK_CROWS];
+        float y = v[0];
+#pragma unroll
+        for (int q = 1; q < SK_BLOCK / (2 * SK_CROWS); q++)
+            if (q < Q) y += v[q];
+        sh.u.c.y[tid / SK_CROWS][tid % SK_CROWS] = y;
     }
     __syncthreads();
     if (tid < SK_CROWS) {
-        const int r = c * SK_CROWS + rl;
+        const int rl = tid;
+        float y[GM_MAX_K + 1];
+#pragma unroll
+        for (int k = 0; k < GM_MAX_K + 1; k++) y[k] = sh.u.c.y[k < NS ? k : 0][rl];
         float acc = 0.0f;
         if (routed_on) {
-            for (int k = 0; k < K; k++) {
-                if (sh.idx[k] < 0) continue;
-                const float yk = ((sh.u.c.acc[0][k][rl] + sh.u.c.acc[1][k][rl]) + sh.u.c.acc[2][k][rl]) + sh.u.c.acc[3][k][rl];
-                acc = __fadd_rn(acc, __fmul_rn(sh.ws[k], yk));
-            }
+#pragma unroll
+            for (int k = 0; k < GM_MAX_K; k++)
+                if (k < K && sh.idx[k] >= 0) acc = __fadd_rn(acc, __fmul_rn(sh.ws[k], y[k]));
         }
-        const float shv = ((sh.u.c.acc[0][K][rl] + sh.u.c.acc[1][K][rl]) + sh.u.c.acc[2][K][rl]) + sh.u.c.acc[3][K][rl];
-        const float xr = (li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x))[r];
+        const float shv = sh.u.c.y[K][rl];
         st_f(a.routed_out + r, acc);
         st_f(a.shared_out + r, shv);
         float *xo = li == a.n_layers - 1 ? a.x_out : ws_at<float>(a, li + 1, a.o.x);
