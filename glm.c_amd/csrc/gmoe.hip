@@ -637,6 +637,7 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     ra.K = K;
     ra.eps = c->cfg.norm_eps;
     ra.routed_scale = c->cfg.routed_scale;
+    ra.force_exact = (flags & GMOE_FLAG_EXACT_ROUTER) != 0;
     ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_ROUTER);
     hipLaunchKernelGGL(k_norm_router, dim3(E, T), dim3(RT_BLOCK), (size_t)D * sizeof(float), st, ra);
     prof_end(pr, st);

@@ -37,6 +37,7 @@ struct RouterArgs {
     unsigned long long *stats; // [GM_STAT_COUNT]
     int D, E, K;
     float eps, routed_scale;
+    int force_exact;           // GMOE_FLAG_EXACT_ROUTER: skip the certificate, always replay
 };
 
 // (float) of the sequential fp64 mean of squares, decided from a parallel fp64 sum.
@@ -190,7 +191,7 @@ __global__ __launch_bounds__(RT_BLOCK) void k_norm_router(RouterArgs a) {
     if (tid < 64) {
         // K rounds of wave argmax over the midpoints; then check strict separation.
         unsigned long long taken = 0ull;  // bit i: lane-local candidate i taken (E <= 256 -> 4 per lane)
-        int ok = 1;
+        int ok = !a.force_exact;
         double prev_lo = 0.0;
         const int kk = K < E ? K : E;
         for (int k = 0; k < kk; k++) {

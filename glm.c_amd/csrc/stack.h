@@ -144,8 +144,6 @@ struct SkShared {
         } r;
         struct {  // top-k selection and its exact replay
             float p[GM_MAX_E], sel[GM_MAX_E];
-            float xn[GM_MAX_COLS];
-            float prod[64][17];  // products of 64 experts x 16 columns
         } s;
         struct {  // expert item
             int8_t dig[3 * GM_MAX_COLS];
@@ -270,6 +268,7 @@ __device__ static inline void dma_copy(void *dst, const void *src, int nbytes) {
 // replays the fp32 router exactly (sk_exact_select) and the others wait for its result.
 // Returns false if the wait timed out or another block failed; sh.sel_ok = certified.
 #define SK_SEL_C (GM_MAX_E / 64)
+#define SK_XT 128  // columns per tile of the exact router replay (prod tile = 32 KB)
 
 // The selection proper on wave 0, over C chunks of 64 experts whose stage words w0, w1
 // are in registers (lane l: experts l + 64c): the top-k into sh.idx / sh.wk (unscaled),
@@ -381,6 +380,7 @@ __device__ __attribute__((always_inline)) static bool sk_stage_select(const Stac
             sk_select_rounds<1>(a, w0, w1, keep_p, sh);
         else
             sk_select_rounds<SK_SEL_C>(a, w0, w1, keep_p, sh);
+        if (tid == 0 && (a.flags & GMOE_FLAG_EXACT_ROUTER)) sh.sel_ok = 0;
         if (tid == 0) sh.ok = alive;
     }
     __syncthreads();
@@ -407,74 +407,126 @@ __device__ __attribute__((always_inline)) static bool sk_stage_select(const Stac
 __device__ static void sk_exact_select(const StackArgs &a, const StackLayer &L, SkShared &sh) {
     const int D = a.D, E = a.E, K = a.K, tid = phase_tid();
     const GM_GLOBAL float *bias = gbl(L.bias);
-    for (int i = tid; i < D; i += SK_BLOCK) sh.u.s.xn[i] = sh.xn_r[i];
-    // infer.c:916-925 for every expert, 16 columns at a time: all threads form the
-    // products fl(g * xn), then lane e adds its expert's 16 in order.
-    float chain[GM_MAX_E / 64];
-    for (int c = 0; c < GM_MAX_E / 64; c++) chain[c] = 0.0f;
-    const GM_GLOBAL float *gi = gbl(L.gate_inp);
+    // infer.c:916-925 for 64 experts at a time, in tiles of SK_XT columns: every thread
+    // forms the products fl(g * xn) of one expert (its lane) and a quarter of the tile's
+    // columns (its wave) into prod[column][expert], then lane e of wave 0 adds its
+    // expert's products in column order. Each thread's gate rows are fetched two tiles
+    // ahead into registers, so the loads overlap the chain.
+    float(*prod)[64] = (float(*)[64])sh.dslice;  // [SK_XT][64]
+    const int lane = tid & 63, w = tid >> 6, qc = SK_XT / 4;  // columns per wave and tile
+    const int ntile = D / SK_XT;
     for (int eb = 0; eb < E; eb += 64) {
         const int ne = E - eb < 64 ? E - eb : 64;
-        for (int c0 = 0; c0 < D; c0 += 16) {
-            __syncthreads();
-            for (int i = tid; i < ne * 16; i += SK_BLOCK) {
-                const int er = i >> 4, cc = i & 15;
-                sh.u.s.prod[er][cc] = __fmul_rn(gi[(size_t)(eb + er) * D + c0 + cc], sh.u.s.xn[c0 + cc]);
+        const float4 *grow = (const float4 *)(L.gate_inp + (size_t)(eb + (lane < ne ? lane : 0)) * D + w * qc);
+        float4 ga[SK_XT / 16], gb[SK_XT / 16];
+#pragma unroll
+        for (int q = 0; q < SK_XT / 16; q++) ga[q] = grow[q];
+#pragma unroll
+        for (int q = 0; q < SK_XT / 16; q++) gb[q] = grow[SK_XT / 4 + q];
+        float chain = 0.0f;
+        // one tile from registers g (tile t), then g refilled with tile t + 2
+        auto tile = [&](float4 *g, int t) {
+            const int c0 = t * SK_XT + w * qc;
+#pragma unroll
+            for (int q = 0; q < SK_XT / 16; q++) {
+                const float4 xq = *(const float4 *)&sh.xn_r[c0 + 4 * q];
+                prod[w * qc + 4 * q + 0][lane] = __fmul_rn(g[q].x, xq.x);
+                prod[w * qc + 4 * q + 1][lane] = __fmul_rn(g[q].y, xq.y);
+                prod[w * qc + 4 * q + 2][lane] = __fmul_rn(g[q].z, xq.z);
+                prod[w * qc + 4 * q + 3][lane] = __fmul_rn(g[q].w, xq.w);
             }
             __syncthreads();
-            if (tid < ne) {
-                float acc = chain[eb >> 6];
-                for (int cc = 0; cc < 16; cc++) acc = __fadd_rn(acc, sh.u.s.prod[tid][cc]);
-                chain[eb >> 6] = acc;
+            if (t + 2 < ntile)
+#pragma unroll
+                for (int q = 0; q < SK_XT / 16; q++) g[q] = grow[(t + 2) * (SK_XT / 4) + q];
+            if (w == 0) {
+                for (int c0 = 0; c0 < SK_XT; c0 += 16) {
+                    float v[16];  // sixteen reads in flight, then the sixteen dependent adds
+#pragma unroll
+                    for (int j = 0; j < 16; j++) v[j] = prod[c0 + j][lane];
+#pragma unroll
+                    for (int j = 0; j < 16; j++) chain = __fadd_rn(chain, v[j]);
+                }
             }
+            __syncthreads();
+        };
+        for (int t = 0; t < ntile; t += 2) {  // ntile = D / 128 is even
+            tile(ga, t);
+            tile(gb, t + 1);
         }
-        __syncthreads();
         if (tid < ne) {
-            const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain[eb >> 6])));
+            const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain)));
             sh.u.s.p[eb + tid] = pr;
             sh.u.s.sel[eb + tid] = __fadd_rn(pr, bias[eb + tid]);
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        atomicAdd(&a.stats[GM_STAT_ROUTE_EXACT], 1ull);
-        int idx[GM_MAX_K];
-        for (int k = 0; k < K; k++) idx[k] = -1;
-        for (int i = 0; i < E; i++) {
-            const float sc = sh.u.s.sel[i];
-            int at = -1;
-            for (int k = 0; k < K && at < 0; k++) {
-                const float held = idx[k] >= 0 ? sh.u.s.sel[idx[k]] : -INFINITY;
-                if (sc > held) at = k;
-            }
-            if (at < 0) continue;
-            for (int k = K - 1; k > at; k--) idx[k] = idx[k - 1];
-            idx[at] = i;
+    // glm.c's insertion top-k (infer.c:1110-1135) keeps the K largest sel by (value desc,
+    // index asc) among values above -inf (NaN is never inserted): K wave-maximum rounds,
+    // the lowest lane winning ties, chunk c of lane l holding expert l + 64c.
+    if (w == 0) {
+        const int nch = (E + 63) >> 6;
+        float key[SK_SEL_C], pv[SK_SEL_C];
+#pragma unroll
+        for (int c = 0; c < SK_SEL_C; c++) {
+            const int e = lane + 64 * c;
+            const bool valid = c < nch && e < E;
+            const float v = valid ? sh.u.s.sel[e] : -INFINITY;
+            key[c] = v == v ? v : -INFINITY;
+            pv[c] = valid ? sh.u.s.p[e] : 0.0f;
         }
-        // libm's expf may differ from the GPU's by an ulp: flag orders decided that closely
-        int unresolved = 0;
-        for (int k = 0; k < K; k++) {
-            if (idx[k] < 0) continue;
-            const float a0 = sh.u.s.sel[idx[k]];
-            const float tol = 4.0f * fmaxf(fabsf(a0), 1e-30f) * 0x1p-23f + 4.0f * 0x1p-24f;
-            for (int i = 0; i < E; i++) {
-                if (i == idx[k]) continue;
-                bool above = false;
-                for (int q = 0; q < k; q++) above |= (idx[q] == i);
-                if (!above && fabsf(sh.u.s.sel[i] - a0) <= tol) unresolved = 1;
-            }
-        }
-        if (unresolved) atomicAdd(&a.stats[GM_STAT_UNRESOLVED], 1ull);
         float total = 0.0f;
+        bool unresolved = false;
         for (int k = 0; k < K; k++) {
-            sh.idx[k] = idx[k];
-            sh.wk[k] = idx[k] >= 0 ? sh.u.s.p[idx[k]] : -1e30f;
-            if (idx[k] >= 0) total = __fadd_rn(total, sh.wk[k]);
+            float bm = key[0];
+#pragma unroll
+            for (int c = 1; c < SK_SEL_C; c++) bm = fmaxf(bm, key[c]);
+            const float gm = wave_max_dpp_f(bm);
+            int ek = -1;
+            float wk = -1e30f;
+            if (gm > -INFINITY) {
+                // the lowest expert index holding the maximum: chunks in index order
+                int ls = -1, cs = 0;
+#pragma unroll
+                for (int c = 0; c < SK_SEL_C; c++) {
+                    const unsigned long long m = __ballot(key[c] == gm);
+                    if (ls < 0 && m != 0ull) {
+                        ls = __ffsll(m) - 1;
+                        cs = c;
+                    }
+                }
+                float mp = pv[0];
+#pragma unroll
+                for (int c = 1; c < SK_SEL_C; c++)
+                    if (cs == c) mp = pv[c];
+                ek = ls + 64 * cs;
+                wk = readlane_f(mp, ls);
+                total = __fadd_rn(total, wk);
+#pragma unroll
+                for (int c = 0; c < SK_SEL_C; c++)
+                    if (lane == ls && c == cs) key[c] = -INFINITY;
+                // libm's expf may differ from the GPU's by an ulp: flag orders decided that
+                // closely (any expert not yet chosen within a few ulps of this one)
+                const float tol = 4.0f * fmaxf(fabsf(gm), 1e-30f) * 0x1p-23f + 4.0f * 0x1p-24f;
+                bool close = false;
+#pragma unroll
+                for (int c = 0; c < SK_SEL_C; c++) close |= key[c] > -INFINITY && fabsf(key[c] - gm) <= tol;
+                unresolved |= __ballot(close) != 0;
+            }
+            if (lane == 0) {
+                sh.idx[k] = ek;
+                sh.wk[k] = wk;
+            }
         }
-        if (total > 0.0f) {
-            const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
-            const float inv_d = __fdiv_rn(1.0f, denom);
-            for (int k = 0; k < K; k++) sh.wk[k] = __fmul_rn(sh.wk[k], inv_d);
+        if (lane == 0) {
+            atomicAdd(&a.stats[GM_STAT_ROUTE_EXACT], 1ull);
+            if (unresolved) atomicAdd(&a.stats[GM_STAT_UNRESOLVED], 1ull);
+            if (total > 0.0f) {
+                // normalisation of infer.c:1136-1145
+                const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
+                const float inv_d = __fdiv_rn(1.0f, denom);
+                for (int k = 0; k < K; k++) sh.wk[k] = __fmul_rn(sh.wk[k], inv_d);
+            }
         }
     }
     __syncthreads();
@@ -1044,7 +1096,7 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
         const StackLayer L = a.layers[li];
         const int layer = a.first_layer + li;
         const long base = (long)li * per_layer;
-        const bool routed_on = !(a.flags & 1) && L.has_routed;
+        const bool routed_on = !(a.flags & GMOE_FLAG_NO_ROUTED) && L.has_routed;
 #define SK_ITEM(idx, call)                                                                    \
     do {                                                                                      \
         sh.trace_item = base + (idx);                                                         \

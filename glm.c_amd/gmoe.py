@@ -19,6 +19,7 @@ LIBGMOE = os.environ.get("GMOE_LIBRARY", os.path.join(HERE, "libgmoe.so"))
 LIBHOST = os.path.join(HERE, "libglm_hip.so")
 
 GMOE_FLAG_NO_ROUTED = 1
+GMOE_FLAG_EXACT_ROUTER = 2
 SYNTH_NORM_ONES, SYNTH_NORM_RANDOM = 0, 1
 SYNTH_BIAS_NORMAL, SYNTH_BIAS_ZIPF = 0, 1
 

@@ -37,6 +37,8 @@ extern "C" {
 
 /* forward() flags */
 #define GMOE_FLAG_NO_ROUTED 1   /* skip routed experts, as GLM_DISABLE_MOE_ROUTED=1 does (infer.c:1161-1166) */
+#define GMOE_FLAG_EXACT_ROUTER 2 /* always replay glm.c's fp32 router chain (infer.c:916-938) instead of
+                                    certifying the fast fp64 result: same routing, slower; for validation */
 
 typedef struct gmoe_ctx gmoe_ctx;
 

@@ -90,3 +90,34 @@ def test_layered_kernels_match_stack_kernel(stack, monkeypatch):
     np.testing.assert_array_equal(sa["topk_idx"], sb["topk_idx"])
     assert np.array_equal(sa["xn"].view(np.uint32), sb["xn"].view(np.uint32))
     assert_close(a, b, "stack vs layered x_out", max_abs=1e-3, rel_l2=1e-5)
+
+
+def test_forced_exact_router_matches_oracle(stack):
+    """GMOE_FLAG_EXACT_ROUTER skips the certificate, so every layer takes the exact fp32
+    replay of the router; routing and outputs must still match the oracle, and the
+    one-launch stack must equal the certified run's routing."""
+    shape, layers, ctx = stack
+    x0 = gmoe.activations(11, 3, 1, shape.D)
+    orc = oracle.Oracle("port")
+    before = ctx.stats()["routing_exact_path"]
+    x = x0.copy()
+    for l in range(1, N_LAYERS + 1):
+        print(f"[case] forced exact router, layer {l}", flush=True)
+        want = orc.layer(shape, layers[l - 1], x)
+        got, st = gmoe.forward_host(ctx, l, x, flags=gmoe.GMOE_FLAG_EXACT_ROUTER)
+        np.testing.assert_array_equal(st["topk_idx"], want["topk_idx"], err_msg=f"layer {l} routing")
+        # the replayed chain is glm.c's; only expf may differ by an ulp from glibc's
+        assert_close(st["router_prob"], want["router_prob"], f"layer {l} router_prob", max_abs=1.2e-7, rel_l2=1e-7)
+        assert_close(st["topk_w"], want["topk_w"], f"layer {l} topk_w", max_abs=1e-6, rel_l2=1e-6)
+        assert_close(got, want["x_out"], f"layer {l} x_out")
+        x = got
+    assert ctx.stats()["routing_exact_path"] - before == N_LAYERS
+    # the whole stack in one launch, forced exact, routes as the certified launch does
+    d_in = gmoe.DeviceArray.from_numpy(x0)
+    d_out = gmoe.DeviceArray(x0.nbytes)
+    ctx.forward_layers(1, N_LAYERS, 1, d_in.ptr, d_out.ptr, flags=gmoe.GMOE_FLAG_EXACT_ROUTER)
+    exact_topk = [ctx.read_topk(l, 1)[0] for l in range(1, N_LAYERS + 1)]
+    ctx.forward_layers(1, N_LAYERS, 1, d_in.ptr, d_out.ptr)
+    cert_topk = [ctx.read_topk(l, 1)[0] for l in range(1, N_LAYERS + 1)]
+    for l in range(N_LAYERS):
+        np.testing.assert_array_equal(exact_topk[l], cert_topk[l], err_msg=f"layer {l + 1}")
