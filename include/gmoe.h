@@ -154,15 +154,16 @@ int gmoe_profile_read(gmoe_ctx *ctx, gmoe_kernel_times *out);
 
 /* Diagnostic timeline of the persistent decode kernel. While enabled, every work
  * item of a T=1 launch records GMOE_TRACE_STAMPS 100 MHz wall-clock stamps (0 where a
- * stage does not apply): 0 picked up, 1 inputs ready, 2 done, 3 top-k known,
- * 4 products done, 5 results stored, 6 activations staged, 7 counter published,
- * 8 router results visible, 11 norm reduced, 12 activation digits published,
- * 13 logits done. Items of one layer are numbered ceil(E/4) router items, F/16
- * shared-expert gate/up items, D/16 shared-expert down items, K*F/16 routed gate/up
- * items, then K*D/16 routed down items; layer after layer. The routed role's
- * per-layer top-k is stamped on its first item of the layer. gmoe_trace_items_read
- * copies the most recent launch's stamps ([n][GMOE_TRACE_STAMPS]) and returns n, or
- * a negative error. Measurement aid only: stamping slows the kernel slightly. */
+ * stage does not apply): 0 picked up, 1 inputs ready (x, the expert items' completion,
+ * or the combine's previous wait), 2 done, 3 top-k known, 4 h computed, 5 results
+ * stored, 6 item weights and activations staged, 8 router results visible,
+ * 11 norm reduced, 12 activation digits published, 13 logits done. Items of one
+ * layer are numbered: n_router router items (min(E, 64) rounded down to a power of
+ * two), D/8 combine chunks, F/16 shared-expert items, then K*F/16 routed items; layer
+ * after layer. A routed block's per-layer top-k (stamps 8 and 3) is stamped on its
+ * first item of the layer. gmoe_trace_items_read copies the most recent launch's
+ * stamps ([n][GMOE_TRACE_STAMPS]) and returns n, or a negative error. Measurement
+ * aid only: stamping slows the kernel slightly. */
 #define GMOE_TRACE_STAMPS 16
 int gmoe_trace_items(gmoe_ctx *ctx, int enable);
 int64_t gmoe_trace_items_read(gmoe_ctx *ctx, uint64_t *out, int64_t max_items);
