@@ -95,6 +95,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (calibrates the PMC byte counters)")
+    ap.add_argument("--prefill", type=int, default=0, metavar="T",
+                    help="instead of decode, time one MoE layer over T tokens (the grouped expert GEMM path)")
+    ap.add_argument("--zipf", action="store_true", help="with --prefill: Zipf(1.2)-skewed router bias")
+    ap.add_argument("--prefill-layers", type=int, default=8, help="with --prefill: seeded layers rotated through")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -115,6 +119,9 @@ def main():
         gmoe.hip_check(gmoe.hip().hipDeviceSynchronize(), "sync")
         print(json.dumps({"copy_probe_bytes": n, "copies": 5}), flush=True)
         return
+
+    if args.prefill:
+        return prefill(args, gmoe, np)
 
     shape = gmoe.GLM47_FLASH
     L = args.layers
@@ -175,7 +182,7 @@ def main():
         raise SystemExit("--profile-steps must be at least 1: the roofline needs the kernel's launch time")
     K1 = shape.K + 1
     mat = shape.F * shape.D * 34 // 32
-    kernel_bytes = {"k_gate_up": K1 * 2 * mat, "k_down_combine": K1 * mat, "k_moe_stack": bytes_per_token}
+    kernel_bytes = {"gate_up": K1 * 2 * mat, "down": K1 * mat, "k_moe_stack": bytes_per_token}
     dom = max(prof, key=lambda k: prof[k][1])
     kernels = {k: {"launches": n, "avg_us": ms * 1e3 / n} for k, (n, ms) in prof.items()}
     for k in kernels:
@@ -220,6 +227,109 @@ def main():
         "cpu_baseline": cpu,
         "routing_stats": stats,
         "expert_bytes_last_layer": per_layer_bytes,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+
+
+def prefill(args, gmoe, np):
+    """One MoE layer over T tokens (SURVEY configs 3 and 4): router, dispatch, grouped
+    gate/up and down GEMMs, combine. Steps rotate over --prefill-layers seeded layers so
+    that no layer's 650 MB of touched experts is still cached from the step before."""
+    shape = gmoe.GLM47_FLASH
+    T, NL = args.prefill, args.prefill_layers
+    bias = gmoe.SYNTH_BIAS_ZIPF if args.zipf else gmoe.SYNTH_BIAS_NORMAL
+    t0 = time.perf_counter()
+    ctx = gmoe.Context(shape, n_layers=NL + 1, max_tokens=T, device=0)
+    host_layers = []
+    for layer in range(1, NL + 1):
+        hl = gmoe.HostLayer(shape, seed=0, layer=layer, bias_mode=bias)
+        ctx.upload(layer, hl)
+        host_layers.append(hl if layer == 1 else None)
+    log(f"generated and uploaded {NL} layers in {time.perf_counter() - t0:.1f}s")
+    x0 = gmoe.activations(0, 1, T, shape.D)
+    d_in = gmoe.DeviceArray.from_numpy(x0)
+    d_out = gmoe.DeviceArray(x0.nbytes)
+    stream = gmoe.Stream()
+    it = [0]
+
+    def step():
+        ctx.forward(1 + it[0] % NL, T, d_in.ptr, d_out.ptr, stream=stream.h)
+        it[0] += 1
+
+    for _ in range(args.warmup):
+        step()
+    stream.sync()
+    t_begin = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    stream.sync()
+    elapsed = time.perf_counter() - t_begin
+    layer_us = elapsed * 1e6 / args.steps
+    # touched experts and routed pairs of every layer (lists are exact, so this is what was read)
+    touched, pairs = [], []
+    for layer in range(1, NL + 1):
+        _, st = gmoe.forward_host(ctx, layer, x0)
+        counts = np.diff(st["expert_offsets"])
+        touched.append(int(np.sum(counts > 0)) + 1)
+        pairs.append(int(counts.sum()) + T)
+    bytes_per_layer = float(np.mean(touched)) * shape.expert_bytes()
+    macs = float(np.mean(pairs)) * 3 * shape.F * shape.D
+    ctx.profile(True)
+    for _ in range(args.profile_steps):
+        step()
+    stream.sync()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    kernels = {k: {"launches": n, "avg_us": round(ms * 1e3 / n, 3)} for k, (n, ms) in prof.items()}
+    # per layer: one gate/up and one down launch
+    gemm_us = sum(kernels[k]["avg_us"] for k in ("gate_up", "down") if k in kernels)
+    tflops = 2.0 * macs / (gemm_us * 1e-6) / 1e12 if gemm_us else 0.0
+    gbs = bytes_per_layer / (layer_us * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        kind = "reference" if oracle.available("reference") else "port"
+        orc = oracle.Oracle(kind)
+        n = min(T, 32)
+        orc.layer(shape, host_layers[0], x0[:2])
+        t_c = time.perf_counter()
+        orc.layer(shape, host_layers[0], x0[:n])
+        dt = time.perf_counter() - t_c
+        cpu = {"value": round(n / dt, 2), "unit": "tokens/s", "cores": omp_threads(), "kind": kind,
+               "sample": f"{n} of the {T} tokens through layer 1 (glm.c routes prefill tokens one at a time, "
+                         f"infer.c:2190-2233), wall clock",
+               "layer_us_for_T": round(dt / n * T * 1e6, 1)}
+    name = f"T={T}" + (" Zipf(1.2) routing" if args.zipf else "")
+    out = {
+        "metric": f"MoE-layer prefill tokens/s ({name}, GLM-4.7-Flash shape, Q8_0, grouped expert GEMM)",
+        "value": round(T / (layer_us * 1e-6), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(layer_us * 1e-3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 x (int8 as fp16) MFMA, fp32 accumulate (activations as fp16 hi+lo)",
+        "data": "synthetic (seeded random-init Q8_0 weights, N(0,1) input)",
+        "config": {"workload": f"one GLM-4.7-Flash MoE layer, prefill {name}", "tokens": T, "layers_rotated": NL,
+                   "dim": shape.D, "moe_ffn_dim": shape.F, "experts": shape.E, "top_k": shape.K, "shared_experts": 1},
+        "layer_us": round(layer_us, 2),
+        "touched_experts": round(float(np.mean(touched)), 2),
+        "hbm_gbps_touched_bytes": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "mfma": {"algorithmic_tflops": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                 "note": "algorithmic 2*MACs of the expert products over the two grouped GEMM kernels' time; the "
+                         "kernels execute 2x those MACs (hi and lo planes) plus tile padding"},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "routing_stats": ctx.stats(),
     }
     print(json.dumps(out), flush=True)
     ctx.close()

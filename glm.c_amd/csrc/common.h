@@ -119,6 +119,15 @@ __device__ static inline float readlane_f(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Maximum over the 64 lanes of a wave, returned to every lane (wave-uniform), by DPP.
+__device__ static inline float wave_max_dpp_f(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_QUAD_1032, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_QUAD_2301, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_ROW_HALF_MIRROR, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_ROW_MIRROR, 0xF, 0xF, false)));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
 // Inclusive prefix sum over the lanes of a wave, in lane order.
 __device__ static inline double wave_incl_scan_dpp(double v) {
     v += dpp_d<DPP_ROW_SHR(1)>(v, 0.0);
@@ -211,6 +220,22 @@ __device__ static inline void split_digits(float v, int e, int8_t *d0, int8_t *d
     *d0 = (int8_t)a0;
     *d1 = (int8_t)a1;
     *d2 = (int8_t)a2;
+}
+
+// Two-digit form for the prefill kernels: X = rint(v * 2^-e) with |X| <= 32639, so that
+// X = d0 + 256 d1 with balanced int8 digits (d0 in [-128, 127], d1 in [-128, 127]).
+__device__ static inline int digit_exponent2(float maxabs) {
+    if (!(maxabs > 0.0f) || !isfinite(maxabs)) return 0;
+    int k;
+    const float m = frexpf(maxabs, &k);  // maxabs = m * 2^k, m in [0.5, 1)
+    return (m * 32768.0f <= 32639.0f) ? k - 15 : k - 14;
+}
+
+__device__ static inline void split_digits2(float v, int e, int8_t *d0, int8_t *d1) {
+    const int X = (int)rintf(ldexpf(v, -e));
+    const int a0 = ((X + 128) & 255) - 128;
+    *d0 = (int8_t)a0;
+    *d1 = (int8_t)((X - a0) >> 8);
 }
 
 // fp32 value of D0 + 256*D1 + 65536*D2 for int32 digit dots (|Di| < 2^20).

@@ -9,9 +9,22 @@
 
 #include "common.h"
 
+#define GP_TOK 32  // tokens per tile of the prefill grouped GEMMs
+
+// One tile of a grouped GEMM: list rows [row, row + count) of expert e (e == E: the
+// shared expert, whose list is every token, at rows TK + t).
+struct GpTile {
+    int e, row, count, pad;
+};
+
 struct DispatchArgs {
     const int *topk_idx;  // [T][K]
     int T, K, E;
+    int TK;               // list rows reserved for routed pairs (Tmax * K); shared rows follow
+    int routed_on, shared_on;
+    GpTile *tiles;        // out: routed experts' tiles in expert order, then the shared expert's
+    int *n_tiles;
+    int *pair_row;        // out: [T][K] list row of (token, slot), -1 if the slot is empty
     int *tmp_tok;         // [E][T]
     int *tmp_slot;        // [E][T]
     int *counts;          // [E]
@@ -69,11 +82,48 @@ __global__ __launch_bounds__(DP_BLOCK) void k_dispatch(DispatchArgs a) {
         a.offsets[a.E] = off;
     }
     __syncthreads();
-    for (int q = 0; q < a.E; q++) {
-        const int n = s_off[q + 1] - s_off[q];
-        for (int i = tid; i < n; i += DP_BLOCK) {
-            a.tokens[s_off[q] + i] = a.tmp_tok[(size_t)q * a.T + i];
-            a.slots[s_off[q] + i] = a.tmp_slot[(size_t)q * a.T + i];
+    for (int i = tid; i < a.T * a.K; i += DP_BLOCK) a.pair_row[i] = -1;
+    __syncthreads();
+    // pack: every thread takes up to 8 list positions at a time, all of whose loads are
+    // issued together (the position's expert comes from a binary search of the offsets)
+    const int listed = s_off[a.E];
+    for (int base = 0; base < listed; base += DP_BLOCK * 8) {
+        int tk[8], sk[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int pos = base + u * DP_BLOCK + tid;
+            tk[u] = sk[u] = 0;
+            if (pos < listed) {
+                int lo = 0, hi = a.E;  // s_off[lo] <= pos < s_off[hi]
+                while (hi - lo > 1) {
+                    const int mid = (lo + hi) >> 1;
+                    if (s_off[mid] <= pos) lo = mid;
+                    else hi = mid;
+                }
+                tk[u] = a.tmp_tok[(size_t)lo * a.T + (pos - s_off[lo])];
+                sk[u] = a.tmp_slot[(size_t)lo * a.T + (pos - s_off[lo])];
+            }
         }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int pos = base + u * DP_BLOCK + tid;
+            if (pos < listed) {
+                a.tokens[pos] = tk[u];
+                a.slots[pos] = sk[u];
+                a.pair_row[tk[u] * a.K + sk[u]] = pos;
+            }
+        }
+    }
+    if (tid == 0) {
+        int nt = 0;
+        if (a.routed_on)
+            for (int q = 0; q < a.E; q++)
+                for (int s = 0; s < s_off[q + 1] - s_off[q]; s += GP_TOK) {
+                    const int n = s_off[q + 1] - s_off[q] - s;
+                    a.tiles[nt++] = GpTile{q, s_off[q] + s, n < GP_TOK ? n : GP_TOK, 0};
+                }
+        if (a.shared_on)
+            for (int s = 0; s < a.T; s += GP_TOK) a.tiles[nt++] = GpTile{a.E, a.TK + s, a.T - s < GP_TOK ? a.T - s : GP_TOK, 0};
+        *a.n_tiles = nt;
     }
 }

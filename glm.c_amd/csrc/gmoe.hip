@@ -18,6 +18,7 @@
 #include "common.h"
 #include "dispatch.h"
 #include "experts.h"
+#include "grouped.h"
 #include "repack.h"
 #include "router.h"
 #include "stack.h"
@@ -83,12 +84,19 @@ struct gmoe_ctx {
     unsigned *tok_counter = nullptr, *panel_counter = nullptr, *disp_counter = nullptr;
     int *disp_tmp_tok = nullptr, *disp_tmp_slot = nullptr, *disp_counts = nullptr;
     int *offsets = nullptr, *tokens = nullptr, *slots = nullptr;
+    // prefill grouped GEMMs (grouped.h): list rows are [Tmax*K routed pairs][Tmax shared]
+    __half *xspl = nullptr, *hspl = nullptr;
+    int *xexp = nullptr, *hexp = nullptr, *pair_row = nullptr, *n_tiles = nullptr;
+    float *hbuf = nullptr, *ybuf = nullptr;
+    GpTile *tiles = nullptr;
+    int max_tiles = 0;
     int *hist_idx = nullptr;
     float *hist_w = nullptr;
     unsigned long long *stats_dev = nullptr;
     float *x_host_io = nullptr;  // [T][D] device copy of gmoe_forward_host's activations
 
     // persistent decode kernel (stack.h)
+    int grouped_min_t = 2;       // T from which batches take the grouped GEMMs (GMOE_GROUPED_MIN_T)
     int stack_ok = 0;            // shape fits k_moe_stack
     int stack_grid = 0;          // co-resident blocks
     uint8_t *sk_ws = nullptr;    // per-layer workspace, L regions of sk_ws_layer bytes
@@ -149,7 +157,8 @@ static void free_ctx(gmoe_ctx *c) {
                     c->stage, c->topk_idx, c->tok_counter, c->panel_counter, c->disp_counter, c->disp_tmp_tok,
                     c->disp_tmp_slot, c->disp_counts, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
                     c->stats_dev, c->x_host_io, c->staging, c->sk_ws, c->sk_ctr, c->sk_error,
-                    c->sk_layers, c->sk_trace};
+                    c->sk_layers, c->sk_trace, c->xspl, c->hspl, c->xexp, c->hexp, c->pair_row, c->n_tiles,
+                    c->hbuf, c->ybuf, c->tiles};
     for (void *b : bufs) dev_free(b);
     delete c;
 }
@@ -237,6 +246,19 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     rc |= dev_alloc(&c->disp_tmp_slot, E * T);
     rc |= dev_alloc(&c->disp_counts, E);
     rc |= dev_alloc(&c->offsets, E + 1);
+    {
+        const size_t rows = T * K + T;  // list rows: routed pairs, then the shared expert's
+        c->max_tiles = (int)(E + (T * K + GP_TOK - 1) / GP_TOK + (T + GP_TOK - 1) / GP_TOK);
+        rc |= dev_alloc(&c->xspl, T * 2 * D);
+        rc |= dev_alloc(&c->xexp, T);
+        rc |= dev_alloc(&c->hbuf, rows * F);
+        rc |= dev_alloc(&c->hspl, rows * 2 * F);
+        rc |= dev_alloc(&c->hexp, rows);
+        rc |= dev_alloc(&c->ybuf, rows * D);
+        rc |= dev_alloc(&c->pair_row, T * K);
+        rc |= dev_alloc(&c->tiles, (size_t)c->max_tiles);
+        rc |= dev_alloc(&c->n_tiles, 1);
+    }
     rc |= dev_alloc(&c->tokens, T * K);
     rc |= dev_alloc(&c->slots, T * K);
     rc |= dev_alloc(&c->hist_idx, (size_t)c->L * T * K);
@@ -286,6 +308,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     // xn in shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots.
     // (the combine stages a chunk's partials, F/16 x (K+1) x 8 floats, in the slice buffer)
     c->stack_ok = c->L <= SK_MAX_LAYERS && (size_t)(F / 16) * (K + 1) * SK_CROWS * sizeof(float) <= sizeof(SkShared::dslice);
+    if (const char *g_env = getenv("GMOE_GROUPED_MIN_T")) c->grouped_min_t = atoi(g_env) > 1 ? atoi(g_env) : 2;
     const char *env = getenv("GMOE_STACK_KERNEL");
     if (env && env[0] == '0') c->stack_ok = 0;
     if (c->stack_ok) {
@@ -478,7 +501,7 @@ extern "C" int gmoe_profile_read(gmoe_ctx *c, gmoe_kernel_times *o) {
     return GMOE_OK;
 }
 
-static int launch_dispatch(gmoe_ctx *c, int T, hipStream_t st) {
+static int launch_dispatch(gmoe_ctx *c, int T, int routed_on, hipStream_t st) {
     DispatchArgs da;
     da.topk_idx = c->topk_idx;
     da.T = T;
@@ -491,6 +514,12 @@ static int launch_dispatch(gmoe_ctx *c, int T, hipStream_t st) {
     da.offsets = c->offsets;
     da.tokens = c->tokens;
     da.slots = c->slots;
+    da.TK = c->Tmax * c->K;
+    da.routed_on = routed_on;
+    da.shared_on = c->S > 0;
+    da.tiles = c->tiles;
+    da.n_tiles = c->n_tiles;
+    da.pair_row = c->pair_row;
     ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_DISPATCH);
     hipLaunchKernelGGL(k_dispatch, dim3(c->E), dim3(DP_BLOCK), 0, st, da);
     prof_end(pr, st);
@@ -623,8 +652,6 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     ra.gate_inp = L.gate_inp;
     ra.bias = L.bias;
     ra.xn = c->xn;
-    ra.stage = c->stage;
-    ra.tok_counter = c->tok_counter;
     ra.router_prob = c->router_prob;
     ra.topk_idx = c->topk_idx;
     ra.topk_w = c->topk_w;
@@ -639,47 +666,114 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     ra.routed_scale = c->cfg.routed_scale;
     ra.force_exact = (flags & GMOE_FLAG_EXACT_ROUTER) != 0;
     ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_ROUTER);
-    hipLaunchKernelGGL(k_norm_router, dim3(E, T), dim3(RT_BLOCK), (size_t)D * sizeof(float), st, ra);
+    hipLaunchKernelGGL(k_router_tok, dim3(T), dim3(RT_BLOCK), 0, st, ra);
     prof_end(pr, st);
-
-    ExpertArgs ea;
-    ea.experts = L.experts;
-    ea.stride = c->stride;
-    ea.off_gq = c->off_gq;
-    ea.off_uq = c->off_uq;
-    ea.off_dq = c->off_dq;
-    ea.off_gs = c->off_gs;
-    ea.off_us = c->off_us;
-    ea.off_ds = c->off_ds;
-    ea.D = D;
-    ea.F = F;
-    ea.E = E;
-    ea.K = K;
-    ea.S = c->S;
-    ea.flags = fl;
-    pr = prof_begin(c, st, GMOE_KERNEL_GATE_UP);
-    hipLaunchKernelGGL(k_gate_up, dim3(F / 16, NS, T), dim3(EX_BLOCK), (size_t)3 * D + (size_t)(D / 32) * 4, st, ea,
-                       (const float *)c->xn, (const int *)c->topk_idx, c->h);
-    prof_end(pr, st);
-
-    CombineArgs ca;
-    ca.topk_idx = c->topk_idx;
-    ca.topk_ws = c->topk_ws;
-    ca.y = c->y;
-    ca.panel_counter = c->panel_counter;
-    ca.x_in = x_in;
-    ca.x_out = x_out;
-    ca.shared_out = c->shared_out;
-    ca.routed_out = c->routed_out;
-    pr = prof_begin(c, st, GMOE_KERNEL_DOWN);
-    hipLaunchKernelGGL(k_down_combine, dim3(D / 16, NS, T), dim3(EX_BLOCK), (size_t)3 * F + (size_t)(F / 32) * 4, st,
-                       ea, ca, (const float *)c->h);
-    prof_end(pr, st);
-    HIP_OK(hipGetLastError());
+    const int routed_on = !(fl & GMOE_FLAG_NO_ROUTED);
     c->last_dispatched = 0;
-    if (T > 1) {
-        int rc = launch_dispatch(c, T, st);
+    if (T >= c->grouped_min_t) {
+        // prefill: digits of xn, the per-expert lists and tiles, grouped gate/up, digits
+        // of h, grouped down, per-token combine (grouped.h)
+        const int TK = c->Tmax * K;
+        pr = prof_begin(c, st, GMOE_KERNEL_DIGITS);
+        hipLaunchKernelGGL(k_act_split, dim3(T), dim3(GP_BLOCK), 0, st, (const float *)c->xn, D, T, (const int *)nullptr,
+                           c->xspl, c->xexp);
+        prof_end(pr, st);
+        int rc = launch_dispatch(c, T, routed_on, st);
         if (rc) return rc;
+        GroupArgs ga;
+        ga.experts = L.experts;
+        ga.stride = c->stride;
+        ga.off_gq = c->off_gq;
+        ga.off_uq = c->off_uq;
+        ga.off_dq = c->off_dq;
+        ga.off_gs = c->off_gs;
+        ga.off_us = c->off_us;
+        ga.off_ds = c->off_ds;
+        ga.D = D;
+        ga.F = F;
+        ga.E = E;
+        ga.T = T;
+        ga.TK = TK;
+        ga.tiles = c->tiles;
+        ga.n_tiles = c->n_tiles;
+        ga.tokens = c->tokens;
+        ga.aspl = c->xspl;
+        ga.aexp = c->xexp;
+        ga.out = c->hbuf;
+        const int max_tiles = (routed_on ? E + (T * K + GP_TOK - 1) / GP_TOK : 0) + (T + GP_TOK - 1) / GP_TOK;
+        pr = prof_begin(c, st, GMOE_KERNEL_GATE_UP);
+        hipLaunchKernelGGL(k_group_gu, dim3(F / 64, max_tiles), dim3(GP_BLOCK), 0, st, ga);
+        prof_end(pr, st);
+        // routed rows [0, offsets[E]) and the shared rows [TK, TK + T)
+        pr = prof_begin(c, st, GMOE_KERNEL_DIGITS);
+        if (routed_on)
+            hipLaunchKernelGGL(k_act_split, dim3(T * K), dim3(GP_BLOCK), 0, st, (const float *)c->hbuf, F, T * K,
+                               (const int *)(c->offsets + E), c->hspl, c->hexp);
+        hipLaunchKernelGGL(k_act_split, dim3(T), dim3(GP_BLOCK), 0, st, (const float *)(c->hbuf + (size_t)TK * F), F, T,
+                           (const int *)nullptr, c->hspl + (size_t)TK * 2 * F, c->hexp + TK);
+        prof_end(pr, st);
+        ga.aspl = c->hspl;
+        ga.aexp = c->hexp;
+        ga.out = c->ybuf;
+        pr = prof_begin(c, st, GMOE_KERNEL_DOWN);
+        hipLaunchKernelGGL(k_group_down, dim3(D / 64, max_tiles), dim3(GP_BLOCK), 0, st, ga);
+        prof_end(pr, st);
+        TokenCombineArgs ta;
+        ta.topk_idx = c->topk_idx;
+        ta.topk_ws = c->topk_ws;
+        ta.pair_row = c->pair_row;
+        ta.y = c->ybuf;
+        ta.x_in = x_in;
+        ta.x_out = x_out;
+        ta.shared_out = c->shared_out;
+        ta.routed_out = c->routed_out;
+        ta.D = D;
+        ta.K = K;
+        ta.TK = TK;
+        ta.routed_on = routed_on;
+        pr = prof_begin(c, st, GMOE_KERNEL_COMBINE);
+        hipLaunchKernelGGL(k_token_combine, dim3((D + GP_BLOCK - 1) / GP_BLOCK, T), dim3(GP_BLOCK), 0, st, ta);
+        prof_end(pr, st);
+        HIP_OK(hipGetLastError());
+    } else {
+        // one token's experts at a time: gate/up (+SwiGLU), then down with the combine
+        ExpertArgs ea;
+        ea.experts = L.experts;
+        ea.stride = c->stride;
+        ea.off_gq = c->off_gq;
+        ea.off_uq = c->off_uq;
+        ea.off_dq = c->off_dq;
+        ea.off_gs = c->off_gs;
+        ea.off_us = c->off_us;
+        ea.off_ds = c->off_ds;
+        ea.D = D;
+        ea.F = F;
+        ea.E = E;
+        ea.K = K;
+        ea.S = c->S;
+        ea.flags = fl;
+        pr = prof_begin(c, st, GMOE_KERNEL_GATE_UP);
+        hipLaunchKernelGGL(k_gate_up, dim3(F / 16, NS, T), dim3(EX_BLOCK), (size_t)3 * D + (size_t)(D / 32) * 4, st, ea,
+                           (const float *)c->xn, (const int *)c->topk_idx, c->h);
+        prof_end(pr, st);
+        CombineArgs ca;
+        ca.topk_idx = c->topk_idx;
+        ca.topk_ws = c->topk_ws;
+        ca.y = c->y;
+        ca.panel_counter = c->panel_counter;
+        ca.x_in = x_in;
+        ca.x_out = x_out;
+        ca.shared_out = c->shared_out;
+        ca.routed_out = c->routed_out;
+        pr = prof_begin(c, st, GMOE_KERNEL_DOWN);
+        hipLaunchKernelGGL(k_down_combine, dim3(D / 16, NS, T), dim3(EX_BLOCK), (size_t)3 * F + (size_t)(F / 32) * 4,
+                           st, ea, ca, (const float *)c->h);
+        prof_end(pr, st);
+        HIP_OK(hipGetLastError());
+        if (T > 1) {
+            int rc = launch_dispatch(c, T, routed_on, st);
+            if (rc) return rc;
+        }
     }
     c->last_layer = layer;
     c->last_T = T;
@@ -758,7 +852,7 @@ extern "C" int gmoe_read_layer_state(gmoe_ctx *c, gmoe_layer_state *o, void *str
     const size_t T = c->last_T, D = c->D, E = c->E, K = c->K;
     if (int erc = check_stack_error(c)) return erc;
     if ((o->expert_offsets || o->expert_tokens) && !c->last_dispatched) {
-        int rc = launch_dispatch(c, (int)T, st);
+        int rc = launch_dispatch(c, (int)T, !(c->last_flags & GMOE_FLAG_NO_ROUTED), st);
         if (rc) return rc;
     }
     HIP_OK(hipStreamSynchronize(st));

@@ -11,9 +11,9 @@
 //    [S-B, S+B] into an interval that must contain the CPU's selection score
 //    p + bias (allowing for expf, the add and the divide in fp32), and accepts the
 //    top-k only when the intervals order the chosen experts strictly.
-// When the proof fails the last block replays every expert's fp32 chain exactly and
-// runs glm.c's insertion top-k on it; only a tie within the last bits of libm's expf
-// could then still differ, and that case is counted in stats[GM_STAT_UNRESOLVED].
+// When the proof fails the block replays every expert's fp32 chain exactly and runs
+// glm.c's insertion top-k on it; only a tie within the last bits of libm's expf could
+// then still differ, and that case is counted in stats[GM_STAT_UNRESOLVED].
 #pragma once
 
 #include "common.h"
@@ -26,8 +26,6 @@ struct RouterArgs {
     const float *gate_inp;     // [E][D]
     const float *bias;         // [E]
     float *xn;                 // [T][D]
-    double2 *stage;            // [T][E]  (S, B)
-    unsigned *tok_counter;     // [T], zero between launches
     float *router_prob;        // [T][E]
     int *topk_idx;             // [T][K]
     float *topk_w;             // [T][K] normalised
@@ -107,203 +105,353 @@ __device__ static inline void wave_argmax(double key, int idx, double *bkey, int
     *bidx = idx;
 }
 
-#define RT_BLOCK 256
-#define RT_MAX_PER 32  // D <= 256 * 32
+#define RT_SEL_C (GM_MAX_E / 64)  // experts per lane in a one-wave selection
+#define RT_XT 128                 // columns per tile of the exact replay (its product tile is 32 KB)
 
-__global__ __launch_bounds__(RT_BLOCK) void k_norm_router(RouterArgs a) {
-    extern __shared__ float s_xn[];  // [D]
+// Certified top-k on one wave, over C chunks of 64 experts whose results are in
+// registers (lane l: experts l + 64c; w0 = fp32 bits of lo | hi << 32, w1 = fp32 bits
+// of p): the K best interval midpoints are taken one at a time (a wave maximum, then the
+// lowest lane holding it), and the result is certified when each chosen interval lies
+// strictly above the next chosen one and the last chosen lies strictly above every
+// expert left out. glm.c's insertion top-k (infer.c:1110-1135) orders strictly by
+// value, so it must then pick the same experts in the same order. Lane 0 writes the
+// top-k to idx / wk (unnormalised p), their sum to *total and the verdict to *sel_ok;
+// with p_out, every probability goes there too.
+template <int C>
+__device__ __attribute__((always_inline)) static void certified_select(int E, int K, int tid, const unsigned long long *w0,
+                                                                       const unsigned long long *w1, float *p_out, int *idx,
+                                                                       float *wk_out, int *sel_ok, float *total_out) {
+    float lo[C], hi[C], pr[C], key[C];
+    bool bad = false;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int e = tid + 64 * c;
+        const bool valid = e < E;
+        lo[c] = valid ? __uint_as_float((unsigned)w0[c]) : -INFINITY;
+        hi[c] = valid ? __uint_as_float((unsigned)(w0[c] >> 32)) : -INFINITY;
+        pr[c] = valid ? __uint_as_float((unsigned)w1[c]) : 0.0f;
+        if (valid) bad |= !(isfinite(lo[c]) && isfinite(hi[c]));
+        key[c] = valid ? 0.5f * lo[c] + 0.5f * hi[c] : -INFINITY;
+        if (p_out && valid) p_out[e] = pr[c];
+    }
+    bool cert = __ballot(bad) == 0;
+    float prev_lo = 0.0f, total = 0.0f;
+    for (int k = 0; k < K; k++) {
+        float bm = key[0];
+        int bc = 0;
+#pragma unroll
+        for (int c = 1; c < C; c++)
+            if (key[c] > bm) {
+                bm = key[c];
+                bc = c;
+            }
+        const float gm = wave_max_dpp_f(bm);
+        int ek = -1;
+        float wk = -1e30f;
+        if (gm > -INFINITY) {  // fewer than K experts leave the rest at -1 (infer.c:1110-1113)
+            const int ls = __ffsll(__ballot(bm == gm)) - 1;
+            const int cs = __builtin_amdgcn_readlane(bc, ls);
+            float ml = lo[0], mh = hi[0], mp = pr[0];
+#pragma unroll
+            for (int c = 1; c < C; c++)
+                if (bc == c) {
+                    ml = lo[c];
+                    mh = hi[c];
+                    mp = pr[c];
+                }
+            const float lk = readlane_f(ml, ls), hk = readlane_f(mh, ls);
+            if (k > 0 && !(prev_lo > hk)) cert = false;
+            prev_lo = lk;
+            ek = ls + 64 * cs;
+            wk = readlane_f(mp, ls);
+            total = __fadd_rn(total, wk);
+#pragma unroll
+            for (int c = 0; c < C; c++)
+                if (tid == ls && c == cs) key[c] = -INFINITY;
+        }
+        if (tid == 0) {
+            idx[k] = ek;
+            wk_out[k] = wk;
+        }
+    }
+    // the last chosen must lie above every expert left out (chosen ones now hold -inf)
+    float rest = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < C; c++)
+        if (key[c] > -INFINITY) rest = fmaxf(rest, hi[c]);
+    rest = wave_max_dpp_f(rest);
+    if (rest > -INFINITY && !(prev_lo > rest)) cert = false;
+    if (tid == 0) {
+        *sel_ok = cert;
+        *total_out = total;
+    }
+}
+
+// glm.c's router replayed exactly in fp32 (infer.c:916-938, 1104-1145) by one block of
+// 256 threads, for the xn in shared memory: every probability into p and selection
+// score into sel (shared, [E]), the top-k into idx and its normalised weights into wk
+// (shared, [K]). prod is 32 KB of shared scratch. Counts the replay in stats, and a
+// top-k whose order hinges on expf's last bits as unresolved.
+__device__ __attribute__((always_inline)) static void exact_router(int D, int E, int K, int tid, const float *gate_inp, const float *bias_p,
+                                    const float *xn, float (*prod)[64], float *p, float *sel, int *idx, float *wk_out,
+                                    unsigned long long *stats) {
+    const GM_GLOBAL float *bias = gbl(bias_p);
+    // infer.c:916-925 for 64 experts at a time, in tiles of RT_XT columns: every thread
+    // forms the products fl(g * xn) of one expert (its lane) and a quarter of the tile's
+    // columns (its wave) into prod[column][expert], then lane e of wave 0 adds its
+    // expert's products in column order. Each thread's gate rows are fetched two tiles
+    // ahead into registers, so the loads overlap the chain.
+    const int lane = tid & 63, w = tid >> 6, qc = RT_XT / 4;  // columns per wave and tile
+    const int ntile = D / RT_XT;
+    for (int eb = 0; eb < E; eb += 64) {
+        const int ne = E - eb < 64 ? E - eb : 64;
+        const float4 *grow = (const float4 *)(gate_inp + (size_t)(eb + (lane < ne ? lane : 0)) * D + w * qc);
+        float4 ga[RT_XT / 16], gb[RT_XT / 16];
+#pragma unroll
+        for (int q = 0; q < RT_XT / 16; q++) ga[q] = grow[q];
+#pragma unroll
+        for (int q = 0; q < RT_XT / 16; q++) gb[q] = grow[RT_XT / 4 + q];
+        float chain = 0.0f;
+        // one tile from registers g (tile t), then g refilled with tile t + 2
+        auto tile = [&](float4 *g, int t) {
+            const int c0 = t * RT_XT + w * qc;
+#pragma unroll
+            for (int q = 0; q < RT_XT / 16; q++) {
+                const float4 xq = *(const float4 *)&xn[c0 + 4 * q];
+                prod[w * qc + 4 * q + 0][lane] = __fmul_rn(g[q].x, xq.x);
+                prod[w * qc + 4 * q + 1][lane] = __fmul_rn(g[q].y, xq.y);
+                prod[w * qc + 4 * q + 2][lane] = __fmul_rn(g[q].z, xq.z);
+                prod[w * qc + 4 * q + 3][lane] = __fmul_rn(g[q].w, xq.w);
+            }
+            __syncthreads();
+            if (t + 2 < ntile)
+#pragma unroll
+                for (int q = 0; q < RT_XT / 16; q++) g[q] = grow[(t + 2) * (RT_XT / 4) + q];
+            if (w == 0) {
+                for (int c0 = 0; c0 < RT_XT; c0 += 16) {
+                    float v[16];  // sixteen reads in flight, then the sixteen dependent adds
+#pragma unroll
+                    for (int j = 0; j < 16; j++) v[j] = prod[c0 + j][lane];
+#pragma unroll
+                    for (int j = 0; j < 16; j++) chain = __fadd_rn(chain, v[j]);
+                }
+            }
+            __syncthreads();
+        };
+        for (int t = 0; t < ntile; t += 2) {  // ntile = D / 128 is even
+            tile(ga, t);
+            tile(gb, t + 1);
+        }
+        if (tid < ne) {
+            const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain)));
+            p[eb + tid] = pr;
+            sel[eb + tid] = __fadd_rn(pr, bias[eb + tid]);
+        }
+    }
+    __syncthreads();
+    // glm.c's insertion top-k (infer.c:1110-1135) keeps the K largest sel by (value desc,
+    // index asc) among values above -inf (NaN is never inserted): K wave-maximum rounds,
+    // the lowest lane winning ties, chunk c of lane l holding expert l + 64c.
+    if (w == 0) {
+        const int nch = (E + 63) >> 6;
+        float key[RT_SEL_C], pv[RT_SEL_C];
+#pragma unroll
+        for (int c = 0; c < RT_SEL_C; c++) {
+            const int e = lane + 64 * c;
+            const bool valid = c < nch && e < E;
+            const float v = valid ? sel[e] : -INFINITY;
+            key[c] = v == v ? v : -INFINITY;
+            pv[c] = valid ? p[e] : 0.0f;
+        }
+        float total = 0.0f;
+        bool unresolved = false;
+        for (int k = 0; k < K; k++) {
+            float bm = key[0];
+#pragma unroll
+            for (int c = 1; c < RT_SEL_C; c++) bm = fmaxf(bm, key[c]);
+            const float gm = wave_max_dpp_f(bm);
+            int ek = -1;
+            float wk = -1e30f;
+            if (gm > -INFINITY) {
+                // the lowest expert index holding the maximum: chunks in index order
+                int ls = -1, cs = 0;
+#pragma unroll
+                for (int c = 0; c < RT_SEL_C; c++) {
+                    const unsigned long long m = __ballot(key[c] == gm);
+                    if (ls < 0 && m != 0ull) {
+                        ls = __ffsll(m) - 1;
+                        cs = c;
+                    }
+                }
+                float mp = pv[0];
+#pragma unroll
+                for (int c = 1; c < RT_SEL_C; c++)
+                    if (cs == c) mp = pv[c];
+                ek = ls + 64 * cs;
+                wk = readlane_f(mp, ls);
+                total = __fadd_rn(total, wk);
+#pragma unroll
+                for (int c = 0; c < RT_SEL_C; c++)
+                    if (lane == ls && c == cs) key[c] = -INFINITY;
+                // libm's expf may differ from the GPU's by an ulp: flag orders decided that
+                // closely (any expert not yet chosen within a few ulps of this one)
+                const float tol = 4.0f * fmaxf(fabsf(gm), 1e-30f) * 0x1p-23f + 4.0f * 0x1p-24f;
+                bool close = false;
+#pragma unroll
+                for (int c = 0; c < RT_SEL_C; c++) close |= key[c] > -INFINITY && fabsf(key[c] - gm) <= tol;
+                unresolved |= __ballot(close) != 0;
+            }
+            if (lane == 0) {
+                idx[k] = ek;
+                wk_out[k] = wk;
+            }
+        }
+        if (lane == 0) {
+            atomicAdd(&stats[GM_STAT_ROUTE_EXACT], 1ull);
+            if (unresolved) atomicAdd(&stats[GM_STAT_UNRESOLVED], 1ull);
+            if (total > 0.0f) {
+                // normalisation of infer.c:1136-1145
+                const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
+                const float inv_d = __fdiv_rn(1.0f, denom);
+                for (int k = 0; k < K; k++) wk_out[k] = __fmul_rn(wk_out[k], inv_d);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+#define RT_BLOCK 256
+#define RT_CPL_MAX (GM_MAX_COLS / 64)  // router columns per lane
+
+// grid (T): the router of one token per block. RMSNorm bit-identical to infer.c:746-752
+// (certified_mean_sq); every expert's fp64 logit with the bound of its fp32 chain, wave
+// w taking experts w, w + 4, ... and lane l the D/64 consecutive columns from l D/64 (so
+// a wave scan yields the chain's partial sums in glm.c's order); then the certified
+// top-k on wave 0 (certified_select) or, when it fails or is forced, the exact replay
+// (exact_router). Outputs as infer.c:1098-1145 leaves them: xn, probabilities, top-k,
+// normalised weights (and times routed_scale).
+__global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
+    __shared__ __align__(16) float s_xn[GM_MAX_COLS];
+    __shared__ __align__(16) float s_prod[RT_XT][64];  // exact replay scratch
     __shared__ double red[4];
-    __shared__ float s_mean;
-    __shared__ int s_last;
-    const int e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int D = a.D, E = a.E, K = a.K;
+    __shared__ float s_mean, s_total;
+    __shared__ unsigned long long s_w0[GM_MAX_E], s_w1[GM_MAX_E];
+    __shared__ float s_p[GM_MAX_E], s_sel[GM_MAX_E], s_wk[GM_MAX_K];
+    __shared__ int s_idx[GM_MAX_K], s_ok;
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int D = a.D, E = a.E, K = a.K, cpl = D >> 6;
     const float *xt = a.x + (size_t)t * D;
 
-    // ---- RMSNorm, bit-identical to infer.c:746-752
-    const float mean = certified_mean_sq(xt, D, red, &s_mean, e == 0, a.stats);
+    const float mean = certified_mean_sq(xt, D, red, &s_mean, true, a.stats);
     const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
     for (int i = tid; i < D; i += RT_BLOCK) {
-        float v = __fmul_rn(__fmul_rn(xt[i], inv), a.norm_w[i]);
+        const float v = __fmul_rn(__fmul_rn(xt[i], inv), a.norm_w[i]);
         s_xn[i] = v;
-        if (e == 0) a.xn[(size_t)t * D + i] = v;
+        a.xn[(size_t)t * D + i] = v;
     }
     __syncthreads();
 
-    // ---- router logit of expert e in fp64 plus the bound on the fp32 chain error
-    const float *g = a.gate_inp + (size_t)e * D;
-    const int per = (D + RT_BLOCK - 1) / RT_BLOCK;
-    double p[RT_MAX_PER];
-    double seg = 0.0, seg_abs = 0.0;
+    // the lane's columns of xn in registers; the gate rows are read per expert (several
+    // blocks per CU hide the latency)
+    float xr[RT_CPL_MAX];
 #pragma unroll
-    for (int j = 0; j < RT_MAX_PER; j++) {
-        if (j < per) {
-            const int i = tid * per + j;
-            const double pj = (i < D) ? (double)g[i] * (double)s_xn[i] : 0.0;
-            p[j] = pj;
+    for (int q = 0; q < RT_CPL_MAX / 4; q++) {
+        const float4 v = q < cpl / 4 ? *(const float4 *)&s_xn[lane * cpl + 4 * q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        xr[4 * q] = v.x;
+        xr[4 * q + 1] = v.y;
+        xr[4 * q + 2] = v.z;
+        xr[4 * q + 3] = v.w;
+    }
+    for (int e = w; e < E; e += 4) {
+        float g[RT_CPL_MAX];
+        const float4 *src = (const float4 *)(a.gate_inp + (size_t)e * D + lane * cpl);
+#pragma unroll
+        for (int q = 0; q < RT_CPL_MAX / 4; q++) {
+            const float4 v = q < cpl / 4 ? src[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+            g[4 * q] = v.x;
+            g[4 * q + 1] = v.y;
+            g[4 * q + 2] = v.z;
+            g[4 * q + 3] = v.w;
+        }
+        // xn stays 32 floats: kept opaque here so that its fp64 conversions are not
+        // hoisted out of the loop as 32 live doubles
+#pragma unroll
+        for (int j = 0; j < RT_CPL_MAX; j++) asm volatile("" : "+v"(xr[j]));
+        // pass 1: the lane's segment sum and the wave's exclusive prefix (products in fp64
+        // are exact); pass 2: |S_k| after each of the lane's columns
+        double seg = 0.0, seg_abs = 0.0;
+#pragma unroll
+        for (int j = 0; j < RT_CPL_MAX; j++) {
+            const double pj = (double)g[j] * (double)xr[j];
             seg += pj;
             seg_abs += fabs(pj);
         }
-    }
-    double S;
-    double run = block_exclusive_scan_d(seg, red, &S);
-    double prefix_abs = 0.0;
+        const double incl = wave_incl_scan_dpp(seg);
+        double run = incl - seg, steps = 0.0;
 #pragma unroll
-    for (int j = 0; j < RT_MAX_PER; j++) {
-        if (j < per) {
-            run += p[j];
-            if (tid * per + j < D) prefix_abs += fabs(run);
+        for (int j = 0; j < RT_CPL_MAX; j++) {
+            if (j < cpl) {
+                run += (double)g[j] * (double)xr[j];
+                steps += fabs(run);
+            }
         }
-    }
-    const double sum_prefix_abs = block_sum_d(prefix_abs, red);
-    const double sum_abs = block_sum_d(seg_abs, red);
-    if (tid == 0) {
-        const double u = 0x1p-24, n = (double)D;
-        const double gamma = n * u / (1.0 - n * u);
-        double B = u * (1.0 + u) * sum_abs + u * sum_prefix_abs + n * u * gamma * sum_abs;
-        B = B * (1.0 + 0x1p-30) + 0x1p-40 * sum_abs + n * 0x1p-149;
-        a.stage[(size_t)t * E + e] = make_double2(S, B);
-    }
-
-    // ---- the last block of token t selects
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&a.tok_counter[t], 1u) == (unsigned)(E - 1));
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    if (tid == 0) a.tok_counter[t] = 0u;
-
-    __shared__ double s_lo[GM_MAX_E], s_hi[GM_MAX_E], s_mid[GM_MAX_E];
-    __shared__ float s_p[GM_MAX_E], s_sel[GM_MAX_E];
-    __shared__ int s_idx[GM_MAX_K];
-    __shared__ int s_ok;
-    for (int i = tid; i < E; i += RT_BLOCK) {
-        const double2 sb = a.stage[(size_t)t * E + i];
-        double lo, hi;
-        selection_interval(sb.x, sb.y, a.bias[i], &lo, &hi);
-        s_lo[i] = lo;
-        s_hi[i] = hi;
-        s_mid[i] = 0.5 * (lo + hi);
-        s_p[i] = (float)(1.0 / (1.0 + exp(-sb.x)));
+        const double S = readlane_d(incl, 63);
+        const double sp = wave_sum_dpp(steps), sa = wave_sum_dpp(seg_abs);
+        if (lane == 0) {
+            const double u = 0x1p-24, n = (double)D;
+            const double gamma = n * u / (1.0 - n * u);
+            const double emax = gamma * sa;  // a priori bound on every partial sum's error
+            double B = u * (1.0 + u) * sa + u * (sp + n * emax + u * sa);
+            B = B * (1.0 + 0x1p-30) + 0x1p-40 * sa + n * 0x1p-149;
+            double lo, hi;
+            selection_interval(S, B, a.bias[e], &lo, &hi);
+            float lo_f = __double2float_rd(lo), hi_f = __double2float_ru(hi);
+            if (!(lo_f <= hi_f)) {  // NaN: an interval that is never certified
+                lo_f = -INFINITY;
+                hi_f = INFINITY;
+            }
+            s_w0[e] = (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32);
+            s_w1[e] = (unsigned long long)__float_as_uint(1.0f / (1.0f + expf(-(float)S)));
+        }
     }
     __syncthreads();
 
     if (tid < 64) {
-        // K rounds of wave argmax over the midpoints; then check strict separation.
-        unsigned long long taken = 0ull;  // bit i: lane-local candidate i taken (E <= 256 -> 4 per lane)
-        int ok = !a.force_exact;
-        double prev_lo = 0.0;
-        const int kk = K < E ? K : E;
-        for (int k = 0; k < kk; k++) {
-            double best = -INFINITY;
-            int bi = 0x7fffffff;
-            for (int c = 0; c < 4; c++) {
-                const int i = tid + 64 * c;
-                if (i < E && !((taken >> c) & 1ull)) {
-                    const double m = s_mid[i];
-                    if (m > best || (m == best && i < bi)) {
-                        best = m;
-                        bi = i;
-                    }
-                }
-            }
-            double wk;
-            int wi;
-            wave_argmax(best, bi, &wk, &wi);
-            if (wi == 0x7fffffff || !(wk == wk)) {
-                ok = 0;
-                break;
-            }
-            if ((wi & 63) == tid) taken |= 1ull << (wi >> 6);
-            if (k > 0 && !(prev_lo > s_hi[wi])) ok = 0;
-            prev_lo = s_lo[wi];
-            if (tid == 0) s_idx[k] = wi;
-        }
-        if (ok && kk < E) {
-            // the last chosen must beat every expert left out
-            double mx = -INFINITY;
-            for (int c = 0; c < 4; c++) {
-                const int i = tid + 64 * c;
-                if (i < E && !((taken >> c) & 1ull)) mx = fmax(mx, s_hi[i]);
-            }
+        unsigned long long w0[RT_SEL_C], w1[RT_SEL_C];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o, 64));
-            if (!(prev_lo > mx)) ok = 0;
+        for (int c = 0; c < RT_SEL_C; c++) {
+            const int e = tid + 64 * c < E ? tid + 64 * c : E - 1;
+            w0[c] = s_w0[e];
+            w1[c] = s_w1[e];
         }
-        if (tid == 0) {
-            s_ok = ok;
-            for (int k = kk; k < K; k++) s_idx[k] = -1;
-        }
+        if (E <= 64)
+            certified_select<1>(E, K, tid, w0, w1, s_p, s_idx, s_wk, &s_ok, &s_total);
+        else
+            certified_select<RT_SEL_C>(E, K, tid, w0, w1, s_p, s_idx, s_wk, &s_ok, &s_total);
+        if (tid == 0 && a.force_exact) s_ok = 0;
     }
     __syncthreads();
-
-    if (!s_ok) {
-        // ---- exact replay: sequential fp32 chains (infer.c:916-925), glm.c's insertion top-k
-        for (int i = tid; i < E; i += RT_BLOCK) {
-            const float *gi = a.gate_inp + (size_t)i * D;
-            float chain = 0.0f;
-            for (int j = 0; j < D; j++) chain = __fadd_rn(chain, __fmul_rn(gi[j], s_xn[j]));
-            const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain)));
-            s_p[i] = pr;
-            s_sel[i] = __fadd_rn(pr, a.bias[i]);
+    if (s_ok) {
+        if (tid < K) {  // normalisation of infer.c:1136-1145
+            const float total = s_total;
+            float wk = s_wk[tid];
+            if (total > 0.0f) {
+                const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
+                wk = __fmul_rn(wk, __fdiv_rn(1.0f, denom));
+            }
+            s_wk[tid] = wk;
         }
         __syncthreads();
-        if (tid == 0) {
-            atomicAdd(&a.stats[GM_STAT_ROUTE_EXACT], 1ull);
-            int idx[GM_MAX_K];
-            for (int k = 0; k < K; k++) idx[k] = -1;
-            for (int i = 0; i < E; i++) {
-                const float sc = s_sel[i];
-                int at = -1;
-                for (int k = 0; k < K && at < 0; k++) {
-                    const float held = idx[k] >= 0 ? s_sel[idx[k]] : -INFINITY;
-                    if (sc > held) at = k;
-                }
-                if (at < 0) continue;
-                for (int k = K - 1; k > at; k--) idx[k] = idx[k - 1];
-                idx[at] = i;
-            }
-            // GPU expf may differ from libm's by an ulp: flag orderings decided that closely.
-            int unresolved = 0;
-            for (int k = 0; k < K; k++) {
-                if (idx[k] < 0) continue;
-                const float a0 = s_sel[idx[k]];
-                const float tol = 4.0f * fmaxf(fabsf(a0), 1e-30f) * 0x1p-23f + 4.0f * 0x1p-24f;
-                for (int i = 0; i < E; i++) {
-                    if (i == idx[k]) continue;
-                    bool above = false;
-                    for (int q = 0; q < k; q++) above |= (idx[q] == i);
-                    if (above) continue;
-                    if (fabsf(s_sel[i] - a0) <= tol) unresolved = 1;
-                }
-            }
-            if (unresolved) atomicAdd(&a.stats[GM_STAT_UNRESOLVED], 1ull);
-            for (int k = 0; k < K; k++) s_idx[k] = idx[k];
-        }
-        __syncthreads();
+    } else {
+        exact_router(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_p, s_sel, s_idx, s_wk, a.stats);
     }
-
-    if (tid == 0) {
-        // weights: unbiased probabilities, normalised as infer.c:1136-1145
-        float w[GM_MAX_K];
-        float total = 0.0f;
-        for (int k = 0; k < K; k++) {
-            w[k] = s_idx[k] >= 0 ? s_p[s_idx[k]] : -1e30f;
-            if (s_idx[k] >= 0) total = __fadd_rn(total, w[k]);
-        }
-        if (total > 0.0f) {
-            const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
-            const float inv_d = __fdiv_rn(1.0f, denom);
-            for (int k = 0; k < K; k++) w[k] = __fmul_rn(w[k], inv_d);
-        }
-        for (int k = 0; k < K; k++) {
-            const size_t o = (size_t)t * K + k;
-            a.topk_idx[o] = s_idx[k];
-            a.topk_w[o] = w[k];
-            a.topk_ws[o] = __fmul_rn(w[k], a.routed_scale);
-            a.hist_idx[o] = s_idx[k];
-            a.hist_w[o] = w[k];
-        }
+    if (tid < K) {
+        const size_t o = (size_t)t * K + tid;
+        a.topk_idx[o] = s_idx[tid];
+        a.topk_w[o] = s_wk[tid];
+        a.topk_ws[o] = __fmul_rn(s_wk[tid], a.routed_scale);
+        a.hist_idx[o] = s_idx[tid];
+        a.hist_w[o] = s_wk[tid];
     }
     for (int i = tid; i < E; i += RT_BLOCK) a.router_prob[(size_t)t * E + i] = s_p[i];
 }

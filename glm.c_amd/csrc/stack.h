@@ -217,15 +217,6 @@ __device__ static inline bool wait_ge(const unsigned *c, unsigned target, int *e
     return sh.ok != 0;
 }
 
-// Maximum over the 64 lanes of a wave, returned to every lane (wave-uniform), by DPP.
-__device__ static inline float wave_max_dpp_f(float v) {
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_QUAD_1032, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_QUAD_2301, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_ROW_HALF_MIRROR, 0xF, 0xF, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_ROW_MIRROR, 0xF, 0xF, false)));
-    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
-}
-
 // threadIdx.x, opaque to the optimiser. The phases of the layer loop take their thread
 // index from this, so that the many addresses derived from it are computed in the phase
 // that uses them rather than hoisted out of the loop and kept live (spilled) throughout.
@@ -267,82 +258,14 @@ __device__ static inline void dma_copy(void *dst, const void *src, int nbytes) {
 // verdict; when it is "not certified" (or an interval is not finite), router block 0
 // replays the fp32 router exactly (sk_exact_select) and the others wait for its result.
 // Returns false if the wait timed out or another block failed; sh.sel_ok = certified.
-#define SK_SEL_C (GM_MAX_E / 64)
-#define SK_XT 128  // columns per tile of the exact router replay (prod tile = 32 KB)
+#define SK_SEL_C RT_SEL_C
 
-// The selection proper on wave 0, over C chunks of 64 experts whose stage words w0, w1
-// are in registers (lane l: experts l + 64c): the top-k into sh.idx / sh.wk (unscaled),
-// their sum into sh.total, the verdict into sh.sel_ok, and with keep_p every probability
-// into sh.u.s.p.
+// The certified selection of the layer (certified_select) into sh.
 template <int C>
 __device__ __attribute__((always_inline)) static void sk_select_rounds(const StackArgs &a, const unsigned long long *w0,
                                                                        const unsigned long long *w1, bool keep_p,
                                                                        SkShared &sh) {
-    const int E = a.E, K = a.K, tid = phase_tid();
-    float lo[C], hi[C], pr[C], key[C];
-    bool bad = false;
-#pragma unroll
-    for (int c = 0; c < C; c++) {
-        const int e = tid + 64 * c;
-        const bool valid = e < E;
-        lo[c] = valid ? __uint_as_float((unsigned)w0[c]) : -INFINITY;
-        hi[c] = valid ? __uint_as_float((unsigned)(w0[c] >> 32)) : -INFINITY;
-        pr[c] = valid ? __uint_as_float((unsigned)w1[c]) : 0.0f;
-        if (valid) bad |= !(isfinite(lo[c]) && isfinite(hi[c]));
-        key[c] = valid ? 0.5f * lo[c] + 0.5f * hi[c] : -INFINITY;
-        if (keep_p && valid) sh.u.s.p[e] = pr[c];
-    }
-    bool cert = __ballot(bad) == 0;
-    float prev_lo = 0.0f, total = 0.0f;
-    for (int k = 0; k < K; k++) {
-        float bm = key[0];
-        int bc = 0;
-#pragma unroll
-        for (int c = 1; c < C; c++)
-            if (key[c] > bm) {
-                bm = key[c];
-                bc = c;
-            }
-        const float gm = wave_max_dpp_f(bm);
-        int ek = -1;
-        float wk = -1e30f;
-        if (gm > -INFINITY) {  // fewer than K experts leave the rest at -1 (infer.c:1110-1113)
-            const int ls = __ffsll(__ballot(bm == gm)) - 1;
-            const int cs = __builtin_amdgcn_readlane(bc, ls);
-            float ml = lo[0], mh = hi[0], mp = pr[0];
-#pragma unroll
-            for (int c = 1; c < C; c++)
-                if (bc == c) {
-                    ml = lo[c];
-                    mh = hi[c];
-                    mp = pr[c];
-                }
-            const float lk = readlane_f(ml, ls), hk = readlane_f(mh, ls);
-            if (k > 0 && !(prev_lo > hk)) cert = false;
-            prev_lo = lk;
-            ek = ls + 64 * cs;
-            wk = readlane_f(mp, ls);
-            total = __fadd_rn(total, wk);
-#pragma unroll
-            for (int c = 0; c < C; c++)
-                if (tid == ls && c == cs) key[c] = -INFINITY;
-        }
-        if (tid == 0) {
-            sh.idx[k] = ek;
-            sh.wk[k] = wk;
-        }
-    }
-    // the last chosen must lie above every expert left out (chosen ones now hold -inf)
-    float rest = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < C; c++)
-        if (key[c] > -INFINITY) rest = fmaxf(rest, hi[c]);
-    rest = wave_max_dpp_f(rest);
-    if (rest > -INFINITY && !(prev_lo > rest)) cert = false;
-    if (tid == 0) {
-        sh.sel_ok = cert;
-        sh.total = total;
-    }
+    certified_select<C>(a.E, a.K, phase_tid(), w0, w1, keep_p ? sh.u.s.p : nullptr, sh.idx, sh.wk, &sh.sel_ok, &sh.total);
 }
 
 __device__ __attribute__((always_inline)) static bool sk_stage_select(const StackArgs &a, int li, bool keep_p,
@@ -401,136 +324,14 @@ __device__ __attribute__((always_inline)) static bool sk_stage_select(const Stac
     return true;
 }
 
-// glm.c's router replayed exactly in fp32 for layer li (infer.c:916-938, 1108-1145), by
-// the router block whose xn is in sh.xn_r, when the certified selection failed: the top-k
-// into sh.idx / sh.wk / sh.ws and every probability into sh.u.s.p.
+// glm.c's router replayed exactly (exact_router) for layer li, by the router block whose
+// xn is in sh.xn_r, when the certified selection failed: the top-k into sh.idx / sh.wk /
+// sh.ws and every probability into sh.u.s.p.
 __device__ static void sk_exact_select(const StackArgs &a, const StackLayer &L, SkShared &sh) {
-    const int D = a.D, E = a.E, K = a.K, tid = phase_tid();
-    const GM_GLOBAL float *bias = gbl(L.bias);
-    // infer.c:916-925 for 64 experts at a time, in tiles of SK_XT columns: every thread
-    // forms the products fl(g * xn) of one expert (its lane) and a quarter of the tile's
-    // columns (its wave) into prod[column][expert], then lane e of wave 0 adds its
-    // expert's products in column order. Each thread's gate rows are fetched two tiles
-    // ahead into registers, so the loads overlap the chain.
-    float(*prod)[64] = (float(*)[64])sh.dslice;  // [SK_XT][64]
-    const int lane = tid & 63, w = tid >> 6, qc = SK_XT / 4;  // columns per wave and tile
-    const int ntile = D / SK_XT;
-    for (int eb = 0; eb < E; eb += 64) {
-        const int ne = E - eb < 64 ? E - eb : 64;
-        const float4 *grow = (const float4 *)(L.gate_inp + (size_t)(eb + (lane < ne ? lane : 0)) * D + w * qc);
-        float4 ga[SK_XT / 16], gb[SK_XT / 16];
-#pragma unroll
-        for (int q = 0; q < SK_XT / 16; q++) ga[q] = grow[q];
-#pragma unroll
-        for (int q = 0; q < SK_XT / 16; q++) gb[q] = grow[SK_XT / 4 + q];
-        float chain = 0.0f;
-        // one tile from registers g (tile t), then g refilled with tile t + 2
-        auto tile = [&](float4 *g, int t) {
-            const int c0 = t * SK_XT + w * qc;
-#pragma unroll
-            for (int q = 0; q < SK_XT / 16; q++) {
-                const float4 xq = *(const float4 *)&sh.xn_r[c0 + 4 * q];
-                prod[w * qc + 4 * q + 0][lane] = __fmul_rn(g[q].x, xq.x);
-                prod[w * qc + 4 * q + 1][lane] = __fmul_rn(g[q].y, xq.y);
-                prod[w * qc + 4 * q + 2][lane] = __fmul_rn(g[q].z, xq.z);
-                prod[w * qc + 4 * q + 3][lane] = __fmul_rn(g[q].w, xq.w);
-            }
-            __syncthreads();
-            if (t + 2 < ntile)
-#pragma unroll
-                for (int q = 0; q < SK_XT / 16; q++) g[q] = grow[(t + 2) * (SK_XT / 4) + q];
-            if (w == 0) {
-                for (int c0 = 0; c0 < SK_XT; c0 += 16) {
-                    float v[16];  // sixteen reads in flight, then the sixteen dependent adds
-#pragma unroll
-                    for (int j = 0; j < 16; j++) v[j] = prod[c0 + j][lane];
-#pragma unroll
-                    for (int j = 0; j < 16; j++) chain = __fadd_rn(chain, v[j]);
-                }
-            }
-            __syncthreads();
-        };
-        for (int t = 0; t < ntile; t += 2) {  // ntile = D / 128 is even
-            tile(ga, t);
-            tile(gb, t + 1);
-        }
-        if (tid < ne) {
-            const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain)));
-            sh.u.s.p[eb + tid] = pr;
-            sh.u.s.sel[eb + tid] = __fadd_rn(pr, bias[eb + tid]);
-        }
-    }
-    __syncthreads();
-    // glm.c's insertion top-k (infer.c:1110-1135) keeps the K largest sel by (value desc,
-    // index asc) among values above -inf (NaN is never inserted): K wave-maximum rounds,
-    // the lowest lane winning ties, chunk c of lane l holding expert l + 64c.
-    if (w == 0) {
-        const int nch = (E + 63) >> 6;
-        float key[SK_SEL_C], pv[SK_SEL_C];
-#pragma unroll
-        for (int c = 0; c < SK_SEL_C; c++) {
-            const int e = lane + 64 * c;
-            const bool valid = c < nch && e < E;
-            const float v = valid ? sh.u.s.sel[e] : -INFINITY;
-            key[c] = v == v ? v : -INFINITY;
-            pv[c] = valid ? sh.u.s.p[e] : 0.0f;
-        }
-        float total = 0.0f;
-        bool unresolved = false;
-        for (int k = 0; k < K; k++) {
-            float bm = key[0];
-#pragma unroll
-            for (int c = 1; c < SK_SEL_C; c++) bm = fmaxf(bm, key[c]);
-            const float gm = wave_max_dpp_f(bm);
-            int ek = -1;
-            float wk = -1e30f;
-            if (gm > -INFINITY) {
-                // the lowest expert index holding the maximum: chunks in index order
-                int ls = -1, cs = 0;
-#pragma unroll
-                for (int c = 0; c < SK_SEL_C; c++) {
-                    const unsigned long long m = __ballot(key[c] == gm);
-                    if (ls < 0 && m != 0ull) {
-                        ls = __ffsll(m) - 1;
-                        cs = c;
-                    }
-                }
-                float mp = pv[0];
-#pragma unroll
-                for (int c = 1; c < SK_SEL_C; c++)
-                    if (cs == c) mp = pv[c];
-                ek = ls + 64 * cs;
-                wk = readlane_f(mp, ls);
-                total = __fadd_rn(total, wk);
-#pragma unroll
-                for (int c = 0; c < SK_SEL_C; c++)
-                    if (lane == ls && c == cs) key[c] = -INFINITY;
-                // libm's expf may differ from the GPU's by an ulp: flag orders decided that
-                // closely (any expert not yet chosen within a few ulps of this one)
-                const float tol = 4.0f * fmaxf(fabsf(gm), 1e-30f) * 0x1p-23f + 4.0f * 0x1p-24f;
-                bool close = false;
-#pragma unroll
-                for (int c = 0; c < SK_SEL_C; c++) close |= key[c] > -INFINITY && fabsf(key[c] - gm) <= tol;
-                unresolved |= __ballot(close) != 0;
-            }
-            if (lane == 0) {
-                sh.idx[k] = ek;
-                sh.wk[k] = wk;
-            }
-        }
-        if (lane == 0) {
-            atomicAdd(&a.stats[GM_STAT_ROUTE_EXACT], 1ull);
-            if (unresolved) atomicAdd(&a.stats[GM_STAT_UNRESOLVED], 1ull);
-            if (total > 0.0f) {
-                // normalisation of infer.c:1136-1145
-                const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
-                const float inv_d = __fdiv_rn(1.0f, denom);
-                for (int k = 0; k < K; k++) sh.wk[k] = __fmul_rn(sh.wk[k], inv_d);
-            }
-        }
-    }
-    __syncthreads();
-    if (tid < K) sh.ws[tid] = __fmul_rn(sh.wk[tid], a.routed_scale);
+    const int tid = phase_tid();
+    exact_router(a.D, a.E, a.K, tid, L.gate_inp, L.bias, sh.xn_r, (float(*)[64])sh.dslice, sh.u.s.p, sh.u.s.sel, sh.idx,
+                 sh.wk, a.stats);
+    if (tid < a.K) sh.ws[tid] = __fmul_rn(sh.wk[tid], a.routed_scale);
     __syncthreads();
 }
 

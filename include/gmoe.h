@@ -144,6 +144,8 @@ int gmoe_get_stats(gmoe_ctx *ctx, gmoe_stats *out);
 #define GMOE_KERNEL_DOWN 2       /* down products + combine + residual */
 #define GMOE_KERNEL_DISPATCH 3   /* per-expert token lists */
 #define GMOE_KERNEL_STACK 4      /* persistent decode kernel (T=1, all requested layers) */
+#define GMOE_KERNEL_DIGITS 5     /* prefill: activations to their int8 digit form */
+#define GMOE_KERNEL_COMBINE 6    /* prefill: per-token combine + residual */
 #define GMOE_KERNEL_COUNT 8
 typedef struct gmoe_kernel_times {
     int64_t launches[GMOE_KERNEL_COUNT];
