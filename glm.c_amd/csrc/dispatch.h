@@ -43,25 +43,35 @@ __global__ __launch_bounds__(DP_BLOCK) void k_dispatch(DispatchArgs a) {
     const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int total = a.T * a.K;
     int base = 0;
-    for (int a0 = 0; a0 < total; a0 += DP_BLOCK) {
-        const int i = a0 + tid;
-        const bool match = i < total && a.topk_idx[i] == e;
-        const unsigned long long bal = __ballot(match);
-        const int before = __popcll(bal & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_cnt[w] = __popcll(bal);
-        __syncthreads();
-        int wbase = 0;
-        for (int q = 0; q < w; q++) wbase += wave_cnt[q];
-        const int tot = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
-        if (match) {
-            const int pos = base + wbase + before;  // < T: a token selects an expert at most once
-            if (pos < a.T) {
-                a.tmp_tok[(size_t)e * a.T + pos] = i / a.K;
-                a.tmp_slot[(size_t)e * a.T + pos] = i % a.K;
-            }
+    for (int a0 = 0; a0 < total; a0 += DP_BLOCK * 8) {
+        // eight groups of DP_BLOCK assignments per pass, all eight loads in flight
+        int v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = a0 + u * DP_BLOCK + tid;
+            v[u] = i < total ? a.topk_idx[i] : -1;
         }
-        base += tot;
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = a0 + u * DP_BLOCK + tid;
+            const bool match = v[u] == e;
+            const unsigned long long bal = __ballot(match);
+            const int before = __popcll(bal & ((1ull << lane) - 1ull));
+            if (lane == 0) wave_cnt[w] = __popcll(bal);
+            __syncthreads();
+            int wbase = 0;
+            for (int q = 0; q < w; q++) wbase += wave_cnt[q];
+            const int tot = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+            if (match) {
+                const int pos = base + wbase + before;  // < T: a token selects an expert at most once
+                if (pos < a.T) {
+                    a.tmp_tok[(size_t)e * a.T + pos] = i / a.K;
+                    a.tmp_slot[(size_t)e * a.T + pos] = i % a.K;
+                }
+            }
+            base += tot;
+            __syncthreads();
+        }
     }
     if (tid == 0) a.counts[e] = base < a.T ? base : a.T;
     __threadfence();
@@ -70,18 +80,21 @@ __global__ __launch_bounds__(DP_BLOCK) void k_dispatch(DispatchArgs a) {
     __syncthreads();
     if (!s_last) return;
     __threadfence();
+    // every count in one parallel read, then the prefix in shared memory
+    for (int q = tid; q < a.E; q += DP_BLOCK) s_off[q + 1] = __hip_atomic_load(a.counts + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
     if (tid == 0) {
         *a.counter = 0u;
         int off = 0;
         for (int q = 0; q < a.E; q++) {
+            const int n = s_off[q + 1];
             s_off[q] = off;
-            a.offsets[q] = off;
-            off += a.counts[q];
+            off += n;
         }
         s_off[a.E] = off;
-        a.offsets[a.E] = off;
     }
     __syncthreads();
+    for (int q = tid; q <= a.E; q += DP_BLOCK) a.offsets[q] = s_off[q];
     for (int i = tid; i < a.T * a.K; i += DP_BLOCK) a.pair_row[i] = -1;
     __syncthreads();
     // pack: every thread takes up to 8 list positions at a time, all of whose loads are

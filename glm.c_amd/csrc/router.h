@@ -351,8 +351,7 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
     }
     __syncthreads();
 
-    // the lane's columns of xn in registers; the gate rows are read per expert (several
-    // blocks per CU hide the latency)
+    // the lane's columns of xn in registers, and each expert's gate row one expert ahead
     float xr[RT_CPL_MAX];
 #pragma unroll
     for (int q = 0; q < RT_CPL_MAX / 4; q++) {
@@ -362,16 +361,22 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
         xr[4 * q + 2] = v.z;
         xr[4 * q + 3] = v.w;
     }
+    auto load_row = [&](int e, float4 *g) {
+        const float4 *src = (const float4 *)(a.gate_inp + (size_t)(e < E ? e : 0) * D + lane * cpl);
+#pragma unroll
+        for (int q = 0; q < RT_CPL_MAX / 4; q++) g[q] = q < cpl / 4 ? src[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    float4 gc[RT_CPL_MAX / 4], gn[RT_CPL_MAX / 4];
+    load_row(w, gc);
     for (int e = w; e < E; e += 4) {
+        load_row(e + 4, gn);
         float g[RT_CPL_MAX];
-        const float4 *src = (const float4 *)(a.gate_inp + (size_t)e * D + lane * cpl);
 #pragma unroll
         for (int q = 0; q < RT_CPL_MAX / 4; q++) {
-            const float4 v = q < cpl / 4 ? src[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-            g[4 * q] = v.x;
-            g[4 * q + 1] = v.y;
-            g[4 * q + 2] = v.z;
-            g[4 * q + 3] = v.w;
+            g[4 * q] = gc[q].x;
+            g[4 * q + 1] = gc[q].y;
+            g[4 * q + 2] = gc[q].z;
+            g[4 * q + 3] = gc[q].w;
         }
         // xn stays 32 floats: kept opaque here so that its fp64 conversions are not
         // hoisted out of the loop as 32 live doubles
@@ -413,6 +418,8 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
             s_w0[e] = (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32);
             s_w1[e] = (unsigned long long)__float_as_uint(1.0f / (1.0f + expf(-(float)S)));
         }
+#pragma unroll
+        for (int q = 0; q < RT_CPL_MAX / 4; q++) gc[q] = gn[q];
     }
     __syncthreads();
 
