@@ -236,7 +236,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 
 
 def prefill(args, gmoe, np):
-    """One MoE layer over T tokens (SURVEY configs 3 and 4): router, dispatch, grouped
+    """One MoE layer over T tokens (T=512 with N(0, 0.01) router bias, or T=128 with the
+    Zipf(1.2) bias): router, dispatch, grouped
     gate/up and down GEMMs, combine. Steps rotate over --prefill-layers seeded layers so
     that no layer's 650 MB of touched experts is still cached from the step before."""
     shape = gmoe.GLM47_FLASH

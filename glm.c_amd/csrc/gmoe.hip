@@ -1,11 +1,17 @@
 // gmoe.hip -- C ABI of the MI355X MoE FFN library (include/gmoe.h).
 //
-// One forward of a MoE layer is three kernels on the caller's stream:
-//   k_norm_router   grid (E, T)        rmsnorm, router logits, certified top-k (router.h)
-//   k_gate_up       grid (F/16, K+1, T) gate/up products and SwiGLU (experts.h)
-//   k_down_combine  grid (D/16, K+1, T) down products, weighted combine, residual (experts.h)
-// plus k_dispatch (dispatch.h) for the per-expert token lists. Expert weights are
-// uploaded once per layer into the tiled Q8_0 layout of common.h and stay resident.
+// A decode call (T=1) is one persistent launch, k_moe_stack (stack.h), that takes
+// the token through any run of layers. A batch (T>1) runs per layer:
+//   k_router_tok    grid (T)               rmsnorm, router logits, certified top-k (router.h)
+//   k_act_split     grid (rows)            xn as fp16 hi+lo planes with a per-row exponent (grouped.h)
+//   k_dispatch      grid (E)               exact per-expert token lists and GEMM tiles (dispatch.h)
+//   k_group_gu      grid (F/64, tiles)     grouped gate/up GEMM + SwiGLU on fp16 MFMA (grouped.h)
+//   k_act_split     grid (rows)            h as fp16 hi+lo planes
+//   k_group_down    grid (D/64, tiles)     grouped down GEMM, one row per (token, slot) (grouped.h)
+//   k_token_combine grid (D/256, T)        weighted combine + shared expert + residual (grouped.h)
+// With GMOE_GROUPED_MIN_T above T, batches take the per-token kernels k_gate_up and
+// k_down_combine (experts.h) instead. Expert weights are uploaded once per layer
+// into the tiled Q8_0 layout of common.h and stay resident.
 #include "gmoe.h"
 
 #include <stdarg.h>

@@ -1,6 +1,6 @@
 // grouped.h -- prefill (T > 1): the expert products as grouped GEMMs over the per-expert
-// token lists (the lists that glm.c never materialises, since it
-// routes prompt tokens one at a time, infer.c:2190-2233).
+// token lists (lists that glm.c never materialises, since it routes prompt tokens one at
+// a time, infer.c:2190-2233).
 //
 // Per layer: the router (router.h) and the dispatch (dispatch.h, which also cuts every
 // list into tiles of GP_TOK tokens) run first. Then
