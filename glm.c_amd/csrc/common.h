@@ -128,6 +128,14 @@ __device__ static inline float wave_max_dpp_f(float v) {
     return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
+// Maximum over each 16-lane row of a wave, returned to every lane of the row, by DPP.
+__device__ static inline float row_max_dpp_f(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_QUAD_1032, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_QUAD_2301, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_ROW_HALF_MIRROR, 0xF, 0xF, false)));
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(-INFINITY), __float_as_int(v), DPP_ROW_MIRROR, 0xF, 0xF, false)));
+}
+
 // Inclusive prefix sum over the lanes of a wave, in lane order.
 __device__ static inline double wave_incl_scan_dpp(double v) {
     v += dpp_d<DPP_ROW_SHR(1)>(v, 0.0);

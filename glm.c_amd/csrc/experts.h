@@ -171,6 +171,25 @@ __device__ static inline void panel_load_q(PanelRegs<NMAT, NB> &r, const uint8_t
         }
 }
 
+// panel_load_q without branches: exactly NB loads per matrix and wave whatever cols is
+// (chunks past cpw reload the wave's first chunk; their scales must be zero), so that the
+// compiler can wait for chunk u's loads alone.
+template <int NMAT, int NB>
+__device__ static inline void panel_load_q_all(PanelRegs<NMAT, NB> &r, const uint8_t *q0, const uint8_t *q1, int p,
+                                               int cols) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int nchunks = cols >> 6, cpw = nchunks >> 2;
+    const int j0 = w * cpw;
+    const uint8_t *qs[2] = {q0, q1};
+    const GM_GLOBAL u32x4 *qp[2];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) qp[m] = gbl((const u32x4 *)(qs[m] + ((size_t)p * nchunks + j0) * GM_CHUNK_BYTES)) + lane;
+#pragma unroll
+    for (int u = 0; u < NB; u++)
+#pragma unroll
+        for (int m = 0; m < NMAT; m++) r.q[m][u] = __builtin_nontemporal_load(qp[m] + (size_t)(u < cpw ? u : 0) * 64);
+}
+
 // panel_compute with the panel's fp16 scales in shared memory: sc[m] holds matrix m's
 // [16 rows][cols/32] scales of the panel.
 template <int NMAT, int NB>

@@ -137,6 +137,13 @@ __device__ static inline void st_u64(unsigned long long *p, unsigned long long v
 }
 __device__ static inline unsigned ld_u(const unsigned *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
+// One trace stamp (the 100 MHz wall clock) at t[idx], through a global rather than a flat
+// store: a flat store also counts against lgkmcnt, so the wave's next shared-memory wait
+// would wait for the store to reach memory, and the stamp would slow what it measures.
+__device__ static inline void trace_put(unsigned long long *t, long idx) {
+    *(GM_GLOBAL unsigned long long *)(t + idx) = wall_clock64();
+}
+
 struct SkShared {
     union {
         struct {  // router item
@@ -166,6 +173,8 @@ struct SkShared {
     float mean, total;
     unsigned old;
     int ok, sel_ok;
+    unsigned zero;  // 0 for the kernel's life (an always-zero operand of gu_products)
+    int xe_local;   // exponent of a routed block's own digits of xn (sk_local_digits)
     int idx[GM_MAX_K];
     float wk[GM_MAX_K], ws[GM_MAX_K];
     long trace_item;
@@ -211,7 +220,7 @@ __device__ static inline bool spin_ge(const unsigned *c, unsigned target, int *e
 __device__ static inline bool wait_ge(const unsigned *c, unsigned target, int *error, SkShared &sh) {
     if (threadIdx.x == 0) {
         sh.ok = spin_ge(c, target, error);
-        if (sh.trace) sh.trace[SK_TRACE_STAMPS * sh.trace_item + 1] = wall_clock64();
+        if (sh.trace) trace_put(sh.trace, SK_TRACE_STAMPS * sh.trace_item + 1);
     }
     __syncthreads();
     return sh.ok != 0;
@@ -228,7 +237,7 @@ __device__ static inline int phase_tid() {
 
 // Diagnostic stamp k of the current item (thread 0, when tracing).
 __device__ static inline void sk_stamp(SkShared &sh, int k) {
-    if (sh.trace && threadIdx.x == 0) sh.trace[SK_TRACE_STAMPS * sh.trace_item + k] = wall_clock64();
+    if (sh.trace && threadIdx.x == 0) trace_put(sh.trace, SK_TRACE_STAMPS * sh.trace_item + k);
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -241,6 +250,15 @@ __device__ static inline void dma_copy(void *dst, const void *src, int nbytes) {
         if (off + 16 * lane < nbytes)
             __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)gbl((const uint8_t *)src + off + 16 * lane),
                                              (lds_void *)((uint8_t *)dst + off), 16, 0, 0);
+}
+
+// dma_copy's 16-byte piece issued by inline assembly, which the compiler does not see as a
+// shared-memory DMA: with a global_load_lds of its own in flight, the compiler waits for
+// all of a wave's loads before using any loaded register, which would serialise the
+// streamed expert weights behind it. The caller waits (vmcnt) before reading `dst`.
+__device__ static inline void dma16_untracked(const GM_GLOBAL void *src, lds_void *dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)dst);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
 }
 
 // ---------------------------------------------------------------- top-k selection
@@ -298,7 +316,7 @@ __device__ __attribute__((always_inline)) static bool sk_stage_select(const Stac
             }
             __builtin_amdgcn_s_sleep(1);
         }
-        if (sh.trace && tid == 0) sh.trace[SK_TRACE_STAMPS * sh.trace_item + 8] = wall_clock64();
+        if (sh.trace && tid == 0) trace_put(sh.trace, SK_TRACE_STAMPS * sh.trace_item + 8);
         if (nch == 1)
             sk_select_rounds<1>(a, w0, w1, keep_p, sh);
         else
@@ -373,6 +391,41 @@ __device__ static inline Seg load_seg(P p, int per) {
     return r;
 }
 
+// ---------------------------------------------------------------- rmsnorm
+//
+// 1 / sqrt(mean + eps) of glm.c's rmsnorm (infer.c:746-752) for the thread's D/256
+// consecutive values xv of x: mean = (float)(sum / D) of the sequential fp64 sum of squares,
+// certified from the parallel sum (whose relative error is below D * 2^-52), else replayed
+// in order by thread 0 from `scratch` (D floats of shared memory). `stat`: count a replay.
+__device__ __attribute__((always_inline)) static float sk_inv_rms(const StackArgs &a, const float *xv, float *scratch,
+                                                                  bool stat, SkShared &sh) {
+    const int D = a.D, per = D / SK_BLOCK, tid = phase_tid();
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < SK_PER_MAX; j++)
+        if (j < per) ss += (double)xv[j] * (double)xv[j];
+    ss = block_sum_fast(ss, sh.red);
+    const double v = ss / (double)D, rho = (double)D * 0x1p-52;
+    const float mlo = (float)(v * (1.0 - rho)), mhi = (float)(v * (1.0 + rho));
+    float mean = mlo;
+    if (mlo != mhi) {
+#pragma unroll
+        for (int j = 0; j < SK_PER_MAX; j++)
+            if (j < per) scratch[tid * per + j] = xv[j];
+        __syncthreads();
+        if (tid == 0) {
+            double sq = 0.0;
+            for (int i = 0; i < D; i++) sq += (double)scratch[i] * (double)scratch[i];
+            sh.mean = (float)(sq / (double)D);
+            if (stat) atomicAdd(&a.stats[GM_STAT_NORM_EXACT], 1ull);
+        }
+        __syncthreads();
+        mean = sh.mean;
+        __syncthreads();
+    }
+    return __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
+}
+
 // ---------------------------------------------------------------- router item
 //
 // Block b: rmsnorm of x (every router block, bit-identical to infer.c:746-752) and the
@@ -393,6 +446,8 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     // would queue the other block (an expert item) behind them for microseconds.
     if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_PART)], 1u, a.error, sh)) return false;
     const Seg nw = load_seg(gbl(L.norm) + tid * per, per);
+    // the selection biases of this block's experts, for lanes 3x of the bound tail below
+    const float bias_x = tid < 3 * nx ? gbl(L.bias)[b + (tid / 3) * NR] : 0.0f;
     Seg gw[SK_RX_MAX];
 #pragma unroll
     for (int x = 0; x < SK_RX_MAX; x++) {
@@ -406,33 +461,8 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_X)], 1u, a.error, sh)) return false;
     Seg xs = load_seg((li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x)) + tid * per, per);
     float *xv = xs.v;
-    double ss = 0.0;
-#pragma unroll
-    for (int j = 0; j < SK_PER_MAX; j++)
-        if (j < per) ss += (double)xv[j] * (double)xv[j];
-    ss = block_sum_fast(ss, sh.red);
+    const float inv = sk_inv_rms(a, xv, sh.xn_r, b == 0, sh);
     sk_stamp(sh, 11);
-    // mean = (float)(sum / D) of the sequential fp64 sum: certified from the parallel sum
-    // (its relative error is below D * 2^-52), else replayed in order
-    const double v = ss / (double)D, rho = (double)D * 0x1p-52;
-    const float mlo = (float)(v * (1.0 - rho)), mhi = (float)(v * (1.0 + rho));
-    float mean = mlo;
-    if (mlo != mhi) {
-#pragma unroll
-        for (int j = 0; j < SK_PER_MAX; j++)
-            if (j < per) sh.xn_r[tid * per + j] = xv[j];
-        __syncthreads();
-        if (tid == 0) {
-            double sq = 0.0;
-            for (int i = 0; i < D; i++) sq += (double)sh.xn_r[i] * (double)sh.xn_r[i];
-            sh.mean = (float)(sq / (double)D);
-            if (b == 0) atomicAdd(&a.stats[GM_STAT_NORM_EXACT], 1ull);
-        }
-        __syncthreads();
-        mean = sh.mean;
-        __syncthreads();
-    }
-    const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
 #pragma unroll
     for (int j = 0; j < SK_PER_MAX; j++) xv[j] = j < per ? __fmul_rn(__fmul_rn(xv[j], inv), nw.v[j]) : 0.0f;
 
@@ -446,7 +476,6 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     mloc = (float)wave_max_dpp((double)mloc);
     if (lane == 0) sh.mxw[w] = mloc;
     __syncthreads();
-
     // Products in fp64 are exact (24 + 24 bits). Pass 1: this thread's segment sums and
     // the block-wide exclusive prefix, in column order.
     double sabs[SK_RX_MAX] = {0.0}, pre[SK_RX_MAX] = {0.0};
@@ -505,7 +534,7 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
         const float phi = __shfl_down(sg, 1, 64), p = __shfl_down(sg, 2, 64);
         if (r == 0 && tid / 3 < nx) {
             double lo, hi;
-            selection_bounds((double)sg, (double)phi, L.bias[e], &lo, &hi);
+            selection_bounds((double)sg, (double)phi, bias_x, &lo, &hi);
             float lo_f = __double2float_rd(lo), hi_f = __double2float_ru(hi);
             if (!(lo_f <= hi_f)) {  // NaN: an interval that is never certified
                 lo_f = -INFINITY;
@@ -602,7 +631,7 @@ __device__ static inline bool sk_read_topk(const StackArgs &a, int li, SkShared 
                 if (4 * wd + q < a.K) sh.idx[4 * wd + q] = (int)((v >> (16 * q)) & 0xffffu) - 2;
         }
         sh.ok = ok;
-        if (sh.trace) sh.trace[SK_TRACE_STAMPS * sh.trace_item + 8] = wall_clock64();
+        if (sh.trace) trace_put(sh.trace, SK_TRACE_STAMPS * sh.trace_item + 8);
     }
     __syncthreads();
     return sh.ok != 0;
@@ -622,6 +651,48 @@ __device__ static inline bool sk_read_weights(const StackArgs &a, int li, SkShar
     return true;
 }
 
+// ---------------------------------------------------------------- a routed block's own digits
+//
+// xn of layer li in its digit form, computed by a routed block itself while the router
+// blocks run: the same rmsnorm of the same x, so the same xn as theirs. The digits go to
+// sh.xn_r's space as [3][D] int8 (thread t: columns 8t .. 8t + 7), the exponent to
+// sh.xe_local. The block's expert items then wait for nothing of the router's but the
+// routing, and their weight requests have nothing queued ahead of them. D == GM_MAX_COLS.
+__device__ __attribute__((always_inline)) static bool sk_local_digits(const StackArgs &a, const StackLayer &L, int li,
+                                                                     SkShared &sh) {
+    const int D = a.D, per = D / SK_BLOCK, tid = phase_tid(), lane = tid & 63, w = tid >> 6;
+    const Seg nw = load_seg(gbl(L.norm) + tid * per, per);
+    if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_X)], 1u, a.error, sh)) return false;
+    Seg xs = load_seg((li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x)) + tid * per, per);
+    float *xv = xs.v;
+    const float inv = sk_inv_rms(a, xv, (float *)sh.dslice, false, sh);
+    float mloc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SK_PER_MAX; j++) {
+        xv[j] = __fmul_rn(__fmul_rn(xv[j], inv), nw.v[j]);
+        mloc = fmaxf(mloc, fabsf(xv[j]));
+    }
+    mloc = wave_max_dpp_f(mloc);
+    if (lane == 0) sh.mxw[w] = mloc;
+    __syncthreads();
+    const int ex = digit_exponent(fmaxf(fmaxf(sh.mxw[0], sh.mxw[1]), fmaxf(sh.mxw[2], sh.mxw[3])));
+    unsigned long long w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+    for (int j = 0; j < SK_PER_MAX; j++) {
+        int8_t d0, d1, d2;
+        split_digits(xv[j], ex, &d0, &d1, &d2);
+        w0 |= (unsigned long long)(uint8_t)d0 << (8 * j);
+        w1 |= (unsigned long long)(uint8_t)d1 << (8 * j);
+        w2 |= (unsigned long long)(uint8_t)d2 << (8 * j);
+    }
+    unsigned long long *dig = (unsigned long long *)sh.xn_r;
+    dig[tid] = w0;
+    dig[D / 8 + tid] = w1;
+    dig[2 * (D / 8) + tid] = w2;
+    if (tid == 0) sh.xe_local = ex;
+    return true;  // the routing wait that follows ends with a barrier
+}
+
 // ---------------------------------------------------------------- expert item
 //
 // Gate and up rows [16j, 16j+16) of one expert dotted with xn, in units of 2^e where e is
@@ -629,11 +700,56 @@ __device__ static inline bool sk_read_weights(const StackArgs &a, int li, SkShar
 // chunks [w*cpw, (w+1)*cpw) held in `r`; each 32-column block is one MFMA per matrix (A =
 // the three digit rows, B = the 16 weight rows), whose int dots lanes 0..15 turn into their
 // row's fp32 block dot and scale by the block's fp16 scale (scg, scu: [16 rows][cols/32]).
-// Every operand is read before the first product, with no branches: chunks past cpw (cols
-// below 2048) get zero digits and zero scales. Lanes 0..15 return their row's sums.
+// Rows 3..15 of A do not reach rows 0..2 of the product, so lanes 3..15 read digit row 0
+// unmasked. Chunks past cpw (cols below 2048) read chunk 0's digits with zero scales
+// (`zero`: a shared word that holds 0). The digits and scales are read before the first
+// product; chunk u's products are then done before chunk u + 1's weights are touched, so
+// that while the weights are still arriving each chunk waits only for its own loads.
+// Lanes 0..15 return their row's sums.
+// The gate/up products from register operands: A[u] = the two 8-byte digit pieces of
+// chunk u for this lane (row lane & 15, column group lane >> 4), sg[u] and su[u] = the fp16
+// scales of chunk u's two blocks for row lane & 15. Chunk u's products and their sums are
+// done before chunk u + 1's weights are touched, so that while the weights are still
+// arriving each chunk waits only for its own loads. Lanes 0..15 return their row's sums.
+template <int NB>
+__device__ static inline void gu_products_r(const PanelRegs<2, NB> &r, const long (&A)[NB][2], const unsigned (&sg)[NB],
+                                            const unsigned (&su)[NB], float out[2]) {
+    float ag = 0.0f, au = 0.0f;
+    u32x4 qg = r.q[0][0], qu = r.q[1][0];
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const v4i g0 = mfma_digits(A[u][0], chunk_half(qg, 0));
+        const v4i g1 = mfma_digits(A[u][1], chunk_half(qg, 1));
+        const v4i u0 = mfma_digits(A[u][0], chunk_half(qu, 0));
+        const v4i u1 = mfma_digits(A[u][1], chunk_half(qu, 1));
+        ag = fmaf(digits_to_float(g0[0], g0[1], g0[2]), __half2float(__ushort_as_half((unsigned short)(sg[u] & 0xffffu))), ag);
+        ag = fmaf(digits_to_float(g1[0], g1[1], g1[2]), __half2float(__ushort_as_half((unsigned short)(sg[u] >> 16))), ag);
+        au = fmaf(digits_to_float(u0[0], u0[1], u0[2]), __half2float(__ushort_as_half((unsigned short)(su[u] & 0xffffu))), au);
+        au = fmaf(digits_to_float(u1[0], u1[1], u1[2]), __half2float(__ushort_as_half((unsigned short)(su[u] >> 16))), au);
+        // the sums here on every lane (not sunk to the lanes that use them), and chunk u + 1's
+        // weights taken only now (so that its products are not hoisted above these)
+        if (u + 1 < NB) {
+            qg = r.q[0][u + 1];
+            qu = r.q[1][u + 1];
+        }
+        asm volatile("" : "+v"(ag), "+v"(au), "+v"(qg), "+v"(qu));
+    }
+    out[0] = ag;
+    out[1] = au;
+}
+
+// Gate and up rows [16j, 16j+16) of one expert dotted with xn, in units of 2^e where e is
+// the single exponent of xn's digit form `dig` ([3][cols] int8, in shared memory). Wave w
+// takes the 64-column chunks [w*cpw, (w+1)*cpw) held in `r`; each 32-column block is one
+// MFMA per matrix (A = the three digit rows, B = the 16 weight rows), whose int dots lanes
+// 0..15 turn into their row's fp32 block dot and scale by the block's fp16 scale (scg, scu:
+// [16 rows][cols/32], in shared memory). Rows 3..15 of A do not reach rows 0..2 of the
+// product, so lanes 3..15 read digit row 0 unmasked. Chunks past cpw (cols below 2048) read
+// chunk 0's digits with zero scales (`zero`: a shared word that holds 0).
 template <int NB>
 __device__ static inline void gu_products(const PanelRegs<2, NB> &r, int cols, const int8_t *dig,
-                                          const unsigned short *scg, const unsigned short *scu, float out[2]) {
+                                          const unsigned short *scg, const unsigned short *scu, const unsigned *zero,
+                                          float out[2]) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int cpw = cols >> 8, j0 = w * cpw, nblocks = cols >> 5;
     const int m = lane & 15;
@@ -645,72 +761,98 @@ __device__ static inline void gu_products(const PanelRegs<2, NB> &r, int cols, c
 #pragma unroll
     for (int u = 0; u < NB; u++) {
         const bool on = u < cpw;
-        const long a0 = *(const long *)(drow + 64 * u), a1 = *(const long *)(drow + 64 * u + 32);
-        A[u][0] = (on && m < 3) ? a0 : 0;
-        A[u][1] = (on && m < 3) ? a1 : 0;
-        const unsigned g = pg[u], v = pu[u];
-        sg[u] = on ? g : 0u;
-        su[u] = on ? v : 0u;
+        A[u][0] = *(const long *)(drow + 64 * (on ? u : 0));
+        A[u][1] = *(const long *)(drow + 64 * (on ? u : 0) + 32);
+        sg[u] = *(on ? pg + u : zero);
+        su[u] = *(on ? pu + u : zero);
     }
-    float ag = 0.0f, au = 0.0f;
-#pragma unroll
-    for (int u = 0; u < NB; u++) {
-        const v4i g0 = mfma_digits(A[u][0], chunk_half(r.q[0][u], 0));
-        const v4i g1 = mfma_digits(A[u][1], chunk_half(r.q[0][u], 1));
-        const v4i u0 = mfma_digits(A[u][0], chunk_half(r.q[1][u], 0));
-        const v4i u1 = mfma_digits(A[u][1], chunk_half(r.q[1][u], 1));
-        ag = fmaf(digits_to_float(g0[0], g0[1], g0[2]), __half2float(__ushort_as_half((unsigned short)(sg[u] & 0xffffu))), ag);
-        ag = fmaf(digits_to_float(g1[0], g1[1], g1[2]), __half2float(__ushort_as_half((unsigned short)(sg[u] >> 16))), ag);
-        au = fmaf(digits_to_float(u0[0], u0[1], u0[2]), __half2float(__ushort_as_half((unsigned short)(su[u] & 0xffffu))), au);
-        au = fmaf(digits_to_float(u1[0], u1[1], u1[2]), __half2float(__ushort_as_half((unsigned short)(su[u] >> 16))), au);
-    }
-    out[0] = ag;
-    out[1] = au;
+    gu_products_r<NB>(r, A, sg, su, out);
 }
 
 // Rows [16j, 16j+16) of F for expert e in `slot` (-1: idle slot, nothing to compute):
 // g, u = gate, up rows . xn (infer.c:1184-1185, 1199-1200), h = silu(g) * u (:1188, :1202),
 // and the partial y = down[:, 16j..16j+16) . h over all D rows (:1190, :1205), stored at
 // ypart[slot][j]. Thread t owns the down rows t + 256 i.
+// LOCAL (routed items, whose block computed xn's digits itself, sk_local_digits) on a
+// full-width layer: the gate/up chunks are the last requests, and the products of chunk u
+// start as soon as chunk u has arrived. Otherwise (shared items, which start before xn
+// exists, and narrower layers) the weights are requested first and the router blocks'
+// digits once the DIG flag is seen.
+template <bool LOCAL>
 __device__ __attribute__((always_inline)) static bool sk_expert_item(const StackArgs &a, const StackLayer &L, int li,
                                                                      int slot, int j, int e, SkShared &sh) {
     const int D = a.D, F = a.F, NPF = F >> 4, tid = phase_tid();
     if (e >= 0) {
         const uint8_t *base = L.experts + (size_t)e * a.stride;
-        // Every weight of the item is requested before anything waits: the gate/up chunks to
-        // registers, the down slice and all scales straight to shared memory, one 16-byte load
-        // per lane (row t + 256 i of the slice lands at dslice[t + 256 i]).
         const int c = D / SK_BLOCK, wave0 = tid & ~63, lane = tid & 63, w = tid >> 6;
-        {
-            // gate then up scales of panel j (D bytes each, contiguous in their s planes),
-            // then the down scales of column block j/2 (one fp16 per row, 2D bytes)
-            const int o = 1024 * w + 16 * lane;
+        const GM_GLOBAL u32x4 *qs = gbl((const u32x4 *)(base + a.off_dq)) + (size_t)j * D + tid;
+        const int o = 1024 * w + 16 * lane;  // this lane's 16 bytes of the item's scale runs
+        PanelRegs<2, EX_NB_MAX> pr;
+        float gu[2];
+        int xe;  // the exponent of all of xn's digits
+        if (LOCAL && D == GM_MAX_COLS) {
+            // The down scales and the down slice go to shared memory first (row t + 256 i of
+            // the slice lands at dslice[t + 256 i]), by DMA that the compiler does not count,
+            // then the gate/up scales and chunks to registers: the compiler then waits for each
+            // chunk by itself.
+            const int m = lane & 15, j0 = w * EX_NB_MAX;
+            dma16_untracked(gbl(base + a.off_ds + (size_t)(j >> 1) * D * 2 + o),
+                            (lds_void *)((uint8_t *)sh.sc_d + 1024 * w));  // o < 2 D here
+#pragma unroll
+            for (int i = 0; i < SK_PER_MAX; i++)
+                dma16_untracked(qs + (size_t)i * SK_BLOCK, (lds_void *)(sh.dslice + i * SK_BLOCK + wave0));
+            // row m's scales of blocks 2 j0 .. 2 j0 + 15 (panel j's plane is [16 rows][D/32])
+            const size_t so = (size_t)j * D + (size_t)m * (D / 16) + 4 * j0;
+            const GM_GLOBAL u32x4 *pg = gbl((const u32x4 *)(base + a.off_gs + so));
+            const GM_GLOBAL u32x4 *pu = gbl((const u32x4 *)(base + a.off_us + so));
+            const u32x4 g0 = pg[0], g1 = pg[1], u0 = pu[0], u1 = pu[1];
+            __builtin_amdgcn_sched_barrier(0);  // the scales are requested before the chunks
+            panel_load_q_all<2, EX_NB_MAX>(pr, base + a.off_gq, base + a.off_uq, j, D);
+            __builtin_amdgcn_sched_barrier(0);  // every request issued before any product
+            // the block's own digits (rows 3..15 of A do not reach the sums: lanes m >= 3
+            // read row 0)
+            const int8_t *drow = (const int8_t *)sh.xn_r + (m < 3 ? m : 0) * D + 64 * j0 + 8 * (lane >> 4);
+            long A[EX_NB_MAX][2];
+#pragma unroll
+            for (int u = 0; u < EX_NB_MAX; u++) {
+                A[u][0] = *(const long *)(drow + 64 * u);
+                A[u][1] = *(const long *)(drow + 64 * u + 32);
+            }
+            const unsigned sg[EX_NB_MAX] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            const unsigned su[EX_NB_MAX] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            gu_products_r<EX_NB_MAX>(pr, A, sg, su, gu);
+            xe = sh.xe_local;
+            // the down slice and scales (not counted by the compiler) are in shared memory
+            // before the barrier below
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        } else {
+            // Every weight of the item is requested before anything waits: the gate/up chunks
+            // to registers, the down slice and all scales straight to shared memory. The
+            // digits follow once the DIG flag is seen.
             if (o < 2 * D) {
+                // gate then up scales of panel j (D bytes each, contiguous in their s planes),
+                // then the down scales of column block j/2 (one fp16 per row, 2D bytes)
                 const uint8_t *src = o < D ? base + a.off_gs + (size_t)j * D + o : base + a.off_us + (size_t)j * D + (o - D);
                 __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)gbl(src), (lds_void *)((uint8_t *)sh.sc_gu + 1024 * w),
                                                  16, 0, 0);
                 __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)gbl(base + a.off_ds + (size_t)(j >> 1) * D * 2 + o),
                                                  (lds_void *)((uint8_t *)sh.sc_d + 1024 * w), 16, 0, 0);
             }
-        }
-        PanelRegs<2, EX_NB_MAX> pr;
-        panel_load_q<2, EX_NB_MAX>(pr, base + a.off_gq, base + a.off_uq, j, D);
-        {
-            const GM_GLOBAL u32x4 *qs = gbl((const u32x4 *)(base + a.off_dq)) + (size_t)j * D + tid;
+            panel_load_q<2, EX_NB_MAX>(pr, base + a.off_gq, base + a.off_uq, j, D);
 #pragma unroll
             for (int i = 0; i < SK_PER_MAX; i++)
                 if (i < c)
                     __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)(qs + (size_t)i * SK_BLOCK),
                                                      (lds_void *)(sh.dslice + i * SK_BLOCK + wave0), 16, 0, 0);
+            if (!wait_ge(&a.ctr[SKF(li, SKF_DIG)], 1u, a.error, sh)) return false;  // digits of xn ready
+            dma_copy(sh.u.g.dig, ws_at<unsigned long long>(a, li, a.o.dig), 3 * D);
+            dma_copy(sh.u.g.dexp, ws_at<int>(a, li, a.o.dexp), D / 8);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();  // every wave's digits, scales and slice rows are in shared memory
+            sk_stamp(sh, 6);
+            gu_products<EX_NB_MAX>(pr, D, sh.u.g.dig, sh.sc_gu, sh.sc_gu + D / 2, &sh.zero, gu);
+            xe = sh.u.g.dexp[0];
         }
-        if (!wait_ge(&a.ctr[SKF(li, SKF_DIG)], 1u, a.error, sh)) return false;  // digits of xn ready
-        dma_copy(sh.u.g.dig, ws_at<unsigned long long>(a, li, a.o.dig), 3 * D);
-        dma_copy(sh.u.g.dexp, ws_at<int>(a, li, a.o.dexp), D / 8);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();  // every wave's digits, scales and slice rows are in shared memory
-        sk_stamp(sh, 6);
-        float gu[2];
-        gu_products<EX_NB_MAX>(pr, D, sh.u.g.dig, sh.sc_gu, sh.sc_gu + D / 2, gu);
         if (lane < 16) {
             sh.u.g.part[w][0][lane] = gu[0];
             sh.u.g.part[w][1][lane] = gu[1];
@@ -718,16 +860,10 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
         __syncthreads();
         if (tid < 16) {
             // SwiGLU of the 16 rows, then their digit form with one exponent
-            const int xe = sh.u.g.dexp[0];  // the exponent of all of xn's digits
             const float g = ldexpf(((sh.u.g.part[0][0][tid] + sh.u.g.part[1][0][tid]) + sh.u.g.part[2][0][tid]) + sh.u.g.part[3][0][tid], xe);
             const float u = ldexpf(((sh.u.g.part[0][1][tid] + sh.u.g.part[1][1][tid]) + sh.u.g.part[2][1][tid]) + sh.u.g.part[3][1][tid], xe);
             const float h = g / (1.0f + expf(-g)) * u;
-            float mx = fabsf(h);
-            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
-            const int ex = digit_exponent(mx);
+            const int ex = digit_exponent(row_max_dpp_f(fabsf(h)));
             int8_t d0, d1, d2;
             split_digits(h, ex, &d0, &d1, &d2);
             int8_t *hb = (int8_t *)sh.u.g.hd;
@@ -744,11 +880,25 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
         const int hexp = sh.u.g.hexp;
         // partials in combine order: [D/8 chunks][F/16][K+1 slots][8 rows]
         const int NS = a.K + 1;
-        float *yp = ws_at<float>(a, li, a.o.ypart) + ((size_t)j * NS + slot) * SK_CROWS + (tid & (SK_CROWS - 1));
+        // row r = 256 i + t goes to combine chunk r / 8 = 32 i + t / 8, at [chunk][j][slot][r % 8]
+        const size_t ychunk = (size_t)NS * NPF * SK_CROWS;
+        float *yp = ws_at<float>(a, li, a.o.ypart) + ((size_t)j * NS + slot) * SK_CROWS + (tid & (SK_CROWS - 1)) +
+                    (size_t)(tid / SK_CROWS) * ychunk;
+        // every slice row and scale of this thread is read before the first product (rows
+        // past D read shared memory that is never used), so the reads cost one latency
+        u32x4 dqs[SK_PER_MAX];
+        unsigned scs[SK_PER_MAX];
+#pragma unroll
+        for (int i = 0; i < SK_PER_MAX; i++) {
+            dqs[i] = sh.dslice[i * SK_BLOCK + tid];
+            scs[i] = sh.sc_d[i * SK_BLOCK + tid];
+        }
+#pragma unroll
+        for (int i = 0; i < SK_PER_MAX; i++) asm volatile("" ::"v"(dqs[i]), "v"(scs[i]));
 #pragma unroll
         for (int i = 0; i < SK_PER_MAX; i++) {
             if (i < c) {
-                const u32x4 dq = sh.dslice[i * SK_BLOCK + tid];
+                const u32x4 dq = dqs[i];
                 const int wq[4] = {(int)dq.x, (int)dq.y, (int)dq.z, (int)dq.w};
                 int acc[3];
 #pragma unroll
@@ -759,9 +909,8 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
                     acc[d] = s;
                 }
                 const float f = digits_to_float(acc[0], acc[1], acc[2]);
-                const int r = i * SK_BLOCK + tid;
-                st_f(yp + (size_t)(r / SK_CROWS) * NS * NPF * SK_CROWS,
-                     f * ldexpf(__half2float(__ushort_as_half(sh.sc_d[r])), hexp));
+                st_f(yp + (size_t)i * (SK_BLOCK / SK_CROWS) * ychunk,
+                     f * ldexpf(__half2float(__ushort_as_half((unsigned short)scs[i])), hexp));
             }
         }
     }
@@ -874,25 +1023,30 @@ __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, 
 }
 
 // Block roles: the first n_router blocks route, and router blocks 1.. then take the shared
-// expert's items beyond the shared blocks' share; the next shared_blocks run one shared
-// item each, then wait until the layer's combine is done before taking the next layer's
-// (so its 10 MB of weights stream during the next router phase, not during the routed
-// burst or the combine's reads); the rest run the routed experts' items and then the
-// combine chunks. Trace items of one layer are numbered: n_router router items, D/8
-// combine chunks, F/16 shared items, K*F/16 routed items (a routed block's top-k is
-// stamped on its first expert item).
+// expert's items beyond the shared blocks' share; shared_blocks blocks from G/2 on run one
+// shared item each, then wait until the layer's combine is done before taking the next
+// layer's (so its 10 MB of weights stream during the next router phase, not during the
+// routed burst or the combine's reads); the rest compute xn's digits themselves, wait for
+// the routing, run the routed experts' items and then the combine chunks. Trace items of
+// one layer are numbered: n_router router items, D/8 combine chunks, F/16 shared items,
+// K*F/16 routed items (a routed block's top-k is stamped on its first expert item).
 __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
     __shared__ SkShared sh;
     if (threadIdx.x == 0) {
         sh.trace = a.trace;
         sh.ok = 1;
+        sh.zero = 0u;
     }
     __syncthreads();
     const int K = a.K, NS = K + 1;
     const int NPF = a.F >> 4, NCH = a.D / SK_CROWS;  // combine chunks
-    const int NR = a.n_router, NSB = a.shared_blocks, NWB = (int)gridDim.x - NR - NSB;
+    const int NR = a.n_router, NSB = a.shared_blocks, G = (int)gridDim.x, NWB = G - NR - NSB;
     const int per_layer = NR + NCH + NS * NPF;
     const int b = blockIdx.x;
+    // the shared blocks start at P = G/2, so that block b < NR shares its CU with shared
+    // block b + G/2 (blocks b and b + G/2 of a two-per-CU grid are dispatched to one CU), not
+    // with a routed block that computes its own digits meanwhile
+    const int P = (G / 2 >= NR && G / 2 + NSB <= G) ? G / 2 : NR;
     for (int li = 0; li < a.n_layers; li++) {
         const StackLayer L = a.layers[li];
         const int layer = a.first_layer + li;
@@ -901,9 +1055,9 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
 #define SK_ITEM(idx, call)                                                                    \
     do {                                                                                      \
         sh.trace_item = base + (idx);                                                         \
-        if (a.trace && threadIdx.x == 0) a.trace[SK_TRACE_STAMPS * sh.trace_item] = wall_clock64(); \
+        if (a.trace && threadIdx.x == 0) trace_put(a.trace, SK_TRACE_STAMPS * sh.trace_item);   \
         if (!(call)) return;                                                                  \
-        if (a.trace && threadIdx.x == 0) a.trace[SK_TRACE_STAMPS * sh.trace_item + 2] = wall_clock64(); \
+        if (a.trace && threadIdx.x == 0) trace_put(a.trace, SK_TRACE_STAMPS * sh.trace_item + 2); \
         __syncthreads();                                                                      \
     } while (0)
         if (b < NR) {
@@ -911,25 +1065,26 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
             // shared items past the shared blocks' share go to router blocks 1.. (block 0
             // also selects and writes the observables)
             if (b > 0)
-                for (int j = NSB + b - 1; j < NPF; j += NR - 1) SK_ITEM(NR + NCH + j, sk_expert_item(a, L, li, K, j, a.E, sh));
-        } else if (b < NR + NSB) {
-            const int sb = b - NR;
+                for (int j = NSB + b - 1; j < NPF; j += NR - 1) SK_ITEM(NR + NCH + j, sk_expert_item<false>(a, L, li, K, j, a.E, sh));
+        } else if (b >= P && b < P + NSB) {
+            const int sb = b - P;
             for (int j = sb; j < NPF; j += NSB) {
                 if (j >= NSB && NR > 1) break;  // the router blocks' share
-                SK_ITEM(NR + NCH + j, sk_expert_item(a, L, li, K, j, a.E, sh));
+                SK_ITEM(NR + NCH + j, sk_expert_item<false>(a, L, li, K, j, a.E, sh));
             }
             sh.trace_item = base + NR + NCH + sb;
             if (!wait_ge(&a.ctr[SKF(li, SKF_X)], 1u, a.error, sh)) return;
         } else {
-            const int wb = b - NR - NSB;
+            const int wb = b < P ? b - NR : b - NR - NSB;
             if (wb < K * NPF && routed_on) {
-                sh.trace_item = base + NR + NCH + NPF + wb;  // stamps 8 and 3 of its first item
+                sh.trace_item = base + NR + NCH + NPF + wb;  // stamps 1, 8 and 3 of its first item
+                if (a.D == GM_MAX_COLS && !sk_local_digits(a, L, li, sh)) return;
                 if (!sk_stage_select(a, li, false, sh)) return;
                 if (!sh.sel_ok && !sk_read_topk(a, li, sh)) return;
             }
             for (int i = wb; i < K * NPF; i += NWB) {
                 const int slot = i / NPF;
-                SK_ITEM(NR + NCH + NPF + i, sk_expert_item(a, L, li, slot, i % NPF, routed_on ? sh.idx[slot] : -1, sh));
+                SK_ITEM(NR + NCH + NPF + i, sk_expert_item<true>(a, L, li, slot, i % NPF, routed_on ? sh.idx[slot] : -1, sh));
             }
             // combine chunks, by the blocks that hold this layer's routing
             const int ncb = NWB < K * NPF ? NWB : K * NPF;
