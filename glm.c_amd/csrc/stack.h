@@ -45,7 +45,7 @@
 #define SK_RX_MAX (GM_MAX_E / SK_NR_MAX)       // experts per router block
 #define SK_PER_MAX (GM_MAX_COLS / SK_BLOCK)    // columns (router) or rows (down) per thread
 #define SK_NPART 16                            // completion counters of the expert items
-#define SK_CROWS 8                             // rows per combine chunk
+#define SK_CROWS 16                            // rows per combine chunk (a 64-byte piece of one item's partials)
 #define SK_CGROUPS (SK_BLOCK / SK_CROWS)       // partial sums per row in the combine
 #define SK_MAX_LAYERS 256
 
@@ -878,7 +878,8 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
 #pragma unroll
         for (int q = 0; q < 12; q++) h4[q] = sh.u.g.hd[q];
         const int hexp = sh.u.g.hexp;
-        // partials in combine order: [D/8 chunks][F/16][K+1 slots][8 rows]
+        // partials in combine order: [D/16 chunks][F/16][K+1 slots][16 rows]: 64-byte pieces, since 32-byte
+        // write-through stores cost the weight stream about a fifth of its bandwidth
         const int NS = a.K + 1;
         // row r = 256 i + t goes to combine chunk r / 8 = 32 i + t / 8, at [chunk][j][slot][r % 8]
         const size_t ychunk = (size_t)NS * NPF * SK_CROWS;
@@ -929,11 +930,11 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
 
 // ---------------------------------------------------------------- combine
 //
-// Rows [8c, 8c+8) of x' = x + (shared + sum_k w_e * y_k) (infer.c:1192, 1212-1214),
+// Rows [16c, 16c+16) of x' = x + (shared + sum_k w_e * y_k) (infer.c:1192, 1212-1214),
 // with y_k the sum of expert k's F/16 partials in a fixed order. The chunk's partials
-// are one contiguous run ([j][slot][8 rows]), copied to shared memory with wide loads.
-// With P = 8 (K+1) (slot, row) pairs and Q = 256 / P groups, thread q P + p adds the
-// partials j = q, q + Q, ... of pair p in order; 8 threads then add the Q group sums in
+// are one contiguous run ([j][slot][16 rows]), copied to shared memory with wide loads.
+// With P = 16 (K+1) (slot, row) pairs and Q = 256 / P groups, thread q P + p adds the
+// partials j = q, q + Q, ... of pair p in order; 16 threads then add the Q group sums in
 // order and apply glm.c's combine order.
 __device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs &a, int li, int c, bool routed_on,
                                                                  SkShared &sh) {
@@ -944,7 +945,7 @@ __device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs
     const float xr = tid < SK_CROWS ? (li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x))[r] : 0.0f;
     if (!wait_ge(&a.ctr[SKF(li, SKF_PART)], 1u, a.error, sh)) return false;  // every expert item is done
     const uint8_t *src = (const uint8_t *)(ws_at<float>(a, li, a.o.ypart) + (size_t)c * NPF * P);
-    const int nbytes = NPF * P * (int)sizeof(float);  // <= sizeof(sh.dslice) for F <= 2048, K <= 8
+    const int nbytes = NPF * P * (int)sizeof(float);  // <= sizeof(sh.dslice): the host checks it
     dma_copy(sh.dslice, src, nbytes);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -997,7 +998,7 @@ __device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs
         st_f(xo + r, __fadd_rn(xr, __fadd_rn(shv, acc)));
     }
     sk_stamp(sh, 5);
-    // two-level count of the layer's D/8 chunks, then the layer's flag
+    // two-level count of the layer's D/16 chunks, then the layer's flag
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -1028,7 +1029,7 @@ __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, 
 // layer's (so its 10 MB of weights stream during the next router phase, not during the
 // routed burst or the combine's reads); the rest compute xn's digits themselves, wait for
 // the routing, run the routed experts' items and then the combine chunks. Trace items of
-// one layer are numbered: n_router router items, D/8 combine chunks, F/16 shared items,
+// one layer are numbered: n_router router items, D/16 combine chunks, F/16 shared items,
 // K*F/16 routed items (a routed block's top-k is stamped on its first expert item).
 __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
     __shared__ SkShared sh;

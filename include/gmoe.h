@@ -161,7 +161,7 @@ int gmoe_profile_read(gmoe_ctx *ctx, gmoe_kernel_times *out);
  * stored, 6 item weights and activations staged, 8 router results visible,
  * 11 norm reduced, 12 activation digits published, 13 logits done. Items of one
  * layer are numbered: n_router router items (min(E, 64) rounded down to a power of
- * two), D/8 combine chunks, F/16 shared-expert items, then K*F/16 routed items; layer
+ * two), D/16 combine chunks, F/16 shared-expert items, then K*F/16 routed items; layer
  * after layer. A routed block's per-layer top-k (stamps 8 and 3) is stamped on its
  * first item of the layer. gmoe_trace_items_read copies the most recent launch's
  * stamps ([n][GMOE_TRACE_STAMPS]) and returns n, or a negative error. Measurement
