@@ -283,7 +283,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         c->sk_o.xn = take(D * sizeof(float));
         c->sk_o.dig = take(3 * D);
         c->sk_o.dexp = take(D / 32 * sizeof(int));
-        c->sk_o.stage = take(E * sizeof(StageEnt));
+        c->sk_o.stage = take(SK_STAGE_COPIES * SK_STAGE_COPY_WORDS * sizeof(unsigned long long));
         c->sk_o.ex_w = take(K * sizeof(float));
         c->sk_o.ypart = take(NS * (F / 16) * D * sizeof(float));
         c->sk_ws_layer = off;

@@ -78,15 +78,19 @@ struct StackLayer {
     int pad;
 };
 
-// One expert's router result, written once per launch by its router block into words that
-// the launch's reset set to SK_UNSET: w0 = fp32 bits of lo | hi << 32, the certified
+// Expert e's router result, written once per launch by its router block into two words
+// that the launch's reset set to SK_UNSET: w0 = fp32 bits of lo | hi << 32, the certified
 // selection interval [lo, hi] of sel = p + bias rounded outward; w1 = fp32 bits of p.
 // Each word is stored and loaded whole (64-bit, single-copy atomic), so a reader that sees
 // neither word unset has the final entry, with no counter or flag in between.
-struct StageEnt {
-    unsigned long long w0, w1;
-};
+// The router block stores its entries in SK_STAGE_COPIES copies (4 KB apart), and a reader
+// polls the copy of its XCD (blockIdx % 8, the dispatch order): 384 readers on one copy
+// make the entries visible ~1.3 us later than 48 readers on each of eight. Within a copy
+// the entries sit in two planes of GM_MAX_E words (all w0, then all w1) at stage_pos(e), which
+// puts the entries of one XCD's router blocks (b % 8 alike) in the same lines.
 #define SK_UNSET (~0ull)
+#define SK_STAGE_COPIES 8
+#define SK_STAGE_COPY_WORDS 512
 
 // Per-layer workspace: one region of `ws_layer_bytes` per layer of the launch.
 struct StackWs {
@@ -126,6 +130,16 @@ template <typename T>
 __device__ static inline T *ws_at(const StackArgs &a, int li, size_t off) {
     return (T *)(a.ws + (size_t)li * a.ws_layer_bytes + off);
 }
+// Position of expert e (computed by router block e % NR) within a stage plane.
+__device__ static inline int stage_pos(int e, int NR) {
+    const int b = e % NR, x = e / NR;
+    return NR >= 8 ? (b % 8) * (NR / 8) + b / 8 + NR * x : e;
+}
+// Copy c's plane (0: w0, 1: w1) of layer li's stage entries.
+__device__ static inline unsigned long long *stage_plane(const StackArgs &a, int li, int c, int plane) {
+    return ws_at<unsigned long long>(a, li, a.o.stage) + (size_t)c * SK_STAGE_COPY_WORDS + plane * GM_MAX_E;
+}
+static_assert(2 * GM_MAX_E <= SK_STAGE_COPY_WORDS, "a stage copy holds two planes of GM_MAX_E words");
 
 __device__ static inline void st_f(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ static inline void st_i(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -290,7 +304,8 @@ __device__ __attribute__((always_inline)) static bool sk_stage_select(const Stac
                                                                       SkShared &sh) {
     const int E = a.E, K = a.K, tid = phase_tid();
     if (tid < 64) {
-        const StageEnt *stage = ws_at<StageEnt>(a, li, a.o.stage);
+        const int cpy = blockIdx.x % SK_STAGE_COPIES;
+        const unsigned long long *sw0 = stage_plane(a, li, cpy, 0), *sw1 = stage_plane(a, li, cpy, 1);
         const int nch = (E + 63) >> 6;
         unsigned long long w0[SK_SEL_C], w1[SK_SEL_C];
         unsigned spins = 0;
@@ -301,8 +316,9 @@ __device__ __attribute__((always_inline)) static bool sk_stage_select(const Stac
             for (int c = 0; c < SK_SEL_C; c++) {
                 const int e = tid + 64 * c < E ? tid + 64 * c : E - 1;
                 if (c < nch) {
-                    w0[c] = __hip_atomic_load(&stage[e].w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    w1[c] = __hip_atomic_load(&stage[e].w1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    const int pe = stage_pos(e, a.n_router);
+                    w0[c] = __hip_atomic_load(sw0 + pe, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    w1[c] = __hip_atomic_load(sw1 + pe, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     miss |= (w0[c] == SK_UNSET) | (w1[c] == SK_UNSET);
                 } else {
                     w0[c] = w1[c] = 0ull;
@@ -540,9 +556,13 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
                 lo_f = -INFINITY;
                 hi_f = INFINITY;
             }
-            StageEnt *st = ws_at<StageEnt>(a, li, a.o.stage) + e;
-            st_u64(&st->w1, (unsigned long long)__float_as_uint(p));
-            st_u64(&st->w0, (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32));
+            const int pe = stage_pos(e, NR);
+            const unsigned long long v0 = (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32);
+#pragma unroll
+            for (int cp = 0; cp < SK_STAGE_COPIES; cp++) {
+                st_u64(stage_plane(a, li, cp, 1) + pe, (unsigned long long)__float_as_uint(p));
+                st_u64(stage_plane(a, li, cp, 0) + pe, v0);
+            }
         }
     }
     sk_stamp(sh, 5);
@@ -1020,7 +1040,7 @@ __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, 
         return;
     }
     unsigned long long *stage = ws_at<unsigned long long>(a, li, a.o.stage);
-    for (int i = tid; i < 2 * a.E; i += SK_BLOCK) stage[i] = SK_UNSET;
+    for (int i = tid; i < SK_STAGE_COPIES * SK_STAGE_COPY_WORDS; i += SK_BLOCK) stage[i] = SK_UNSET;
 }
 
 // Block roles: the first n_router blocks route, and router blocks 1.. then take the shared
