@@ -55,10 +55,14 @@
 // slows those atomics down badly (the phase's completion then arrives microseconds
 // late); polling a word that is written once costs nothing measurable. Every counter and
 // flag sits 64 words (256 bytes) from the next. The expert items count on SK_NPART
-// counters, whose last arrivals count on a second level.
+// counters, whose last arrivals count on a second level; the items of group A (see
+// sk_early_slots) count a second time on counters of their own, for the PARTA flag.
 #define SKC_PAD 64
-enum { SKC_DIG = 0, SKC_X2 = 1, SKC_PART2 = 2, SKC_PART = 3, SKC_X = SKC_PART + SK_NPART, SKC_FIXED = SKC_X + SK_NPART };
-enum { SKF_SEL = 0, SKF_SELW = 1, SKF_DIG = 2, SKF_PART = 3, SKF_X = 4, SKF_PER_LAYER = 5 };
+enum {
+    SKC_DIG = 0, SKC_X2 = 1, SKC_PART2 = 2, SKC_PA2 = 3, SKC_PART = 4, SKC_PA = SKC_PART + SK_NPART,
+    SKC_X = SKC_PA + SK_NPART, SKC_FIXED = SKC_X + SK_NPART
+};
+enum { SKF_SEL = 0, SKF_SELW = 1, SKF_DIG = 2, SKF_PART = 3, SKF_X = 4, SKF_PARTA = 5, SKF_PER_LAYER = 6 };
 #define SKC(i) ((i) * SKC_PAD)
 #define SKF(li, f) SKC(SKC_FIXED + SKF_PER_LAYER * (li) + (f))  // per-layer flags
 // The SEL flag carries the top-k itself, so that its consumers need nothing else: one
@@ -197,6 +201,29 @@ struct SkShared {
 
 __device__ static inline void st_u(unsigned *p, unsigned v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ static inline unsigned add_u(unsigned *p) { return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Group A of a layer's expert items: the routed slots 0..KA-1, whose items run on the first
+// block of each CU (blocks b < G/2 hold items 0 .. G/2 - n_router - 1 when every routed
+// block runs one item), and the shared expert's. Their data arrives microseconds before
+// that of the items on the CUs' second blocks, so they count on their own flag and their
+// partials lie apart, and the combine sums them while the rest still stream.
+__device__ static inline int sk_early_slots(const StackArgs &a) {
+    const int G = (int)gridDim.x, NR = a.n_router, NSB = a.shared_blocks, NPF = a.F >> 4;
+    const int P = (G / 2 >= NR && G / 2 + NSB <= G) ? G / 2 : NR;  // as in k_moe_stack
+    if (G - NR - NSB < a.K * NPF || P <= NR) return 0;
+    const int ka = (P - NR) / NPF;
+    return ka < a.K ? ka : a.K;
+}
+
+// Position of `slot` among a chunk's partials: slots 0..KA-1, the shared expert's (slot K),
+// then slots KA..K-1; group A is positions 0..KA.
+__device__ static inline int sk_pos(int slot, int K, int KA) { return slot < KA ? slot : slot == K ? KA : slot + 1; }
+
+// Offset (floats) of (j, position)'s 16 rows inside a combine chunk's partials: group A as
+// [F/16][KA+1][16], then group B as [F/16][K-KA][16], each contiguous.
+__device__ static inline int sk_piece(int j, int pos, int NPF, int NS, int NA) {
+    return pos < NA ? (j * NA + pos) * SK_CROWS : (NPF * NA + j * (NS - NA) + (pos - NA)) * SK_CROWS;
+}
 
 // All of this block's write-through stores have completed; then thread 0 sets `flag`.
 __device__ static inline void signal(unsigned *flag) {
@@ -900,11 +927,12 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
         const int hexp = sh.u.g.hexp;
         // partials in combine order: [D/16 chunks][F/16][K+1 slots][16 rows]: 64-byte pieces, since 32-byte
         // write-through stores cost the weight stream about a fifth of its bandwidth
-        const int NS = a.K + 1;
-        // row r = 256 i + t goes to combine chunk r / 8 = 32 i + t / 8, at [chunk][j][slot][r % 8]
+        const int NS = a.K + 1, KA = sk_early_slots(a);
+        // row r = 256 i + t goes to combine chunk r / 16 = 16 i + t / 16, at row r % 16 of
+        // piece (j, position of slot)
         const size_t ychunk = (size_t)NS * NPF * SK_CROWS;
-        float *yp = ws_at<float>(a, li, a.o.ypart) + ((size_t)j * NS + slot) * SK_CROWS + (tid & (SK_CROWS - 1)) +
-                    (size_t)(tid / SK_CROWS) * ychunk;
+        float *yp = ws_at<float>(a, li, a.o.ypart) + sk_piece(j, sk_pos(slot, a.K, KA), NPF, NS, KA + 1) +
+                    (tid & (SK_CROWS - 1)) + (size_t)(tid / SK_CROWS) * ychunk;
         // every slice row and scale of this thread is read before the first product (rows
         // past D read shared memory that is never used), so the reads cost one latency
         u32x4 dqs[SK_PER_MAX];
@@ -936,7 +964,8 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
         }
     }
     sk_stamp(sh, 5);
-    // two-level count of the layer's (K+1) * F/16 items, then the layer's flag
+    // two-level count of the layer's (K+1) * F/16 items, then the layer's flag; group A's
+    // items also count for the PARTA flag (on another wave, so the two run side by side)
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -944,6 +973,12 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
         if (add_u(&a.ctr[SKC(SKC_PART + (slot * NPF + j) % SK_NPART)]) + 1u == (unsigned)(li + 1) * per_ctr &&
             add_u(&a.ctr[SKC(SKC_PART2)]) + 1u == (unsigned)(li + 1) * SK_NPART)
             st_u(&a.ctr[SKF(li, SKF_PART)], 1u);
+    } else if (tid == 64) {
+        const int KA = sk_early_slots(a), pos = sk_pos(slot, a.K, KA);
+        const unsigned per_a = (unsigned)((KA + 1) * NPF / SK_NPART);
+        if (pos <= KA && add_u(&a.ctr[SKC(SKC_PA + (pos * NPF + j) % SK_NPART)]) + 1u == (unsigned)(li + 1) * per_a &&
+            add_u(&a.ctr[SKC(SKC_PA2)]) + 1u == (unsigned)(li + 1) * SK_NPART)
+            st_u(&a.ctr[SKF(li, SKF_PARTA)], 1u);
     }
     return true;
 }
@@ -951,27 +986,19 @@ __device__ __attribute__((always_inline)) static bool sk_expert_item(const Stack
 // ---------------------------------------------------------------- combine
 //
 // Rows [16c, 16c+16) of x' = x + (shared + sum_k w_e * y_k) (infer.c:1192, 1212-1214),
-// with y_k the sum of expert k's F/16 partials in a fixed order. The chunk's partials
-// are one contiguous run ([j][slot][16 rows]), copied to shared memory with wide loads.
-// With P = 16 (K+1) (slot, row) pairs and Q = 256 / P groups, thread q P + p adds the
-// partials j = q, q + Q, ... of pair p in order; 16 threads then add the Q group sums in
-// order and apply glm.c's combine order.
-__device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs &a, int li, int c, bool routed_on,
-                                                                 SkShared &sh) {
-    const int D = a.D, K = a.K, NS = K + 1, NPF = a.F >> 4, tid = phase_tid();
-    const int P = NS * SK_CROWS, Q = SK_BLOCK / P;
-    // the residual rows, fetched while the expert items finish
-    const int r = c * SK_CROWS + (tid & (SK_CROWS - 1));
-    const float xr = tid < SK_CROWS ? (li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x))[r] : 0.0f;
-    if (!wait_ge(&a.ctr[SKF(li, SKF_PART)], 1u, a.error, sh)) return false;  // every expert item is done
-    const uint8_t *src = (const uint8_t *)(ws_at<float>(a, li, a.o.ypart) + (size_t)c * NPF * P);
-    const int nbytes = NPF * P * (int)sizeof(float);  // <= sizeof(sh.dslice): the host checks it
-    dma_copy(sh.dslice, src, nbytes);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    const float *buf = (const float *)sh.dslice;
-    // Shared-memory reads are issued eight at a time (clamped indices, masked values), so
-    // each batch costs one latency rather than eight.
+// with y_k the sum of expert k's F/16 partials in a fixed order. Group A's partials
+// (sk_early_slots) are summed first, while group B's items still run, then group B's.
+// Each group's partials are one contiguous run ([j][position][16 rows]), copied to
+// shared memory with wide loads.
+//
+// A group of np positions has P = 16 np (position, row) pairs and Q = min(8, 256 / P)
+// groups of threads: thread q P + p adds the partials j = q, q + Q, ... of pair p in
+// order, then P threads add the Q group sums in order. Shared-memory reads are issued
+// eight at a time (clamped indices, masked values), so each batch costs one latency.
+__device__ __attribute__((always_inline)) static void sk_combine_sums(const float *gb, int np, int p0, int NPF,
+                                                                      SkShared &sh) {
+    const int tid = phase_tid();
+    const int P = np * SK_CROWS, Qm = SK_BLOCK / P, Q = Qm < 8 ? Qm : 8;
     if (tid < P * Q) {
         const int q = tid / P, pr = tid - q * P;
         float s = 0.0f;
@@ -980,38 +1007,59 @@ __device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int jq = j0 + u * Q;
-                v[u] = buf[(jq < NPF ? jq : q) * P + pr];
+                v[u] = gb[(jq < NPF ? jq : q) * P + pr];
             }
 #pragma unroll
             for (int u = 0; u < 8; u++)
                 if (j0 + u * Q < NPF) s += v[u];
         }
-        sh.u.c.acc[q][pr / SK_CROWS][pr % SK_CROWS] = s;
+        sh.u.c.acc[q][p0 + pr / SK_CROWS][pr % SK_CROWS] = s;
     }
     __syncthreads();
     if (tid < P) {  // each pair's Q group sums, in order
-        float v[SK_BLOCK / (2 * SK_CROWS)];
+        float v[8];
 #pragma unroll
-        for (int q = 0; q < SK_BLOCK / (2 * SK_CROWS); q++) v[q] = sh.u.c.acc[q < Q ? q : 0][tid / SK_CROWS][tid % SK_CROWS];
+        for (int q = 0; q < 8; q++) v[q] = sh.u.c.acc[q < Q ? q : 0][p0 + tid / SK_CROWS][tid % SK_CROWS];
         float y = v[0];
 #pragma unroll
-        for (int q = 1; q < SK_BLOCK / (2 * SK_CROWS); q++)
+        for (int q = 1; q < 8; q++)
             if (q < Q) y += v[q];
-        sh.u.c.y[tid / SK_CROWS][tid % SK_CROWS] = y;
+        sh.u.c.y[p0 + tid / SK_CROWS][tid % SK_CROWS] = y;
+    }
+}
+
+__device__ __attribute__((always_inline)) static bool sk_combine(const StackArgs &a, int li, int c, bool routed_on,
+                                                                 SkShared &sh) {
+    const int D = a.D, K = a.K, NS = K + 1, NPF = a.F >> 4, tid = phase_tid();
+    const int KA = sk_early_slots(a), NA = KA + 1;
+    // the residual rows, fetched while the expert items finish
+    const int r = c * SK_CROWS + (tid & (SK_CROWS - 1));
+    const float xr = tid < SK_CROWS ? (li == 0 ? a.x_in : ws_at<float>(a, li, a.o.x))[r] : 0.0f;
+    // the chunk's partials: NPF * NS * 16 floats <= sizeof(sh.dslice) (the host checks it)
+    const float *chunk = ws_at<float>(a, li, a.o.ypart) + (size_t)c * NPF * NS * SK_CROWS;
+    for (int g = 0; g < 2; g++) {
+        const int p0 = g == 0 ? 0 : NA, np = g == 0 ? NA : NS - NA;
+        if (np == 0) break;  // block-uniform
+        if (!wait_ge(&a.ctr[SKF(li, g == 0 ? SKF_PARTA : SKF_PART)], 1u, a.error, sh)) return false;
+        const int off = p0 * NPF * SK_CROWS;  // group B follows group A's NPF * NA pieces
+        dma_copy((float *)sh.dslice + off, chunk + off, np * NPF * SK_CROWS * (int)sizeof(float));
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        sk_combine_sums((const float *)sh.dslice + off, np, p0, NPF, sh);
     }
     __syncthreads();
     if (tid < SK_CROWS) {
         const int rl = tid;
-        float y[GM_MAX_K + 1];
+        float y[GM_MAX_K];
 #pragma unroll
-        for (int k = 0; k < GM_MAX_K + 1; k++) y[k] = sh.u.c.y[k < NS ? k : 0][rl];
+        for (int k = 0; k < GM_MAX_K; k++) y[k] = sh.u.c.y[k < K ? sk_pos(k, K, KA) : 0][rl];
         float acc = 0.0f;
         if (routed_on) {
 #pragma unroll
             for (int k = 0; k < GM_MAX_K; k++)
                 if (k < K && sh.idx[k] >= 0) acc = __fadd_rn(acc, __fmul_rn(sh.ws[k], y[k]));
         }
-        const float shv = sh.u.c.y[K][rl];
+        const float shv = sh.u.c.y[KA][rl];  // the shared expert's position
         st_f(a.routed_out + r, acc);
         st_f(a.shared_out + r, shv);
         float *xo = li == a.n_layers - 1 ? a.x_out : ws_at<float>(a, li + 1, a.o.x);
