@@ -326,10 +326,22 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
 // grid (T): the router of one token per block. RMSNorm bit-identical to infer.c:746-752
 // (certified_mean_sq); every expert's fp64 logit with the bound of its fp32 chain, wave
 // w taking experts w, w + 4, ... and lane l the D/64 consecutive columns from l D/64 (so
-// a wave scan yields the chain's partial sums in glm.c's order); then the certified
-// top-k on wave 0 (certified_select) or, when it fails or is forced, the exact replay
-// (exact_router). Outputs as infer.c:1098-1145 leaves them: xn, probabilities, top-k,
-// normalised weights (and times routed_scale).
+// a wave scan yields the chain's partial sums in glm.c's order); then, one thread per
+// expert, the bounds and selection intervals; then the certified top-k on wave 0
+// (certified_select) or, when it fails or is forced, the exact replay (exact_router).
+// Outputs as infer.c:1098-1145 leaves them: xn, probabilities, top-k, normalised weights
+// (and times routed_scale).
+//
+// The loop over experts is what the kernel's time goes to (512 tokens x 64 experts of
+// wave work, the SIMDs shared by three blocks), so only the estimate S = sum p_k uses
+// fp64 (exact products, fp64 sums and scan). The bound's terms, sum |p_k| and the sum of
+// the partial sums' magnitudes, are taken in fp32 and then enlarged by their own rounding
+// bound: for the lane's m columns, with r_k the fp32 running sum started from fl(R_0),
+// R_0 the exact sum before the lane, and q_k = fl(p_k),
+//   sum_k |R_k| <= T + m u (|R_0| + A + (1 + u) T),
+//   T = sum_k |r_k| <= fl-sum * (1 + 2(m+1)u), A = sum_k |p_k| <= fl-sum |q_k| * (1 + 2(m+2)u)
+// (each fp32 add or product errs by at most u relative, plus 2^-150 absolute below the
+// normal range, counted as 2m 2^-149).
 __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
     __shared__ __align__(16) float s_xn[GM_MAX_COLS];
     __shared__ __align__(16) float s_prod[RT_XT][64];  // exact replay scratch
@@ -338,6 +350,8 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
     __shared__ unsigned long long s_w0[GM_MAX_E], s_w1[GM_MAX_E];
     __shared__ float s_p[GM_MAX_E], s_sel[GM_MAX_E], s_wk[GM_MAX_K];
     __shared__ int s_idx[GM_MAX_K], s_ok;
+    __shared__ double s_S[GM_MAX_E];
+    __shared__ float s_sp[GM_MAX_E], s_sa[GM_MAX_E];
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int D = a.D, E = a.E, K = a.K, cpl = D >> 6;
     const float *xt = a.x + (size_t)t * D;
@@ -382,44 +396,53 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
         // hoisted out of the loop as 32 live doubles
 #pragma unroll
         for (int j = 0; j < RT_CPL_MAX; j++) asm volatile("" : "+v"(xr[j]));
-        // pass 1: the lane's segment sum and the wave's exclusive prefix (products in fp64
-        // are exact); pass 2: |S_k| after each of the lane's columns
-        double seg = 0.0, seg_abs = 0.0;
+        // pass 1: the lane's segment sum (products in fp64 are exact) and the wave's
+        // exclusive prefix R_0; pass 2, in fp32: the running sum's magnitudes and |q_k|
+        double seg = 0.0;
 #pragma unroll
-        for (int j = 0; j < RT_CPL_MAX; j++) {
-            const double pj = (double)g[j] * (double)xr[j];
-            seg += pj;
-            seg_abs += fabs(pj);
-        }
-        const double incl = wave_incl_scan_dpp(seg);
-        double run = incl - seg, steps = 0.0;
+        for (int j = 0; j < RT_CPL_MAX; j++) seg += (double)g[j] * (double)xr[j];
+        const double incl = wave_incl_scan_dpp(seg), r0 = incl - seg;
+        float run = (float)r0, steps = 0.0f, sabs = 0.0f;
 #pragma unroll
         for (int j = 0; j < RT_CPL_MAX; j++) {
             if (j < cpl) {
-                run += (double)g[j] * (double)xr[j];
-                steps += fabs(run);
+                const float q = __fmul_rn(g[j], xr[j]);
+                run = __fadd_rn(run, q);
+                steps = __fadd_rn(steps, fabsf(run));
+                sabs = __fadd_rn(sabs, fabsf(q));
             }
         }
+        const double u = 0x1p-24, m = (double)cpl;
+        const double T = (double)steps * (1.0 + 2.0 * (m + 1.0) * u), A = (double)sabs * (1.0 + 2.0 * (m + 2.0) * u);
+        const double spl = T + m * u * (fabs(r0) * (1.0 + 0x1p-40) + A + (1.0 + u) * T) + 2.0 * m * 0x1p-149;
         const double S = readlane_d(incl, 63);
-        const double sp = wave_sum_dpp(steps), sa = wave_sum_dpp(seg_abs);
+        const double sp = wave_sum_dpp(spl), sa = wave_sum_dpp(A);
         if (lane == 0) {
-            const double u = 0x1p-24, n = (double)D;
-            const double gamma = n * u / (1.0 - n * u);
-            const double emax = gamma * sa;  // a priori bound on every partial sum's error
-            double B = u * (1.0 + u) * sa + u * (sp + n * emax + u * sa);
-            B = B * (1.0 + 0x1p-30) + 0x1p-40 * sa + n * 0x1p-149;
-            double lo, hi;
-            selection_interval(S, B, a.bias[e], &lo, &hi);
-            float lo_f = __double2float_rd(lo), hi_f = __double2float_ru(hi);
-            if (!(lo_f <= hi_f)) {  // NaN: an interval that is never certified
-                lo_f = -INFINITY;
-                hi_f = INFINITY;
-            }
-            s_w0[e] = (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32);
-            s_w1[e] = (unsigned long long)__float_as_uint(1.0f / (1.0f + expf(-(float)S)));
+            s_S[e] = S;
+            s_sp[e] = __double2float_ru(sp);
+            s_sa[e] = __double2float_ru(sa);
         }
 #pragma unroll
         for (int q = 0; q < RT_CPL_MAX / 4; q++) gc[q] = gn[q];
+    }
+    __syncthreads();
+    // every expert's bound and selection interval, one thread each
+    for (int e = tid; e < E; e += RT_BLOCK) {
+        const double S = s_S[e], sp = (double)s_sp[e], sa = (double)s_sa[e];
+        const double u = 0x1p-24, n = (double)D;
+        const double gamma = n * u / (1.0 - n * u);
+        const double emax = gamma * sa;  // a priori bound on every partial sum's error
+        double B = u * (1.0 + u) * sa + u * (sp + n * emax + u * sa);
+        B = B * (1.0 + 0x1p-30) + 0x1p-40 * sa + n * 0x1p-149;
+        double lo, hi;
+        selection_interval(S, B, a.bias[e], &lo, &hi);
+        float lo_f = __double2float_rd(lo), hi_f = __double2float_ru(hi);
+        if (!(lo_f <= hi_f)) {  // NaN: an interval that is never certified
+            lo_f = -INFINITY;
+            hi_f = INFINITY;
+        }
+        s_w0[e] = (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32);
+        s_w1[e] = (unsigned long long)__float_as_uint(1.0f / (1.0f + expf(-(float)S)));
     }
     __syncthreads();
 
