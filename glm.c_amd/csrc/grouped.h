@@ -30,8 +30,10 @@
 #include "dispatch.h"
 #include "experts.h"
 
-#define GP_KC 256    // columns per K chunk staged in shared memory (8 quant blocks)
+#define GP_KC 128             // columns per K chunk staged in shared memory
+#define GP_NB (GP_KC / 32)    // quant blocks per chunk
 #define GP_BLOCK 256
+#define GP_OCC 3              // blocks per CU the GEMMs are built for (32 KB of LDS each)
 
 // Split form of `rows` rows of n values (n a multiple of 8): sp[r][0][:] = hi and
 // sp[r][1][:] = lo (fp16), ex[r] the exponent. One block per row; rows past *n_rows
@@ -180,12 +182,14 @@ __device__ static inline void gp_barrier() { __builtin_amdgcn_s_barrier(); }
 
 // grid (F/64, max tiles). Wave w computes rows 64 p + 16 w .. +16 of F, gate and up, for
 // the tile's GP_TOK tokens, and from them h = silu(g) * u.
+typedef unsigned gp_sw __attribute__((ext_vector_type(GP_NB / 2)));  // a chunk's GP_NB fp16 block scales
 struct GuRegs {
-    u32x4 q[2][4];  // gate, up: the chunk's four 64-column pieces
-    u32x4 s[2];     // gate, up: the chunk's eight block scales (fp16)
+    u32x4 q[2][GP_NB / 2];  // gate, up: the chunk's 64-column pieces
+    gp_sw s[2];             // gate, up: the chunk's block scales
 };
+#define GU_LOADS (2 * (GP_NB / 2) + 2 + GP_STAGE_ITERS)  // loads per chunk and thread
 
-__global__ __launch_bounds__(GP_BLOCK, 2) void k_group_gu(GroupArgs a) {
+__global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
     __shared__ __align__(16) uint8_t abuf[2][GP_TOK * 2 * GP_RB];
     const int p = blockIdx.x, ti = blockIdx.y;
     if (ti >= *a.n_tiles) return;
@@ -197,9 +201,9 @@ __global__ __launch_bounds__(GP_BLOCK, 2) void k_group_gu(GroupArgs a) {
     const GM_GLOBAL u32x4 *qg = gbl((const u32x4 *)(base + a.off_gq + (size_t)P * nchunks * GM_CHUNK_BYTES)) + lane;
     const GM_GLOBAL u32x4 *qu = gbl((const u32x4 *)(base + a.off_uq + (size_t)P * nchunks * GM_CHUNK_BYTES)) + lane;
     const int row = 16 * P + (lane & 15);
-    // the row's fp16 scales, eight (one chunk's blocks) per 16-byte load
-    const GM_GLOBAL u32x4 *sg = gbl((const u32x4 *)(base + a.off_gs + (size_t)row * nblocks * 2));
-    const GM_GLOBAL u32x4 *su = gbl((const u32x4 *)(base + a.off_us + (size_t)row * nblocks * 2));
+    // the row's fp16 scales, one chunk's blocks per load
+    const GM_GLOBAL gp_sw *sg = gbl((const gp_sw *)(base + a.off_gs + (size_t)row * nblocks * 2));
+    const GM_GLOBAL gp_sw *su = gbl((const gp_sw *)(base + a.off_us + (size_t)row * nblocks * 2));
     auto src_row = [&](int i) { return gp_token(a, tl.row + (i < tl.count ? i : 0)); };
     const GpStage stg = gp_stage_init(a.aspl, D, src_row);
     const int nkc = D / GP_KC;  // K chunks
@@ -209,11 +213,11 @@ __global__ __launch_bounds__(GP_BLOCK, 2) void k_group_gu(GroupArgs a) {
     for (int i = 0; i < GP_TOK / 16; i++)
 #pragma unroll
         for (int k = 0; k < 4; k++) ag[i][k] = au[i][k] = 0.0f;
-    auto issue = [&](GuRegs &r, int kc) {  // 10 + GP_STAGE_ITERS loads
+    auto issue = [&](GuRegs &r, int kc) {  // GU_LOADS loads
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            r.q[0][u] = qg[(size_t)(4 * kc + u) * 64];
-            r.q[1][u] = qu[(size_t)(4 * kc + u) * 64];
+        for (int u = 0; u < GP_NB / 2; u++) {
+            r.q[0][u] = qg[(size_t)((GP_NB / 2) * kc + u) * 64];
+            r.q[1][u] = qu[(size_t)((GP_NB / 2) * kc + u) * 64];
         }
         r.s[0] = sg[kc];
         r.s[1] = su[kc];
@@ -222,13 +226,12 @@ __global__ __launch_bounds__(GP_BLOCK, 2) void k_group_gu(GroupArgs a) {
     auto compute = [&](const GuRegs &r, int kc) {
         const uint8_t *buf = abuf[kc & 1];
 #pragma unroll
-        for (int b = 0; b < 8; b++) {
+        for (int b = 0; b < GP_NB; b++) {
 #pragma unroll
             for (int m = 0; m < 2; m++) {
                 const u32x4 c = r.q[m][b >> 1];
                 const gp_h8 B = (b & 1) ? gp_i8_to_h8(c.z, c.w) : gp_i8_to_h8(c.x, c.y);
-                const unsigned sw[4] = {r.s[m].x, r.s[m].y, r.s[m].z, r.s[m].w};
-                const unsigned s2 = sw[b >> 1];
+                const unsigned s2 = r.s[m][b >> 1];
                 const float sc = __half2float(__ushort_as_half((unsigned short)((b & 1) ? s2 >> 16 : s2 & 0xffffu)));
                 gp_block(buf, b, B, sc, m ? au : ag);
             }
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(GP_BLOCK, 2) void k_group_gu(GroupArgs a) {
     // (every full step issues the same loads, so the compiler's own wait counts agree)
     auto step = [&](GuRegs &r, GuRegs &rn, int kc) {
         issue(rn, kc + 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(10 + GP_STAGE_ITERS) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(GU_LOADS) : "memory");
         gp_barrier();  // every wave's part of chunk kc's activations is in shared memory
         compute(r, kc);
         gp_barrier();  // every wave is done with buffer kc&1 before it is refilled
@@ -279,11 +282,12 @@ __global__ __launch_bounds__(GP_BLOCK, 2) void k_group_gu(GroupArgs a) {
 // grid (D/64, max tiles). Wave w computes D rows 64 p + 16 w .. +16 for the tile's
 // inputs (list rows), from h's split form; down is in the column-slice layout.
 struct DnRegs {
-    unsigned long long q[8];  // the chunk's eight blocks: 8 bytes of the row each
-    unsigned short s[8];
+    unsigned long long q[GP_NB];  // the chunk's blocks: 8 bytes of the row each
+    unsigned short s[GP_NB];
 };
+#define DN_LOADS (2 * GP_NB + GP_STAGE_ITERS)  // loads per chunk and thread
 
-__global__ __launch_bounds__(GP_BLOCK, 2) void k_group_down(GroupArgs a) {
+__global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_down(GroupArgs a) {
     __shared__ __align__(16) uint8_t abuf[2][GP_TOK * 2 * GP_RB];
     const int p = blockIdx.x, ti = blockIdx.y;
     if (ti >= *a.n_tiles) return;
@@ -302,10 +306,10 @@ __global__ __launch_bounds__(GP_BLOCK, 2) void k_group_down(GroupArgs a) {
     for (int i = 0; i < GP_TOK / 16; i++)
 #pragma unroll
         for (int k = 0; k < 4; k++) acc[i][k] = 0.0f;
-    auto issue = [&](DnRegs &r, int kc) {  // 16 + GP_STAGE_ITERS loads
+    auto issue = [&](DnRegs &r, int kc) {  // DN_LOADS loads
 #pragma unroll
-        for (int b = 0; b < 8; b++) {
-            const int blk = 8 * kc + b;
+        for (int b = 0; b < GP_NB; b++) {
+            const int blk = GP_NB * kc + b;
             r.q[b] = *(const GM_GLOBAL unsigned long long *)(qd + ((size_t)(2 * blk + (qh >> 1)) * D) * 16);
             r.s[b] = sd[(size_t)blk * D];
         }
@@ -314,12 +318,12 @@ __global__ __launch_bounds__(GP_BLOCK, 2) void k_group_down(GroupArgs a) {
     auto compute = [&](const DnRegs &r, int kc) {
         const uint8_t *buf = abuf[kc & 1];
 #pragma unroll
-        for (int b = 0; b < 8; b++)
+        for (int b = 0; b < GP_NB; b++)
             gp_block(buf, b, gp_i8_to_h8((unsigned)r.q[b], (unsigned)(r.q[b] >> 32)), __half2float(__ushort_as_half(r.s[b])), acc);
     };
     auto step = [&](DnRegs &r, DnRegs &rn, int kc) {
         issue(rn, kc + 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + GP_STAGE_ITERS) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DN_LOADS) : "memory");
         gp_barrier();
         compute(r, kc);
         gp_barrier();
