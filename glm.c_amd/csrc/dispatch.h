@@ -4,7 +4,10 @@
 // List e holds every token t with e in topk(t), in ascending t, with the top-k slot it
 // came from. One block per expert scans the [T][K] assignments in order and compacts
 // its matches with a ballot prefix, so the order never depends on atomics; the last
-// block to finish turns the counts into offsets and packs the lists.
+// block to finish turns the counts into offsets and packs the lists. The blocks hand
+// their lists to the last one through write-through (agent-scope) stores and loads
+// after their own store counts reach zero, not through __threadfence(), which would
+// write back and invalidate the L2 of every XCD.
 #pragma once
 
 #include "common.h"
@@ -65,21 +68,21 @@ __global__ __launch_bounds__(DP_BLOCK) void k_dispatch(DispatchArgs a) {
             if (match) {
                 const int pos = base + wbase + before;  // < T: a token selects an expert at most once
                 if (pos < a.T) {
-                    a.tmp_tok[(size_t)e * a.T + pos] = i / a.K;
-                    a.tmp_slot[(size_t)e * a.T + pos] = i % a.K;
+                    __hip_atomic_store(&a.tmp_tok[(size_t)e * a.T + pos], i / a.K, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&a.tmp_slot[(size_t)e * a.T + pos], i % a.K, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
             base += tot;
             __syncthreads();
         }
     }
-    if (tid == 0) a.counts[e] = base < a.T ? base : a.T;
-    __threadfence();
+    if (tid == 0) __hip_atomic_store(&a.counts[e], base < a.T ? base : a.T, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's write-through stores are done
     __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(a.counter, 1u) == (unsigned)(a.E - 1));
+    if (tid == 0)
+        s_last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(a.E - 1);
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     // every count in one parallel read, then the prefix in shared memory
     for (int q = tid; q < a.E; q += DP_BLOCK) s_off[q + 1] = __hip_atomic_load(a.counts + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
@@ -113,8 +116,8 @@ __global__ __launch_bounds__(DP_BLOCK) void k_dispatch(DispatchArgs a) {
                     if (s_off[mid] <= pos) lo = mid;
                     else hi = mid;
                 }
-                tk[u] = a.tmp_tok[(size_t)lo * a.T + (pos - s_off[lo])];
-                sk[u] = a.tmp_slot[(size_t)lo * a.T + (pos - s_off[lo])];
+                tk[u] = __hip_atomic_load(&a.tmp_tok[(size_t)lo * a.T + (pos - s_off[lo])], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                sk[u] = __hip_atomic_load(&a.tmp_slot[(size_t)lo * a.T + (pos - s_off[lo])], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
 #pragma unroll

@@ -64,13 +64,19 @@ __global__ __launch_bounds__(GP_BLOCK) void k_act_split(const float *__restrict_
     if (tid == 0) ex[r] = e;
     __half *hi = sp + (size_t)r * 2 * n, *lo = hi + n;
     for (int i = tid * 8; i < n; i += GP_BLOCK * 8) {
+        const float4 a = *(const float4 *)(src + i), b = *(const float4 *)(src + i + 4);
+        const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        unsigned hw[4], lw[4];  // eight halves of each plane, one 16-byte store each
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float x = ldexpf(src[i + k], -e);
-            const __half h = __float2half_rn(x);
-            hi[i + k] = h;
-            lo[i + k] = __float2half_rn(x - __half2float(h));
+        for (int k = 0; k < 4; k++) {
+            const float x0 = ldexpf(xs[2 * k], -e), x1 = ldexpf(xs[2 * k + 1], -e);
+            const __half h0 = __float2half_rn(x0), h1 = __float2half_rn(x1);
+            const __half l0 = __float2half_rn(x0 - __half2float(h0)), l1 = __float2half_rn(x1 - __half2float(h1));
+            hw[k] = (unsigned)__half_as_ushort(h0) | ((unsigned)__half_as_ushort(h1) << 16);
+            lw[k] = (unsigned)__half_as_ushort(l0) | ((unsigned)__half_as_ushort(l1) << 16);
         }
+        *(uint4 *)(hi + i) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        *(uint4 *)(lo + i) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
 }
 
