@@ -35,6 +35,19 @@ __device__ static inline const GM_GLOBAL T *gbl(const T *p) {
 }
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16-byte piece per lane from global memory straight into shared memory (lane l at
+// dst + 16 l), issued by inline assembly, which the compiler does not see as a
+// shared-memory DMA: with a global_load_lds of its own in flight, the compiler waits for
+// all of a wave's loads before using any loaded register or reading shared memory, which
+// would serialise whatever is streamed behind it. The caller waits (vmcnt) before reading
+// `dst`.
+__device__ static inline void dma16_untracked(const GM_GLOBAL void *src, lds_void *dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)dst);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __host__ __device__ static inline size_t gm_q_offset(int r, int c, int cols) {

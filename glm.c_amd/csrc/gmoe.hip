@@ -2,7 +2,9 @@
 //
 // A decode call (T=1) is one persistent launch, k_moe_stack (stack.h), that takes
 // the token through any run of layers. A batch (T>1) runs per layer:
-//   k_router_tok    grid (T)               rmsnorm, router logits, certified top-k (router.h)
+//   k_rt_norm       grid (T)               rmsnorm (router.h; E <= 64, else k_router_tok does all three)
+//   k_rt_dots       grid (T/4, 4)          router logits' sums, a thread per (token, expert, quarter of D)
+//   k_rt_select     grid (T)               bounds, certified top-k, exact replay when needed
 //   k_act_split     grid (rows)            xn as fp16 hi+lo planes with a per-row exponent (grouped.h)
 //   k_dispatch      grid (E)               exact per-expert token lists and GEMM tiles (dispatch.h)
 //   k_group_gu      grid (F/64, tiles)     grouped gate/up GEMM + SwiGLU on fp16 MFMA (grouped.h)
@@ -84,6 +86,8 @@ struct gmoe_ctx {
     LayerDev *layers = nullptr;
 
     float *xn = nullptr, *router_prob = nullptr, *topk_w = nullptr, *topk_ws = nullptr;
+    double *rt_t = nullptr, *rt_sp = nullptr;  // the batch router's quarter sums [T][4][E] (E <= 64)
+    float *rt_sa = nullptr;
     float *h = nullptr, *y = nullptr, *shared_out = nullptr, *routed_out = nullptr;
     double2 *stage = nullptr;
     int *topk_idx = nullptr;
@@ -164,7 +168,7 @@ static void free_ctx(gmoe_ctx *c) {
                     c->disp_tmp_slot, c->disp_counts, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
                     c->stats_dev, c->x_host_io, c->staging, c->sk_ws, c->sk_ctr, c->sk_error,
                     c->sk_layers, c->sk_trace, c->xspl, c->hspl, c->xexp, c->hexp, c->pair_row, c->n_tiles,
-                    c->hbuf, c->ybuf, c->tiles};
+                    c->hbuf, c->ybuf, c->tiles, c->rt_t, c->rt_sp, c->rt_sa};
     for (void *b : bufs) dev_free(b);
     delete c;
 }
@@ -237,6 +241,11 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     int rc = GMOE_OK;
     rc |= dev_alloc(&c->xn, T * D);
     rc |= dev_alloc(&c->router_prob, T * E);
+    if (E <= 64) {
+        rc |= dev_alloc(&c->rt_t, T * 4 * E);
+        rc |= dev_alloc(&c->rt_sp, T * 4 * E);
+        rc |= dev_alloc(&c->rt_sa, T * 4 * E);
+    }
     rc |= dev_alloc(&c->topk_w, T * K);
     rc |= dev_alloc(&c->topk_ws, T * K);
     rc |= dev_alloc(&c->h, T * NS * F);
@@ -672,7 +681,17 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     ra.routed_scale = c->cfg.routed_scale;
     ra.force_exact = (flags & GMOE_FLAG_EXACT_ROUTER) != 0;
     ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_ROUTER);
-    hipLaunchKernelGGL(k_router_tok, dim3(T), dim3(RT_BLOCK), 0, st, ra);
+    if (E <= 64) {
+        RtParts rp;
+        rp.t = c->rt_t;
+        rp.sp = c->rt_sp;
+        rp.sa = c->rt_sa;
+        hipLaunchKernelGGL(k_rt_norm, dim3(T), dim3(RT_BLOCK), 0, st, ra);
+        hipLaunchKernelGGL(k_rt_dots, dim3((T + 3) / 4, 4), dim3(RT_BLOCK), 0, st, ra, rp, T);
+        hipLaunchKernelGGL(k_rt_select, dim3(T), dim3(RT_BLOCK), 0, st, ra, rp);
+    } else {
+        hipLaunchKernelGGL(k_router_tok, dim3(T), dim3(RT_BLOCK), 0, st, ra);
+    }
     prof_end(pr, st);
     const int routed_on = !(fl & GMOE_FLAG_NO_ROUTED);
     c->last_dispatched = 0;

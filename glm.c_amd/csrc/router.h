@@ -485,3 +485,165 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
     }
     for (int i = tid; i < E; i += RT_BLOCK) a.router_prob[(size_t)t * E + i] = s_p[i];
 }
+
+// ---------------------------------------------------------------- the router of T > 1, in three kernels
+//
+// For E <= 64 the router of a batch runs as k_rt_norm (rmsnorm, one block per token),
+// k_rt_dots (the logits' sums) and k_rt_select (bounds, certified top-k, exact replay),
+// rather than k_router_tok's one block per token: there, each expert's dot is a
+// wave-wide reduction, and its fp64 scans and sums leave the SIMDs issue-bound.
+// k_rt_dots gives every (token, expert, quarter of D) its own thread, which runs the
+// quarter's columns in order: one fp64 FMA chain P_k (the estimate; products exact, each
+// step rounds once), the sum of |P_k| in fp64 and the sum of |g_k x_k| in fp32.
+// k_rt_select joins the quarters: S = t_0 + t_1 + t_2 + t_3 in order, and the bound's
+// sum of the chain's partial-sum magnitudes, with Q_q the exact sum before quarter q and
+// L_k the running sum inside it, as sum_{k in q} |Q_q + L_k| <= (D/4) |Q_q| + sum |L_k|.
+struct RtParts {
+    double *t;   // [T][4][E] quarter sums
+    double *sp;  // [T][4][E] quarter sums of |running sum|
+    float *sa;   // [T][4][E] quarter sums of |g x| (fp32)
+};
+
+// grid (T): xn of every token (infer.c:746-752), bit-identical to glm.c.
+__global__ __launch_bounds__(RT_BLOCK) void k_rt_norm(RouterArgs a) {
+    __shared__ double red[4];
+    __shared__ float s_mean;
+    const int t = blockIdx.x, tid = threadIdx.x, D = a.D;
+    const float *xt = a.x + (size_t)t * D;
+    const float mean = certified_mean_sq(xt, D, red, &s_mean, true, a.stats);
+    const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
+    for (int i = tid; i < D; i += RT_BLOCK) a.xn[(size_t)t * D + i] = __fmul_rn(__fmul_rn(xt[i], inv), a.norm_w[i]);
+}
+
+#define RT_QMAX (GM_MAX_COLS / 4)  // columns per quarter
+
+// grid (ceil(T/4), 4): wave w takes token 4 blockIdx.x + w, lane e expert e, over the
+// columns of quarter blockIdx.y. The gate rows come through shared memory in tiles of
+// 64 columns, [64 experts][16 four-column groups] with group g of row e at slot
+// g ^ (e % 16) (so that the 64 lanes' reads of one group spread over the banks), two
+// tiles in flight; xn's quarter of the block's tokens is staged once.
+__global__ __launch_bounds__(RT_BLOCK) void k_rt_dots(RouterArgs a, RtParts p, int T) {
+    __shared__ __align__(16) float4 gt[2][64 * 16];
+    __shared__ __align__(16) float xs[4][RT_QMAX];
+    const int tg = blockIdx.x, q = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int D = a.D, E = a.E, Lq = D / 4, c0 = q * Lq, ntile = Lq / 64;
+    const int t = 4 * tg + w;
+    for (int i = tid; i < 4 * Lq; i += RT_BLOCK) {
+        const int tw = i / Lq, k = i - tw * Lq, tt = 4 * tg + tw;
+        xs[tw][k] = tt < T ? a.xn[(size_t)tt * D + c0 + k] : 0.0f;
+    }
+    auto stage = [&](int j, int buf) {  // 1024 pieces of 16 bytes: four per lane
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int unit = (4 * w + i) * 64 + lane, e = unit >> 4, g = (unit & 15) ^ (e & 15);
+            const int ee = e < E ? e : 0;
+            dma16_untracked(gbl(a.gate_inp + (size_t)ee * D + c0 + 64 * j + 4 * g), (lds_void *)(gt[buf] + (4 * w + i) * 64));
+        }
+    };
+    stage(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    double acc = 0.0, sp = 0.0;
+    float sa = 0.0f;
+    for (int j = 0; j < ntile; j++) {
+        if (j + 1 < ntile) stage(j + 1, (j + 1) & 1);
+        const float4 *gb = gt[j & 1] + lane * 16;
+        const float *xw = xs[w] + 64 * j;
+#pragma unroll
+        for (int g = 0; g < 16; g++) {
+            const float4 gv = gb[g ^ (lane & 15)];
+            const float4 xv = *(const float4 *)(xw + 4 * g);
+            const float gg[4] = {gv.x, gv.y, gv.z, gv.w}, xx[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                acc = fma((double)gg[c], (double)xx[c], acc);
+                sp += fabs(acc);
+                sa = fmaf(fabsf(gg[c]), fabsf(xx[c]), sa);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next tile is in shared memory
+        __syncthreads();                                    // and every wave is done with this one
+    }
+    if (t < T && lane < E) {
+        const size_t o = ((size_t)t * 4 + q) * E + lane;
+        p.t[o] = acc;
+        p.sp[o] = sp;
+        p.sa[o] = sa;
+    }
+}
+
+// grid (T): the quarters joined into each expert's estimate and bound (one thread per
+// expert), the selection intervals, the certified top-k and, when it fails or is
+// forced, the exact replay; outputs as k_router_tok.
+__global__ __launch_bounds__(RT_BLOCK) void k_rt_select(RouterArgs a, RtParts p) {
+    __shared__ __align__(16) float s_xn[GM_MAX_COLS];
+    __shared__ __align__(16) float s_prod[RT_XT][64];  // exact replay scratch
+    __shared__ float s_total;
+    __shared__ unsigned long long s_w0[64], s_w1[64];
+    __shared__ float s_p[GM_MAX_E], s_sel[GM_MAX_E], s_wk[GM_MAX_K];
+    __shared__ int s_idx[GM_MAX_K], s_ok;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int D = a.D, E = a.E, K = a.K;
+    if (tid < E) {
+        const int e = tid;
+        const size_t o = (size_t)t * 4 * E + e;
+        const double t0 = p.t[o], t1 = p.t[o + E], t2 = p.t[o + 2 * E], t3 = p.t[o + 3 * E];
+        const double S = ((t0 + t1) + t2) + t3;
+        const double q1 = t0, q2 = t0 + t1, q3 = q2 + t2, Lq = (double)(D / 4);
+        const double u = 0x1p-24, n = (double)D;
+        // (fp64 roundings of the running sums and of these sums: a relative 2^-40)
+        const double sp = (p.sp[o] + (Lq * fabs(q1) + p.sp[o + E]) + (Lq * fabs(q2) + p.sp[o + 2 * E]) +
+                           (Lq * fabs(q3) + p.sp[o + 3 * E])) * (1.0 + 0x1p-40);
+        // each quarter's fp32 sum of |g x| (exact products inside the fma) errs by at most
+        // (D/4) u relative; below the normal range by 2^-150 a step
+        const double sa = (((double)p.sa[o] + (double)p.sa[o + E]) + ((double)p.sa[o + 2 * E] + (double)p.sa[o + 3 * E])) *
+                              (1.0 + 2.0 * Lq * u) + n * 0x1p-149;
+        const double gamma = n * u / (1.0 - n * u);
+        const double emax = gamma * sa;  // a priori bound on every partial sum's error
+        double B = u * (1.0 + u) * sa + u * (sp + n * emax + u * sa);
+        B = B * (1.0 + 0x1p-30) + 0x1p-40 * sa + n * 0x1p-149;
+        double lo, hi;
+        selection_interval(S, B, a.bias[e], &lo, &hi);
+        float lo_f = __double2float_rd(lo), hi_f = __double2float_ru(hi);
+        if (!(lo_f <= hi_f)) {  // NaN: an interval that is never certified
+            lo_f = -INFINITY;
+            hi_f = INFINITY;
+        }
+        s_w0[e] = (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32);
+        s_w1[e] = (unsigned long long)__float_as_uint(1.0f / (1.0f + expf(-(float)S)));
+    }
+    __syncthreads();
+    if (tid < 64) {
+        unsigned long long w0[1], w1[1];
+        w0[0] = s_w0[tid < E ? tid : E - 1];
+        w1[0] = s_w1[tid < E ? tid : E - 1];
+        certified_select<1>(E, K, tid, w0, w1, s_p, s_idx, s_wk, &s_ok, &s_total);
+        if (tid == 0 && a.force_exact) s_ok = 0;
+    }
+    __syncthreads();
+    if (s_ok) {
+        if (tid < K) {  // normalisation of infer.c:1136-1145
+            const float total = s_total;
+            float wk = s_wk[tid];
+            if (total > 0.0f) {
+                const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;
+                wk = __fmul_rn(wk, __fdiv_rn(1.0f, denom));
+            }
+            s_wk[tid] = wk;
+        }
+        __syncthreads();
+    } else {
+        for (int i = tid; i < D; i += RT_BLOCK) s_xn[i] = a.xn[(size_t)t * D + i];
+        __syncthreads();
+        exact_router(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_p, s_sel, s_idx, s_wk, a.stats);
+    }
+    if (tid < K) {
+        const size_t o = (size_t)t * K + tid;
+        a.topk_idx[o] = s_idx[tid];
+        a.topk_w[o] = s_wk[tid];
+        a.topk_ws[o] = __fmul_rn(s_wk[tid], a.routed_scale);
+        a.hist_idx[o] = s_idx[tid];
+        a.hist_w[o] = s_wk[tid];
+    }
+    for (int i = tid; i < E; i += RT_BLOCK) a.router_prob[(size_t)t * E + i] = s_p[i];
+}

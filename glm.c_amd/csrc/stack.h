@@ -281,8 +281,6 @@ __device__ static inline void sk_stamp(SkShared &sh, int k) {
     if (sh.trace && threadIdx.x == 0) trace_put(sh.trace, SK_TRACE_STAMPS * sh.trace_item + k);
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // Copy `nbytes` (a multiple of 16) from global memory straight into shared memory, 1 KB
 // per wave instruction. Completion is this wave's vmcnt.
 __device__ static inline void dma_copy(void *dst, const void *src, int nbytes) {
@@ -293,14 +291,6 @@ __device__ static inline void dma_copy(void *dst, const void *src, int nbytes) {
                                              (lds_void *)((uint8_t *)dst + off), 16, 0, 0);
 }
 
-// dma_copy's 16-byte piece issued by inline assembly, which the compiler does not see as a
-// shared-memory DMA: with a global_load_lds of its own in flight, the compiler waits for
-// all of a wave's loads before using any loaded register, which would serialise the
-// streamed expert weights behind it. The caller waits (vmcnt) before reading `dst`.
-__device__ static inline void dma16_untracked(const GM_GLOBAL void *src, lds_void *dst) {
-    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)dst);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
-}
 
 // ---------------------------------------------------------------- top-k selection
 //
