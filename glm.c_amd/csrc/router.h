@@ -106,7 +106,7 @@ __device__ static inline void wave_argmax(double key, int idx, double *bkey, int
 }
 
 #define RT_SEL_C (GM_MAX_E / 64)  // experts per lane in a one-wave selection
-#define RT_XT 128                 // columns per tile of the exact replay (its product tile is 32 KB)
+#define RT_XT 128                 // scratch of the exact replay: RT_XT x 64 floats (two 16 KB gate tiles)
 
 // Certified top-k on one wave, over C chunks of 64 experts whose results are in
 // registers (lane l: experts l + 64c; w0 = fp32 bits of lo | hi << 32, w1 = fp32 bits
@@ -190,57 +190,69 @@ __device__ __attribute__((always_inline)) static void certified_select(int E, in
 // glm.c's router replayed exactly in fp32 (infer.c:916-938, 1104-1145) by one block of
 // 256 threads, for the xn in shared memory: every probability into p and selection
 // score into sel (shared, [E]), the top-k into idx and its normalised weights into wk
-// (shared, [K]). prod is 32 KB of shared scratch. Counts the replay in stats, and a
+// (shared, [K]). prod is 32 KB of shared scratch (16-byte aligned). Counts the replay in stats, and a
 // top-k whose order hinges on expf's last bits as unresolved.
 __device__ __attribute__((always_inline)) static void exact_router(int D, int E, int K, int tid, const float *gate_inp, const float *bias_p,
                                     const float *xn, float (*prod)[64], float *p, float *sel, int *idx, float *wk_out,
                                     unsigned long long *stats) {
     const GM_GLOBAL float *bias = gbl(bias_p);
-    // infer.c:916-925 for 64 experts at a time, in tiles of RT_XT columns: every thread
-    // forms the products fl(g * xn) of one expert (its lane) and a quarter of the tile's
-    // columns (its wave) into prod[column][expert], then lane e of wave 0 adds its
-    // expert's products in column order. Each thread's gate rows are fetched two tiles
-    // ahead into registers, so the loads overlap the chain.
-    const int lane = tid & 63, w = tid >> 6, qc = RT_XT / 4;  // columns per wave and tile
-    const int ntile = D / RT_XT;
+    // infer.c:916-925 for 64 experts at a time: lane e of wave 0 forms fl(g * xn) and adds
+    // it to its expert's chain, column by column. The gate rows reach shared memory in
+    // tiles of 64 columns by DMA from every wave, [64 experts][16 four-column groups] with
+    // group g of row e at slot g ^ (e % 16), two tiles in flight (prod's 32 KB); the chain
+    // reads the next four groups before adding the current ones.
+    const int lane = tid & 63, w = tid >> 6;
+    float4(*gt)[1024] = (float4(*)[1024])prod;
+    const int ntile = D / 64;
     for (int eb = 0; eb < E; eb += 64) {
         const int ne = E - eb < 64 ? E - eb : 64;
-        const float4 *grow = (const float4 *)(gate_inp + (size_t)(eb + (lane < ne ? lane : 0)) * D + w * qc);
-        float4 ga[RT_XT / 16], gb[RT_XT / 16];
+        auto stage = [&](int j, int buf) {  // 1024 pieces of 16 bytes: four per lane
 #pragma unroll
-        for (int q = 0; q < RT_XT / 16; q++) ga[q] = grow[q];
-#pragma unroll
-        for (int q = 0; q < RT_XT / 16; q++) gb[q] = grow[RT_XT / 4 + q];
-        float chain = 0.0f;
-        // one tile from registers g (tile t), then g refilled with tile t + 2
-        auto tile = [&](float4 *g, int t) {
-            const int c0 = t * RT_XT + w * qc;
-#pragma unroll
-            for (int q = 0; q < RT_XT / 16; q++) {
-                const float4 xq = *(const float4 *)&xn[c0 + 4 * q];
-                prod[w * qc + 4 * q + 0][lane] = __fmul_rn(g[q].x, xq.x);
-                prod[w * qc + 4 * q + 1][lane] = __fmul_rn(g[q].y, xq.y);
-                prod[w * qc + 4 * q + 2][lane] = __fmul_rn(g[q].z, xq.z);
-                prod[w * qc + 4 * q + 3][lane] = __fmul_rn(g[q].w, xq.w);
+            for (int i = 0; i < 4; i++) {
+                const int unit = (4 * w + i) * 64 + lane, e = unit >> 4, g = (unit & 15) ^ (e & 15);
+                const int ee = eb + (e < ne ? e : 0);
+                dma16_untracked(gbl(gate_inp + (size_t)ee * D + 64 * j + 4 * g), (lds_void *)(gt[buf] + (4 * w + i) * 64));
             }
-            __syncthreads();
-            if (t + 2 < ntile)
-#pragma unroll
-                for (int q = 0; q < RT_XT / 16; q++) g[q] = grow[(t + 2) * (RT_XT / 4) + q];
+        };
+        stage(0, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        float chain = 0.0f;
+        for (int j = 0; j < ntile; j++) {
+            if (j + 1 < ntile) stage(j + 1, (j + 1) & 1);
             if (w == 0) {
-                for (int c0 = 0; c0 < RT_XT; c0 += 16) {
-                    float v[16];  // sixteen reads in flight, then the sixteen dependent adds
+                const float4 *gb = gt[j & 1] + lane * 16;
+                const float4 *xb = (const float4 *)(xn + 64 * j);
+                float4 ga[4], xa[4], gn[4], xq[4];
 #pragma unroll
-                    for (int j = 0; j < 16; j++) v[j] = prod[c0 + j][lane];
+                for (int u = 0; u < 4; u++) {
+                    ga[u] = gb[u ^ (lane & 15)];
+                    xa[u] = xb[u];
+                }
 #pragma unroll
-                    for (int j = 0; j < 16; j++) chain = __fadd_rn(chain, v[j]);
+                for (int g0 = 0; g0 < 16; g0 += 4) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {  // the next four groups (the last batch re-reads the first)
+                        const int gg = g0 + 4 < 16 ? g0 + 4 + u : u;
+                        gn[u] = gb[gg ^ (lane & 15)];
+                        xq[u] = xb[gg];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        chain = __fadd_rn(chain, __fmul_rn(ga[u].x, xa[u].x));
+                        chain = __fadd_rn(chain, __fmul_rn(ga[u].y, xa[u].y));
+                        chain = __fadd_rn(chain, __fmul_rn(ga[u].z, xa[u].z));
+                        chain = __fadd_rn(chain, __fmul_rn(ga[u].w, xa[u].w));
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        ga[u] = gn[u];
+                        xa[u] = xq[u];
+                    }
                 }
             }
-            __syncthreads();
-        };
-        for (int t = 0; t < ntile; t += 2) {  // ntile = D / 128 is even
-            tile(ga, t);
-            tile(gb, t + 1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next tile is in shared memory
+            __syncthreads();                                    // and wave 0 is done with this one
         }
         if (tid < ne) {
             const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain)));
