@@ -2,7 +2,7 @@
 //
 // A decode call (T=1) is one persistent launch, k_moe_stack (stack.h), that takes
 // the token through any run of layers. A batch (T>1) runs per layer:
-//   k_rt_norm       grid (T)               rmsnorm (router.h; E <= 64, else k_router_tok does all three)
+//   k_rt_norm       grid (T/4)             rmsnorm, a wave per token (router.h; E <= 64, else k_router_tok does all three)
 //   k_rt_dots       grid (T/4, 4)          router logits' sums, a thread per (token, expert, quarter of D)
 //   k_rt_select     grid (T)               bounds, certified top-k, exact replay when needed
 //   k_act_split     grid (rows)            xn as fp16 hi+lo planes with a per-row exponent (grouped.h)
@@ -10,7 +10,7 @@
 //   k_group_gu      grid (F/64, tiles)     grouped gate/up GEMM + SwiGLU on fp16 MFMA (grouped.h)
 //   k_act_split     grid (rows)            h as fp16 hi+lo planes
 //   k_group_down    grid (D/64, tiles)     grouped down GEMM, one row per (token, slot) (grouped.h)
-//   k_token_combine grid (D/256, T)        weighted combine + shared expert + residual (grouped.h)
+//   k_token_combine grid (D/1024, T)       weighted combine + shared expert + residual (grouped.h)
 // With GMOE_GROUPED_MIN_T above T, batches take the per-token kernels k_gate_up and
 // k_down_combine (experts.h) instead. Expert weights are uploaded once per layer
 // into the tiled Q8_0 layout of common.h and stay resident.
@@ -686,7 +686,7 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
         rp.t = c->rt_t;
         rp.sp = c->rt_sp;
         rp.sa = c->rt_sa;
-        hipLaunchKernelGGL(k_rt_norm, dim3(T), dim3(RT_BLOCK), 0, st, ra);
+        hipLaunchKernelGGL(k_rt_norm, dim3((T + 3) / 4), dim3(RT_BLOCK), 0, st, ra, T);
         hipLaunchKernelGGL(k_rt_dots, dim3((T + 3) / 4, 4), dim3(RT_BLOCK), 0, st, ra, rp, T);
         hipLaunchKernelGGL(k_rt_select, dim3(T), dim3(RT_BLOCK), 0, st, ra, rp);
     } else {
@@ -757,7 +757,11 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
         ta.TK = TK;
         ta.routed_on = routed_on;
         pr = prof_begin(c, st, GMOE_KERNEL_COMBINE);
-        hipLaunchKernelGGL(k_token_combine, dim3((D + GP_BLOCK - 1) / GP_BLOCK, T), dim3(GP_BLOCK), 0, st, ta);
+        const bool vec = (((uintptr_t)ta.x_in | (uintptr_t)ta.x_out) & 15) == 0;
+        if (vec)
+            hipLaunchKernelGGL(k_token_combine<true>, dim3((D + 4 * GP_BLOCK - 1) / (4 * GP_BLOCK), T), dim3(GP_BLOCK), 0, st, ta);
+        else
+            hipLaunchKernelGGL(k_token_combine<false>, dim3((D + 4 * GP_BLOCK - 1) / (4 * GP_BLOCK), T), dim3(GP_BLOCK), 0, st, ta);
         prof_end(pr, st);
         HIP_OK(hipGetLastError());
     } else {

@@ -374,22 +374,35 @@ struct TokenCombineArgs {
     int D, K, TK, routed_on;
 };
 
-// grid (D/256, T): x' = x + (shared + sum_k fl(w_k y_k)) in top-k order (infer.c:1192,
-// 1212-1214), with the shared and routed sums kept as observables.
+// grid (D/1024, T): x' = x + (shared + sum_k fl(w_k y_k)) in top-k order (infer.c:1192,
+// 1212-1214), with the shared and routed sums kept as observables; four consecutive
+// elements per thread (D is a multiple of 256), in 16-byte loads and stores when the
+// caller's x_in and x_out are 16-byte aligned (VEC), else element by element.
+template <bool VEC>
 __global__ __launch_bounds__(GP_BLOCK) void k_token_combine(TokenCombineArgs a) {
-    const int t = blockIdx.y, d = blockIdx.x * GP_BLOCK + threadIdx.x;
+    const int t = blockIdx.y, d = 4 * (blockIdx.x * GP_BLOCK + threadIdx.x);
     if (d >= a.D) return;
-    float acc = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (a.routed_on) {
         for (int k = 0; k < a.K; k++) {
             if (a.topk_idx[t * a.K + k] < 0) continue;
-            const float yk = a.y[(size_t)a.pair_row[t * a.K + k] * a.D + d];
-            acc = __fadd_rn(acc, __fmul_rn(a.topk_ws[t * a.K + k], yk));
+            const float4 yk = *(const float4 *)&a.y[(size_t)a.pair_row[t * a.K + k] * a.D + d];
+            const float w = a.topk_ws[t * a.K + k], yv[4] = {yk.x, yk.y, yk.z, yk.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] = __fadd_rn(acc[c], __fmul_rn(w, yv[c]));
         }
     }
-    const float shv = a.y[(size_t)(a.TK + t) * a.D + d];
+    const float4 sh4 = *(const float4 *)&a.y[(size_t)(a.TK + t) * a.D + d];
     const size_t o = (size_t)t * a.D + d;
-    a.routed_out[o] = acc;
-    a.shared_out[o] = shv;
-    a.x_out[o] = __fadd_rn(a.x_in[o], __fadd_rn(shv, acc));
+    *(float4 *)&a.routed_out[o] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *(float4 *)&a.shared_out[o] = sh4;
+    const float shv[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
+    if (VEC) {
+        const float4 x4 = *(const float4 *)&a.x_in[o];
+        *(float4 *)&a.x_out[o] = make_float4(__fadd_rn(x4.x, __fadd_rn(shv[0], acc[0])), __fadd_rn(x4.y, __fadd_rn(shv[1], acc[1])),
+                                             __fadd_rn(x4.z, __fadd_rn(shv[2], acc[2])), __fadd_rn(x4.w, __fadd_rn(shv[3], acc[3])));
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; c++) a.x_out[o + c] = __fadd_rn(a.x_in[o + c], __fadd_rn(shv[c], acc[c]));
+    }
 }

@@ -516,15 +516,52 @@ struct RtParts {
     float *sa;   // [T][4][E] quarter sums of |g x| (fp32)
 };
 
-// grid (T): xn of every token (infer.c:746-752), bit-identical to glm.c.
-__global__ __launch_bounds__(RT_BLOCK) void k_rt_norm(RouterArgs a) {
-    __shared__ double red[4];
-    __shared__ float s_mean;
-    const int t = blockIdx.x, tid = threadIdx.x, D = a.D;
+// grid (ceil(T/4)): xn of token 4 blockIdx.x + w on wave w (infer.c:746-752),
+// bit-identical to glm.c: lane l holds the row's D/64 consecutive values from l D/64, the
+// mean of squares is certified from the wave's fp64 sum (relative error below D 2^-52)
+// or else replayed in order by lane 0, and xn is formed from the registers.
+__global__ __launch_bounds__(RT_BLOCK) void k_rt_norm(RouterArgs a, int T) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, t = 4 * blockIdx.x + w, D = a.D;
+    if (t >= T) return;  // wave-uniform
+    const int per = D / 64;  // a multiple of 4, at most RT_CPL_MAX
     const float *xt = a.x + (size_t)t * D;
-    const float mean = certified_mean_sq(xt, D, red, &s_mean, true, a.stats);
+    float xv[RT_CPL_MAX];
+    if (((uintptr_t)a.x & 15) == 0) {  // the caller's x: 16-byte loads when aligned
+#pragma unroll
+        for (int q = 0; q < RT_CPL_MAX / 4; q++) {
+            const float4 v = q < per / 4 ? *(const float4 *)(xt + lane * per + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[4 * q] = v.x;
+            xv[4 * q + 1] = v.y;
+            xv[4 * q + 2] = v.z;
+            xv[4 * q + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < RT_CPL_MAX; j++) xv[j] = j < per ? xt[lane * per + j] : 0.0f;
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < RT_CPL_MAX; j++) ss += (double)xv[j] * (double)xv[j];
+    ss = wave_sum_dpp(ss);
+    const double v = ss / (double)D, rho = (double)D * 0x1p-52;
+    float mean = (float)(v * (1.0 - rho));
+    if (mean != (float)(v * (1.0 + rho))) {  // wave-uniform
+        double sq = 0.0;
+        if (lane == 0) {
+            for (int i = 0; i < D; i++) sq += (double)xt[i] * (double)xt[i];
+            atomicAdd(&a.stats[GM_STAT_NORM_EXACT], 1ull);
+        }
+        mean = (float)(readlane_d(sq, 0) / (double)D);
+    }
     const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, a.eps)));
-    for (int i = tid; i < D; i += RT_BLOCK) a.xn[(size_t)t * D + i] = __fmul_rn(__fmul_rn(xt[i], inv), a.norm_w[i]);
+#pragma unroll
+    for (int q = 0; q < RT_CPL_MAX / 4; q++)
+        if (q < per / 4) {
+            const float4 nw = *(const float4 *)(a.norm_w + lane * per + 4 * q);
+            *(float4 *)(a.xn + (size_t)t * D + lane * per + 4 * q) =
+                make_float4(__fmul_rn(__fmul_rn(xv[4 * q], inv), nw.x), __fmul_rn(__fmul_rn(xv[4 * q + 1], inv), nw.y),
+                            __fmul_rn(__fmul_rn(xv[4 * q + 2], inv), nw.z), __fmul_rn(__fmul_rn(xv[4 * q + 3], inv), nw.w));
+        }
 }
 
 #define RT_QMAX (GM_MAX_COLS / 4)  // columns per quarter
