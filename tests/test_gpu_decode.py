@@ -14,6 +14,10 @@ from conftest import assert_close
 pytestmark = pytest.mark.gpu
 
 SMALL = gmoe.Shape(dim=256, moe_ffn_dim=256, n_routed_experts=16, n_experts_used=4)
+# more experts than a wave's lanes: decode router blocks hold several experts each, the
+# batch router takes its one-block-per-token form (k_router_tok), selection spans chunks
+WIDE = gmoe.Shape(dim=512, moe_ffn_dim=256, n_routed_experts=128, n_experts_used=6)
+WIDEST = gmoe.Shape(dim=256, moe_ffn_dim=256, n_routed_experts=256, n_experts_used=8)
 
 
 def run_case(shape, seed, T, norm_mode=gmoe.SYNTH_NORM_ONES, flags=0, layer=1):
@@ -63,3 +67,13 @@ def test_glm_shape_t1():
 
 def test_glm_shape_batch8():
     check(*run_case(gmoe.GLM47_FLASH, seed=5, T=8, norm_mode=gmoe.SYNTH_NORM_RANDOM))
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_wide_expert_count(T):
+    check(*run_case(WIDE, seed=6, T=T, norm_mode=gmoe.SYNTH_NORM_RANDOM))
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_widest_expert_count(T):
+    check(*run_case(WIDEST, seed=7, T=T))
