@@ -145,6 +145,18 @@ __device__ static inline unsigned long long *stage_plane(const StackArgs &a, int
 }
 static_assert(2 * GM_MAX_E <= SK_STAGE_COPY_WORDS, "a stage copy holds two planes of GM_MAX_E words");
 
+// fp32 of v rounded toward -inf or +inf: the round-to-nearest conversion lies within one
+// ulp of v, so one step toward v from its wrong side gives the directed rounding (also
+// at overflow, inf -> FLT_MAX; NaN stays NaN), without a rounding-mode switch.
+__device__ static inline float f32_rd(double v) {
+    const float f = (float)v;
+    return (double)f > v ? nextafterf(f, -INFINITY) : f;
+}
+__device__ static inline float f32_ru(double v) {
+    const float f = (float)v;
+    return (double)f < v ? nextafterf(f, INFINITY) : f;
+}
+
 __device__ static inline void st_f(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ static inline void st_i(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ static inline void st_d(double *p, double v) {
@@ -479,8 +491,8 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     // would queue the other block (an expert item) behind them for microseconds.
     if (li > 0 && !wait_ge(&a.ctr[SKF(li - 1, SKF_PART)], 1u, a.error, sh)) return false;
     const Seg nw = load_seg(gbl(L.norm) + tid * per, per);
-    // the selection biases of this block's experts, for lanes 3x of the bound tail below
-    const float bias_x = tid < 3 * nx ? gbl(L.bias)[b + (tid / 3) * NR] : 0.0f;
+    // the selection biases of this block's experts, for lanes 4x of the bound tail below
+    const float bias_x = tid < 4 * nx ? gbl(L.bias)[b + (tid >> 2) * NR] : 0.0f;
     Seg gw[SK_RX_MAX];
 #pragma unroll
     for (int x = 0; x < SK_RX_MAX; x++) {
@@ -549,9 +561,9 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
     __syncthreads();
     sk_stamp(sh, 13);
     // The bound and the three sigmoids of each expert's entry (interval ends and p) on
-    // three lanes of wave 0, lane 3x + r for expert x.
+    // three lanes of wave 0, lane 4x + r (r < 3) for expert x.
     if (tid < 64) {
-        const int x = tid / 3 < nx ? tid / 3 : 0, r = tid % 3, e = b + x * NR;
+        const int x = (tid >> 2) < nx ? tid >> 2 : 0, r = tid & 3, e = b + x * NR;
         const double S = ((sh.u.r.wv[0][x][0] + sh.u.r.wv[1][x][0]) + sh.u.r.wv[2][x][0]) + sh.u.r.wv[3][x][0];
         const double sp = ((sh.u.r.wv[0][x][1] + sh.u.r.wv[1][x][1]) + sh.u.r.wv[2][x][1]) + sh.u.r.wv[3][x][1];
         const double sa = ((sh.u.r.wv[0][x][2] + sh.u.r.wv[1][x][2]) + sh.u.r.wv[2][x][2]) + sh.u.r.wv[3][x][2];
@@ -562,13 +574,15 @@ __device__ __attribute__((always_inline)) static bool sk_router_item(const Stack
         // that, and each product adds u|p_k|
         double B = u * (1.0 + u) * sa + u * (sp + n * emax + u * sa);
         B = B * (1.0 + 0x1p-30) + 0x1p-40 * sa + n * 0x1p-149;
-        const float arg = r == 0 ? __double2float_rd(S - B) : r == 1 ? __double2float_ru(S + B) : (float)S;
+        const float arg = r == 0 ? f32_rd(S - B) : r == 1 ? f32_ru(S + B) : (float)S;
         const float sg = 1.0f / (1.0f + expf(-arg));
-        const float phi = __shfl_down(sg, 1, 64), p = __shfl_down(sg, 2, 64);
-        if (r == 0 && tid / 3 < nx) {
+        // lanes 4x + 1 and 4x + 2 of the quad, to lane 4x (quad_perm [1,1,2,3] and [2,1,2,3])
+        const float phi = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sg), 0xE5, 0xF, 0xF, false));
+        const float p = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sg), 0xE6, 0xF, 0xF, false));
+        if (r == 0 && (tid >> 2) < nx) {
             double lo, hi;
             selection_bounds((double)sg, (double)phi, bias_x, &lo, &hi);
-            float lo_f = __double2float_rd(lo), hi_f = __double2float_ru(hi);
+            float lo_f = f32_rd(lo), hi_f = f32_ru(hi);
             if (!(lo_f <= hi_f)) {  // NaN: an interval that is never certified
                 lo_f = -INFINITY;
                 hi_f = INFINITY;
