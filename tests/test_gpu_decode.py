@@ -77,3 +77,15 @@ def test_wide_expert_count(T):
 @pytest.mark.parametrize("T", [1, 8])
 def test_widest_expert_count(T):
     check(*run_case(WIDEST, seed=7, T=T))
+
+
+@pytest.mark.parametrize("name,T", [("small", 16), ("glm", 8), ("wide", 8)])
+def test_forced_exact_router_batch(name, T):
+    """GMOE_FLAG_EXACT_ROUTER on a batch: every token replays glm.c's fp32 chains (in the
+    batch router's last kernel, or k_router_tok for more than 64 experts)."""
+    shape = {"small": SMALL, "glm": gmoe.GLM47_FLASH, "wide": WIDE}[name]
+    want, got, st, stats = run_case(shape, seed=8, T=T, flags=gmoe.GMOE_FLAG_EXACT_ROUTER)
+    check(want, got, st, stats)
+    # the replayed chain is glm.c's; only expf may differ by an ulp from glibc's
+    assert_close(st["router_prob"], want["router_prob"], "router_prob", max_abs=1.2e-7, rel_l2=1e-7)
+    assert stats["routing_exact_path"] >= T
