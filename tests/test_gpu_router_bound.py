@@ -1,8 +1,8 @@
-"""The decode router's certificate under heavy cancellation.
+"""The routers' certificates under heavy cancellation.
 
-glm.c's logit is a sequential fp32 chain (infer.c:916-938); the decode kernel
-estimates it in fp64 and certifies the top-k only when the chain's rounding bound
-separates the candidates, else it replays the chain exactly. These cases build two
+glm.c's logit is a sequential fp32 chain (infer.c:916-938); the decode kernel and
+the batch routers estimate it in fp64 and certify the top-k only when the chain's
+rounding bound separates the candidates, else they replay the chain exactly. These cases build two
 router rows whose products climb to partial sums near D/2 and return near zero, so
 that the chains' roundings (ulps of ~1e3) exceed the rows' exact difference (3e-4 to
 6e-4), which is chosen so that the fp32 chain orders the pair against the exact order.
@@ -70,12 +70,12 @@ def adversarial_rows(xn, rng):
     raise AssertionError("no order-flipping pair found")
 
 
-def make_adversarial(L, xn, rng):
+def make_adversarial(L, xn, rng, shape=SHAPE):
     g1, g2 = adversarial_rows(xn, rng)
     L.gate_inp[PAIR[0]] = g1
     L.gate_inp[PAIR[1]] = g2
-    b = np.full(SHAPE.E, -10.0, np.float32)
-    b[:SHAPE.K - 1] = 10.0 * np.arange(SHAPE.K - 1, 0, -1)  # certainly selected, in order, never tied
+    b = np.full(shape.E, -10.0, np.float32)
+    b[:shape.K - 1] = 10.0 * np.arange(shape.K - 1, 0, -1)  # certainly selected, in order, never tied
     b[list(PAIR)] = 0.0  # the pair competes for the last slot
     L.exp_probs_b[:] = b
 
@@ -109,6 +109,35 @@ def test_cancellation_routing_against_oracle(seed):
         np.testing.assert_array_equal(ctx.read_topk(2, 1)[0], want2["topk_idx"], err_msg="stack layer 2 routing")
         assert_close(d_out.download((1, SHAPE.D), np.float32), want2["x_out"], "stack x_out")
         assert ctx.stats()["routing_unresolved"] == 0
+    finally:
+        ctx.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("E", [64, 128])
+def test_cancellation_routing_batch(E):
+    """The batch router's certificates under the same cancellation: with 64 experts the
+    four-quarter partial sums and their joined bound, with 128 the one-block-per-token
+    router. Other tokens would meet the rows' large norms and tie at a saturated sigmoid,
+    so the batch repeats the adversarial token."""
+    shape = gmoe.Shape(dim=2048, moe_ffn_dim=256, n_routed_experts=E, n_experts_used=4)
+    T = 8
+    rng = np.random.default_rng(31 + E)
+    orc = oracle.Oracle("port")
+    L = gmoe.HostLayer(shape, seed=31, layer=1, norm_mode=gmoe.SYNTH_NORM_RANDOM)
+    x = np.repeat(gmoe.activations(31, 7, 1, shape.D), T, axis=0)
+    make_adversarial(L, orc.layer(shape, L, x[:1])["xn"][0], rng, shape)
+    ctx = gmoe.Context(shape, n_layers=2, max_tokens=T)
+    try:
+        ctx.upload(1, L)
+        print(f"[case] cancellation batch E={E} T={T}", flush=True)
+        want = orc.layer(shape, L, x)
+        got, st = gmoe.forward_host(ctx, 1, x)
+        np.testing.assert_array_equal(st["topk_idx"], want["topk_idx"], err_msg="batch routing")
+        assert_close(got, want["x_out"], "batch x_out")
+        stats = ctx.stats()
+        assert stats["routing_unresolved"] == 0
+        assert stats["routing_exact_path"] >= T  # no certificate may hold at this cancellation
     finally:
         ctx.close()
 
