@@ -91,8 +91,7 @@ struct gmoe_ctx {
     float *h = nullptr, *y = nullptr, *shared_out = nullptr, *routed_out = nullptr;
     double2 *stage = nullptr;
     int *topk_idx = nullptr;
-    unsigned *tok_counter = nullptr, *panel_counter = nullptr, *disp_counter = nullptr;
-    int *disp_tmp_tok = nullptr, *disp_tmp_slot = nullptr, *disp_counts = nullptr;
+    unsigned *tok_counter = nullptr, *panel_counter = nullptr;
     int *offsets = nullptr, *tokens = nullptr, *slots = nullptr;
     // prefill grouped GEMMs (grouped.h): list rows are [Tmax*K routed pairs][Tmax shared]
     __half *xspl = nullptr, *hspl = nullptr;
@@ -164,8 +163,7 @@ static void free_ctx(gmoe_ctx *c) {
         delete[] c->layers;
     }
     void *bufs[] = {c->xn, c->router_prob, c->topk_w, c->topk_ws, c->h, c->y, c->shared_out, c->routed_out,
-                    c->stage, c->topk_idx, c->tok_counter, c->panel_counter, c->disp_counter, c->disp_tmp_tok,
-                    c->disp_tmp_slot, c->disp_counts, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
+                    c->stage, c->topk_idx, c->tok_counter, c->panel_counter, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
                     c->stats_dev, c->x_host_io, c->staging, c->sk_ws, c->sk_ctr, c->sk_error,
                     c->sk_layers, c->sk_trace, c->xspl, c->hspl, c->xexp, c->hexp, c->pair_row, c->n_tiles,
                     c->hbuf, c->ybuf, c->tiles, c->rt_t, c->rt_sp, c->rt_sa};
@@ -256,10 +254,6 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     rc |= dev_alloc(&c->topk_idx, T * K);
     rc |= dev_alloc(&c->tok_counter, T);
     rc |= dev_alloc(&c->panel_counter, T * (D / 16));
-    rc |= dev_alloc(&c->disp_counter, 1);
-    rc |= dev_alloc(&c->disp_tmp_tok, E * T);
-    rc |= dev_alloc(&c->disp_tmp_slot, E * T);
-    rc |= dev_alloc(&c->disp_counts, E);
     rc |= dev_alloc(&c->offsets, E + 1);
     {
         const size_t rows = T * K + T;  // list rows: routed pairs, then the shared expert's
@@ -308,13 +302,12 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     // Counters start at zero; each kernel's last block puts its counter back to zero.
     hipError_t e0 = hipMemset(c->tok_counter, 0, T * sizeof(unsigned));
     hipError_t e1 = hipMemset(c->panel_counter, 0, T * (D / 16) * sizeof(unsigned));
-    hipError_t e2 = hipMemset(c->disp_counter, 0, sizeof(unsigned));
     hipError_t e3 = hipMemset(c->stats_dev, 0, GM_STAT_COUNT * sizeof(unsigned long long));
     hipError_t e4 = hipMemset(c->hist_idx, 0xff, (size_t)c->L * T * K * sizeof(int));
     hipError_t e6 = hipMemset(c->sk_error, 0, sizeof(int));
     hipError_t e7 = hipMemset(c->sk_layers, 0, (size_t)c->L * sizeof(StackLayer));
     hipError_t e5 = hipDeviceSynchronize();
-    if (e0 || e1 || e2 || e3 || e4 || e5 || e6 || e7) {
+    if (e0 || e1 || e3 || e4 || e5 || e6 || e7) {
         set_err("gmoe_create: initialising device buffers failed");
         free_ctx(c);
         return GMOE_ERR_HIP;
@@ -522,10 +515,6 @@ static int launch_dispatch(gmoe_ctx *c, int T, int routed_on, hipStream_t st) {
     da.T = T;
     da.K = c->K;
     da.E = c->E;
-    da.tmp_tok = c->disp_tmp_tok;
-    da.tmp_slot = c->disp_tmp_slot;
-    da.counts = c->disp_counts;
-    da.counter = c->disp_counter;
     da.offsets = c->offsets;
     da.tokens = c->tokens;
     da.slots = c->slots;
