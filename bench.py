@@ -1,22 +1,35 @@
 #!/usr/bin/env python3
 """MoE-stack decode benchmark on one MI355X.
 
-Workload: the MoE half of one GLM-4.7-Flash decode step -- 46 MoE layers in
-sequence (hidden 2048, 64 routed experts + 1 shared, moe_intermediate 1536,
-top-4, Q8_0 experts), T=1, per-layer seeded synthetic weights resident in HBM
-(~30 GB), RMSNorm inside every layer (infer.c:1098). A step is one token through
-all 46 layers via gmoe_forward_layers; every step starts from the same input.
+Headline workload: the MoE half of one GLM-4.7-Flash decode step -- 46 MoE layers in
+sequence (hidden 2048, 64 routed experts + 1 shared, moe_intermediate 1536, top-4,
+Q8_0 experts), T=1, per-layer seeded synthetic weights resident in HBM (~30 GB),
+RMSNorm inside every layer (infer.c:1098). A step is one token through all 46 layers
+via gmoe_forward_layers; every step starts from the same input.
 
-Prints one JSON line: tokens/s (value), the per-layer time and the HBM rate on
-the selected experts' Q8_0 bytes, the roofline of the dominant kernel (its
-HIP-event launch time against MI355X's 8 TB/s) and the reference CPU path timed
-on this host (glm.c's own infer.c built from source, OpenMP, same weights).
+Prints one JSON line: tokens/s (value), the per-layer time and the HBM rate on the
+selected experts' Q8_0 bytes, the roofline of the dominant kernel (its HIP-event launch
+time against MI355X's 8 TB/s) and the reference CPU path timed on this host (glm.c's
+own infer.c built from source, OpenMP bound to cores as glm.c's Makefile runs it, same
+weights). Extra keys time the other workloads on the same resident layers: one MoE
+layer per launch (rotating over the 46), prefill batches of T=512 (near-uniform
+routing) and T=128 (Zipf(1.2)-skewed routing) on the grouped expert GEMMs, and the
+glm.c drop-in hook (glm_backend_try_hip_moe on a RunState in host memory).
 """
-import argparse
-import json
 import os
-import sys
-import time
+
+# glm.c's Makefile runs the CPU path with threads bound to cores (Makefile:89-92). libgomp
+# reads these when it loads, so they are set before anything loads it.
+os.environ.setdefault("OMP_PROC_BIND", "true")
+os.environ.setdefault("OMP_PLACES", "cores")
+# the CPUs this process may use, read before libgomp binds the initial thread to one of them
+CPUS_ALLOWED = len(os.sched_getaffinity(0))
+
+import argparse  # noqa: E402
+import json  # noqa: E402
+import subprocess  # noqa: E402
+import sys  # noqa: E402
+import time  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 for _p in (os.path.join(ROOT, "glm.c_amd"), os.path.join(ROOT, "oracle")):
@@ -24,6 +37,7 @@ for _p in (os.path.join(ROOT, "glm.c_amd"), os.path.join(ROOT, "oracle")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 N_MOE_LAYERS = 46
 METRIC = "MoE-stack decode tokens/s (46 GLM-4.7-Flash MoE layers, Q8_0, T=1)"
 
@@ -41,6 +55,20 @@ def omp_threads():
         return int(os.environ.get("OMP_NUM_THREADS", "1"))
 
 
+def host_cpus():
+    """Physical cores of this host (lscpu: cores per socket x sockets) and the CPUs this
+    process may run on."""
+    phys = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        phys = int(kv["Core(s) per socket"].strip()) * int(kv["Socket(s)"].strip())
+    except (OSError, KeyError, ValueError, subprocess.SubprocessError):
+        pass
+    return {"host_physical_cores": phys, "cpus_allowed": CPUS_ALLOWED,
+            "omp_proc_bind": os.environ.get("OMP_PROC_BIND"), "omp_places": os.environ.get("OMP_PLACES")}
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -52,36 +80,154 @@ def traffic_from_profiles(kernel):
         return None
 
 
+def median(v):
+    v = sorted(v)
+    return v[len(v) // 2]
+
+
 def cpu_baseline(shape, host_layers, x0, seconds):
-    """glm.c's CPU MoE path on the same layers: tokens through the 46-layer stack until
-    `seconds` of wall time have passed (at least 2 tokens)."""
+    """glm.c's CPU MoE path (infer.c, OpenMP) on the same layers: decode tokens through the
+    46-layer stack, every layer call timed with glm.c's monotonic clock (infer.c:1426-1430).
+    All of the process's threads (OMP_NUM_THREADS) for about `seconds`, then one thread
+    for two tokens."""
     import numpy as np
     import oracle
 
-    kind = "reference" if oracle.available("reference") else "port"
-    orc = oracle.Oracle(kind)
-    x = np.array(x0, np.float32)
-    orc.stack(shape, host_layers, x)  # warm the page cache and the thread pool
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        orc.stack(shape, host_layers, x)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 2 and time.perf_counter() - t_start >= seconds:
-            break
-    times.sort()
-    med = times[len(times) // 2]
+    if not oracle.available("reference"):
+        return None
+    threads = omp_threads()
+    oracle.stack_timed(shape, host_layers, x0, 1, threads)  # warm the page cache and the thread pool
+    ms = oracle.stack_timed(shape, host_layers, x0, 1, threads)
+    n_tok = max(20, int(seconds * 1e3 / max(1e-3, float(ms.sum()))))
+    ms = oracle.stack_timed(shape, host_layers, x0, n_tok, threads)
+    tok_ms = median(ms.sum(axis=1).tolist())
+    one = oracle.stack_timed(shape, host_layers, x0, 2, 1)
+    oracle.stack_timed(shape, host_layers[:1], x0, 1, threads)  # back to the full team
+    per_layer_bytes = (shape.K + 1) * shape.expert_bytes()
+    layer_ms = median(ms.ravel().tolist())
     return {
-        "value": 1.0 / med,
+        "value": round(1e3 / tok_ms, 3),
         "unit": "tokens/s",
-        "cores": omp_threads(),
-        "kind": kind,
-        "sample": f"{len(times)} decode tokens through the same {len(host_layers)}-layer stack, median of per-token "
-                  f"wall times (monotonic clock), OpenMP threads = OMP_NUM_THREADS",
-        "ms_per_token": med * 1e3,
-        "layer_us": med * 1e6 / len(host_layers),
+        "cores": threads,
+        "kind": "reference",
+        "sample": f"{n_tok} decode tokens through the same {len(host_layers)}-layer stack (glm.c's infer.c built "
+                  f"with its Makefile flags, OpenMP threads bound to cores), median per-token time; "
+                  f"{n_tok * len(host_layers)} timed layer calls",
+        "ms_per_token": round(tok_ms, 3),
+        "layer_us": round(layer_ms * 1e3, 1),
+        "layer_gbs_expert_bytes": round(per_layer_bytes / (layer_ms * 1e-3) / 1e9, 2),
+        "one_thread": {"tokens_s": round(1e3 / median(one.sum(axis=1).tolist()), 3),
+                       "layer_us": round(median(one.ravel().tolist()) * 1e3, 1),
+                       "sample": f"2 tokens x {len(host_layers)} layers, one OpenMP thread"},
+        **host_cpus(),
     }
+
+
+def cpu_prefill_baseline(shape, host_layer, x, n_calls=24):
+    """glm.c's prefill is one decode call per prompt token (infer.c:2190-2233): the median
+    of n_calls timed single-token layer calls on tokens of the same batch."""
+    import oracle
+
+    if not oracle.available("reference"):
+        return None
+    threads = omp_threads()
+    oracle.layer_timed(shape, host_layer, x[:2], threads)
+    ms = oracle.layer_timed(shape, host_layer, x[:n_calls], threads)
+    med = median(ms.tolist())
+    return {"value": round(1e3 / med, 2), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"median of {n_calls} single-token layer calls (glm.c routes prefill tokens one at a time)",
+            "token_us": round(med * 1e3, 1)}
+
+
+def hip_events_us(gmoe, stream, fn, n):
+    """Average µs per call of fn() over n calls, from HIP events on `stream`."""
+    a, b = gmoe.Event(), gmoe.Event()
+    a.record(stream)
+    for _ in range(n):
+        fn()
+    b.record(stream)
+    return a.elapsed_ms(b) * 1e3 / n
+
+
+def time_prefill(gmoe, np, ctx, shape, layer_ids, T, x, warmup, steps, profile_steps):
+    """One layer over T tokens per launch sequence, rotating over layer_ids (so no layer's
+    touched experts are still cached from the step before). Returns a result dict."""
+    d_in = gmoe.DeviceArray.from_numpy(x)
+    d_out = gmoe.DeviceArray(x.nbytes)
+    stream = gmoe.Stream()
+    it = [0]
+
+    def step():
+        ctx.forward(layer_ids[it[0] % len(layer_ids)], T, d_in.ptr, d_out.ptr, stream=stream.h)
+        it[0] += 1
+
+    for _ in range(warmup):
+        step()
+    stream.sync()
+    t_begin = time.perf_counter()
+    for _ in range(steps):
+        step()
+    stream.sync()
+    layer_us = (time.perf_counter() - t_begin) * 1e6 / steps
+    touched, pairs = [], []
+    for layer in layer_ids:
+        _, st = gmoe.forward_host(ctx, layer, x)
+        counts = np.diff(st["expert_offsets"])
+        touched.append(int(np.sum(counts > 0)) + 1)
+        pairs.append(int(counts.sum()) + T)
+    bytes_per_layer = float(np.mean(touched)) * shape.expert_bytes()
+    macs = float(np.mean(pairs)) * 3 * shape.F * shape.D
+    ctx.profile(True)
+    for _ in range(profile_steps):
+        step()
+    stream.sync()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    kernels = {k: {"launches": n, "avg_us": round(ms * 1e3 / n, 3)} for k, (n, ms) in prof.items()}
+    gemm_us = sum(kernels[k]["avg_us"] for k in ("gate_up", "down") if k in kernels)
+    tflops = 2.0 * macs / (gemm_us * 1e-6) / 1e12 if gemm_us else 0.0
+    gbs = bytes_per_layer / (layer_us * 1e-6) / 1e9
+    return {
+        "tokens_s": round(T / (layer_us * 1e-6), 1),
+        "layer_us": round(layer_us, 2),
+        "touched_experts": round(float(np.mean(touched)), 2),
+        "hbm_gbps_touched_bytes": round(gbs, 1),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "mfma": {"algorithmic_tflops": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                 "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                 "note": "algorithmic 2*MACs of the expert products over the two grouped GEMM kernels' time; the "
+                         "kernels execute 2x those MACs (hi and lo planes) plus tile padding"},
+        "kernels": kernels,
+    }
+
+
+def backend_hook_us(gmoe, np, shape, host_layers, x0, tokens=2):
+    """glm.c's drop-in path: glm_backend_init(BACKEND_HIP) uploads the layers, then
+    glm_backend_try_hip_moe runs each MoE layer on a RunState in host memory (an H2D copy of
+    x, the layer, a synchronisation and the D2H copies of x and the intermediates glm.c
+    keeps in its RunState). Median µs per layer call over `tokens` decode tokens."""
+    import glm_model
+
+    model = glm_model.GlmModel(shape, host_layers)
+    if model.init() != glm_model.BACKEND_HIP:
+        raise SystemExit("glm_backend_init(BACKEND_HIP) did not select the HIP backend")
+    try:
+        model.buf["x"][:] = x0[0]
+        for layer in range(1, len(host_layers) + 1):  # warm-up token
+            if model.try_moe(layer) != 0:
+                raise SystemExit(f"glm_backend_try_hip_moe declined layer {layer}")
+        times = []
+        for _ in range(tokens):
+            for layer in range(1, len(host_layers) + 1):
+                t0 = time.perf_counter()
+                rc = model.try_moe(layer)
+                times.append(time.perf_counter() - t0)
+                if rc != 0:
+                    raise SystemExit(f"glm_backend_try_hip_moe declined layer {layer}")
+    finally:
+        model.free()
+    return {"layer_us": round(median(times) * 1e6, 2), "calls": len(times),
+            "note": "per-layer wall time of glm_backend_try_hip_moe, host RunState in and out (PCIe-inclusive)"}
 
 
 def main():
@@ -91,14 +237,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=N_MOE_LAYERS)
     ap.add_argument("--profile-steps", type=int, default=50)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="only the headline decode stack (no single-layer, prefill or drop-in hook timings)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 5 times (calibrates the PMC byte counters)")
     ap.add_argument("--prefill", type=int, default=0, metavar="T",
                     help="instead of decode, time one MoE layer over T tokens (the grouped expert GEMM path)")
     ap.add_argument("--zipf", action="store_true", help="with --prefill: Zipf(1.2)-skewed router bias")
-    ap.add_argument("--prefill-layers", type=int, default=8, help="with --prefill: seeded layers rotated through")
+    ap.add_argument("--prefill-layers", type=int, default=8, help="seeded layers the prefill timings rotate through")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -121,17 +269,18 @@ def main():
         return
 
     if args.prefill:
-        return prefill(args, gmoe, np)
+        return prefill_only(args, gmoe, np)
 
     shape = gmoe.GLM47_FLASH
     L = args.layers
-    n_dev = gmoe.device_count()
-    if n_dev < 1:
+    if gmoe.device_count() < 1:
         raise SystemExit("no HIP device visible")
+    extras = not args.no_extras
+    max_tokens = 512 if extras else 1
 
     t0 = time.perf_counter()
-    ctx = gmoe.Context(shape, n_layers=L + 1, max_tokens=1, device=0)
-    keep = not args.no_cpu
+    ctx = gmoe.Context(shape, n_layers=L + 1, max_tokens=max_tokens, device=0)
+    keep = not args.no_cpu or extras
     host_layers = []
     for layer in range(1, L + 1):
         hl = gmoe.HostLayer(shape, seed=0, layer=layer)
@@ -162,7 +311,7 @@ def main():
     elapsed = time.perf_counter() - t_begin
     ms_per_step = elapsed * 1e3 / args.steps
     tokens_per_s = args.steps / elapsed
-    per_layer_bytes = ctx.expert_bytes_last()  # T=1: (K valid + shared) experts of the last layer
+    stats = ctx.stats()  # also reports a timed-out launch of the timed steps as an error
     bytes_per_token = 0
     for layer in range(1, L + 1):
         idx, _ = ctx.read_topk(layer, 1)
@@ -195,10 +344,60 @@ def main():
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
                 "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3)}
-    stats = ctx.stats()
+
+    extra = {}
+    if extras:
+        # config 1: one MoE layer per launch, rotating over the resident layers so that no
+        # layer's experts are still cached from the launch before
+        it = [0]
+
+        def one_layer():
+            lay = 1 + it[0] % L
+            ctx.forward_layers(lay, 1, 1, d_in.ptr, d_out.ptr, stream=stream.h)
+            it[0] += 1
+
+        for _ in range(L):
+            one_layer()
+        stream.sync()
+        us = hip_events_us(gmoe, stream, one_layer, 4 * L)
+        lb = (shape.K + 1) * shape.expert_bytes()
+        extra["single_layer"] = {
+            "workload": "one GLM-4.7-Flash MoE layer per launch, T=1, rotating over the 46 resident layers",
+            "layer_us": round(us, 3), "expert_bytes": lb, "hbm_gbps": round(lb / (us * 1e-6) / 1e9, 1),
+            "hbm_frac": round(lb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "launches": 4 * L}
+        log(f"single layer: {us:.2f} us")
+        # configs 3 and 4: prefill batches on the grouped expert GEMMs
+        NL = min(args.prefill_layers, L)
+        x512 = gmoe.activations(0, 1, 512, shape.D)
+        extra["prefill_t512"] = time_prefill(gmoe, np, ctx, shape, list(range(1, NL + 1)), 512, x512,
+                                             max(2, args.warmup), max(10, args.steps), 10)
+        extra["prefill_t512"]["workload"] = f"one GLM-4.7-Flash MoE layer, T=512, N(0, 0.01) bias, {NL} layers rotated"
+        log(f"prefill T=512: {extra['prefill_t512']['layer_us']} us/layer")
+        zctx = gmoe.Context(shape, n_layers=NL + 1, max_tokens=128, device=0)
+        zipf_l1 = None
+        for layer in range(1, NL + 1):
+            hl = gmoe.HostLayer(shape, seed=0, layer=layer, bias_mode=gmoe.SYNTH_BIAS_ZIPF)
+            zctx.upload(layer, hl)
+            if layer == 1:
+                zipf_l1 = hl
+        x128 = gmoe.activations(0, 1, 128, shape.D)
+        extra["prefill_t128_zipf"] = time_prefill(gmoe, np, zctx, shape, list(range(1, NL + 1)), 128, x128,
+                                                  max(2, args.warmup), max(10, args.steps), 10)
+        extra["prefill_t128_zipf"]["workload"] = f"one GLM-4.7-Flash MoE layer, T=128, Zipf(1.2) bias, {NL} layers rotated"
+        zstats = zctx.stats()
+        zctx.close()
+        log(f"prefill T=128 Zipf: {extra['prefill_t128_zipf']['layer_us']} us/layer")
+        if not args.no_cpu:
+            extra["prefill_t512"]["cpu_baseline"] = cpu_prefill_baseline(shape, host_layers[0], x512)
+            extra["prefill_t128_zipf"]["cpu_baseline"] = cpu_prefill_baseline(shape, zipf_l1, x128)
+        extra["prefill_t128_zipf"]["routing_stats"] = zstats
+        del zipf_l1
+        # the glm.c drop-in hook on host memory (uploads its own copy of the layers)
+        extra["backend_hook"] = backend_hook_us(gmoe, np, shape, host_layers, x0)
+        log(f"backend hook: {extra['backend_hook']['layer_us']} us/layer")
 
     cpu = None
-    if keep:
+    if not args.no_cpu:
         log(f"timing the CPU reference path for ~{args.cpu_seconds:.0f}s")
         cpu = cpu_baseline(shape, host_layers, x0, args.cpu_seconds)
 
@@ -226,94 +425,40 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "routing_stats": stats,
-        "expert_bytes_last_layer": per_layer_bytes,
+        **extra,
     }
     print(json.dumps(out), flush=True)
     ctx.close()
 
 
-MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
-
-
-def prefill(args, gmoe, np):
-    """One MoE layer over T tokens (T=512 with N(0, 0.01) router bias, or T=128 with the
-    Zipf(1.2) bias): router, dispatch, grouped
-    gate/up and down GEMMs, combine. Steps rotate over --prefill-layers seeded layers so
-    that no layer's 650 MB of touched experts is still cached from the step before."""
+def prefill_only(args, gmoe, np):
+    """--prefill T: one MoE layer over T tokens (T=512 with N(0, 0.01) router bias, or
+    T=128 with the Zipf(1.2) bias), the workload of the prefill profiles."""
     shape = gmoe.GLM47_FLASH
     T, NL = args.prefill, args.prefill_layers
     bias = gmoe.SYNTH_BIAS_ZIPF if args.zipf else gmoe.SYNTH_BIAS_NORMAL
     t0 = time.perf_counter()
     ctx = gmoe.Context(shape, n_layers=NL + 1, max_tokens=T, device=0)
-    host_layers = []
+    first = None
     for layer in range(1, NL + 1):
         hl = gmoe.HostLayer(shape, seed=0, layer=layer, bias_mode=bias)
         ctx.upload(layer, hl)
-        host_layers.append(hl if layer == 1 else None)
+        if layer == 1:
+            first = hl
     log(f"generated and uploaded {NL} layers in {time.perf_counter() - t0:.1f}s")
     x0 = gmoe.activations(0, 1, T, shape.D)
-    d_in = gmoe.DeviceArray.from_numpy(x0)
-    d_out = gmoe.DeviceArray(x0.nbytes)
-    stream = gmoe.Stream()
-    it = [0]
-
-    def step():
-        ctx.forward(1 + it[0] % NL, T, d_in.ptr, d_out.ptr, stream=stream.h)
-        it[0] += 1
-
-    for _ in range(args.warmup):
-        step()
-    stream.sync()
-    t_begin = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    stream.sync()
-    elapsed = time.perf_counter() - t_begin
-    layer_us = elapsed * 1e6 / args.steps
-    # touched experts and routed pairs of every layer (lists are exact, so this is what was read)
-    touched, pairs = [], []
-    for layer in range(1, NL + 1):
-        _, st = gmoe.forward_host(ctx, layer, x0)
-        counts = np.diff(st["expert_offsets"])
-        touched.append(int(np.sum(counts > 0)) + 1)
-        pairs.append(int(counts.sum()) + T)
-    bytes_per_layer = float(np.mean(touched)) * shape.expert_bytes()
-    macs = float(np.mean(pairs)) * 3 * shape.F * shape.D
-    ctx.profile(True)
-    for _ in range(args.profile_steps):
-        step()
-    stream.sync()
-    prof = ctx.profile_read()
-    ctx.profile(False)
-    kernels = {k: {"launches": n, "avg_us": round(ms * 1e3 / n, 3)} for k, (n, ms) in prof.items()}
-    # per layer: one gate/up and one down launch
-    gemm_us = sum(kernels[k]["avg_us"] for k in ("gate_up", "down") if k in kernels)
-    tflops = 2.0 * macs / (gemm_us * 1e-6) / 1e12 if gemm_us else 0.0
-    gbs = bytes_per_layer / (layer_us * 1e-6) / 1e9
-
-    cpu = None
-    if not args.no_cpu:
-        import oracle
-        kind = "reference" if oracle.available("reference") else "port"
-        orc = oracle.Oracle(kind)
-        n = min(T, 32)
-        orc.layer(shape, host_layers[0], x0[:2])
-        t_c = time.perf_counter()
-        orc.layer(shape, host_layers[0], x0[:n])
-        dt = time.perf_counter() - t_c
-        cpu = {"value": round(n / dt, 2), "unit": "tokens/s", "cores": omp_threads(), "kind": kind,
-               "sample": f"{n} of the {T} tokens through layer 1 (glm.c routes prefill tokens one at a time, "
-                         f"infer.c:2190-2233), wall clock",
-               "layer_us_for_T": round(dt / n * T * 1e6, 1)}
+    res = time_prefill(gmoe, np, ctx, shape, list(range(1, NL + 1)), T, x0, args.warmup, args.steps,
+                       args.profile_steps)
+    cpu = None if args.no_cpu else cpu_prefill_baseline(shape, first, x0)
     name = f"T={T}" + (" Zipf(1.2) routing" if args.zipf else "")
     out = {
         "metric": f"MoE-layer prefill tokens/s ({name}, GLM-4.7-Flash shape, Q8_0, grouped expert GEMM)",
-        "value": round(T / (layer_us * 1e-6), 1),
+        "value": res["tokens_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(layer_us * 1e-3, 4),
+        "ms_per_step": round(res["layer_us"] * 1e-3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -321,14 +466,7 @@ def prefill(args, gmoe, np):
         "data": "synthetic (seeded random-init Q8_0 weights, N(0,1) input)",
         "config": {"workload": f"one GLM-4.7-Flash MoE layer, prefill {name}", "tokens": T, "layers_rotated": NL,
                    "dim": shape.D, "moe_ffn_dim": shape.F, "experts": shape.E, "top_k": shape.K, "shared_experts": 1},
-        "layer_us": round(layer_us, 2),
-        "touched_experts": round(float(np.mean(touched)), 2),
-        "hbm_gbps_touched_bytes": round(gbs, 1),
-        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "mfma": {"algorithmic_tflops": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                 "note": "algorithmic 2*MACs of the expert products over the two grouped GEMM kernels' time; the "
-                         "kernels execute 2x those MACs (hi and lo planes) plus tile padding"},
-        "kernels": kernels,
+        **{k: v for k, v in res.items() if k != "tokens_s"},
         "cpu_baseline": cpu,
         "routing_stats": ctx.stats(),
     }

@@ -113,6 +113,9 @@ struct gmoe_ctx {
     StackWs sk_o{};
     unsigned *sk_ctr = nullptr;  // [GM_STACK_COUNTERS]
     int *sk_error = nullptr;
+    int *sk_error_host = nullptr;      // pinned host word a failing launch sets (hipHostMalloc)
+    int *sk_error_host_dev = nullptr;  // its device address
+    unsigned sk_spin_limit = SK_SPIN_LIMIT;
     StackLayer *sk_layers = nullptr;  // [L], device
     unsigned long long *sk_trace = nullptr;  // per-item timestamps when tracing
     size_t sk_trace_items = 0;
@@ -125,6 +128,7 @@ struct gmoe_ctx {
     long long tokens_routed = 0;
     long long scale_inexact = 0;
     int last_layer = -1, last_T = 0, last_flags = 0, last_dispatched = 0, stack_launched = 0;
+    int stack_last = 0;  // the most recent forward was a persistent launch
 };
 
 extern "C" const char *gmoe_last_error(void) { return g_err; }
@@ -168,6 +172,7 @@ static void free_ctx(gmoe_ctx *c) {
                     c->sk_layers, c->sk_trace, c->xspl, c->hspl, c->xexp, c->hexp, c->pair_row, c->n_tiles,
                     c->hbuf, c->ybuf, c->tiles, c->rt_t, c->rt_sp, c->rt_sa};
     for (void *b : bufs) dev_free(b);
+    if (c->sk_error_host) (void)hipHostFree(c->sk_error_host);
     delete c;
 }
 
@@ -295,10 +300,22 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     rc |= dev_alloc(&c->sk_ctr, GM_STACK_COUNTERS);
     rc |= dev_alloc(&c->sk_error, 1);
     rc |= dev_alloc(&c->sk_layers, (size_t)c->L);
+    if (rc == GMOE_OK) {
+        if (hipHostMalloc((void **)&c->sk_error_host, sizeof(int), hipHostMallocDefault) != hipSuccess ||
+            hipHostGetDevicePointer((void **)&c->sk_error_host_dev, c->sk_error_host, 0) != hipSuccess) {
+            set_err("gmoe_create: pinned host memory for the launch status failed");
+            rc = GMOE_ERR_NOMEM;
+        } else {
+            *(volatile int *)c->sk_error_host = 0;
+        }
+    }
     if (rc != GMOE_OK) {
         free_ctx(c);
         return GMOE_ERR_NOMEM;
     }
+    // Diagnostic: a lower poll limit for the persistent kernel's waits (tests force a
+    // timed-out launch with it; every wait still ends, the kernel exits normally).
+    if (const char *sl = getenv("GMOE_SPIN_LIMIT")) c->sk_spin_limit = (unsigned)strtoul(sl, nullptr, 10);
     // Counters start at zero; each kernel's last block puts its counter back to zero.
     hipError_t e0 = hipMemset(c->tok_counter, 0, T * sizeof(unsigned));
     hipError_t e1 = hipMemset(c->panel_counter, 0, T * (D / 16) * sizeof(unsigned));
@@ -569,6 +586,8 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.ctr = c->sk_ctr;
     a.stats = c->stats_dev;
     a.error = c->sk_error;
+    a.error_host = c->sk_error_host_dev;
+    a.spin_limit = c->sk_spin_limit;
     a.trace = nullptr;
     {
         // One routed block per routed item when the grid allows, the rest of the non-router
@@ -613,17 +632,33 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     c->last_dispatched = 0;
     c->tokens_routed += n;
     c->stack_launched = 1;
+    c->stack_last = 1;
     return GMOE_OK;
 }
 
-// 0, or GMOE_ERR_HIP if a persistent-kernel dependency wait timed out (synchronises).
+static const char k_timeout_msg[] =
+    "persistent decode kernel: a dependency wait timed out (grid not co-resident?); its outputs are invalid";
+
+// Without synchronising: GMOE_ERR_HIP if a persistent launch that has already ended gave up
+// on a wait since the last report (the failing block sets the pinned host word). The
+// report clears the word, so the next launch starts clean.
+static int take_launch_error(gmoe_ctx *c) {
+    volatile int *w = c->sk_error_host;
+    if (!c->stack_launched || !w || *w == 0) return GMOE_OK;
+    *w = 0;
+    set_err("%s", k_timeout_msg);
+    return GMOE_ERR_HIP;
+}
+
+// 0, or GMOE_ERR_HIP if the most recent persistent launch timed out (synchronises).
 static int check_stack_error(gmoe_ctx *c) {
     if (!c->stack_launched) return GMOE_OK;
     int err = 0;
     HIP_OK(hipDeviceSynchronize());
-    HIP_OK(hipMemcpy(&err, c->sk_error, sizeof(int), hipMemcpyDeviceToHost));
-    if (err) {
-        set_err("persistent decode kernel: a dependency wait timed out (grid not co-resident?)");
+    if (c->stack_last) HIP_OK(hipMemcpy(&err, c->sk_error, sizeof(int), hipMemcpyDeviceToHost));
+    const int host_rc = take_launch_error(c);
+    if (err || host_rc) {
+        set_err("%s", k_timeout_msg);
         return GMOE_ERR_HIP;
     }
     return GMOE_OK;
@@ -644,6 +679,7 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
         return GMOE_ERR_INVALID;
     }
     HIP_OK(hipSetDevice(c->device));
+    if (int erc = take_launch_error(c)) return erc;
     hipStream_t st = (hipStream_t)stream;
     LayerDev &L = c->layers[layer];
     if (T == 1 && c->stack_ok) return launch_stack(c, layer, 1, x_in, x_out, flags, st);
@@ -796,6 +832,7 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     c->last_layer = layer;
     c->last_T = T;
     c->last_flags = fl;
+    c->stack_last = 0;
     L.last_T = T;
     c->tokens_routed += T;
     return GMOE_OK;
@@ -819,6 +856,7 @@ extern "C" int gmoe_forward_layers(gmoe_ctx *c, int first, int n, int T, const f
     }
     if (T == 1 && c->stack_ok) {
         HIP_OK(hipSetDevice(c->device));
+        if (int erc = take_launch_error(c)) return erc;
         return launch_stack(c, first, n, x_in, x_out, flags, (hipStream_t)stream);
     }
     for (int i = 0; i < n; i++) {
@@ -851,6 +889,8 @@ extern "C" int gmoe_forward_host(gmoe_ctx *c, int layer, int T, const float *x_i
     HIP_OK(hipMemcpy(c->x_host_io, x_in, bytes, hipMemcpyHostToDevice));
     int rc = gmoe_forward(c, layer, T, c->x_host_io, c->x_host_io, flags, nullptr);
     if (rc) return rc;
+    // a timed-out launch leaves x_out untouched, so a caller may rerun the layer from it
+    if ((rc = check_stack_error(c))) return rc;
     HIP_OK(hipMemcpy(x_out, c->x_host_io, bytes, hipMemcpyDeviceToHost));
     if (state) return gmoe_read_layer_state(c, state, nullptr);
     return GMOE_OK;
@@ -917,9 +957,27 @@ extern "C" int gmoe_get_stats(gmoe_ctx *c, gmoe_stats *o) {
     HIP_OK(hipMemcpy(s, c->stats_dev, sizeof(s), hipMemcpyDeviceToHost));
     o->tokens_routed = c->tokens_routed;
     o->routing_exact_path = (int64_t)s[GM_STAT_ROUTE_EXACT];
-    o->routing_unresolved = (int64_t)s[GM_STAT_UNRESOLVED];
     o->norm_exact_path = (int64_t)s[GM_STAT_NORM_EXACT];
     o->scale_inexact = c->scale_inexact;
+    return GMOE_OK;
+}
+
+__global__ void k_expf_eval(uint32_t first, int64_t count, int which, float *out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const float x = __uint_as_float(first + (uint32_t)i);
+    out[i] = which == 0 ? expf_libm(x) : expf(x);
+}
+
+extern "C" int gmoe_expf_eval(uint32_t first_bits, int64_t count, int which, float *out, void *stream) {
+    if (!out || count < 0 || count > ((int64_t)1 << 32) || (which != 0 && which != 1)) {
+        set_err("gmoe_expf_eval: bad arguments");
+        return GMOE_ERR_INVALID;
+    }
+    if (count == 0) return GMOE_OK;
+    const int64_t blocks = (count + 255) / 256;
+    hipLaunchKernelGGL(k_expf_eval, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, first_bits, count, which, out);
+    HIP_OK(hipGetLastError());
     return GMOE_OK;
 }
 

@@ -11,14 +11,15 @@
 //    [S-B, S+B] into an interval that must contain the CPU's selection score
 //    p + bias (allowing for expf, the add and the divide in fp32), and accepts the
 //    top-k only when the intervals order the chosen experts strictly.
-// When the proof fails the block replays every expert's fp32 chain exactly and runs
-// glm.c's insertion top-k on it; only a tie within the last bits of libm's expf could
-// then still differ, and that case is counted in stats[GM_STAT_UNRESOLVED].
+// When the proof fails the block replays every expert's fp32 chain exactly, with libm's
+// own expf results (expf_exact.h), and runs glm.c's insertion top-k on it: the same
+// scores bit for bit, so the same experts in the same order, ties to the lower index.
 #pragma once
 
 #include "common.h"
+#include "expf_exact.h"
 
-enum { GM_STAT_NORM_EXACT = 0, GM_STAT_ROUTE_EXACT = 1, GM_STAT_UNRESOLVED = 2, GM_STAT_COUNT = 4 };
+enum { GM_STAT_NORM_EXACT = 0, GM_STAT_ROUTE_EXACT = 1, GM_STAT_COUNT = 4 };
 
 struct RouterArgs {
     const float *x;            // [T][D]
@@ -190,8 +191,7 @@ __device__ __attribute__((always_inline)) static void certified_select(int E, in
 // glm.c's router replayed exactly in fp32 (infer.c:916-938, 1104-1145) by one block of
 // 256 threads, for the xn in shared memory: every probability into p and selection
 // score into sel (shared, [E]), the top-k into idx and its normalised weights into wk
-// (shared, [K]). prod is 32 KB of shared scratch (16-byte aligned). Counts the replay in stats, and a
-// top-k whose order hinges on expf's last bits as unresolved.
+// (shared, [K]). prod is 32 KB of shared scratch (16-byte aligned). Counts the replay in stats.
 __device__ __attribute__((always_inline)) static void exact_router(int D, int E, int K, int tid, const float *gate_inp, const float *bias_p,
                                     const float *xn, float (*prod)[64], float *p, float *sel, int *idx, float *wk_out,
                                     unsigned long long *stats) {
@@ -255,7 +255,7 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
             __syncthreads();                                    // and wave 0 is done with this one
         }
         if (tid < ne) {
-            const float pr = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-chain)));
+            const float pr = sigmoid_libm(chain);  // infer.c:1105, libm's expf bits
             p[eb + tid] = pr;
             sel[eb + tid] = __fadd_rn(pr, bias[eb + tid]);
         }
@@ -276,7 +276,6 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
             pv[c] = valid ? p[e] : 0.0f;
         }
         float total = 0.0f;
-        bool unresolved = false;
         for (int k = 0; k < K; k++) {
             float bm = key[0];
 #pragma unroll
@@ -305,13 +304,6 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
 #pragma unroll
                 for (int c = 0; c < RT_SEL_C; c++)
                     if (lane == ls && c == cs) key[c] = -INFINITY;
-                // libm's expf may differ from the GPU's by an ulp: flag orders decided that
-                // closely (any expert not yet chosen within a few ulps of this one)
-                const float tol = 4.0f * fmaxf(fabsf(gm), 1e-30f) * 0x1p-23f + 4.0f * 0x1p-24f;
-                bool close = false;
-#pragma unroll
-                for (int c = 0; c < RT_SEL_C; c++) close |= key[c] > -INFINITY && fabsf(key[c] - gm) <= tol;
-                unresolved |= __ballot(close) != 0;
             }
             if (lane == 0) {
                 idx[k] = ek;
@@ -320,7 +312,6 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
         }
         if (lane == 0) {
             atomicAdd(&stats[GM_STAT_ROUTE_EXACT], 1ull);
-            if (unresolved) atomicAdd(&stats[GM_STAT_UNRESOLVED], 1ull);
             if (total > 0.0f) {
                 // normalisation of infer.c:1136-1145
                 const float denom = total < 6.103515625e-5f ? 6.103515625e-5f : total;

@@ -39,7 +39,7 @@
 #include "router.h"
 
 #define SK_BLOCK 256
-#define SK_SPIN_LIMIT (1u << 22)               // polls before a wait is declared dead (~seconds)
+#define SK_SPIN_LIMIT (1u << 22)               // default polls before a wait is declared dead (~seconds)
 #define SK_TRACE_STAMPS 16
 #define SK_NR_MAX 64                           // router blocks
 #define SK_RX_MAX (GM_MAX_E / SK_NR_MAX)       // experts per router block
@@ -124,7 +124,9 @@ struct StackArgs {
     int hist_stride;
     unsigned *ctr;             // counters, zero at launch
     unsigned long long *stats;
-    int *error;                // nonzero: a wait timed out
+    int *error;                // nonzero: a wait timed out (device word, cleared by k_stack_reset)
+    int *error_host;           // host-visible copy, set by a failing block and left for the host to clear
+    unsigned spin_limit;       // polls before a wait gives up (SK_SPIN_LIMIT unless the host lowers it)
     unsigned long long *trace; // optional: SK_TRACE_STAMPS timestamps per item (see k_moe_stack)
     int n_router;              // router blocks: a power of two, <= min(E, 64)
     int shared_blocks;         // blocks in the shared-expert role
@@ -205,6 +207,7 @@ struct SkShared {
     int ok, sel_ok;
     unsigned zero;  // 0 for the kernel's life (an always-zero operand of gu_products)
     int xe_local;   // exponent of a routed block's own digits of xn (sk_local_digits)
+    unsigned spin_limit;
     int idx[GM_MAX_K];
     float wk[GM_MAX_K], ws[GM_MAX_K];
     long trace_item;
@@ -255,11 +258,11 @@ __device__ static inline void arrive(unsigned *c, unsigned target, unsigned *fla
 
 // Bounded spin of one thread until *c >= target; false if it timed out or another block
 // already failed.
-__device__ static inline bool spin_ge(const unsigned *c, unsigned target, int *error) {
+__device__ static inline bool spin_ge(const unsigned *c, unsigned target, int *error, unsigned limit) {
     unsigned spins = 0;
     while (ld_u(c) < target) {
         if (__hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
-        if (++spins > SK_SPIN_LIMIT) {
+        if (++spins > limit) {
             __hip_atomic_store(error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return false;
         }
@@ -272,7 +275,7 @@ __device__ static inline bool spin_ge(const unsigned *c, unsigned target, int *e
 // out or another block already failed (the caller then returns from the kernel).
 __device__ static inline bool wait_ge(const unsigned *c, unsigned target, int *error, SkShared &sh) {
     if (threadIdx.x == 0) {
-        sh.ok = spin_ge(c, target, error);
+        sh.ok = spin_ge(c, target, error, sh.spin_limit);
         if (sh.trace) trace_put(sh.trace, SK_TRACE_STAMPS * sh.trace_item + 1);
     }
     __syncthreads();
@@ -354,7 +357,7 @@ __device__ __attribute__((always_inline)) static bool sk_stage_select(const Stac
                 }
             }
             if (__ballot(miss) == 0) break;
-            if (__hip_atomic_load(a.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > SK_SPIN_LIMIT) {
+            if (__hip_atomic_load(a.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > a.spin_limit) {
                 if (tid == 0) __hip_atomic_store(a.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 alive = false;
                 break;
@@ -671,7 +674,7 @@ __device__ static inline bool sk_read_topk(const StackArgs &a, int li, SkShared 
             unsigned spins = 0;
             unsigned long long v;
             while ((v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0ull) {
-                if (__hip_atomic_load(a.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > SK_SPIN_LIMIT) {
+                if (__hip_atomic_load(a.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > a.spin_limit) {
                     __hip_atomic_store(a.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     ok = false;
                     break;
@@ -1103,14 +1106,7 @@ __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, 
 // the routing, run the routed experts' items and then the combine chunks. Trace items of
 // one layer are numbered: n_router router items, D/16 combine chunks, F/16 shared items,
 // K*F/16 routed items (a routed block's top-k is stamped on its first expert item).
-__global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
-    __shared__ SkShared sh;
-    if (threadIdx.x == 0) {
-        sh.trace = a.trace;
-        sh.ok = 1;
-        sh.zero = 0u;
-    }
-    __syncthreads();
+__device__ __attribute__((always_inline)) static bool sk_run(const StackArgs &a, SkShared &sh) {
     const int K = a.K, NS = K + 1;
     const int NPF = a.F >> 4, NCH = a.D / SK_CROWS;  // combine chunks
     const int NR = a.n_router, NSB = a.shared_blocks, G = (int)gridDim.x, NWB = G - NR - NSB;
@@ -1129,7 +1125,7 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
     do {                                                                                      \
         sh.trace_item = base + (idx);                                                         \
         if (a.trace && threadIdx.x == 0) trace_put(a.trace, SK_TRACE_STAMPS * sh.trace_item);   \
-        if (!(call)) return;                                                                  \
+        if (!(call)) return false;                                                            \
         if (a.trace && threadIdx.x == 0) trace_put(a.trace, SK_TRACE_STAMPS * sh.trace_item + 2); \
         __syncthreads();                                                                      \
     } while (0)
@@ -1146,14 +1142,14 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
                 SK_ITEM(NR + NCH + j, sk_expert_item<false>(a, L, li, K, j, a.E, sh));
             }
             sh.trace_item = base + NR + NCH + sb;
-            if (!wait_ge(&a.ctr[SKF(li, SKF_X)], 1u, a.error, sh)) return;
+            if (!wait_ge(&a.ctr[SKF(li, SKF_X)], 1u, a.error, sh)) return false;
         } else {
             const int wb = b < P ? b - NR : b - NR - NSB;
             if (wb < K * NPF && routed_on) {
                 sh.trace_item = base + NR + NCH + NPF + wb;  // stamps 1, 8 and 3 of its first item
-                if (a.D == GM_MAX_COLS && !sk_local_digits(a, L, li, sh)) return;
-                if (!sk_stage_select(a, li, false, sh)) return;
-                if (!sh.sel_ok && !sk_read_topk(a, li, sh)) return;
+                if (a.D == GM_MAX_COLS && !sk_local_digits(a, L, li, sh)) return false;
+                if (!sk_stage_select(a, li, false, sh)) return false;
+                if (!sh.sel_ok && !sk_read_topk(a, li, sh)) return false;
             }
             for (int i = wb; i < K * NPF; i += NWB) {
                 const int slot = i / NPF;
@@ -1162,10 +1158,26 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
             // combine chunks, by the blocks that hold this layer's routing
             const int ncb = NWB < K * NPF ? NWB : K * NPF;
             if (wb < ncb && wb < NCH) {
-                if (routed_on && !sh.sel_ok && !sk_read_weights(a, li, sh)) return;
+                if (routed_on && !sh.sel_ok && !sk_read_weights(a, li, sh)) return false;
                 for (int c = wb; c < NCH; c += ncb) SK_ITEM(NR + c, sk_combine(a, li, c, routed_on, sh));
             }
         }
 #undef SK_ITEM
     }
+    return true;
+}
+
+__global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_stack(StackArgs a) {
+    __shared__ SkShared sh;
+    if (threadIdx.x == 0) {
+        sh.trace = a.trace;
+        sh.ok = 1;
+        sh.zero = 0u;
+        sh.spin_limit = a.spin_limit;
+    }
+    __syncthreads();
+    // a block whose wait gave up leaves the launch's failure where the host reads it
+    // without synchronising (the next forward call reports it)
+    if (!sk_run(a, sh) && threadIdx.x == 0)
+        __hip_atomic_store(a.error_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }

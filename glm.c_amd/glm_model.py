@@ -1,0 +1,138 @@
+"""ctypes mirror of include/glm_model.h (glm.c's model.h:7-164) and a driver for the
+--backend hip drop-in (include/glm_backend.h, libglm_hip.so).
+
+GlmModel builds the Runtime / RunState pair that glm.c hands its backend: a
+checkpoint view whose MoE layers point at HostLayer arrays (LayerMoeShared and
+LayerMoeRouted per layer, model.h:65-84, indexed 1..n_layers-1 as infer.c:668,717
+fill them) and the decode-time RunState buffers the MoE layer reads and writes
+(model.h:132-159). It is plumbing for tests and the benchmark: every computation
+goes through libglm_hip.so's C entry points.
+"""
+import ctypes as C
+
+import numpy as np
+
+import gmoe
+
+BACKEND_CPU, BACKEND_METAL, BACKEND_HIP = 0, 1, 2
+
+_i32, _u32, _u64, _P = C.c_int32, C.c_uint32, C.c_uint64, C.c_void_p
+
+
+class RuntimeConfig(C.Structure):
+    _fields_ = [("magic", _u32), ("version", _u32), ("dim", _i32), ("hidden_dim", _i32), ("n_layers", _i32),
+                ("n_heads", _i32), ("n_kv_heads", _i32), ("vocab_size", _i32), ("seq_len", _i32), ("rope_dim", _i32),
+                ("q_lora_rank", _i32), ("kv_lora_rank", _i32), ("kv_mqa_width", _i32), ("n_routed_experts", _i32),
+                ("n_experts_used", _i32), ("n_shared_experts", _i32), ("bos_id", _i32), ("eos_id", _i32),
+                ("group_size", _u64), ("off_norm", _u64), ("off_tok_q", _u64), ("off_tok_s", _u64),
+                ("off_out_q", _u64), ("off_out_s", _u64), ("total_bytes", _u64), ("off_l0_ffn_norm", _u64),
+                ("off_l0_ffn_gate_q", _u64), ("off_l0_ffn_gate_s", _u64), ("off_l0_ffn_up_q", _u64),
+                ("off_l0_ffn_up_s", _u64), ("off_l0_ffn_down_q", _u64), ("off_l0_ffn_down_s", _u64),
+                ("l0_qk_nope_dim", _i32), ("l0_head_k_dim", _i32), ("l0_v_head_dim", _i32), ("l0_flags", _i32),
+                ("moe_ffn_dim", _i32)]
+
+
+class LayerAttnWeights(C.Structure):
+    _fields_ = [(n, _P) for n in ("attn_norm", "q_a_norm", "kv_a_norm", "q_a_q", "q_a_s", "q_b_q", "q_b_s", "kv_a_q",
+                                  "kv_a_s", "k_b_q", "k_b_s", "v_b_q", "v_b_s", "attn_out_q", "attn_out_s")]
+
+
+SHARED_FIELDS = ("ffn_norm", "gate_inp", "exp_probs_b", "gate_sh_q", "gate_sh_s", "up_sh_q", "up_sh_s", "down_sh_q",
+                 "down_sh_s")
+ROUTED_FIELDS = ("gate_q", "gate_s", "up_q", "up_s", "down_q", "down_s")
+
+
+class LayerMoeShared(C.Structure):
+    _fields_ = [(n, _P) for n in SHARED_FIELDS]
+
+
+class LayerMoeRouted(C.Structure):
+    _fields_ = [(n, _P) for n in ROUTED_FIELDS]
+
+
+class Runtime(C.Structure):
+    _fields_ = ([("cfg", RuntimeConfig), ("data", _P), ("file_size", C.c_size_t)]
+                + [(n, _P) for n in ("output_norm", "tok_q", "tok_s", "out_q", "out_s")]
+                + [("has_l0_ffn", C.c_int)]
+                + [(n, _P) for n in ("l0_ffn_norm", "l0_ffn_gate_q", "l0_ffn_gate_s", "l0_ffn_up_q", "l0_ffn_up_s",
+                                     "l0_ffn_down_q", "l0_ffn_down_s")]
+                + [("has_l0_attn", C.c_int)]
+                + [(n, _P) for n in ("l0_attn_norm", "l0_q_a_norm", "l0_kv_a_norm", "l0_q_a_q", "l0_q_a_s", "l0_q_b_q",
+                                     "l0_q_b_s", "l0_kv_a_q", "l0_kv_a_s", "l0_k_b_q", "l0_k_b_s", "l0_v_b_q",
+                                     "l0_v_b_s", "l0_attn_out_q", "l0_attn_out_s")]
+                + [("has_all_attn", C.c_int), ("attn_layers", C.POINTER(LayerAttnWeights)),
+                   ("has_moe_shared", C.c_int), ("moe_layers", C.POINTER(LayerMoeShared)),
+                   ("has_moe_routed", C.c_int), ("moe_routed_layers", C.POINTER(LayerMoeRouted))])
+
+
+class RunState(C.Structure):
+    _fields_ = ([(n, _P) for n in ("x", "xn", "xb", "ff_gate", "ff_up", "logits")]
+                + [("cache_cap", C.c_int), ("n_attn_layers", C.c_int)]
+                + [(n, _P) for n in ("k_cache_comp", "k_cache_pe", "q_a", "q_full", "kv_a", "q_nope", "q_pe", "q_abs",
+                                     "att_scores", "att_ctx", "att_concat", "moe_gate", "moe_up", "moe_router",
+                                     "moe_out_acc", "moe_topk_idx", "moe_topk_w")])
+
+
+STRUCTS = {"RuntimeConfig": RuntimeConfig, "LayerAttnWeights": LayerAttnWeights, "LayerMoeShared": LayerMoeShared,
+           "LayerMoeRouted": LayerMoeRouted, "Runtime": Runtime, "RunState": RunState}
+
+
+def backend_lib():
+    lib = gmoe.host_lib()
+    if not getattr(lib, "_backend_typed", False):
+        RP, SP = C.POINTER(Runtime), C.POINTER(RunState)
+        lib.glm_backend_init.argtypes = [C.c_int, RP, SP]
+        lib.glm_backend_init.restype = C.c_int
+        lib.glm_backend_free.argtypes = [C.c_int]
+        lib.glm_backend_free.restype = None
+        lib.glm_backend_try_hip_moe.argtypes = [RP, SP, C.c_int, C.c_int]
+        lib.glm_backend_try_hip_moe.restype = C.c_int
+        lib._backend_typed = True
+    return lib
+
+
+class GlmModel:
+    """A glm.c Runtime whose MoE layers 1..len(layers) are the given HostLayers (layer 0
+    has no MoE block, as in GLM-4.7-Flash), and a RunState sized for one decode token."""
+
+    def __init__(self, shape, layers):
+        self.shape = shape
+        self.layers = list(layers)  # keep the arrays alive
+        n_layers = len(self.layers) + 1
+        cfg = RuntimeConfig()
+        cfg.dim, cfg.n_layers, cfg.moe_ffn_dim = shape.D, n_layers, shape.F
+        cfg.n_routed_experts, cfg.n_experts_used, cfg.n_shared_experts = shape.E, shape.K, 1
+        cfg.group_size = shape.gs
+        self.shared = (LayerMoeShared * n_layers)()
+        self.routed = (LayerMoeRouted * n_layers)()
+        for l, hl in enumerate(self.layers, start=1):
+            for n in SHARED_FIELDS:
+                setattr(self.shared[l], n, gmoe.ptr(getattr(hl, n)))
+            for n in ROUTED_FIELDS:
+                setattr(self.routed[l], n, gmoe.ptr(getattr(hl, n)))
+        rt = Runtime()
+        rt.cfg = cfg
+        rt.has_moe_shared = 1
+        rt.moe_layers = C.cast(self.shared, C.POINTER(LayerMoeShared))
+        rt.has_moe_routed = 1
+        rt.moe_routed_layers = C.cast(self.routed, C.POINTER(LayerMoeRouted))
+        self.rt = rt
+        D, E, K = shape.D, shape.E, shape.K
+        self.buf = {"x": np.zeros(D, np.float32), "xn": np.zeros(D, np.float32), "xb": np.zeros(D, np.float32),
+                    "moe_router": np.zeros(E, np.float32), "moe_out_acc": np.zeros(D, np.float32),
+                    "moe_topk_idx": np.zeros(K, np.int32), "moe_topk_w": np.zeros(K, np.float32)}
+        st = RunState()
+        for n, a in self.buf.items():
+            setattr(st, n, gmoe.ptr(a))
+        self.st = st
+
+    def init(self, backend=BACKEND_HIP):
+        """glm_backend_init (backend.h:7): uploads every MoE layer; exits the process on failure."""
+        return backend_lib().glm_backend_init(backend, C.byref(self.rt), C.byref(self.st))
+
+    def try_moe(self, layer, debug=0):
+        """glm_backend_try_hip_moe: 0 if the GPU ran the layer on the RunState, else -1."""
+        return backend_lib().glm_backend_try_hip_moe(C.byref(self.rt), C.byref(self.st), layer, debug)
+
+    def free(self, backend=BACKEND_HIP):
+        backend_lib().glm_backend_free(backend)

@@ -62,8 +62,8 @@ class GmoeKernelTimes(C.Structure):
 
 
 class GmoeStats(C.Structure):
-    _fields_ = [("tokens_routed", C.c_int64), ("routing_exact_path", C.c_int64), ("routing_unresolved", C.c_int64),
-                ("norm_exact_path", C.c_int64), ("scale_inexact", C.c_int64)]
+    _fields_ = [("tokens_routed", C.c_int64), ("routing_exact_path", C.c_int64), ("norm_exact_path", C.c_int64),
+                ("scale_inexact", C.c_int64)]
 
 
 class SynthSpec(C.Structure):
@@ -123,6 +123,10 @@ def gmoe_lib():
         lib.gmoe_profile.restype = C.c_int
         lib.gmoe_profile_read.argtypes = [P, C.POINTER(GmoeKernelTimes)]
         lib.gmoe_profile_read.restype = C.c_int
+        lib.gmoe_forward_host.argtypes = [P, C.c_int, C.c_int, P, P, C.c_int, P]
+        lib.gmoe_forward_host.restype = C.c_int
+        lib.gmoe_expf_eval.argtypes = [C.c_uint32, C.c_int64, C.c_int, P, P]
+        lib.gmoe_expf_eval.restype = C.c_int
         lib.gmoe_destroy.argtypes = [P]
         lib.gmoe_destroy.restype = None
         lib.gmoe_last_error.argtypes = []
@@ -426,8 +430,6 @@ def forward_host(ctx, layer, x, flags=0, with_state=True):
             "expert_tokens": np.zeros(max(1, T * s.K), np.int32),
         }
         state_p = C.byref(GmoeLayerState(*[ptr(st[n]) for n, _ in GmoeLayerState._fields_]))
-    lib.gmoe_forward_host.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
-    lib.gmoe_forward_host.restype = C.c_int
     check(lib.gmoe_forward_host(ctx.h, layer, T, ptr(x), ptr(out), flags, state_p), "gmoe_forward_host")
     if st is not None:
         n = int(st["expert_offsets"][-1])

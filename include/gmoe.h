@@ -95,7 +95,6 @@ typedef struct gmoe_layer_state {
 typedef struct gmoe_stats {
     int64_t tokens_routed;       /* token-layer routings performed */
     int64_t routing_exact_path;  /* routings that needed the exact sequential-fp32 router replay */
-    int64_t routing_unresolved;  /* routings whose order still hinged on the last bit of libm expf */
     int64_t norm_exact_path;     /* rmsnorms that needed the exact sequential-fp64 sum replay */
     int64_t scale_inexact;       /* weight scales that were not fp16-exact at upload */
 } gmoe_stats;
@@ -169,6 +168,14 @@ int gmoe_profile_read(gmoe_ctx *ctx, gmoe_kernel_times *out);
 #define GMOE_TRACE_STAMPS 16
 int gmoe_trace_items(gmoe_ctx *ctx, int enable);
 int64_t gmoe_trace_items_read(gmoe_ctx *ctx, uint64_t *out, int64_t max_items);
+
+/* Self-check of the router's device expf: evaluates it on the `count` fp32 inputs whose
+ * bit patterns are first_bits, first_bits + 1, ... (wrapping past 0xffffffff) into the
+ * device buffer out[count]. which = 0: the libm-exact expf of the exact router replay,
+ * equal to the C library's expf(x) bit for bit (infer.c:1105 calls it); which = 1: the
+ * fast expf that evaluates the ends of a certified selection interval, where any result
+ * within 2 ulp is sound. Asynchronous on `stream`. */
+int gmoe_expf_eval(uint32_t first_bits, int64_t count, int which, float *out, void *stream);
 
 /* Algorithmic Q8_0 bytes (34 per 32 weights) that one forward of n_tokens reads
  * for its experts, given the routing of its most recent call; used for GB/s. */

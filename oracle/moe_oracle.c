@@ -239,3 +239,35 @@ int oracle_dispatch(int T, int K, int E, const int32_t *topk_idx, int32_t *offse
     free(fill);
     return offsets[E];
 }
+
+/* glm.c's sigmoid calls the C library's expf (infer.c:1105). Compares `got` (a device
+ * expf on the inputs with bit patterns first, first + 1, ...) against this libm's expf:
+ * returns the number of inputs more than max_ulp apart (max_ulp 0: bitwise; NaN matches
+ * NaN) and, in *first_bad, the bit pattern of the first such input (or -1). */
+int64_t oracle_expf_compare(uint32_t first, int64_t count, const float *got, int max_ulp, int64_t *first_bad) {
+    int64_t bad = 0, where = INT64_MAX;
+#pragma omp parallel for schedule(static) reduction(+ : bad) reduction(min : where)
+    for (int64_t i = 0; i < count; i++) {
+        const uint32_t u = first + (uint32_t)i;
+        float x;
+        memcpy(&x, &u, 4);
+        const float want = expf(x), g = got[i];
+        int ok;
+        if (want != want || g != g) {
+            ok = (want != want) && (g != g);
+        } else {
+            uint32_t a, b;
+            memcpy(&a, &want, 4);
+            memcpy(&b, &g, 4);
+            /* expf is never negative: bit patterns order as values */
+            const int64_t dist = (int64_t)a - (int64_t)b;
+            ok = (dist < 0 ? -dist : dist) <= max_ulp;
+        }
+        if (!ok) {
+            bad++;
+            if (i < where) where = i;
+        }
+    }
+    if (first_bad) *first_bad = bad ? (int64_t)(uint32_t)(first + (uint32_t)where) : -1;
+    return bad;
+}

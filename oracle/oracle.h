@@ -62,6 +62,15 @@ int oracle_moe_stack(const oracle_dims *d, const oracle_layer *layers, int n_lay
 int ref_moe_stack(const oracle_dims *d, const oracle_layer *layers, int n_layers, int T, float *x,
                   int32_t *topk_idx);
 
+/* CPU-baseline timing (reference build only): n_tokens decode tokens through the stack
+ * from x, every layer call timed with glm.c's monotonic_ms (infer.c:1426-1430) into
+ * layer_ms[n_tokens][n_layers]; and T tokens through one layer, one timed call each
+ * (token_ms[T]). n_threads > 0 sets the OpenMP team size first. */
+int ref_moe_stack_timed(const oracle_dims *d, const oracle_layer *layers, int n_layers, int n_tokens, float *x,
+                        double *layer_ms, int n_threads);
+int ref_moe_layer_timed(const oracle_dims *d, const oracle_layer *w, int T, const float *x_in, double *token_ms,
+                        int n_threads);
+
 /* Per-expert token lists derived from [T][K] top-k indices: expert e owns
  * tokens[offsets[e] .. offsets[e+1]) in ascending token order, and slots[]
  * holds the top-k slot each entry came from. Returns the number of entries. */
@@ -75,6 +84,10 @@ float oracle_sigmoid(float logit);
 float oracle_silu(float x);
 void oracle_topk(const float *prob, const float *bias, int E, int K, int32_t *idx, float *w);
 void oracle_matvec_q8(const int8_t *q, const float *s, const float *x, float *y, int rows, int cols, int gs);
+
+/* The C library's expf on the fp32 inputs first, first + 1, ... against `got`: the
+ * number of inputs more than max_ulp apart, the first one's bit pattern in *first_bad. */
+int64_t oracle_expf_compare(uint32_t first, int64_t count, const float *got, int max_ulp, int64_t *first_bad);
 
 #ifdef __cplusplus
 }

@@ -59,6 +59,14 @@ class Oracle:
         self._stack = getattr(self.lib, pre + "moe_stack")
         self._stack.argtypes = [C.POINTER(Dims), C.POINTER(Layer), C.c_int, C.c_int, C.c_void_p, C.c_void_p]
         self._stack.restype = C.c_int
+        if kind == "reference":
+            L = self.lib
+            L.ref_moe_stack_timed.argtypes = [C.POINTER(Dims), C.POINTER(Layer), C.c_int, C.c_int, C.c_void_p,
+                                              C.c_void_p, C.c_int]
+            L.ref_moe_stack_timed.restype = C.c_int
+            L.ref_moe_layer_timed.argtypes = [C.POINTER(Dims), C.POINTER(Layer), C.c_int, C.c_void_p, C.c_void_p,
+                                              C.c_int]
+            L.ref_moe_layer_timed.restype = C.c_int
         if kind == "port":
             L = self.lib
             L.oracle_dispatch.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
@@ -71,6 +79,8 @@ class Oracle:
             L.oracle_silu.restype = C.c_float
             L.oracle_topk.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
             L.oracle_matvec_q8.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]
+            L.oracle_expf_compare.argtypes = [C.c_uint32, C.c_int64, C.c_void_p, C.c_int, C.POINTER(C.c_int64)]
+            L.oracle_expf_compare.restype = C.c_int64
 
     @staticmethod
     def dims(shape):
@@ -102,6 +112,43 @@ class Oracle:
         if rc != 0:
             raise RuntimeError("oracle stack failed")
         return x, topk
+
+
+def stack_timed(shape, host_layers, x, n_tokens, n_threads=0):
+    """CPU baseline: n_tokens decode tokens through the reference build's stack from x;
+    returns the per-layer-call wall times in ms, [n_tokens][n_layers]."""
+    orc = Oracle("reference")
+    x = np.array(x, np.float32, copy=True).reshape(-1)
+    arr = (Layer * len(host_layers))(*[layer_struct(h) for h in host_layers])
+    ms = np.zeros((n_tokens, len(host_layers)), np.float64)
+    rc = orc.lib.ref_moe_stack_timed(C.byref(Oracle.dims(shape)), arr, len(host_layers), n_tokens, _p(x), _p(ms),
+                                     n_threads)
+    if rc != 0:
+        raise RuntimeError("ref_moe_stack_timed failed")
+    return ms
+
+
+def layer_timed(shape, host_layer, x, n_threads=0):
+    """CPU baseline: every token of x through one layer of the reference build, one timed
+    call each; returns the per-token wall times in ms."""
+    orc = Oracle("reference")
+    x = np.ascontiguousarray(x, np.float32)
+    ms = np.zeros(x.shape[0], np.float64)
+    rc = orc.lib.ref_moe_layer_timed(C.byref(Oracle.dims(shape)), C.byref(layer_struct(host_layer)), x.shape[0],
+                                     _p(x), _p(ms), n_threads)
+    if rc != 0:
+        raise RuntimeError("ref_moe_layer_timed failed")
+    return ms
+
+
+def expf_compare(first_bits, got, max_ulp=0):
+    """(mismatches, first mismatching bit pattern or -1) of `got` against libm's expf on
+    the fp32 inputs with bit patterns first_bits, first_bits + 1, ..."""
+    lib = Oracle("port").lib
+    got = np.ascontiguousarray(got, np.float32)
+    where = C.c_int64(-1)
+    n = lib.oracle_expf_compare(first_bits, got.size, _p(got), max_ulp, C.byref(where))
+    return int(n), int(where.value)
 
 
 def dispatch(topk_idx, n_experts):

@@ -117,3 +117,63 @@ int ref_moe_stack(const oracle_dims *d, const oracle_layer *layers, int n_layers
     free(ro);
     return 0;
 }
+
+/* CPU baseline timing (bench.py): n_tokens tokens through the stack from x (updated in
+ * place), each layer call timed with glm.c's own monotonic_ms (infer.c:1426-1430) into
+ * layer_ms[t * n_layers + l]. n_threads > 0 sets the OpenMP team (omp_set_num_threads). */
+int ref_moe_stack_timed(const oracle_dims *d, const oracle_layer *layers, int n_layers, int n_tokens, float *x,
+                        double *layer_ms, int n_threads) {
+    if (!d || !layers || !x || !layer_ms || n_layers < 1 || n_tokens < 0) return -1;
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+    Runtime rt;
+    LayerMoeShared *sh = (LayerMoeShared *)calloc((size_t)n_layers + 1, sizeof(LayerMoeShared));
+    LayerMoeRouted *ro = (LayerMoeRouted *)calloc((size_t)n_layers + 1, sizeof(LayerMoeRouted));
+    if (!sh || !ro) {
+        free(sh);
+        free(ro);
+        return -1;
+    }
+    make_runtime(&rt, sh, ro, d, layers, n_layers);
+    RunState st;
+    runstate_build(&st, &rt, 1);
+    unsetenv("GLM_DISABLE_MOE_ROUTED");
+    const int D = d->dim, gs = d->group_size;
+    memcpy(st.x, x, (size_t)D * sizeof(float));
+    for (int t = 0; t < n_tokens; t++) {
+        for (int l = 1; l <= n_layers; l++) {
+            const double t0 = monotonic_ms();
+            apply_moe_shared_ffn_layer(&rt, &st, gs, l, 0, 0);
+            layer_ms[(size_t)t * n_layers + (l - 1)] = monotonic_ms() - t0;
+        }
+    }
+    memcpy(x, st.x, (size_t)D * sizeof(float));
+    runstate_free(&st);
+    free(sh);
+    free(ro);
+    return 0;
+}
+
+/* CPU baseline timing of a batch: glm.c routes prompt tokens one at a time
+ * (infer.c:2190-2233), so each of the T tokens of x_in is one timed layer call
+ * (token_ms[t]). */
+int ref_moe_layer_timed(const oracle_dims *d, const oracle_layer *w, int T, const float *x_in, double *token_ms,
+                        int n_threads) {
+    if (!d || !w || !x_in || !token_ms || T < 0) return -1;
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+    Runtime rt;
+    LayerMoeShared sh[2];
+    LayerMoeRouted ro[2];
+    make_runtime(&rt, sh, ro, d, w, 1);
+    RunState st;
+    runstate_build(&st, &rt, 1);
+    unsetenv("GLM_DISABLE_MOE_ROUTED");
+    const int D = d->dim, gs = d->group_size;
+    for (int t = 0; t < T; t++) {
+        memcpy(st.x, x_in + (size_t)t * D, (size_t)D * sizeof(float));
+        const double t0 = monotonic_ms();
+        apply_moe_shared_ffn_layer(&rt, &st, gs, 1, 0, 0);
+        token_ms[t] = monotonic_ms() - t0;
+    }
+    runstate_free(&st);
+    return 0;
+}

@@ -181,3 +181,20 @@ def test_backend_matvec_offload_declines():
     r = run_backend("print(lib.glm_backend_try_metal_matvec(None, None, None, None, 64, 64, 32),"
                     " lib.glm_backend_metal_matvec_enabled())")
     assert r.returncode == 0 and r.stdout.split() == ["-1", "0"]
+
+
+def test_glm_model_ctypes_mirror_matches_the_c_header():
+    """glm.c_amd/glm_model.py (the Runtime/RunState the GPU backend tests and the benchmark
+    build) has include/glm_model.h's layout, field for field."""
+    import glm_model
+
+    text = open(os.path.join(INC, "glm_model.h")).read()
+    fields = {s: struct_fields(text, s) for s in MODEL_STRUCTS}
+    for s, fl in fields.items():
+        assert [n for n, _ in glm_model.STRUCTS[s]._fields_] == fl, f"{s}: field list differs from glm_model.h"
+    out = compile_and_run(layout_probe(os.path.join(INC, "glm_model.h"), fields), [INC])
+    for line in out.splitlines():
+        sname, field, val = line.split()
+        cls = glm_model.STRUCTS[sname]
+        want = C.sizeof(cls) if field == "sizeof" else getattr(cls, field).offset
+        assert int(val) == want, f"{sname}.{field}: C {val}, ctypes {want}"

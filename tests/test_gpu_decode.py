@@ -44,7 +44,6 @@ def check(want, got, st, stats):
     assert_close(st["shared_out"], want["shared_out"], "shared_out")
     assert_close(st["routed_out"], want["routed_out"], "routed_out")
     assert_close(got, want["x_out"], "x_out")
-    assert stats["routing_unresolved"] == 0
 
 
 def test_small_t1():
@@ -86,8 +85,10 @@ def test_forced_exact_router_batch(name, T):
     shape = {"small": SMALL, "glm": gmoe.GLM47_FLASH, "wide": WIDE}[name]
     want, got, st, stats = run_case(shape, seed=8, T=T, flags=gmoe.GMOE_FLAG_EXACT_ROUTER)
     check(want, got, st, stats)
-    # the replayed chain is glm.c's; only expf may differ by an ulp from glibc's
-    assert_close(st["router_prob"], want["router_prob"], "router_prob", max_abs=1.2e-7, rel_l2=1e-7)
+    # the replay is glm.c's fp32 chain with libm's expf bits: probabilities and weights are
+    # the reference's bit for bit
+    assert np.array_equal(st["router_prob"].view(np.uint32), want["router_prob"].view(np.uint32)), "router_prob bits"
+    assert np.array_equal(st["topk_w"].view(np.uint32), want["topk_w"].view(np.uint32)), "topk_w bits"
     assert stats["routing_exact_path"] >= T
 
 
@@ -100,9 +101,10 @@ def lists_from_topk(topk, E):
     return np.array(offs, np.int32), np.array(toks, np.int32)
 
 
-# seed 12 of the 256-expert case holds an exact tie among one token's top K+1 scores
-# (which the router rightly reports as unresolved); seed 17's smallest gap there is 6e-5
-@pytest.mark.parametrize("name,T,seed", [("small", 200, 12), ("small", 33, 12), ("widest", 45, 17)])
+# seed 12 of the 256-expert case holds an exact tie among one token's top K+1 scores,
+# which the exact replay must break as glm.c does (the lower expert index first)
+@pytest.mark.parametrize("name,T,seed", [("small", 200, 12), ("small", 33, 12), ("widest", 45, 12),
+                                         ("widest", 45, 17)])
 def test_ragged_batch_lists(name, T, seed):
     """Batches that are no multiple of the GEMM tile (32 rows): experts with two
     tiles, the second partial (16 experts, T=200), and many empty or single-row lists

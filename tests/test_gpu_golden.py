@@ -5,11 +5,13 @@ independent decode step of the reference (infer.c:2190-2233).
 
 Bar: top-k indices and the per-expert token lists exact; xn bit-identical; float
 outputs within max-abs 1e-2 and rel-L2 1e-3 (router probabilities and weights
-within 1e-5)."""
+within 1e-5). The batches are also compared row by row, all T rows, with the oracle
+run on the same tokens."""
 import numpy as np
 import pytest
 
 import gmoe
+import oracle
 from conftest import assert_close
 from golden_data import load
 
@@ -19,12 +21,17 @@ S = gmoe.GLM47_FLASH
 
 
 @pytest.fixture(scope="module")
-def ctx():
-    """Layer slot 1: seed-0 layer 1 with N(0, 0.01) bias; slot 2: the same layer with Zipf bias."""
+def layers():
+    """Slot 1: seed-0 layer 1 with N(0, 0.01) bias; slot 2: the same layer with Zipf bias."""
+    return {1: gmoe.HostLayer(S, seed=0, layer=1), 2: gmoe.HostLayer(S, seed=0, layer=1, bias_mode=gmoe.SYNTH_BIAS_ZIPF)}
+
+
+@pytest.fixture(scope="module")
+def ctx(layers):
     print("[setup] GLM-4.7-Flash layer 1, normal and Zipf bias, max_tokens 512", flush=True)
     c = gmoe.Context(S, n_layers=3, max_tokens=512)
-    c.upload(1, gmoe.HostLayer(S, seed=0, layer=1))
-    c.upload(2, gmoe.HostLayer(S, seed=0, layer=1, bias_mode=gmoe.SYNTH_BIAS_ZIPF))
+    for slot, hl in layers.items():
+        c.upload(slot, hl)
     yield c
     c.close()
 
@@ -43,7 +50,7 @@ def test_glm_t1(ctx):
 
 
 @pytest.mark.parametrize("name,slot,T,stream", [("dispatch_t128_zipf", 2, 128, 1), ("dispatch_t512", 1, 512, 2)])
-def test_batched_tokens(ctx, name, slot, T, stream):
+def test_batched_tokens(ctx, layers, name, slot, T, stream):
     g = load(name)
     print(f"[case] {name} T={T}", flush=True)
     x = gmoe.activations(0, stream, T, S.D)
@@ -57,3 +64,11 @@ def test_batched_tokens(ctx, name, slot, T, stream):
     assert_close(got.astype(np.float64).sum(axis=1), g["x_out_row_sums"], "x_out row sums", max_abs=0.1)
     sumsq = float((got.astype(np.float64) ** 2).sum())
     assert abs(sumsq / float(g["x_out_sumsq"]) - 1) < 1e-5
+    # every row against the oracle (the fixture stores six): each token is its own decode step
+    want = oracle.Oracle("port").layer(S, layers[slot], x)
+    np.testing.assert_array_equal(want["topk_idx"], g["topk_idx"], err_msg="oracle vs fixture top-k")
+    for what in ("shared_out", "routed_out"):
+        assert_close(st[what], want[what], f"all rows {what}")
+    assert_close(got, want["x_out"], "all rows x_out")
+    row_err = np.abs(got.astype(np.float64) - want["x_out"]).max(axis=1)
+    assert row_err.max() <= 1e-2, f"row {int(row_err.argmax())} max-abs {row_err.max():.3e}"

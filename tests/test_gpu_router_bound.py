@@ -108,7 +108,6 @@ def test_cancellation_routing_against_oracle(seed):
         np.testing.assert_array_equal(ctx.read_topk(1, 1)[0], want1["topk_idx"], err_msg="stack layer 1 routing")
         np.testing.assert_array_equal(ctx.read_topk(2, 1)[0], want2["topk_idx"], err_msg="stack layer 2 routing")
         assert_close(d_out.download((1, SHAPE.D), np.float32), want2["x_out"], "stack x_out")
-        assert ctx.stats()["routing_unresolved"] == 0
     finally:
         ctx.close()
 
@@ -136,7 +135,6 @@ def test_cancellation_routing_batch(E):
         np.testing.assert_array_equal(st["topk_idx"], want["topk_idx"], err_msg="batch routing")
         assert_close(got, want["x_out"], "batch x_out")
         stats = ctx.stats()
-        assert stats["routing_unresolved"] == 0
         assert stats["routing_exact_path"] >= T  # no certificate may hold at this cancellation
     finally:
         ctx.close()

@@ -58,7 +58,6 @@ def test_each_layer_against_oracle(stack):
         assert_close(st["routed_out"], want["routed_out"], f"layer {l} routed_out")
         assert_close(got, want["x_out"], f"layer {l} x_out")
         x = got  # next layer starts from the GPU's own output
-    assert ctx.stats()["routing_unresolved"] == 0
 
 
 def test_stack_against_oracle_stack(stack):
@@ -106,9 +105,9 @@ def test_forced_exact_router_matches_oracle(stack):
         want = orc.layer(shape, layers[l - 1], x)
         got, st = gmoe.forward_host(ctx, l, x, flags=gmoe.GMOE_FLAG_EXACT_ROUTER)
         np.testing.assert_array_equal(st["topk_idx"], want["topk_idx"], err_msg=f"layer {l} routing")
-        # the replayed chain is glm.c's; only expf may differ by an ulp from glibc's
-        assert_close(st["router_prob"], want["router_prob"], f"layer {l} router_prob", max_abs=1.2e-7, rel_l2=1e-7)
-        assert_close(st["topk_w"], want["topk_w"], f"layer {l} topk_w", max_abs=1e-6, rel_l2=1e-6)
+        # the replay is glm.c's fp32 chain with libm's expf bits
+        assert np.array_equal(st["router_prob"].view(np.uint32), want["router_prob"].view(np.uint32)), f"layer {l} router_prob"
+        assert np.array_equal(st["topk_w"].view(np.uint32), want["topk_w"].view(np.uint32)), f"layer {l} topk_w"
         assert_close(got, want["x_out"], f"layer {l} x_out")
         x = got
     assert ctx.stats()["routing_exact_path"] - before == N_LAYERS

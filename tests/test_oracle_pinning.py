@@ -245,3 +245,26 @@ def test_layer_routed_off(small_layer_run):
     r = oracle.Oracle("port").layer(SMALL, hl, x, disable_routed=True)
     assert not r["routed_out"].any()
     assert np.array_equal(r["x_out"], (x + r["shared_out"]).astype(F32))
+
+
+def test_expf_compare_counts_bitwise_and_ulp_differences():
+    """oracle_expf_compare, the checker of the GPU's expf, against numpy's bit patterns:
+    a result one ulp off fails the bitwise comparison and passes at max_ulp=1; NaN
+    matches NaN only."""
+    import ctypes
+
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.argtypes = [ctypes.c_float]
+    libm.expf.restype = ctypes.c_float
+    first = np.float32(-3.0).view(np.uint32)
+    n = 4096
+    xs = (np.uint32(first) + np.arange(n, dtype=np.uint32)).view(np.float32)
+    exact = np.array([libm.expf(float(v)) for v in xs], np.float32)
+    assert oracle.expf_compare(int(first), exact) == (0, -1)
+    off = exact.copy()
+    off[17] = np.nextafter(off[17], np.float32(np.inf))
+    assert oracle.expf_compare(int(first), off) == (1, int(first) + 17)
+    assert oracle.expf_compare(int(first), off, max_ulp=1) == (0, -1)
+    nan_first = np.float32(np.nan).view(np.uint32)
+    assert oracle.expf_compare(int(nan_first), np.array([np.nan], np.float32)) == (0, -1)
+    assert oracle.expf_compare(int(nan_first), np.array([1.0], np.float32))[0] == 1
