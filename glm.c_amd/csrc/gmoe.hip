@@ -19,6 +19,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <vector>
 #include <stdlib.h>
 #include <string.h>
@@ -32,6 +33,15 @@
 #include "stack.h"
 
 static_assert(SK_TRACE_STAMPS == GMOE_TRACE_STAMPS, "trace stamps per item: kernel and ABI disagree");
+
+// Workspace of gmoe_forward_layers_noalloc: one fixed array per GPU, held until the
+// process ends, so that the call allocates nothing. In host code `scratch` is only a
+// host-side stand-in for the array, not a device address: gmoe_create looks up each
+// device's own address once (scratch_lookup) and launches use that address.
+static __device__ __align__(256) unsigned char scratch[GMOE_NOALLOC_SCRATCH_BYTES];
+#define GM_MAX_DEVICES 64
+static void *g_scratch_dev[GM_MAX_DEVICES];
+static std::mutex g_scratch_mu;
 
 // Router blocks of the persistent kernel: the largest power of two <= min(E, 64), so
 // that every block holds at most GM_MAX_E / 64 experts.
@@ -129,9 +139,28 @@ struct gmoe_ctx {
     long long scale_inexact = 0;
     int last_layer = -1, last_T = 0, last_flags = 0, last_dispatched = 0, stack_launched = 0;
     int stack_last = 0;  // the most recent forward was a persistent launch
+    int *stack_error_dev = nullptr;  // the device error word that launch used
 };
 
 extern "C" const char *gmoe_last_error(void) { return g_err; }
+
+// The device address of `scratch` on `device` (current), looked up once per device.
+static int scratch_lookup(int device) {
+    if (device < 0 || device >= GM_MAX_DEVICES) {
+        set_err("device %d: at most %d devices are supported", device, GM_MAX_DEVICES);
+        return GMOE_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_dev[device]) return GMOE_OK;
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        set_err("hipGetSymbolAddress(scratch) on device %d failed: %s", device, hipGetErrorString(e));
+        return GMOE_ERR_HIP;
+    }
+    g_scratch_dev[device] = p;
+    return GMOE_OK;
+}
 
 template <typename T>
 static int dev_alloc(T **p, size_t count) {
@@ -218,6 +247,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         return GMOE_ERR_INVALID;
     }
     HIP_OK(hipSetDevice(device));
+    if (int src = scratch_lookup(device)) return src;
 
     gmoe_ctx *c = new gmoe_ctx();
     c->device = device;
@@ -549,8 +579,20 @@ static int launch_dispatch(gmoe_ctx *c, int T, int routed_on, hipStream_t st) {
     return GMOE_OK;
 }
 
-// T=1 through layers first..first+n-1 with the persistent kernel.
-static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float *x_out, int flags, hipStream_t st) {
+// Where a persistent launch keeps its workspace: the context's buffers, or the fixed
+// device array of gmoe_forward_layers_noalloc.
+struct StackSpace {
+    uint8_t *ws;   // n_layers regions of ws_layer bytes
+    unsigned *ctr; // SK_CTR_WORDS(n_layers)
+    int *error;
+};
+
+// T=1 through layers first..first+n-1 with the persistent kernel. With `space` the launch
+// uses that workspace and records neither trace nor profile (both may allocate).
+static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float *x_out, int flags, hipStream_t st,
+                        const StackSpace *space = nullptr) {
+    const StackSpace own = {c->sk_ws, c->sk_ctr, c->sk_error};
+    const StackSpace &sp = space ? *space : own;
     StackArgs a;
     a.layers = c->sk_layers + first;
     a.n_layers = n;
@@ -571,7 +613,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.off_gs = c->off_gs;
     a.off_us = c->off_us;
     a.off_ds = c->off_ds;
-    a.ws = c->sk_ws;
+    a.ws = sp.ws;
     a.ws_layer_bytes = c->sk_ws_layer;
     a.o = c->sk_o;
     a.xn = c->xn;
@@ -583,9 +625,9 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.hist_stride = c->Tmax * c->K;
     a.shared_out = c->shared_out;
     a.routed_out = c->routed_out;
-    a.ctr = c->sk_ctr;
+    a.ctr = sp.ctr;
     a.stats = c->stats_dev;
-    a.error = c->sk_error;
+    a.error = sp.error;
     a.error_host = c->sk_error_host_dev;
     a.spin_limit = c->sk_spin_limit;
     a.trace = nullptr;
@@ -603,7 +645,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         a.n_router = nr;
         a.shared_blocks = nsb;
     }
-    if (c->sk_trace_on) {
+    if (c->sk_trace_on && !space) {
         const size_t items = (size_t)(stack_routers(c->E) + c->D / SK_CROWS + (c->K + 1) * (c->F / 16)) * n;
         if (items > c->sk_trace_items) {
             dev_free(c->sk_trace);
@@ -617,8 +659,8 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         HIP_OK(hipMemsetAsync(c->sk_trace, 0, SK_TRACE_STAMPS * items * sizeof(uint64_t), st));
     }
     const int n_ctr = SK_CTR_WORDS(n);
-    hipLaunchKernelGGL(k_stack_reset, dim3(n + 1), dim3(SK_BLOCK), 0, st, c->sk_ctr, n_ctr, c->sk_error, a);
-    ProfRecord *pr = prof_begin(c, st, GMOE_KERNEL_STACK);
+    hipLaunchKernelGGL(k_stack_reset, dim3(n + 1), dim3(SK_BLOCK), 0, st, sp.ctr, n_ctr, sp.error, a);
+    ProfRecord *pr = space ? nullptr : prof_begin(c, st, GMOE_KERNEL_STACK);
     hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
     prof_end(pr, st);
     HIP_OK(hipGetLastError());
@@ -633,6 +675,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     c->tokens_routed += n;
     c->stack_launched = 1;
     c->stack_last = 1;
+    c->stack_error_dev = sp.error;
     return GMOE_OK;
 }
 
@@ -655,7 +698,7 @@ static int check_stack_error(gmoe_ctx *c) {
     if (!c->stack_launched) return GMOE_OK;
     int err = 0;
     HIP_OK(hipDeviceSynchronize());
-    if (c->stack_last) HIP_OK(hipMemcpy(&err, c->sk_error, sizeof(int), hipMemcpyDeviceToHost));
+    if (c->stack_last) HIP_OK(hipMemcpy(&err, c->stack_error_dev, sizeof(int), hipMemcpyDeviceToHost));
     const int host_rc = take_launch_error(c);
     if (err || host_rc) {
         set_err("%s", k_timeout_msg);
@@ -864,6 +907,57 @@ extern "C" int gmoe_forward_layers(gmoe_ctx *c, int first, int n, int T, const f
         if (rc) return rc;
     }
     return GMOE_OK;
+}
+
+// Workspace bytes of an n-layer launch inside `scratch`: the layers' regions, the counters
+// (on 256-byte lines) and the error word.
+static size_t noalloc_bytes(const gmoe_ctx *c, int n) {
+    const size_t ctr = ((size_t)SK_CTR_WORDS(n) * sizeof(unsigned) + 255) & ~(size_t)255;
+    return (size_t)n * c->sk_ws_layer + ctr + 256;
+}
+
+extern "C" int gmoe_forward_layers_noalloc(gmoe_ctx *c, int first, int n, const float *x_in, float *x_out, int flags,
+                                           void *stream) {
+    if (!c || n < 1 || !x_in || !x_out) {
+        set_err("gmoe_forward_layers_noalloc: bad arguments");
+        return GMOE_ERR_INVALID;
+    }
+    if (!c->stack_ok) {
+        set_err("gmoe_forward_layers_noalloc: this shape does not run on the persistent decode kernel");
+        return GMOE_ERR_INVALID;
+    }
+    if (noalloc_bytes(c, n) > GMOE_NOALLOC_SCRATCH_BYTES) {
+        int most = 0;
+        while (noalloc_bytes(c, most + 1) <= GMOE_NOALLOC_SCRATCH_BYTES) most++;
+        set_err("gmoe_forward_layers_noalloc: %d layers need %zu bytes of workspace; the fixed array holds %u, "
+                "at most %d layers of this shape per call",
+                n, noalloc_bytes(c, n), (unsigned)GMOE_NOALLOC_SCRATCH_BYTES, most);
+        return GMOE_ERR_INVALID;
+    }
+    if (first < 1 || first + n > c->L) {
+        set_err("gmoe_forward_layers_noalloc: layers %d..%d outside 1..%d", first, first + n - 1, c->L - 1);
+        return GMOE_ERR_INVALID;
+    }
+    for (int l = first; l < first + n; l++) {
+        if (!c->layers[l].uploaded) {
+            set_err("gmoe_forward_layers_noalloc: layer %d is not uploaded", l);
+            return GMOE_ERR_INVALID;
+        }
+    }
+    HIP_OK(hipSetDevice(c->device));
+    if (int erc = take_launch_error(c)) return erc;
+    uint8_t *base;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        base = (uint8_t *)g_scratch_dev[c->device];  // set by gmoe_create on this device
+    }
+    const size_t ws_bytes = (size_t)n * c->sk_ws_layer;
+    const size_t ctr_bytes = noalloc_bytes(c, n) - ws_bytes - 256;
+    StackSpace sp;
+    sp.ws = base;
+    sp.ctr = (unsigned *)(base + ws_bytes);
+    sp.error = (int *)(base + ws_bytes + ctr_bytes);
+    return launch_stack(c, first, n, x_in, x_out, flags, (hipStream_t)stream, &sp);
 }
 
 static int copy_out(void *dst, const void *src, size_t bytes) {

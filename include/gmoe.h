@@ -117,6 +117,22 @@ int gmoe_forward(gmoe_ctx *ctx, int layer, int n_tokens, const float *x_in, floa
 int gmoe_forward_layers(gmoe_ctx *ctx, int first_layer, int n_layers, int n_tokens,
                         const float *x_in, float *x_out, int flags, void *stream);
 
+/* gmoe_forward_layers for one token (n_tokens = 1) that allocates nothing. It has no
+ * counterpart in glm.c: it is for callers that cannot allocate device memory, such as code
+ * under HIP graph capture or a tight serving loop. The persistent launch keeps its
+ * workspace (every layer's activations, router entries and partial sums, the counters
+ * and the error word) in one fixed device array of GMOE_NOALLOC_SCRATCH_BYTES per GPU,
+ * which the library holds until the process ends, instead of the context's buffers.
+ * At most as many layers per call as fit in that array (16 at GLM-4.7-Flash's shape):
+ * a longer run is refused with GMOE_ERR_INVALID. Trace and profile recording are
+ * skipped. Every call on one GPU shares the array, so calls that overlap on one GPU
+ * (other streams, threads or contexts) race; calls in order on one stream do not. A
+ * timed-out launch is reported by the context's next call. Results equal
+ * gmoe_forward_layers' bit for bit. */
+#define GMOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int gmoe_forward_layers_noalloc(gmoe_ctx *ctx, int first_layer, int n_layers, const float *x_in, float *x_out,
+                                int flags, void *stream);
+
 /* Host-memory form of gmoe_forward for callers that make no HIP calls themselves,
  * such as glm.c's C host: copies x_in ([n_tokens][D] fp32, host) to the device, runs
  * the layer on the default stream, copies the result to x_out (host, may alias x_in)
