@@ -331,7 +331,8 @@ def main():
         raise SystemExit("--profile-steps must be at least 1: the roofline needs the kernel's launch time")
     K1 = shape.K + 1
     mat = shape.F * shape.D * 34 // 32
-    kernel_bytes = {"gate_up": K1 * 2 * mat, "down": K1 * mat, "k_moe_stack": bytes_per_token}
+    kernel_bytes = {"gate_up": K1 * 2 * mat, "down": K1 * mat, "k_moe_stack": bytes_per_token,
+                    "k_moe_decode": bytes_per_token}
     dom = max(prof, key=lambda k: prof[k][1])
     kernels = {k: {"launches": n, "avg_us": ms * 1e3 / n} for k, (n, ms) in prof.items()}
     for k in kernels:

@@ -34,6 +34,11 @@ __device__ static inline const GM_GLOBAL T *gbl(const T *p) {
     return (const GM_GLOBAL T *)p;
 }
 
+// s_waitcnt immediate (gfx9 encoding) for vmcnt(0) alone: expcnt and lgkmcnt at their
+// maxima. Passed to __builtin_amdgcn_s_waitcnt, which the compiler's wait insertion sees,
+// unlike an asm wait.
+#define GM_WAIT_VM0 0x0F70
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 typedef __attribute__((address_space(3))) void lds_void;

@@ -25,6 +25,7 @@
 #include <string.h>
 
 #include "common.h"
+#include "decode.h"
 #include "dispatch.h"
 #include "experts.h"
 #include "grouped.h"
@@ -75,6 +76,7 @@ struct LayerDev {
     float *norm = nullptr;       // [D]
     float *gate_inp = nullptr;   // [E][D]
     float *bias = nullptr;       // [E]
+    double *nu = nullptr;        // [E] sum_i |gate_inp[e][i]| (|ffn_norm[i]| + 1), for the router records' bound
     int has_routed = 0;
     int uploaded = 0;
     int last_T = 0;
@@ -118,6 +120,7 @@ struct gmoe_ctx {
     int grouped_min_t = 2;       // T from which batches take the grouped GEMMs (GMOE_GROUPED_MIN_T)
     int stack_ok = 0;            // shape fits k_moe_stack
     int stack_grid = 0;          // co-resident blocks
+    int decode_rows = 0;         // T=1 runs k_moe_decode (decode.h) rather than k_moe_stack
     uint8_t *sk_ws = nullptr;    // per-layer workspace, L regions of sk_ws_layer bytes
     size_t sk_ws_layer = 0;
     StackWs sk_o{};
@@ -192,6 +195,7 @@ static void free_ctx(gmoe_ctx *c) {
             dev_free(c->layers[l].norm);
             dev_free(c->layers[l].gate_inp);
             dev_free(c->layers[l].bias);
+            dev_free(c->layers[l].nu);
         }
         delete[] c->layers;
     }
@@ -309,6 +313,33 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     rc |= dev_alloc(&c->hist_w, (size_t)c->L * T * K);
     rc |= dev_alloc(&c->stats_dev, GM_STAT_COUNT);
     rc |= dev_alloc(&c->x_host_io, T * D);
+    // The persistent decode kernels hold one panel's chunks per wave in registers and xn in
+    // shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots. k_moe_stack
+    // stages a combine chunk's partials, F/16 x (K+1) x 8 floats, in the slice buffer;
+    // k_moe_decode (decode.h) runs shapes whose expert items and router finishers fit its grid.
+    c->stack_ok = c->L <= SK_MAX_LAYERS && (size_t)(F / 16) * (K + 1) * SK_CROWS * sizeof(float) <= sizeof(SkShared::dslice);
+    if (const char *g_env = getenv("GMOE_GROUPED_MIN_T")) c->grouped_min_t = atoi(g_env) > 1 ? atoi(g_env) : 2;
+    const char *env = getenv("GMOE_STACK_KERNEL");
+    if (env && env[0] == '0') c->stack_ok = 0;
+    if (c->stack_ok) {
+        int per_cu = 0, per_cu_dk = 0, cus = 0;
+        hipDeviceProp_t prop;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_stack, SK_BLOCK, 0) != hipSuccess ||
+            hipGetDeviceProperties(&prop, device) != hipSuccess || per_cu < 1) {
+            c->stack_ok = 0;
+        } else {
+            cus = prop.multiProcessorCount;
+            const int want = per_cu < 2 ? per_cu : 2;  // 2 blocks (8 waves) per CU
+            c->stack_grid = want * cus;
+            // roles: the router blocks, at least one shared-expert and one routed block
+            if (c->stack_grid < stack_routers(c->E) + 2) c->stack_ok = 0;
+            const char *dk_env = getenv("GMOE_DECODE_KERNEL");
+            // the row-owner kernel is opted into (GMOE_DECODE_KERNEL=1): k_moe_stack is the default
+            c->decode_rows = c->stack_ok && dk_env && dk_env[0] == '1' &&
+                             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_dk, k_moe_decode, SK_BLOCK, 0) == hipSuccess &&
+                             per_cu_dk >= want && dk_fits(c->stack_grid, c->D, c->F, c->E, c->K);
+        }
+    }
     {
         // per-layer regions of the persistent kernel, each buffer on its own 256-byte lines
         size_t off = 0;
@@ -323,7 +354,11 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         c->sk_o.dexp = take(D / 32 * sizeof(int));
         c->sk_o.stage = take(SK_STAGE_COPIES * SK_STAGE_COPY_WORDS * sizeof(unsigned long long));
         c->sk_o.ex_w = take(K * sizeof(float));
-        c->sk_o.ypart = take(NS * (F / 16) * D * sizeof(float));
+        // k_moe_stack's partial sums, or k_moe_decode's h records and router records
+        c->sk_o.ypart = take(c->decode_rows ? 0 : NS * (F / 16) * D * sizeof(float));
+        c->sk_o.h = take(c->decode_rows ? NS * (F / 16) * DK_HREC : 0);
+        c->sk_o.rec = take(c->decode_rows ? (D / DK_ROWS) * E * sizeof(DkRec) : 0);
+        c->sk_o.xsq = take(c->decode_rows ? (D / DK_ROWS) * sizeof(double) : 0);
         c->sk_ws_layer = off;
         rc |= dev_alloc(&c->sk_ws, (size_t)c->L * off);
     }
@@ -358,27 +393,6 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         set_err("gmoe_create: initialising device buffers failed");
         free_ctx(c);
         return GMOE_ERR_HIP;
-    }
-    // The persistent decode kernel holds one panel's chunks per wave in registers and
-    // xn in shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots.
-    // (the combine stages a chunk's partials, F/16 x (K+1) x 8 floats, in the slice buffer)
-    c->stack_ok = c->L <= SK_MAX_LAYERS && (size_t)(F / 16) * (K + 1) * SK_CROWS * sizeof(float) <= sizeof(SkShared::dslice);
-    if (const char *g_env = getenv("GMOE_GROUPED_MIN_T")) c->grouped_min_t = atoi(g_env) > 1 ? atoi(g_env) : 2;
-    const char *env = getenv("GMOE_STACK_KERNEL");
-    if (env && env[0] == '0') c->stack_ok = 0;
-    if (c->stack_ok) {
-        int per_cu = 0, cus = 0;
-        hipDeviceProp_t prop;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_stack, SK_BLOCK, 0) != hipSuccess ||
-            hipGetDeviceProperties(&prop, device) != hipSuccess || per_cu < 1) {
-            c->stack_ok = 0;
-        } else {
-            cus = prop.multiProcessorCount;
-            const int want = per_cu < 2 ? per_cu : 2;  // 2 blocks (8 waves) per CU
-            c->stack_grid = want * cus;
-            // roles: the router blocks, at least one shared-expert and one routed block
-            if (c->stack_grid < stack_routers(c->E) + 2) c->stack_ok = 0;
-        }
     }
     *out = c;
     return GMOE_OK;
@@ -443,10 +457,22 @@ extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weight
     if (!L.norm && dev_alloc(&L.norm, (size_t)D) != GMOE_OK) return GMOE_ERR_NOMEM;
     if (!L.gate_inp && dev_alloc(&L.gate_inp, (size_t)E * D) != GMOE_OK) return GMOE_ERR_NOMEM;
     if (!L.bias && dev_alloc(&L.bias, (size_t)E) != GMOE_OK) return GMOE_ERR_NOMEM;
+    if (!L.nu && dev_alloc(&L.nu, (size_t)E) != GMOE_OK) return GMOE_ERR_NOMEM;
     int rc;
     if ((rc = copy_in(L.norm, w->ffn_norm, (size_t)D * sizeof(float)))) return rc;
     if ((rc = copy_in(L.gate_inp, w->gate_inp, (size_t)E * D * sizeof(float)))) return rc;
     if ((rc = copy_in(L.bias, w->exp_probs_b, (size_t)E * sizeof(float)))) return rc;
+    {
+        // nu_e = sum_i |gate_inp[e][i]| (|ffn_norm[i]| + 1), rounded up: bounds what underflow in
+        // xn's two fp32 roundings can add to expert e's router logit (decode.h)
+        std::vector<double> nu((size_t)E);
+        for (int e = 0; e < E; e++) {
+            double s = 0.0;
+            for (int i = 0; i < D; i++) s += fabs((double)w->gate_inp[(size_t)e * D + i]) * (fabs((double)w->ffn_norm[i]) + 1.0);
+            nu[(size_t)e] = s * (1.0 + 0x1p-40);
+        }
+        if ((rc = copy_in(L.nu, nu.data(), (size_t)E * sizeof(double)))) return rc;
+    }
 
     unsigned long long *inexact = nullptr;
     if (dev_alloc(&inexact, 1) != GMOE_OK) return GMOE_ERR_NOMEM;
@@ -480,6 +506,7 @@ extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weight
     sl.norm = L.norm;
     sl.gate_inp = L.gate_inp;
     sl.bias = L.bias;
+    sl.nu = L.nu;
     sl.has_routed = has_routed;
     sl.pad = 0;
     if ((rc = copy_in(c->sk_layers + layer, &sl, sizeof(sl)))) return rc;
@@ -642,11 +669,13 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
             nwb = avail - nsb;
         }
         if (nsb > npf) nsb = npf;
-        a.n_router = nr;
+        a.n_router = c->decode_rows ? dk_finishers(c->stack_grid, c->E, c->K, c->F) : nr;
         a.shared_blocks = nsb;
     }
     if (c->sk_trace_on && !space) {
-        const size_t items = (size_t)(stack_routers(c->E) + c->D / SK_CROWS + (c->K + 1) * (c->F / 16)) * n;
+        // k_moe_stack: its work items; k_moe_decode: one item per (layer, block)
+        const size_t items = c->decode_rows ? (size_t)c->stack_grid * n
+                                            : (size_t)(stack_routers(c->E) + c->D / SK_CROWS + (c->K + 1) * (c->F / 16)) * n;
         if (items > c->sk_trace_items) {
             dev_free(c->sk_trace);
             c->sk_trace = nullptr;
@@ -660,8 +689,11 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     }
     const int n_ctr = SK_CTR_WORDS(n);
     hipLaunchKernelGGL(k_stack_reset, dim3(n + 1), dim3(SK_BLOCK), 0, st, sp.ctr, n_ctr, sp.error, a);
-    ProfRecord *pr = space ? nullptr : prof_begin(c, st, GMOE_KERNEL_STACK);
-    hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+    ProfRecord *pr = space ? nullptr : prof_begin(c, st, c->decode_rows ? GMOE_KERNEL_DECODE : GMOE_KERNEL_STACK);
+    if (c->decode_rows)
+        hipLaunchKernelGGL(k_moe_decode, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
     prof_end(pr, st);
     HIP_OK(hipGetLastError());
     for (int l = first; l < first + n; l++) {

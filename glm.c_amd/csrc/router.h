@@ -188,6 +188,9 @@ __device__ __attribute__((always_inline)) static void certified_select(int E, in
     }
 }
 
+__device__ __attribute__((always_inline)) static void exact_topk(int E, int K, int tid, const float *p, const float *sel,
+                                                                 int *idx, float *wk_out, unsigned long long *stats);
+
 // glm.c's router replayed exactly in fp32 (infer.c:916-938, 1104-1145) by one block of
 // 256 threads, for the xn in shared memory: every probability into p and selection
 // score into sel (shared, [E]), the top-k into idx and its normalised weights into wk
@@ -261,9 +264,18 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
         }
     }
     __syncthreads();
-    // glm.c's insertion top-k (infer.c:1110-1135) keeps the K largest sel by (value desc,
-    // index asc) among values above -inf (NaN is never inserted): K wave-maximum rounds,
-    // the lowest lane winning ties, chunk c of lane l holding expert l + 64c.
+    exact_topk(E, K, tid, p, sel, idx, wk_out, stats);
+}
+
+// glm.c's insertion top-k (infer.c:1110-1135) on wave 0 of the block, from every expert's
+// probability p and selection score sel (shared memory): the K largest sel by (value desc,
+// index asc) among values above -inf (NaN is never inserted), by K wave-maximum rounds with
+// the lowest lane winning ties, chunk c of lane l holding expert l + 64c; their unbiased
+// p, normalised (infer.c:1136-1145), into idx / wk_out (shared, [K]). Counts the replay in
+// stats. Ends with a barrier.
+__device__ __attribute__((always_inline)) static void exact_topk(int E, int K, int tid, const float *p, const float *sel,
+                                                                 int *idx, float *wk_out, unsigned long long *stats) {
+    const int lane = tid & 63, w = tid >> 6;
     if (w == 0) {
         const int nch = (E + 63) >> 6;
         float key[RT_SEL_C], pv[RT_SEL_C];

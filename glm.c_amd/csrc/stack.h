@@ -40,7 +40,7 @@
 
 #define SK_BLOCK 256
 #define SK_SPIN_LIMIT (1u << 22)               // default polls before a wait is declared dead (~seconds)
-#define SK_TRACE_STAMPS 16
+#define SK_TRACE_STAMPS 32
 #define SK_NR_MAX 64                           // router blocks
 #define SK_RX_MAX (GM_MAX_E / SK_NR_MAX)       // experts per router block
 #define SK_PER_MAX (GM_MAX_COLS / SK_BLOCK)    // columns (router) or rows (down) per thread
@@ -78,6 +78,7 @@ struct StackLayer {
     const float *norm;
     const float *gate_inp;
     const float *bias;
+    const double *nu;  // [E]: sum_i |gate_inp[e][i]| (|norm[i]| + 1), rounded up (the router bound's underflow term)
     int has_routed;
     int pad;
 };
@@ -99,6 +100,7 @@ struct StackLayer {
 // Per-layer workspace: one region of `ws_layer_bytes` per layer of the launch.
 struct StackWs {
     size_t x, xn, dig, dexp, stage, ex_w, ypart;  // byte offsets inside a layer region
+    size_t h, rec, xsq;                           // the row-owner kernel's (decode.h): h digits, router records
 };
 
 struct StackArgs {
@@ -208,10 +210,14 @@ struct SkShared {
     unsigned zero;  // 0 for the kernel's life (an always-zero operand of gu_products)
     int xe_local;   // exponent of a routed block's own digits of xn (sk_local_digits)
     unsigned spin_limit;
+    float xr4[4];   // the row-owner kernel's (decode.h): an owner's new rows of x
+    unsigned long long hrec[8];  // and an item's h record
     int idx[GM_MAX_K];
     float wk[GM_MAX_K], ws[GM_MAX_K];
     long trace_item;
     unsigned long long *trace;
+    unsigned long long *dk_trace;  // the row-owner kernel's: stamps of the current layer, flushed at its end
+    unsigned long long stamps[SK_TRACE_STAMPS];
 };
 
 __device__ static inline void st_u(unsigned *p, unsigned v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }

@@ -1,3 +1,4 @@
+import contextlib
 import os
 import sys
 
@@ -31,6 +32,48 @@ def assert_close(got, want, what, max_abs=MAX_ABS, rel_l2=REL_L2):
     assert err.max() <= max_abs, f"{what}: max-abs {err.max():.3e} > {max_abs} (at {np.unravel_index(err.argmax(), err.shape)})"
     assert rel <= rel_l2, f"{what}: rel-L2 {rel:.3e} > {rel_l2}"
     return err.max(), rel
+
+
+# The two persistent T=1 kernels, chosen when a context is created: k_moe_stack (the
+# default) and the row-owner k_moe_decode (GMOE_DECODE_KERNEL=1).
+DECODE_KERNELS = {"stack": "0", "rows": "1"}
+DECODE_KERNEL_NAMES = {"stack": "k_moe_stack", "rows": "k_moe_decode"}
+
+
+@contextlib.contextmanager
+def decode_kernel(kind):
+    """Contexts created inside run their T=1 launches on `kind` ("stack" or "rows")."""
+    old = os.environ.get("GMOE_DECODE_KERNEL")
+    os.environ["GMOE_DECODE_KERNEL"] = DECODE_KERNELS[kind]
+    try:
+        yield
+    finally:
+        if old is None:
+            os.environ.pop("GMOE_DECODE_KERNEL", None)
+        else:
+            os.environ["GMOE_DECODE_KERNEL"] = old
+
+
+@pytest.fixture(params=list(DECODE_KERNELS))
+def dkernel(request):
+    """Runs the test once per persistent T=1 kernel (contexts created in the test)."""
+    with decode_kernel(request.param):
+        yield request.param
+
+
+def launched(ctx, run):
+    """gmoe_profile bucket names of the kernels that run() launched on ctx."""
+    ctx.profile(True)
+    run()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    return set(prof)
+
+
+def assert_decode_kernel(ran, kind):
+    """The persistent T=1 kernel of `kind` ran, and the other one did not."""
+    assert DECODE_KERNEL_NAMES[kind] in ran, ran
+    assert not (set(DECODE_KERNEL_NAMES.values()) - {DECODE_KERNEL_NAMES[kind]}) & ran, ran
 
 
 @pytest.fixture(scope="session")

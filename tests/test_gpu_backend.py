@@ -28,7 +28,7 @@ def run_backend_layers(shape, layers, x0, env=None, monkeypatch=None):
     return model
 
 
-def test_backend_runs_each_moe_layer_on_the_run_state():
+def test_backend_runs_each_moe_layer_on_the_run_state(dkernel):
     shape = gmoe.GLM47_FLASH
     layers = [gmoe.HostLayer(shape, seed=21, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM) for l in (1, 2, 3)]
     model = run_backend_layers(shape, layers, None)
@@ -56,7 +56,7 @@ def test_backend_runs_each_moe_layer_on_the_run_state():
         model.free()
 
 
-def test_backend_declines_a_failed_layer_and_keeps_x(monkeypatch):
+def test_backend_declines_a_failed_layer_and_keeps_x(monkeypatch, dkernel):
     """A GPU layer that fails returns -1 so glm.c runs the layer on the CPU, and that
     needs st->x as it was: the forced timeout (GMOE_SPIN_LIMIT=0) must leave it intact."""
     shape = gmoe.Shape(dim=256, moe_ffn_dim=256, n_routed_experts=16, n_experts_used=4)

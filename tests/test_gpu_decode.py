@@ -4,12 +4,14 @@ Each token of a batch is an independent decode step (infer.c:2190-2233), so a
 batch of T tokens checks T decode cases at once; T=1 is checked on its own too.
 Bar: top-k indices exact, xn bitwise (both pinned to glm.c's arithmetic), float
 outputs within max-abs 1e-2 and rel-L2 1e-3."""
+import os
+
 import numpy as np
 import pytest
 
 import gmoe
 import oracle
-from conftest import assert_close
+from conftest import DECODE_KERNELS, assert_close, assert_decode_kernel, decode_kernel, launched
 
 pytestmark = pytest.mark.gpu
 
@@ -29,7 +31,12 @@ def run_case(shape, seed, T, norm_mode=gmoe.SYNTH_NORM_ONES, flags=0, layer=1):
     ctx = gmoe.Context(shape, n_layers=layer + 1, max_tokens=T)
     try:
         ctx.upload(layer, L)
-        got, st = gmoe.forward_host(ctx, layer, x, flags=flags)
+        out = {}
+        ran = launched(ctx, lambda: out.update(r=gmoe.forward_host(ctx, layer, x, flags=flags)))
+        got, st = out["r"]
+        if T == 1:  # the persistent kernel the environment asks for
+            kind = "rows" if os.environ.get("GMOE_DECODE_KERNEL") == DECODE_KERNELS["rows"] else "stack"
+            assert_decode_kernel(ran, kind)
         stats = ctx.stats()
     finally:
         ctx.close()
@@ -46,7 +53,7 @@ def check(want, got, st, stats):
     assert_close(got, want["x_out"], "x_out")
 
 
-def test_small_t1():
+def test_small_t1(dkernel):
     check(*run_case(SMALL, seed=1, T=1))
 
 
@@ -60,7 +67,7 @@ def test_small_no_routed():
     assert np.all(st["routed_out"] == 0)
 
 
-def test_glm_shape_t1():
+def test_glm_shape_t1(dkernel):
     check(*run_case(gmoe.GLM47_FLASH, seed=0, T=1))
 
 
@@ -68,14 +75,16 @@ def test_glm_shape_batch8():
     check(*run_case(gmoe.GLM47_FLASH, seed=5, T=8, norm_mode=gmoe.SYNTH_NORM_RANDOM))
 
 
-@pytest.mark.parametrize("T", [1, 8])
-def test_wide_expert_count(T):
-    check(*run_case(WIDE, seed=6, T=T, norm_mode=gmoe.SYNTH_NORM_RANDOM))
+@pytest.mark.parametrize("T,kind", [(1, "stack"), (1, "rows"), (8, "stack")])
+def test_wide_expert_count(T, kind):
+    with decode_kernel(kind):
+        check(*run_case(WIDE, seed=6, T=T, norm_mode=gmoe.SYNTH_NORM_RANDOM))
 
 
-@pytest.mark.parametrize("T", [1, 8])
-def test_widest_expert_count(T):
-    check(*run_case(WIDEST, seed=7, T=T))
+@pytest.mark.parametrize("T,kind", [(1, "stack"), (1, "rows"), (8, "stack")])
+def test_widest_expert_count(T, kind):
+    with decode_kernel(kind):
+        check(*run_case(WIDEST, seed=7, T=T))
 
 
 @pytest.mark.parametrize("name,T", [("small", 16), ("glm", 8), ("wide", 8)])

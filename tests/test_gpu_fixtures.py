@@ -43,7 +43,7 @@ def check_layer(st, got, g, prefix, what):
 
 @pytest.mark.parametrize("variant", ["base", "tie_nan"])
 @pytest.mark.parametrize("per_token", [False, True])
-def test_layer_against_fixture(golden, variant, per_token):
+def test_layer_against_fixture(golden, dkernel, variant, per_token):
     g = golden
     hl = base_layer()
     if variant == "tie_nan":
@@ -67,7 +67,7 @@ def test_layer_against_fixture(golden, variant, per_token):
         ctx.close()
 
 
-def test_tie_goes_to_the_lower_index_and_nan_is_never_chosen(golden):
+def test_tie_goes_to_the_lower_index_and_nan_is_never_chosen(golden, dkernel):
     """The fixture's own facts, restated on the GPU's routing: experts 3 and 5 tie exactly
     and 3 ranks first, expert 9 (NaN) is never selected."""
     hl = with_ties_and_nan(base_layer())
@@ -85,7 +85,7 @@ def test_tie_goes_to_the_lower_index_and_nan_is_never_chosen(golden):
     assert stats["routing_exact_path"] >= 4  # an exact tie is never certified: the replay decides it
 
 
-def test_routed_off_against_fixture(golden):
+def test_routed_off_against_fixture(golden, dkernel):
     ctx = gmoe.Context(SMALL, n_layers=2, max_tokens=4)
     try:
         ctx.upload(1, base_layer())
@@ -101,7 +101,7 @@ def test_routed_off_against_fixture(golden):
         ctx.close()
 
 
-def test_three_layer_stack_against_fixture(golden):
+def test_three_layer_stack_against_fixture(golden, dkernel):
     """Layers 1-3 (seed 11): the batch through gmoe_forward_layers (grouped path per layer)
     and each token through one persistent launch over the three layers."""
     layers = [gmoe.HostLayer(SMALL, seed=11, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM) for l in (1, 2, 3)]

@@ -9,18 +9,20 @@ import pytest
 
 import gmoe
 import oracle
-from conftest import assert_close
+from conftest import DECODE_KERNEL_NAMES, assert_close, assert_decode_kernel, decode_kernel, launched
 
 pytestmark = pytest.mark.gpu
 
 N_LAYERS = 6
 
 
-@pytest.fixture(scope="module")
-def stack():
+@pytest.fixture(scope="module", params=list(DECODE_KERNEL_NAMES))
+def stack(request):
     shape = gmoe.GLM47_FLASH
     layers = [gmoe.HostLayer(shape, seed=11, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM) for l in range(1, N_LAYERS + 1)]
-    ctx = gmoe.Context(shape, n_layers=N_LAYERS + 1, max_tokens=1)
+    with decode_kernel(request.param):
+        ctx = gmoe.Context(shape, n_layers=N_LAYERS + 1, max_tokens=1)
+    ctx.kind = request.param
     for l, hl in enumerate(layers, start=1):
         ctx.upload(l, hl)
     yield shape, layers, ctx
@@ -30,10 +32,11 @@ def stack():
 def test_one_launch_equals_layer_by_layer(stack):
     shape, layers, ctx = stack
     x0 = gmoe.activations(11, 1, 1, shape.D)
-    print(f"[case] stack {N_LAYERS} layers, one launch vs per-layer", flush=True)
+    print(f"[case] stack {N_LAYERS} layers, one launch vs per-layer ({ctx.kind})", flush=True)
     d_in = gmoe.DeviceArray.from_numpy(x0)
     d_out = gmoe.DeviceArray(x0.nbytes)
-    ctx.forward_layers(1, N_LAYERS, 1, d_in.ptr, d_out.ptr)
+    ran = launched(ctx, lambda: ctx.forward_layers(1, N_LAYERS, 1, d_in.ptr, d_out.ptr))
+    assert_decode_kernel(ran, ctx.kind)
     x_one = d_out.download((1, shape.D), np.float32)
     topk_one = [ctx.read_topk(l, 1)[0] for l in range(1, N_LAYERS + 1)]
     x = x0.copy()

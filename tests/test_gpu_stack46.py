@@ -12,17 +12,19 @@ import pytest
 
 import gmoe
 import oracle
-from conftest import assert_close
+from conftest import DECODE_KERNEL_NAMES, assert_close, assert_decode_kernel, decode_kernel, launched
 
 pytestmark = pytest.mark.gpu
 
 N_LAYERS = 46
 
 
-@pytest.fixture(scope="module")
-def stack46():
+@pytest.fixture(scope="module", params=list(DECODE_KERNEL_NAMES))
+def stack46(request):
     shape = gmoe.GLM47_FLASH
-    ctx = gmoe.Context(shape, n_layers=N_LAYERS + 1, max_tokens=1)
+    with decode_kernel(request.param):
+        ctx = gmoe.Context(shape, n_layers=N_LAYERS + 1, max_tokens=1)
+    ctx.kind = request.param
     layers = []
     for l in range(1, N_LAYERS + 1):
         hl = gmoe.HostLayer(shape, seed=0, layer=l)
@@ -37,10 +39,11 @@ def stack46():
 def test_46_layers_one_launch_against_oracle(stack46):
     shape, layers, ctx = stack46
     x0 = gmoe.activations(0, 0, 1, shape.D)  # the benchmark's input
-    print("[case] 46 layers in one persistent launch", flush=True)
+    print(f"[case] 46 layers in one persistent launch ({ctx.kind})", flush=True)
     d_in = gmoe.DeviceArray.from_numpy(x0)
     d_out = gmoe.DeviceArray(x0.nbytes)
-    ctx.forward_layers(1, N_LAYERS, 1, d_in.ptr, d_out.ptr)
+    ran = launched(ctx, lambda: ctx.forward_layers(1, N_LAYERS, 1, d_in.ptr, d_out.ptr))
+    assert_decode_kernel(ran, ctx.kind)
     x_one = d_out.download((1, shape.D), np.float32)
     topk_one = [ctx.read_topk(l, 1)[0] for l in range(1, N_LAYERS + 1)]
 

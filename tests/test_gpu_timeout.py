@@ -15,7 +15,7 @@ SMALL = gmoe.Shape(dim=256, moe_ffn_dim=256, n_routed_experts=16, n_experts_used
 
 
 @pytest.fixture
-def starved_ctx(monkeypatch):
+def starved_ctx(monkeypatch, dkernel):
     monkeypatch.setenv("GMOE_SPIN_LIMIT", "0")
     ctx = gmoe.Context(SMALL, n_layers=3, max_tokens=1)
     monkeypatch.delenv("GMOE_SPIN_LIMIT")
@@ -50,7 +50,7 @@ def test_device_forward_reports_on_the_next_call(starved_ctx):
     assert "timed out" in gmoe.last_error()
 
 
-def test_normal_context_after_a_failed_one():
+def test_normal_context_after_a_failed_one(dkernel):
     """The failure is per context: a context with the default limit computes normally."""
     ctx = gmoe.Context(SMALL, n_layers=2, max_tokens=1)
     try:

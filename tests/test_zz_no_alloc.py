@@ -3,11 +3,13 @@ the C ABI and compared with gmoe_forward_layers (same kernels, the context's wor
 bit for bit, on two calls in a row, the second over fewer layers; and a run longer than
 the fixed workspace holds is refused before anything is launched."""
 import ctypes as C
+import re
 
 import numpy as np
 import pytest
 
 import gmoe
+from conftest import DECODE_KERNELS, decode_kernel
 
 pytestmark = pytest.mark.gpu
 
@@ -15,9 +17,10 @@ S = gmoe.GLM47_FLASH
 N_UPLOADED = 5
 
 
-@pytest.fixture(scope="module")
-def ctx():
-    c = gmoe.Context(S, n_layers=21, max_tokens=1)
+@pytest.fixture(scope="module", params=list(DECODE_KERNELS))
+def ctx(request):
+    with decode_kernel(request.param):
+        c = gmoe.Context(S, n_layers=21, max_tokens=1)
     for l in range(1, N_UPLOADED + 1):
         c.upload(l, gmoe.HostLayer(S, seed=31, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM))
     yield c
@@ -55,8 +58,10 @@ def test_noalloc_refuses_a_run_longer_than_its_workspace(ctx):
     x0 = gmoe.activations(31, 9, 1, S.D)
     d_in = gmoe.DeviceArray.from_numpy(x0)
     d_out = gmoe.DeviceArray(x0.nbytes)
-    print("[case] noalloc over 20 layers (more than the fixed array holds)", flush=True)
-    rc = noalloc(ctx, 1, 20, d_in, d_out)
+    print("[case] noalloc over 400 layers (more than the fixed array holds)", flush=True)
+    rc = noalloc(ctx, 1, 400, d_in, d_out)
     assert rc == -1
     msg = gmoe.last_error()
-    assert "at most 16 layers" in msg, msg
+    m = re.search(r"at most (\d+) layers", msg)
+    assert m, msg
+    assert N_UPLOADED <= int(m.group(1)) < 400, msg
