@@ -1,23 +1,24 @@
 // decode.h -- the row-owner decode kernel: T=1 through a run of MoE layers in one launch
 // (k_moe_decode), for shapes whose expert items fit the grid (see dk_fits).
 //
-// Each layer (infer.c:1087-1216) is three dependent phases, separated by device-wide flags:
+// Each layer (infer.c:1087-1216) is three dependent phases, separated by device-wide flags
+// (X, H) and the selection entries:
 //
-//  1. x of the layer is complete (flag X). The router finishers turn the layer's router
+//  1. x of the layer is complete (X). The router finishers turn the layer's router
 //     records (below) into each expert's certified selection entry (router.h), while every
 //     block with an expert item computes xn and its digit form from x itself (the rmsnorm of
 //     infer.c:746-752, bit-identical).
 //  2. Every block takes the top-k from the entries (the certified selection, or the exact
 //     replay's result). Expert items -- 16 rows of gate and up of one expert, K routed slots
 //     and the shared expert -- form h = silu(g) * u for their rows and publish it in digit
-//     form; the last one sets flag H. The shared expert's weights are requested before x
-//     exists, the routed ones right after the selection.
-//  3. Every block owns DK_ROWS consecutive rows of D. With the routing known it requests
-//     those rows of each selected expert's down matrix into registers; after H it reads h,
-//     forms its rows of y for every slot (int8 dot4 on h's digits), the residual combine
+//     form, and arrives on H. The shared expert's weights are requested before x exists, the
+//     routed ones right after the selection.
+//  3. Every block owns DK_ROWS consecutive rows of D. With the routing known (a block with a
+//     routed item: once its h is out) it requests those rows of each selected expert's down
+//     matrix into shared memory; after H it reads h, forms its rows of y for every slot
+//     (int8 dot4 on h's digits), the residual combine
 //     x' = x + (shared + sum_k w_k y_k) (infer.c:1192, 1212-1214), and from x' and the next
-//     layer's router and norm rows that layer's router record. The last owner sets the next
-//     layer's X.
+//     layer's router and norm rows that layer's router record, and arrives on X.
 //
 // Router records. glm.c's logit is a sequential fp32 chain over p_i = g_i * xn_i with
 // xn_i = fl(fl(x_i * inv) * w_i) (infer.c:746-752, 916-925). Since inv is one scalar, the
@@ -32,10 +33,12 @@
 // with nu_e = sum |g_i| (|w_i| + 1), computed at upload.
 //
 // Signalling is stack.h's: write-through stores, counters nobody polls, a write-once flag
-// per layer and phase, bounded waits that set the error flag instead of hanging. Every
-// wait is on work of the same layer or the one before that other blocks produce without
-// waiting on the waiter, and all blocks are resident (one block per SIMD pair), so the
-// schedule cannot deadlock.
+// per layer and phase (X, H), bounded waits that set the error flag instead of hanging.
+// Every wait is on work of the same layer or the one before that other blocks produce
+// without waiting on the waiter, and all blocks are resident (one block per SIMD pair), so
+// the schedule cannot deadlock. (Arrivals without the returned count, with every waiter
+// polling all first-level counters, were slower: 512 blocks polling 16 lines each turn
+// those lines into hot spots that the increments queue behind.)
 #pragma once
 
 #include "stack.h"
@@ -46,8 +49,8 @@
 #define DK_RC_MAX (GM_MAX_E / 64)
 
 // per-layer flags (SKF slots) and counters (SKC) of this kernel
-enum { DKF_SEL = SKF_SEL, DKF_SELW = SKF_SELW, DKF_H = 2, DKF_X = 3 };
-enum { DKC_H = SKC_PART, DKC_H2 = SKC_PART2, DKC_X = SKC_X, DKC_X2 = SKC_X2 };
+enum { DKF_SEL = SKF_SEL, DKF_SELW = SKF_SELW, DKF_X = 3 };
+enum { DKC_X = SKC_X, DKC_X2 = SKC_X2 };
 
 // Router record of one owner piece and expert (16 bytes): fp64 sum of t_i over the piece's
 // rows, and upper bounds of the sums of |partial sums| and |t_i|, rounded up to fp32.
@@ -430,8 +433,10 @@ __device__ __attribute__((always_inline)) static void dk_item_load(const StackAr
 
 // Item (slot, j) of layer li: gate and up rows 16j..16j+15 dotted with xn's digits
 // (gu_products_r), h = silu(g) * u (infer.c:1184-1188, 1199-1202) for those rows, stored
-// as its digit form with one exponent (DK_HREC bytes). An idle item (no expert in the slot)
-// only counts its arrival.
+// as its digit form with one exponent: the h record (DK_HREC bytes), 16 dwords of three
+// digit bytes each under a marker byte, exponent + 128. The launch starts with the records
+// zeroed, so a reader knows a dword has arrived when it is nonzero: no count, no flag. An
+// idle item (no expert in the slot) writes nothing, and nobody reads its record.
 __device__ __attribute__((always_inline)) static void dk_item(const StackArgs &a, int li, int slot, int j, bool live,
                                                               const DkItem &it, SkShared &sh) {
     const int D = a.D, NPF = a.F >> 4, tid = phase_tid(), lane = tid & 63, w = tid >> 6, m = lane & 15;
@@ -458,33 +463,39 @@ __device__ __attribute__((always_inline)) static void dk_item(const StackArgs &a
             const float g = ldexpf(((sh.u.g.part[0][0][r] + sh.u.g.part[1][0][r]) + sh.u.g.part[2][0][r]) + sh.u.g.part[3][0][r], xe);
             const float u = ldexpf(((sh.u.g.part[0][1][r] + sh.u.g.part[1][1][r]) + sh.u.g.part[2][1][r]) + sh.u.g.part[3][1][r], xe);
             const float h = g / (1.0f + expf(-g)) * u;
-            const int ex = digit_exponent(row_max_dpp_f(fabsf(h)));  // lanes 0..15: the item's rows
+            int ex = digit_exponent(row_max_dpp_f(fabsf(h)));  // lanes 0..15: the item's rows
+            ex = ex < -127 ? -127 : ex;  // the marker's range (below 2^-150, the values are lost anyway)
             int8_t d0, d1, d2;
             split_digits(h, ex, &d0, &d1, &d2);
-            int8_t *hb = (int8_t *)sh.hrec;  // 48 bytes of digits, then the exponent and zeros
+            uint8_t *hb = (uint8_t *)sh.hrec;  // the 48 digit bytes: rows 0..15 of digit 0, 1, 2
             if (lane < 16) {
-                hb[lane] = d0;
-                hb[16 + lane] = d1;
-                hb[32 + lane] = d2;
-            } else if (lane < 20) {
-                ((int *)hb)[12 + (lane - 16)] = lane == 16 ? ex : 0;
+                hb[lane] = (uint8_t)d0;
+                hb[16 + lane] = (uint8_t)d1;
+                hb[32 + lane] = (uint8_t)d2;
             }
+            asm volatile("" ::: "memory");  // one wave's shared-memory operations complete in order
             if (lane < 8) {
+                // word `lane`: digit bytes 6 lane .. 6 lane + 5, three to a dword, each dword
+                // topped by the marker (ex + 128, never 0)
+                const unsigned mk = (unsigned)(ex + 128) << 24;
+                const uint8_t *bp = hb + 6 * lane;
+                const unsigned lo = (unsigned)bp[0] | ((unsigned)bp[1] << 8) | ((unsigned)bp[2] << 16) | mk;
+                const unsigned hi = (unsigned)bp[3] | ((unsigned)bp[4] << 8) | ((unsigned)bp[5] << 16) | mk;
                 unsigned long long *dst = (unsigned long long *)(ws_at<uint8_t>(a, li, a.o.h) + (size_t)(slot * NPF + j) * DK_HREC);
-                st_u64(dst + lane, ((const unsigned long long *)hb)[lane]);
+                st_u64(dst + lane, (unsigned long long)lo | ((unsigned long long)hi << 32));
             }
         }
     }
-    dk_arrive(a, DKC_H, DKC_H2, slot * NPF + j, (unsigned)((a.K + 1) * NPF / SK_NPART), li, &a.ctr[SKF(li, DKF_H)]);
     dk_stamp(sh, 12);
 }
 
 // ---------------------------------------------------------------- down projection, combine
 //
 // The owner's down pairs: pair pi = (slot pi / (F/16), slice pi % (F/16)) holds the
-// slice's 16 weights of rows r0..r0+3 (64 contiguous bytes in the slice layout of
-// common.h), staged in shared memory at sh.dslice[4 pi + i] by DMA that the compiler does
-// not count (so that no wait of the layer's expert item includes them). Thread t computes
+// slice's 16 weights of rows r0..r0+3 (64 contiguous bytes; the row-group layout of
+// common.h puts an owner's slices of one matrix in a row), staged in shared memory at
+// sh.dslice[4 pi + i] by DMA that the compiler does not count (so that no wait of the
+// layer's expert item includes them). Thread t computes
 // pairs t + 256 k; sc[k] holds their four rows' fp16 scales of the slice's 32-column block.
 // pi / NPF for pair indices pi < 2^12 and NPF <= 128, by a float product: the quotient's
 // fractional part lies in [1/(2 NPF), 1 - 1/(2 NPF)] after adding 1/2, far above the
@@ -500,7 +511,7 @@ struct DkDown {
 __device__ __attribute__((always_inline)) static void dk_down_load(const StackArgs &a, const StackLayer &L, int r0,
                                                                    bool routed_on, const int *idx, SkShared &sh,
                                                                    DkDown &dd) {
-    const int D = a.D, K = a.K, NPF = a.F >> 4, NPAIR = (K + 1) * NPF, tid = phase_tid();
+    const int K = a.K, NPF = a.F >> 4, NPAIR = (K + 1) * NPF, tid = phase_tid();
     const int lane = tid & 63;
     // piece z = 4 pi + i of the layer's pairs; DMA chunk c covers pieces 64c..64c+63, which
     // lie in one slot (a slot has F/256 chunks). Of the at most DK_PAIRS * SK_BLOCK / 16
@@ -519,9 +530,9 @@ __device__ __attribute__((always_inline)) static void dk_down_load(const StackAr
         if (c < nch) {
             const int e = s == K ? a.E : (routed_on ? idx[s] : -1);
             if (e >= 0) {
-                const uint8_t *base = L.experts + (size_t)e * a.stride;
-                const int j = 16 * cr + (lane >> 2), i = lane & 3;
-                dma16_untracked(gbl((const u32x4 *)(base + a.off_dq)) + (size_t)j * D + r0 + i,
+                // the chunk's 16 slices of the owner's 4 rows: 1 KB in a row (row-group layout)
+                const uint8_t *base = L.experts + (size_t)e * a.stride + a.off_rq;
+                dma16_untracked(gbl((const u32x4 *)base) + ((size_t)(r0 >> 2) * NPF + 16 * cr) * 4 + lane,
                                 (lds_void *)(sh.dslice + 64 * c));
             }
         }
@@ -538,8 +549,8 @@ __device__ __attribute__((always_inline)) static void dk_down_load(const StackAr
     for (int k = 0; k < DK_PAIRS; k++) {
         const int pi = tid + SK_BLOCK * k, pc = pi < NPAIR ? pi : 0, s = dk_slot(pc, rnpf), j = pc - s * NPF;
         const int ei = s == K ? a.E : (routed_on ? idx[s] : -1);
-        const uint8_t *base = L.experts + (size_t)(ei >= 0 ? ei : a.E) * a.stride;
-        dd.sc[k] = *gbl((const unsigned long long *)(base + a.off_ds + ((size_t)(j >> 1) * D + r0) * 2));
+        const uint8_t *base = L.experts + (size_t)(ei >= 0 ? ei : a.E) * a.stride + a.off_rs;
+        dd.sc[k] = *gbl((const unsigned long long *)base + (size_t)(r0 >> 2) * (a.F >> 5) + (j >> 1));
     }
 }
 
@@ -555,81 +566,134 @@ __device__ __attribute__((always_inline)) static bool dk_down(const StackArgs &a
     // builtin, which the compiler sees (after an asm wait it would still count the loads as
     // pending and wait for them again at the next write of their registers)
     __builtin_amdgcn_s_waitcnt(GM_WAIT_VM0);
-    if (!wait_ge(&a.ctr[SKF(li, DKF_H)], 1u, a.error, sh)) return false;
-    dk_stamp(sh, 6);
+    dk_stamp(sh, 13);
     if (routed_on && !sh.sel_ok) dk_stamp(sh, 11);
     if (routed_on && !sh.sel_ok && !sk_read_weights(a, li, sh)) return false;
-    const uint8_t *hbase = ws_at<uint8_t>(a, li, a.o.h);
-    u32x4 hr[DK_PAIRS][4];
-    bool live[DK_PAIRS];
+    // the h records of the live pairs, polled until every dword has its marker (coherent
+    // 8-byte loads: a record's words arrive in any order, each one whole)
+    const unsigned long long *hbase = ws_at<unsigned long long>(a, li, a.o.h);
+    unsigned long long hw[DK_PAIRS][8];
+    bool live[DK_PAIRS], need[DK_PAIRS];
 #pragma unroll
     for (int k = 0; k < DK_PAIRS; k++) {
         const int pi = tid + SK_BLOCK * k, s = dk_slot(pi, rnpf);
         live[k] = pi < NPAIR && (s == K || (routed_on && sh.idx[s] >= 0));
-        const GM_GLOBAL u32x4 *hp = gbl((const u32x4 *)(hbase + (size_t)(pi < NPAIR ? pi : 0) * DK_HREC));
+        need[k] = live[k];
 #pragma unroll
-        for (int c = 0; c < 4; c++) hr[k][c] = live[k] ? hp[c] : u32x4{0u, 0u, 0u, 0u};
+        for (int c = 0; c < 8; c++) hw[k][c] = 0ull;
     }
-    float *red = sh.xn_r;  // [NS][4 rows][NPF] (xn's digits are no longer needed)
+    {
+        unsigned spins = 0;
+        bool alive = true;
+        for (;;) {
+            bool miss = false;
+#pragma unroll
+            for (int k = 0; k < DK_PAIRS; k++) {
+                if (need[k]) {
+                    const unsigned long long *hp = hbase + (size_t)(tid + SK_BLOCK * k) * (DK_HREC / 8);
+                    bool full = true;
+#pragma unroll
+                    for (int c = 0; c < 8; c++) {
+                        hw[k][c] = __hip_atomic_load(hp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        full &= (unsigned)hw[k][c] != 0u && (unsigned)(hw[k][c] >> 32) != 0u;
+                    }
+                    need[k] = !full;
+                    miss |= !full;
+                }
+            }
+            if (__ballot(miss) == 0) break;
+            if (__hip_atomic_load(a.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || ++spins > sh.spin_limit) {
+                if ((tid & 63) == 0) __hip_atomic_store(a.error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                alive = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (!alive) sh.ok = 0;  // a write of 0 by any wave; read after the barrier
+        dk_stamp(sh, 6);
+        __syncthreads();
+        if (!sh.ok) return false;
+    }
+    // digit ints q = 0..11 (bytes 4q..4q+3 of the 48-byte stream, byte n in dword n / 3 at
+    // n % 3) from the record's dwords; the exponent from any marker
+    u32x4 hr[DK_PAIRS][4];
 #pragma unroll
     for (int k = 0; k < DK_PAIRS; k++) {
-        const int pi = tid + SK_BLOCK * k, s = dk_slot(pi, rnpf), j = pi - s * NPF;
-        if (pi < NPAIR) {
-            const int hexp = (int)hr[k][3].x;
-            const int hd[3][4] = {{(int)hr[k][0].x, (int)hr[k][0].y, (int)hr[k][0].z, (int)hr[k][0].w},
-                                  {(int)hr[k][1].x, (int)hr[k][1].y, (int)hr[k][1].z, (int)hr[k][1].w},
-                                  {(int)hr[k][2].x, (int)hr[k][2].y, (int)hr[k][2].z, (int)hr[k][2].w}};
+        unsigned dw[16];
 #pragma unroll
-            for (int i = 0; i < DK_ROWS; i++) {
-                float v = 0.0f;
-                if (live[k]) {
-                    const u32x4 dq = sh.dslice[4 * pi + i];
-                    const int wq[4] = {(int)dq.x, (int)dq.y, (int)dq.z, (int)dq.w};
-                    int acc[3];
+        for (int c = 0; c < 8; c++) {
+            dw[2 * c] = (unsigned)hw[k][c];
+            dw[2 * c + 1] = (unsigned)(hw[k][c] >> 32);
+        }
+        unsigned q4[12];
 #pragma unroll
-                    for (int d = 0; d < 3; d++) {
-                        int sacc = 0;
+        for (int q = 0; q < 12; q++) {
+            const int d0 = (4 * q) / 3;
+            unsigned sel = 0;
 #pragma unroll
-                        for (int q = 0; q < 4; q++) sacc = __builtin_amdgcn_sdot4(wq[q], hd[d][q], sacc, false);
-                        acc[d] = sacc;
-                    }
-                    const unsigned short sc16 = (unsigned short)(dd.sc[k] >> (16 * i));
-                    v = digits_to_float(acc[0], acc[1], acc[2]) * ldexpf(__half2float(__ushort_as_half(sc16)), hexp);
-                }
-                red[(s * DK_ROWS + i) * NPF + j] = v;
+            for (int t = 0; t < 4; t++) {
+                const int n = 4 * q + t;
+                sel |= (unsigned)((n / 3 == d0 ? 0 : 4) + n % 3) << (8 * t);
             }
+            q4[q] = __builtin_amdgcn_perm(dw[d0 + 1 < 16 ? d0 + 1 : 15], dw[d0], sel);
+        }
+        hr[k][0] = u32x4{q4[0], q4[1], q4[2], q4[3]};
+        hr[k][1] = u32x4{q4[4], q4[5], q4[6], q4[7]};
+        hr[k][2] = u32x4{q4[8], q4[9], q4[10], q4[11]};
+        hr[k][3] = u32x4{(unsigned)((int)(dw[0] >> 24) - 128), 0u, 0u, 0u};
+    }
+    // v[k][i]: pair tid + 256 k's product for row i (0 for a dead pair or none); the sums
+    // over each 16 consecutive pairs (within one slot: F/16 is a multiple of 16) by DPP, into
+    // gsum[i][g] for pair group g (xn's digits in sh.xn_r are no longer needed)
+    const int NG = NPAIR / 16;
+    float *gsum = sh.xn_r;
+#pragma unroll
+    for (int k = 0; k < DK_PAIRS; k++) {
+        const int pi = tid + SK_BLOCK * k;
+        const int hexp = (int)hr[k][3].x;
+        const int hd[3][4] = {{(int)hr[k][0].x, (int)hr[k][0].y, (int)hr[k][0].z, (int)hr[k][0].w},
+                              {(int)hr[k][1].x, (int)hr[k][1].y, (int)hr[k][1].z, (int)hr[k][1].w},
+                              {(int)hr[k][2].x, (int)hr[k][2].y, (int)hr[k][2].z, (int)hr[k][2].w}};
+        float v[DK_ROWS];
+#pragma unroll
+        for (int i = 0; i < DK_ROWS; i++) {
+            v[i] = 0.0f;
+            if (live[k]) {
+                const u32x4 dq = sh.dslice[4 * pi + i];
+                const int wq[4] = {(int)dq.x, (int)dq.y, (int)dq.z, (int)dq.w};
+                int acc[3];
+#pragma unroll
+                for (int d = 0; d < 3; d++) {
+                    int sacc = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sacc = __builtin_amdgcn_sdot4(wq[q], hd[d][q], sacc, false);
+                    acc[d] = sacc;
+                }
+                const unsigned short sc16 = (unsigned short)(dd.sc[k] >> (16 * i));
+                v[i] = digits_to_float(acc[0], acc[1], acc[2]) * ldexpf(__half2float(__ushort_as_half(sc16)), hexp);
+            }
+            v[i] = row_sum_dpp_f(v[i]);
+        }
+        if ((pi & 15) == 0 && pi < NPAIR) {
+#pragma unroll
+            for (int i = 0; i < DK_ROWS; i++) gsum[i * NG + (pi >> 4)] = v[i];
         }
     }
     __syncthreads();
     dk_stamp(sh, 19);
-    // y[s][i] = sum over the slices in order, in segments of 8
-    const int nseg = NPF / 8, ntask = NS * DK_ROWS * nseg;
-    float *seg = (float *)sh.sc_gu;  // segment sums, then y [NS][4]
-    for (int t = tid; t < ntask; t += SK_BLOCK) {
-        const float *src = red + (t / nseg) * NPF + (t % nseg) * 8;
-        float s = src[0];
-#pragma unroll
-        for (int u = 1; u < 8; u++) s += src[u];
-        seg[t] = s;
-    }
-    __syncthreads();
-    float *y = seg + ntask;
-    for (int t = tid; t < NS * DK_ROWS; t += SK_BLOCK) {
-        const float *src = seg + t * nseg;
-        float s = src[0];
-        for (int u = 1; u < nseg; u++) s += src[u];
-        y[t] = s;
-    }
-    __syncthreads();
     if (tid < DK_ROWS) {
-        const int i = tid, r = r0 + i;
-        float acc = 0.0f;
-        if (routed_on) {
-#pragma unroll
-            for (int k = 0; k < GM_MAX_K; k++)
-                if (k < K && sh.idx[k] >= 0) acc = __fadd_rn(acc, __fmul_rn(sh.ws[k], y[k * DK_ROWS + i]));
+        // y[s][i] = the slot's group sums in order; x' = x + (shared + sum_k w_k y_k)
+        const int i = tid, r = r0 + i, gps = NPF / 16;
+        const float *g = gsum + i * NG;
+        float acc = 0.0f, shv = 0.0f;
+        for (int s = 0; s < NS; s++) {
+            float y = g[s * gps];
+            for (int u = 1; u < gps; u++) y += g[s * gps + u];
+            if (s == K)
+                shv = y;
+            else if (routed_on && sh.idx[s] >= 0)
+                acc = __fadd_rn(acc, __fmul_rn(sh.ws[s], y));
         }
-        const float shv = y[K * DK_ROWS + i];
         const float xo = __fadd_rn(xr, __fadd_rn(shv, acc));
         if (li == a.n_layers - 1) {
             st_f(a.x_out + r, xo);
@@ -928,10 +992,15 @@ __device__ __attribute__((always_inline)) static bool dk_run(const StackArgs &a,
         dk_stamp(sh, 3);
         const bool item_live = routed_on && routed_item && sh.idx[slot] >= 0;
         if (item_live) dk_item_load(a, L, sh.idx[slot], jp, it);
-        if (owner) dk_down_load(a, L, r0, routed_on, sh.idx, sh, dd);
-        __builtin_amdgcn_sched_barrier(0);  // every weight request of the layer issued before the products
+        // an owner with a routed item requests its down rows after the item's products: the
+        // gate/up weights that every item waits for then have the memory system to themselves
+        if (owner && !routed_item) dk_down_load(a, L, r0, routed_on, sh.idx, sh, dd);
+        __builtin_amdgcn_sched_barrier(0);  // every weight request issued before the products
         dk_stamp(sh, 4);
-        if (routed_item) dk_item(a, li, slot, jp, item_live, it, sh);
+        if (routed_item) {
+            dk_item(a, li, slot, jp, item_live, it, sh);
+            if (owner) dk_down_load(a, L, r0, routed_on, sh.idx, sh, dd);
+        }
         if (owner) {
             // the next layer's router rows and this layer's x rows, fetched while the items finish
             DkRouter rr;

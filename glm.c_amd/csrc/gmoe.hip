@@ -95,6 +95,7 @@ struct gmoe_ctx {
     gmoe_config cfg{};
     int D = 0, F = 0, E = 0, K = 0, S = 0, L = 0, Tmax = 0;
     size_t stride = 0, off_gq = 0, off_uq = 0, off_dq = 0, off_gs = 0, off_us = 0, off_ds = 0;
+    size_t off_rq = 0, off_rs = 0;  // down in the row-group layout (decode_rows only)
     LayerDev *layers = nullptr;
 
     float *xn = nullptr, *router_prob = nullptr, *topk_w = nullptr, *topk_ws = nullptr;
@@ -340,6 +341,12 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
                              per_cu_dk >= want && dk_fits(c->stack_grid, c->D, c->F, c->E, c->K);
         }
     }
+    if (c->decode_rows) {
+        // each expert also holds its down matrix in the row-group layout, after the rest
+        c->off_rq = c->stride;
+        c->off_rs = c->off_rq + qb;
+        c->stride = (c->off_rs + sb + 255) & ~(size_t)255;
+    }
     {
         // per-layer regions of the persistent kernel, each buffer on its own 256-byte lines
         size_t off = 0;
@@ -407,8 +414,23 @@ static int copy_in(void *dst, const void *src, size_t bytes) {
 
 // Upload n_mat raw matrices (rows x cols int8 + fp32 scales) and repack them to
 // dst + m*dst_stride (+off_q for q, +off_s for scales).
+static void repack_staged(gmoe_ctx *c, int n_mat, int rows, int cols, uint8_t *dst, size_t dst_stride, size_t off_q,
+                          size_t off_s, int layout, unsigned long long *inexact_dev) {
+    const size_t qbytes = (size_t)n_mat * rows * cols;
+    const size_t units = qbytes / 16;
+    hipLaunchKernelGGL(k_repack_q, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, 0,
+                       (const int8_t *)c->staging, dst + off_q, dst_stride, rows, cols, n_mat, layout);
+    const size_t ns = (size_t)n_mat * rows * (cols / GM_QBLOCK);
+    hipLaunchKernelGGL(k_repack_s, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, 0,
+                       (const float *)(c->staging + qbytes), dst + off_s, dst_stride, rows, cols, n_mat, layout,
+                       inexact_dev);
+}
+
+// Copies n_mat matrices to the staging buffer and repacks them into `layout`; with
+// layout2 >= 0 also into layout2 at off_q2 / off_s2 (scales counted once).
 static int upload_matrices(gmoe_ctx *c, const int8_t *q, const float *s, int n_mat, int rows, int cols, uint8_t *dst,
-                           size_t dst_stride, size_t off_q, size_t off_s, int layout, unsigned long long *inexact_dev) {
+                           size_t dst_stride, size_t off_q, size_t off_s, int layout, unsigned long long *inexact_dev,
+                           int layout2 = -1, size_t off_q2 = 0, size_t off_s2 = 0) {
     const size_t qbytes = (size_t)n_mat * rows * cols;
     const size_t sbytes = (size_t)n_mat * rows * (cols / GM_QBLOCK) * sizeof(float);
     if (qbytes + sbytes > c->staging_bytes) {
@@ -422,13 +444,8 @@ static int upload_matrices(gmoe_ctx *c, const int8_t *q, const float *s, int n_m
     if (rc) return rc;
     rc = copy_in(c->staging + qbytes, s, sbytes);
     if (rc) return rc;
-    const size_t units = qbytes / 16;
-    hipLaunchKernelGGL(k_repack_q, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, 0,
-                       (const int8_t *)c->staging, dst + off_q, dst_stride, rows, cols, n_mat, layout);
-    const size_t ns = sbytes / sizeof(float);
-    hipLaunchKernelGGL(k_repack_s, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, 0,
-                       (const float *)(c->staging + qbytes), dst + off_s, dst_stride, rows, cols, n_mat, layout,
-                       inexact_dev);
+    repack_staged(c, n_mat, rows, cols, dst, dst_stride, off_q, off_s, layout, inexact_dev);
+    if (layout2 >= 0) repack_staged(c, n_mat, rows, cols, dst, dst_stride, off_q2, off_s2, layout2, nullptr);
     HIP_OK(hipGetLastError());
     HIP_OK(hipDeviceSynchronize());
     return GMOE_OK;
@@ -481,12 +498,15 @@ extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weight
     const int P = GM_LAYOUT_PANELS, S = GM_LAYOUT_SLICES;  // gate/up in row panels, down in column slices
     rc = upload_matrices(c, w->gate_sh_q, w->gate_sh_s, 1, F, D, sh, c->stride, c->off_gq, c->off_gs, P, inexact);
     if (!rc) rc = upload_matrices(c, w->up_sh_q, w->up_sh_s, 1, F, D, sh, c->stride, c->off_uq, c->off_us, P, inexact);
-    if (!rc) rc = upload_matrices(c, w->down_sh_q, w->down_sh_s, 1, D, F, sh, c->stride, c->off_dq, c->off_ds, S, inexact);
+    const int R = c->decode_rows ? GM_LAYOUT_ROWGROUPS : -1;
+    if (!rc) rc = upload_matrices(c, w->down_sh_q, w->down_sh_s, 1, D, F, sh, c->stride, c->off_dq, c->off_ds, S, inexact,
+                                  R, c->off_rq, c->off_rs);
     if (has_routed) {
         uint8_t *ex = L.experts;
         if (!rc) rc = upload_matrices(c, w->gate_q, w->gate_s, E, F, D, ex, c->stride, c->off_gq, c->off_gs, P, inexact);
         if (!rc) rc = upload_matrices(c, w->up_q, w->up_s, E, F, D, ex, c->stride, c->off_uq, c->off_us, P, inexact);
-        if (!rc) rc = upload_matrices(c, w->down_q, w->down_s, E, D, F, ex, c->stride, c->off_dq, c->off_ds, S, inexact);
+        if (!rc) rc = upload_matrices(c, w->down_q, w->down_s, E, D, F, ex, c->stride, c->off_dq, c->off_ds, S, inexact,
+                                      R, c->off_rq, c->off_rs);
     }
     unsigned long long n_inexact = 0;
     if (!rc && hipMemcpy(&n_inexact, inexact, sizeof(n_inexact), hipMemcpyDeviceToHost) != hipSuccess) {
@@ -640,6 +660,8 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.off_gs = c->off_gs;
     a.off_us = c->off_us;
     a.off_ds = c->off_ds;
+    a.off_rq = c->off_rq;
+    a.off_rs = c->off_rs;
     a.ws = sp.ws;
     a.ws_layer_bytes = c->sk_ws_layer;
     a.o = c->sk_o;
@@ -672,6 +694,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         a.n_router = c->decode_rows ? dk_finishers(c->stack_grid, c->E, c->K, c->F) : nr;
         a.shared_blocks = nsb;
     }
+    a.h_words = c->decode_rows ? (c->K + 1) * (c->F / 16) * DK_HREC / 8 : 0;
     if (c->sk_trace_on && !space) {
         // k_moe_stack: its work items; k_moe_decode: one item per (layer, block)
         const size_t items = c->decode_rows ? (size_t)c->stack_grid * n

@@ -111,6 +111,7 @@ struct StackArgs {
     int D, F, E, K, flags;
     float eps, routed_scale;
     size_t stride, off_gq, off_uq, off_dq, off_gs, off_us, off_ds;  // down in the column-slice layout
+    size_t off_rq, off_rs;     // down in the row-group layout (k_moe_decode only)
     uint8_t *ws;               // per-layer workspace base
     size_t ws_layer_bytes;
     StackWs o;
@@ -132,6 +133,7 @@ struct StackArgs {
     unsigned long long *trace; // optional: SK_TRACE_STAMPS timestamps per item (see k_moe_stack)
     int n_router;              // router blocks: a power of two, <= min(E, 64)
     int shared_blocks;         // blocks in the shared-expert role
+    int h_words;               // 8-byte words of each layer's h records, zeroed before the launch (decode.h; 0 otherwise)
 };
 
 template <typename T>
@@ -1102,6 +1104,8 @@ __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, 
     }
     unsigned long long *stage = ws_at<unsigned long long>(a, li, a.o.stage);
     for (int i = tid; i < SK_STAGE_COPIES * SK_STAGE_COPY_WORDS; i += SK_BLOCK) stage[i] = SK_UNSET;
+    unsigned long long *h = ws_at<unsigned long long>(a, li, a.o.h);
+    for (int i = tid; i < a.h_words; i += SK_BLOCK) h[i] = 0ull;
 }
 
 // Block roles: the first n_router blocks route, and router blocks 1.. then take the shared
