@@ -29,6 +29,7 @@
 #include "dispatch.h"
 #include "experts.h"
 #include "grouped.h"
+#include "native.h"
 #include "repack.h"
 #include "router.h"
 #include "stack.h"
@@ -122,6 +123,7 @@ struct gmoe_ctx {
     int stack_ok = 0;            // shape fits k_moe_stack
     int stack_grid = 0;          // co-resident blocks
     int decode_rows = 0;         // T=1 runs k_moe_decode (decode.h) rather than k_moe_stack
+    int native = 0;              // GMOE_Q8_NATIVE: checkpoint layout, fp32 scales, native.h kernels
     uint8_t *sk_ws = nullptr;    // per-layer workspace, L regions of sk_ws_layer bytes
     size_t sk_ws_layer = 0;
     StackWs sk_o{};
@@ -236,8 +238,19 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
                 g.n_shared_experts);
         return GMOE_ERR_INVALID;
     }
-    if (g.group_size != GM_QBLOCK) {
-        set_err("gmoe_create: group_size must be %d (got %d)", GM_QBLOCK, g.group_size);
+    if (g.q8_form != GMOE_Q8_AUTO && g.q8_form != GMOE_Q8_TILED && g.q8_form != GMOE_Q8_NATIVE) {
+        set_err("gmoe_create: q8_form %d is not a GMOE_Q8_* value", g.q8_form);
+        return GMOE_ERR_INVALID;
+    }
+    const bool native = g.q8_form == GMOE_Q8_NATIVE || (g.q8_form == GMOE_Q8_AUTO && g.group_size != GM_QBLOCK);
+    if (!native && g.group_size != GM_QBLOCK) {
+        set_err("gmoe_create: the tiled form needs group_size %d (got %d); GMOE_Q8_NATIVE takes other sizes",
+                GM_QBLOCK, g.group_size);
+        return GMOE_ERR_INVALID;
+    }
+    if (native && (g.group_size < 16 || g.group_size % 16 || g.dim % g.group_size || g.moe_ffn_dim % g.group_size)) {
+        set_err("gmoe_create: the native form needs a group_size that is a multiple of 16 and divides dim and "
+                "moe_ffn_dim (got %d)", g.group_size);
         return GMOE_ERR_INVALID;
     }
     if (g.n_layers < 2 || g.max_tokens < 1 || g.max_tokens > 65535) {
@@ -273,6 +286,15 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     c->off_us = 3 * qb + sb;
     c->off_ds = 3 * qb + 2 * sb;
     c->stride = (3 * qb + 3 * sb + 255) & ~(size_t)255;
+    if (native) {
+        // glm.c's layout per expert: gate, up, down int8 rows, then their fp32 scales
+        const size_t sn = qb / (size_t)g.group_size * sizeof(float);
+        c->native = 1;
+        c->off_gs = 3 * qb;
+        c->off_us = 3 * qb + sn;
+        c->off_ds = 3 * qb + 2 * sn;
+        c->stride = (3 * qb + 3 * sn + 255) & ~(size_t)255;
+    }
     c->layers = new LayerDev[c->L];
 
     const size_t T = c->Tmax, D = c->D, F = c->F, E = c->E, K = c->K, NS = c->K + c->S;
@@ -318,7 +340,8 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     // shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots. k_moe_stack
     // stages a combine chunk's partials, F/16 x (K+1) x 8 floats, in the slice buffer;
     // k_moe_decode (decode.h) runs shapes whose expert items and router finishers fit its grid.
-    c->stack_ok = c->L <= SK_MAX_LAYERS && (size_t)(F / 16) * (K + 1) * SK_CROWS * sizeof(float) <= sizeof(SkShared::dslice);
+    c->stack_ok = !c->native && c->L <= SK_MAX_LAYERS &&
+                  (size_t)(F / 16) * (K + 1) * SK_CROWS * sizeof(float) <= sizeof(SkShared::dslice);
     if (const char *g_env = getenv("GMOE_GROUPED_MIN_T")) c->grouped_min_t = atoi(g_env) > 1 ? atoi(g_env) : 2;
     const char *env = getenv("GMOE_STACK_KERNEL");
     if (env && env[0] == '0') c->stack_ok = 0;
@@ -495,6 +518,34 @@ extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weight
     if (dev_alloc(&inexact, 1) != GMOE_OK) return GMOE_ERR_NOMEM;
     HIP_OK(hipMemset(inexact, 0, sizeof(unsigned long long)));
     uint8_t *sh = L.experts + (size_t)E * c->stride;
+    if (c->native) {
+        // the checkpoint's matrices and scales as they are, one expert per stride
+        const int gs = c->cfg.group_size;
+        const size_t qb = (size_t)F * D, sn = qb / gs * sizeof(float);
+        struct {
+            const void *src;
+            size_t off, bytes;
+            int n;
+            uint8_t *dst;
+        } parts[] = {{w->gate_sh_q, c->off_gq, qb, 1, sh},         {w->up_sh_q, c->off_uq, qb, 1, sh},
+                     {w->down_sh_q, c->off_dq, qb, 1, sh},         {w->gate_sh_s, c->off_gs, sn, 1, sh},
+                     {w->up_sh_s, c->off_us, sn, 1, sh},           {w->down_sh_s, c->off_ds, sn, 1, sh},
+                     {w->gate_q, c->off_gq, qb, E, L.experts},     {w->up_q, c->off_uq, qb, E, L.experts},
+                     {w->down_q, c->off_dq, qb, E, L.experts},     {w->gate_s, c->off_gs, sn, E, L.experts},
+                     {w->up_s, c->off_us, sn, E, L.experts},       {w->down_s, c->off_ds, sn, E, L.experts}};
+        for (auto &pt : parts) {
+            if (pt.n == E && !has_routed) continue;
+            if (hipMemcpy2D(pt.dst + pt.off, c->stride, pt.src, pt.bytes, pt.bytes, pt.n, hipMemcpyHostToDevice) != hipSuccess) {
+                set_err("gmoe_upload_layer: copy of layer %d failed", layer);
+                dev_free(inexact);
+                return GMOE_ERR_HIP;
+            }
+        }
+        dev_free(inexact);
+        L.uploaded = 1;
+        L.has_routed = has_routed;
+        return GMOE_OK;
+    }
     const int P = GM_LAYOUT_PANELS, S = GM_LAYOUT_SLICES;  // gate/up in row panels, down in column slices
     rc = upload_matrices(c, w->gate_sh_q, w->gate_sh_s, 1, F, D, sh, c->stride, c->off_gq, c->off_gs, P, inexact);
     if (!rc) rc = upload_matrices(c, w->up_sh_q, w->up_sh_s, 1, F, D, sh, c->stride, c->off_uq, c->off_us, P, inexact);
@@ -818,7 +869,44 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
     prof_end(pr, st);
     const int routed_on = !(fl & GMOE_FLAG_NO_ROUTED);
     c->last_dispatched = 0;
-    if (T >= c->grouped_min_t) {
+    if (c->native) {
+        // checkpoint-layout experts (native.h): gate/up + SwiGLU, down, combine; the
+        // per-expert lists for T > 1 as on the other paths
+        NativeArgs na;
+        na.experts = L.experts;
+        na.stride = c->stride;
+        na.off_gq = c->off_gq;
+        na.off_uq = c->off_uq;
+        na.off_dq = c->off_dq;
+        na.off_gs = c->off_gs;
+        na.off_us = c->off_us;
+        na.off_ds = c->off_ds;
+        na.D = D;
+        na.F = F;
+        na.E = E;
+        na.K = K;
+        na.S = c->S;
+        na.gs = c->cfg.group_size;
+        na.flags = fl;
+        pr = prof_begin(c, st, GMOE_KERNEL_GATE_UP);
+        hipLaunchKernelGGL(k_native_gate_up, dim3(F / 16, NS, T), dim3(NV_BLOCK), 0, st, na, (const float *)c->xn,
+                           (const int *)c->topk_idx, c->h);
+        prof_end(pr, st);
+        pr = prof_begin(c, st, GMOE_KERNEL_DOWN);
+        hipLaunchKernelGGL(k_native_down, dim3(D / 4, NS, T), dim3(NV_BLOCK), 0, st, na, (const float *)c->h,
+                           (const int *)c->topk_idx, c->y);
+        prof_end(pr, st);
+        pr = prof_begin(c, st, GMOE_KERNEL_COMBINE);
+        hipLaunchKernelGGL(k_native_combine, dim3((D + NV_BLOCK - 1) / NV_BLOCK, T), dim3(NV_BLOCK), 0, st, na,
+                           (const float *)c->y, (const int *)c->topk_idx, (const float *)c->topk_ws, x_in, x_out,
+                           c->shared_out, c->routed_out);
+        prof_end(pr, st);
+        HIP_OK(hipGetLastError());
+        if (T > 1) {
+            int rc = launch_dispatch(c, T, routed_on, st);
+            if (rc) return rc;
+        }
+    } else if (T >= c->grouped_min_t) {
         // prefill: digits of xn, the per-expert lists and tiles, grouped gate/up, digits
         // of h, grouped down, per-token combine (grouped.h)
         const int TK = c->Tmax * K;

@@ -20,8 +20,11 @@ LIBHOST = os.path.join(HERE, "libglm_hip.so")
 
 GMOE_FLAG_NO_ROUTED = 1
 GMOE_FLAG_EXACT_ROUTER = 2
+# gmoe_config.q8_form: device form of the expert matrices
+GMOE_Q8_AUTO, GMOE_Q8_TILED, GMOE_Q8_NATIVE = 0, 1, 2
 SYNTH_NORM_ONES, SYNTH_NORM_RANDOM = 0, 1
 SYNTH_BIAS_NORMAL, SYNTH_BIAS_ZIPF = 0, 1
+SYNTH_SCALES_FP16, SYNTH_SCALES_FP32 = 0, 1
 
 # Zipf-shaped router bias for the skewed-routing workload: popularity ~ rank^-1.2,
 # gain chosen so the 4 most popular experts take about 40% of top-4 assignments.
@@ -33,7 +36,7 @@ class GmoeConfig(C.Structure):
     _fields_ = [("dim", C.c_int32), ("moe_ffn_dim", C.c_int32), ("n_routed_experts", C.c_int32),
                 ("n_experts_used", C.c_int32), ("n_shared_experts", C.c_int32), ("group_size", C.c_int32),
                 ("n_layers", C.c_int32), ("max_tokens", C.c_int32), ("routed_scale", C.c_float),
-                ("norm_eps", C.c_float)]
+                ("norm_eps", C.c_float), ("q8_form", C.c_int32)]
 
 
 _LAYER_FIELDS = ["ffn_norm", "gate_inp", "exp_probs_b", "gate_sh_q", "gate_sh_s", "up_sh_q", "up_sh_s",
@@ -69,7 +72,8 @@ class GmoeStats(C.Structure):
 class SynthSpec(C.Structure):
     _fields_ = [("seed", C.c_uint64), ("dim", C.c_int32), ("moe_ffn_dim", C.c_int32),
                 ("n_routed_experts", C.c_int32), ("group_size", C.c_int32), ("norm_mode", C.c_int32),
-                ("bias_mode", C.c_int32), ("zipf_s", C.c_double), ("zipf_beta", C.c_double)]
+                ("bias_mode", C.c_int32), ("zipf_s", C.c_double), ("zipf_beta", C.c_double),
+                ("scale_mode", C.c_int32)]
 
 
 _libs = {}
@@ -163,7 +167,8 @@ class HostLayer:
     no resident memory."""
 
     def __init__(self, shape, seed=0, layer=1, experts=None, norm_mode=SYNTH_NORM_ONES,
-                 bias_mode=SYNTH_BIAS_NORMAL, zipf_s=ZIPF_S, zipf_beta=ZIPF_BETA, routed=True):
+                 bias_mode=SYNTH_BIAS_NORMAL, zipf_s=ZIPF_S, zipf_beta=ZIPF_BETA, routed=True,
+                 scale_mode=SYNTH_SCALES_FP16):
         s = shape
         self.shape, self.seed, self.layer = s, seed, layer
         D, F, E, gs = s.D, s.F, s.E, s.gs
@@ -185,7 +190,7 @@ class HostLayer:
             self.down_s = np.zeros((E, D, F // gs), np.float32)
         else:
             self.gate_q = self.gate_s = self.up_q = self.up_s = self.down_q = self.down_s = None
-        spec = SynthSpec(seed, D, F, E, gs, norm_mode, bias_mode, zipf_s, zipf_beta)
+        spec = SynthSpec(seed, D, F, E, gs, norm_mode, bias_mode, zipf_s, zipf_beta, scale_mode)
         e0, e1 = (0, E) if experts is None else experts
         if not routed:
             e0 = e1 = 0
@@ -216,12 +221,13 @@ def check(rc, what):
 class Context:
     """A gmoe_ctx: weights resident on one device, forward calls on device pointers."""
 
-    def __init__(self, shape, n_layers, max_tokens, device=0, routed_scale=1.8, norm_eps=1e-5, n_shared=1):
+    def __init__(self, shape, n_layers, max_tokens, device=0, routed_scale=1.8, norm_eps=1e-5, n_shared=1,
+                 q8_form=GMOE_Q8_AUTO):
         self.lib = gmoe_lib()
         self.shape = shape
         self.max_tokens = max_tokens
         cfg = GmoeConfig(shape.D, shape.F, shape.E, shape.K, n_shared, shape.gs, n_layers, max_tokens,
-                         routed_scale, norm_eps)
+                         routed_scale, norm_eps, q8_form)
         h = C.c_void_p()
         check(self.lib.gmoe_create(C.byref(h), device, C.byref(cfg)), "gmoe_create")
         self.h = h

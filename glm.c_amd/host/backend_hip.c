@@ -28,6 +28,8 @@ int glm_cpu_forward_token(const Runtime *rt, RunState *st, int token, int pos, i
 
 static gmoe_ctx *g_ctx = NULL;
 static int g_active = 0;
+static gmoe_config g_cfg;  /* the context's config, kept to re-create it in the native form */
+static int g_device = 0;
 
 /* "0"/"false" (any case of the first letter, as backend.c:48-55 accepts) mean off. */
 static int env_on(const char *name, int fallback) {
@@ -65,6 +67,7 @@ int glm_hip_init(const Runtime *rt, RunState *st) {
     cfg.max_tokens = 1; /* the decode loop feeds one token at a time */
     cfg.routed_scale = 1.8f; /* infer.c:1171 */
     cfg.norm_eps = 1e-5f;    /* infer.c:750 */
+    cfg.q8_form = GMOE_Q8_AUTO; /* tiled at group size 32, glm.c's own layout otherwise */
     const char *dev = getenv("GLM_HIP_DEVICE");
     int device = dev ? atoi(dev) : 0;
     if (gmoe_create(&g_ctx, device, &cfg) != GMOE_OK) {
@@ -72,6 +75,8 @@ int glm_hip_init(const Runtime *rt, RunState *st) {
         g_ctx = NULL;
         return -1;
     }
+    g_cfg = cfg;
+    g_device = device;
     return 0;
 }
 
@@ -101,7 +106,23 @@ int glm_hip_prepare(const Runtime *rt, RunState *st) {
             w.down_q = r->down_q;
             w.down_s = r->down_s;
         }
-        if (gmoe_upload_layer(g_ctx, l, &w) != GMOE_OK) {
+        const int rc = gmoe_upload_layer(g_ctx, l, &w);
+        if (rc == GMOE_ERR_SCALE && g_cfg.q8_form != GMOE_Q8_NATIVE) {
+            /* fp32 scales that fp16 cannot hold (an exporter's max|w|/127): keep the
+             * checkpoint's own layout instead, from the first layer again */
+            fprintf(stderr, "[glm-hip] layer %d: %s; keeping glm.c's Q8_0 layout\n", l, gmoe_last_error());
+            gmoe_destroy(g_ctx);
+            g_ctx = NULL;
+            g_cfg.q8_form = GMOE_Q8_NATIVE;
+            if (gmoe_create(&g_ctx, g_device, &g_cfg) != GMOE_OK) {
+                fprintf(stderr, "[glm-hip] %s\n", gmoe_last_error());
+                g_ctx = NULL;
+                return -1;
+            }
+            l = 0;
+            continue;
+        }
+        if (rc != GMOE_OK) {
             fprintf(stderr, "[glm-hip] upload of layer %d failed: %s\n", l, gmoe_last_error());
             return -1;
         }

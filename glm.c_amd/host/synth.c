@@ -75,7 +75,7 @@ float synth_round_fp16(float f) {
     return (float)copysign(r, (double)f);
 }
 
-static void fill_q8_matrix(uint64_t kq, uint64_t ks, int rows, int cols, int gs, int8_t *q, float *s) {
+static void fill_q8_matrix(uint64_t kq, uint64_t ks, int rows, int cols, int gs, int fp32_scales, int8_t *q, float *s) {
     const int groups = cols / gs;
     if (q) {
 #pragma omp parallel for schedule(static)
@@ -92,7 +92,7 @@ static void fill_q8_matrix(uint64_t kq, uint64_t ks, int rows, int cols, int gs,
             uint64_t base = (uint64_t)r * (uint64_t)groups;
             for (int g = 0; g < groups; g++) {
                 double z = fabs(synth_normal_at(ks, base + (uint64_t)g));
-                row[g] = synth_round_fp16((float)(z * 0.002));
+                row[g] = fp32_scales ? (float)(z * 0.002) : synth_round_fp16((float)(z * 0.002));
             }
         }
     }
@@ -141,20 +141,20 @@ int synth_layer(const synth_spec *sp, int layer, int e_begin, int e_end, const s
         }
     }
 
-    const int dg = D / gs, fg = F / gs;
+    const int dg = D / gs, fg = F / gs, f32 = sp->scale_mode == SYNTH_SCALES_FP32;
     const size_t mq = (size_t)F * D; /* weights per expert matrix */
     fill_q8_matrix(synth_key(seed, layer, T_GATE_Q, SHARED_EXPERT_ID), synth_key(seed, layer, T_GATE_S, SHARED_EXPERT_ID),
-                   F, D, gs, b->gate_sh_q, b->gate_sh_s);
+                   F, D, gs, f32, b->gate_sh_q, b->gate_sh_s);
     fill_q8_matrix(synth_key(seed, layer, T_UP_Q, SHARED_EXPERT_ID), synth_key(seed, layer, T_UP_S, SHARED_EXPERT_ID),
-                   F, D, gs, b->up_sh_q, b->up_sh_s);
+                   F, D, gs, f32, b->up_sh_q, b->up_sh_s);
     fill_q8_matrix(synth_key(seed, layer, T_DOWN_Q, SHARED_EXPERT_ID), synth_key(seed, layer, T_DOWN_S, SHARED_EXPERT_ID),
-                   D, F, gs, b->down_sh_q, b->down_sh_s);
+                   D, F, gs, f32, b->down_sh_q, b->down_sh_s);
     for (int e = e_begin; e < e_end; e++) {
-        fill_q8_matrix(synth_key(seed, layer, T_GATE_Q, e), synth_key(seed, layer, T_GATE_S, e), F, D, gs,
+        fill_q8_matrix(synth_key(seed, layer, T_GATE_Q, e), synth_key(seed, layer, T_GATE_S, e), F, D, gs, f32,
                        b->gate_q ? b->gate_q + (size_t)e * mq : NULL, b->gate_s ? b->gate_s + (size_t)e * F * dg : NULL);
-        fill_q8_matrix(synth_key(seed, layer, T_UP_Q, e), synth_key(seed, layer, T_UP_S, e), F, D, gs,
+        fill_q8_matrix(synth_key(seed, layer, T_UP_Q, e), synth_key(seed, layer, T_UP_S, e), F, D, gs, f32,
                        b->up_q ? b->up_q + (size_t)e * mq : NULL, b->up_s ? b->up_s + (size_t)e * F * dg : NULL);
-        fill_q8_matrix(synth_key(seed, layer, T_DOWN_Q, e), synth_key(seed, layer, T_DOWN_S, e), D, F, gs,
+        fill_q8_matrix(synth_key(seed, layer, T_DOWN_Q, e), synth_key(seed, layer, T_DOWN_S, e), D, F, gs, f32,
                        b->down_q ? b->down_q + (size_t)e * mq : NULL, b->down_s ? b->down_s + (size_t)e * D * fg : NULL);
     }
     return 0;

@@ -30,6 +30,11 @@ enum {
     SYNTH_BIAS_ZIPF = 1,      /* beta * (-s * ln rank_e) + N(0, 0.01), ranks a random permutation */
 };
 
+enum {
+    SYNTH_SCALES_FP16 = 0,    /* |N(0,1)| * 0.002 rounded to fp16 (the tiled device form holds them exactly) */
+    SYNTH_SCALES_FP32 = 1,    /* |N(0,1)| * 0.002 in fp32, as an exporter's max|w|/127 scales are */
+};
+
 typedef struct synth_spec {
     uint64_t seed;
     int32_t dim, moe_ffn_dim, n_routed_experts, group_size;
@@ -37,6 +42,7 @@ typedef struct synth_spec {
     int32_t bias_mode;
     double zipf_s;            /* Zipf exponent for SYNTH_BIAS_ZIPF */
     double zipf_beta;         /* bias gain for SYNTH_BIAS_ZIPF */
+    int32_t scale_mode;       /* SYNTH_SCALES_* */
 } synth_spec;
 
 /* Pointers to caller-owned host buffers in checkpoint layout; NULL entries are skipped. */

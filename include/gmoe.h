@@ -49,12 +49,27 @@ typedef struct gmoe_config {
     int32_t n_routed_experts;  /* E (model.h:21); 1..256 */
     int32_t n_experts_used;    /* K (model.h:22); 1..8 */
     int32_t n_shared_experts;  /* S (model.h:23); 0 or 1 */
-    int32_t group_size;        /* quantisation group (model.h:26); must be 32 */
+    int32_t group_size;        /* quantisation group (model.h:26): 32 for the tiled form, a multiple of 16
+                                * dividing dim and moe_ffn_dim for the native form */
     int32_t n_layers;          /* total layers; MoE layers are 1..n_layers-1 (infer.c:1844-1845) */
     int32_t max_tokens;        /* largest n_tokens passed to the forward calls */
     float routed_scale;        /* routed expert scale, hard-coded 1.8f at infer.c:1171 */
     float norm_eps;            /* rmsnorm epsilon, 1e-5f at infer.c:750 */
+    int32_t q8_form;           /* GMOE_Q8_*: how the expert matrices are kept on the device */
 } gmoe_config;
+
+/* Device form of the Q8_0 expert matrices.
+ * TILED: repacked into MFMA tiles with fp16 scales; needs group_size 32 and scales that
+ *   fp16 holds exactly (gmoe_upload_layer returns GMOE_ERR_SCALE otherwise). The persistent
+ *   decode kernels and the grouped prefill GEMMs run on this form.
+ * NATIVE: glm.c's own layout, int8 rows and fp32 scales, for any group size that is a
+ *   multiple of 16 and divides dim and moe_ffn_dim (the exporter writes group size 16 and
+ *   scales max|w|/127, glm47_flash_export.py:36,157-169). Every T runs the native
+ *   kernels: one wave per matrix row, each group's sum scaled by its own fp32 scale.
+ * AUTO (0): TILED when group_size is 32, NATIVE otherwise. */
+#define GMOE_Q8_AUTO 0
+#define GMOE_Q8_TILED 1
+#define GMOE_Q8_NATIVE 2
 
 /* Host-side weights of one MoE layer in glm.c's checkpoint layout:
  * LayerMoeShared (model.h:65-75) followed by LayerMoeRouted (model.h:77-84).
@@ -104,7 +119,8 @@ typedef struct gmoe_stats {
 int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg);
 
 /* Upload and repack one MoE layer (1 <= layer < n_layers) from host memory into
- * the device layout. Scales must be fp16-representable (checked; GMOE_ERR_SCALE). */
+ * the device form (q8_form). In the tiled form scales must be fp16-representable (checked;
+ * GMOE_ERR_SCALE); the native form keeps them as they are. */
 int gmoe_upload_layer(gmoe_ctx *ctx, int layer, const gmoe_layer_weights *w);
 
 /* One MoE layer for n_tokens tokens: x_out = x_in + shared + routed.

@@ -93,22 +93,26 @@ def test_error_codes_and_flags():
     assert codes["GMOE_FLAG_NO_ROUTED"] == gmoe.GMOE_FLAG_NO_ROUTED
 
 
-@pytest.mark.parametrize("field,value,needle", [
-    ("dim", 100, "multiples of 256"),
-    ("dim", 4096, "multiples of 256"),
-    ("moe_ffn_dim", 0, "multiples of 256"),
-    ("n_routed_experts", 300, "n_routed_experts"),
-    ("n_experts_used", 9, "n_experts_used"),
-    ("n_shared_experts", 2, "shared expert"),
-    ("group_size", 16, "group_size"),
-    ("n_layers", 1, "n_layers"),
-    ("max_tokens", 0, "max_tokens"),
+@pytest.mark.parametrize("fields,needle", [
+    ({"dim": 100}, "multiples of 256"),
+    ({"dim": 4096}, "multiples of 256"),
+    ({"moe_ffn_dim": 0}, "multiples of 256"),
+    ({"n_routed_experts": 300}, "n_routed_experts"),
+    ({"n_experts_used": 9}, "n_experts_used"),
+    ({"n_shared_experts": 2}, "shared expert"),
+    ({"group_size": 16, "q8_form": gmoe.GMOE_Q8_TILED}, "tiled form needs group_size 32"),
+    ({"group_size": 8}, "multiple of 16"),
+    ({"group_size": 48}, "divides dim"),
+    ({"q8_form": 7}, "q8_form"),
+    ({"n_layers": 1}, "n_layers"),
+    ({"max_tokens": 0}, "max_tokens"),
 ])
-def test_create_rejects_bad_config_before_touching_a_device(field, value, needle):
+def test_create_rejects_bad_config_before_touching_a_device(fields, needle):
     lib = gmoe.gmoe_lib()
     s = gmoe.GLM47_FLASH
-    cfg = gmoe.GmoeConfig(s.D, s.F, s.E, s.K, 1, s.gs, 48, 1, 1.8, 1e-5)
-    setattr(cfg, field, value)
+    cfg = gmoe.GmoeConfig(s.D, s.F, s.E, s.K, 1, s.gs, 48, 1, 1.8, 1e-5, gmoe.GMOE_Q8_AUTO)
+    for field, value in fields.items():
+        setattr(cfg, field, value)
     h = C.c_void_p(1)
     rc = lib.gmoe_create(C.byref(h), 0, C.byref(cfg))
     assert rc == -1

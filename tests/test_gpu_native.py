@@ -1,0 +1,123 @@
+"""Checkpoints in glm.c's own Q8_0 form on the GPU (GMOE_Q8_NATIVE): group size 16 as the
+exporter writes it (glm47_flash_export.py:36), fp32 scales that fp16 cannot hold
+(max|w|/127 there, glm47_flash_export.py:157-169; random fp32 here), and other group sizes
+(infer.c:380-385, 646 take any). Each case runs against the oracle, which follows
+infer.c:765-786 for any group size. Bar as elsewhere: top-k exact, xn bit for bit, router
+probabilities and weights within 1e-5, outputs within max-abs 1e-2 and rel-L2 1e-3."""
+import numpy as np
+import pytest
+
+import gmoe
+import glm_model
+import oracle
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+GLM16 = gmoe.Shape(group_size=16)
+SMALL64 = gmoe.Shape(dim=512, moe_ffn_dim=256, n_routed_experts=16, n_experts_used=4, group_size=64)
+
+
+def check(want, got, st, what):
+    np.testing.assert_array_equal(st["topk_idx"], want["topk_idx"], err_msg=f"{what}: top-k")
+    assert np.array_equal(st["xn"].view(np.uint32), want["xn"].view(np.uint32)), f"{what}: xn"
+    assert_close(st["router_prob"], want["router_prob"], f"{what}: router_prob", max_abs=1e-5, rel_l2=1e-5)
+    assert_close(st["topk_w"], want["topk_w"], f"{what}: topk_w", max_abs=1e-5, rel_l2=1e-5)
+    assert_close(st["shared_out"], want["shared_out"], f"{what}: shared_out")
+    assert_close(st["routed_out"], want["routed_out"], f"{what}: routed_out")
+    assert_close(got, want["x_out"], f"{what}: x_out")
+
+
+def run(shape, seed, T, q8_form=gmoe.GMOE_Q8_AUTO, flags=0, n_layers=1):
+    layers = [gmoe.HostLayer(shape, seed=seed, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM,
+                             scale_mode=gmoe.SYNTH_SCALES_FP32) for l in range(1, n_layers + 1)]
+    ctx = gmoe.Context(shape, n_layers=n_layers + 1, max_tokens=T, q8_form=q8_form)
+    orc = oracle.Oracle("port")
+    try:
+        for l, hl in enumerate(layers, start=1):
+            ctx.upload(l, hl)
+        x = gmoe.activations(seed, 7, T, shape.D)
+        for l, hl in enumerate(layers, start=1):
+            print(f"[case] native gs={shape.gs} D={shape.D} E={shape.E} T={T} layer {l} flags={flags}", flush=True)
+            want = orc.layer(shape, hl, x, disable_routed=bool(flags & gmoe.GMOE_FLAG_NO_ROUTED))
+            got, st = gmoe.forward_host(ctx, l, x, flags=flags)
+            check(want, got, st, f"gs={shape.gs} T={T} layer {l}")
+            x = got
+    finally:
+        ctx.close()
+
+
+def test_gs16_fp32_scales_decode():
+    run(GLM16, seed=41, T=1, n_layers=3)
+
+
+def test_gs16_fp32_scales_batch_and_lists():
+    shape, T = GLM16, 6
+    hl = gmoe.HostLayer(shape, seed=42, layer=1, scale_mode=gmoe.SYNTH_SCALES_FP32)
+    ctx = gmoe.Context(shape, n_layers=2, max_tokens=T)
+    try:
+        ctx.upload(1, hl)
+        x = gmoe.activations(42, 1, T, shape.D)
+        print(f"[case] native gs=16 T={T} with per-expert lists", flush=True)
+        want = oracle.Oracle("port").layer(shape, hl, x)
+        got, st = gmoe.forward_host(ctx, 1, x)
+        check(want, got, st, "gs=16 batch")
+        # per-expert lists: the ascending tokens of each expert, a brute-force grouping
+        offs, toks = [0], []
+        for e in range(shape.E):
+            toks += [t for t in range(T) if e in want["topk_idx"][t]]
+            offs.append(len(toks))
+        np.testing.assert_array_equal(st["expert_offsets"], np.array(offs, np.int32), err_msg="per-expert offsets")
+        np.testing.assert_array_equal(st["expert_tokens"], np.array(toks, np.int32), err_msg="per-expert token lists")
+    finally:
+        ctx.close()
+
+
+def test_gs16_routed_experts_off():
+    run(GLM16, seed=43, T=2, flags=gmoe.GMOE_FLAG_NO_ROUTED)
+
+
+def test_gs64_small_shape():
+    run(SMALL64, seed=44, T=3, n_layers=2)
+
+
+def test_gs32_fp32_scales_need_the_native_form():
+    """fp32 scales at group size 32: the tiled form refuses them (GMOE_ERR_SCALE); the
+    native form computes them as glm.c does."""
+    shape = gmoe.GLM47_FLASH
+    hl = gmoe.HostLayer(shape, seed=45, layer=1, scale_mode=gmoe.SYNTH_SCALES_FP32)
+    ctx = gmoe.Context(shape, n_layers=2, max_tokens=1)
+    try:
+        print("[case] tiled form refuses fp32 scales", flush=True)
+        rc = ctx.lib.gmoe_upload_layer(ctx.h, 1, gmoe.C.byref(hl.weights()))
+        assert rc == -4, rc
+        assert "fp16" in gmoe.last_error()
+    finally:
+        ctx.close()
+    run(shape, seed=45, T=1, q8_form=gmoe.GMOE_Q8_NATIVE)
+
+
+@pytest.mark.parametrize("shape", [GLM16, gmoe.GLM47_FLASH], ids=["gs16", "gs32_fp32"])
+def test_backend_takes_exporter_checkpoints(shape):
+    """glm_backend_init(BACKEND_HIP) on a checkpoint with fp32 scales: at group size 16 the
+    context is native from the start; at 32 the tiled upload fails on the scales and the
+    backend re-creates the context in glm.c's layout. Either way the RunState matches."""
+    layers = [gmoe.HostLayer(shape, seed=46, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM,
+                             scale_mode=gmoe.SYNTH_SCALES_FP32) for l in (1, 2)]
+    model = glm_model.GlmModel(shape, layers)
+    print(f"[case] backend with fp32 scales, gs={shape.gs}", flush=True)
+    assert model.init() == glm_model.BACKEND_HIP
+    orc = oracle.Oracle("port")
+    try:
+        model.buf["x"][:] = gmoe.activations(46, 0, 1, shape.D)[0]
+        for l in (1, 2):
+            x_in = model.buf["x"].copy()
+            want = orc.layer(shape, layers[l - 1], x_in[None, :])
+            assert model.try_moe(l) == 0
+            b = model.buf
+            np.testing.assert_array_equal(b["moe_topk_idx"], want["topk_idx"][0], err_msg=f"layer {l} moe_topk_idx")
+            assert_close(b["xb"], want["shared_out"][0], f"layer {l} xb")
+            assert_close(b["moe_out_acc"], want["routed_out"][0], f"layer {l} moe_out_acc")
+            assert_close(b["x"], want["x_out"][0], f"layer {l} x")
+    finally:
+        model.free()
