@@ -91,12 +91,73 @@ def backend_lib():
     return lib
 
 
-class GlmModel:
-    """A glm.c Runtime whose MoE layers 1..len(layers) are the given HostLayers (layer 0
-    has no MoE block, as in GLM-4.7-Flash), and a RunState sized for one decode token."""
+class CkptSpec(C.Structure):
+    """glm_ckpt_spec (include/glm_ckpt.h): shape and draws of a synthetic v4 checkpoint."""
+    _fields_ = ([(n, C.c_int32) for n in ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size",
+                                          "seq_len", "rope_dim", "q_lora_rank", "kv_lora_rank", "n_routed_experts",
+                                          "n_experts_used", "bos_id", "eos_id", "qk_nope_dim", "v_head_dim",
+                                          "moe_ffn_dim", "group_size")]
+                + [("seed", C.c_uint64)]
+                + [(n, C.c_int32) for n in ("norm_mode", "bias_mode", "scale_mode")])
 
-    def __init__(self, shape, layers):
+
+def ckpt_lib():
+    lib = gmoe.host_lib()
+    if not getattr(lib, "_ckpt_typed", False):
+        RP = C.POINTER(Runtime)
+        lib.glm_ckpt_write_synth.argtypes = [C.c_char_p, C.POINTER(CkptSpec)]
+        lib.glm_ckpt_write_synth.restype = C.c_int
+        lib.glm_ckpt_open.argtypes = [C.c_char_p, RP]
+        lib.glm_ckpt_open.restype = C.c_int
+        lib.glm_ckpt_close.argtypes = [RP]
+        lib.glm_ckpt_close.restype = None
+        lib.glm_ckpt_error.argtypes = []
+        lib.glm_ckpt_error.restype = C.c_char_p
+        lib.glm_ckpt_layout.argtypes = [RP, C.POINTER(C.c_uint64), C.c_int]
+        lib.glm_ckpt_layout.restype = C.c_int
+        lib._ckpt_typed = True
+    return lib
+
+
+def write_synth_checkpoint(path, spec):
+    """glm_ckpt_write_synth: a synthetic v4 .bin of this CkptSpec at path."""
+    lib = ckpt_lib()
+    if lib.glm_ckpt_write_synth(str(path).encode(), C.byref(spec)) != 0:
+        raise RuntimeError(f"glm_ckpt_write_synth: {lib.glm_ckpt_error().decode()}")
+
+
+class Checkpoint:
+    """A v4 .bin mapped by glm_ckpt_open: its Runtime, as glm.c's runtime_open fills it."""
+
+    def __init__(self, path):
+        self.lib = ckpt_lib()
+        self.rt = Runtime()
+        if self.lib.glm_ckpt_open(str(path).encode(), C.byref(self.rt)) != 0:
+            raise RuntimeError(f"glm_ckpt_open: {self.lib.glm_ckpt_error().decode()}")
+
+    def layout(self):
+        n = self.lib.glm_ckpt_layout(C.byref(self.rt), None, 0)
+        out = (C.c_uint64 * n)()
+        self.lib.glm_ckpt_layout(C.byref(self.rt), out, n)
+        return np.frombuffer(out, np.uint64).copy()
+
+    def close(self):
+        if self.rt.data:
+            self.lib.glm_ckpt_close(C.byref(self.rt))
+
+
+class GlmModel:
+    """A glm.c Runtime and a RunState sized for one decode token. The Runtime's MoE layers
+    1..len(layers) are the given HostLayers (layer 0 has no MoE block, as in
+    GLM-4.7-Flash), or it is a Checkpoint's."""
+
+    def __init__(self, shape, layers=None, checkpoint=None):
         self.shape = shape
+        if checkpoint is not None:
+            self.ckpt = checkpoint  # keeps the mapping alive
+            self.rt = checkpoint.rt
+            self._state(shape)
+            return
         self.layers = list(layers)  # keep the arrays alive
         n_layers = len(self.layers) + 1
         cfg = RuntimeConfig()
@@ -117,6 +178,9 @@ class GlmModel:
         rt.has_moe_routed = 1
         rt.moe_routed_layers = C.cast(self.routed, C.POINTER(LayerMoeRouted))
         self.rt = rt
+        self._state(shape)
+
+    def _state(self, shape):
         D, E, K = shape.D, shape.E, shape.K
         self.buf = {"x": np.zeros(D, np.float32), "xn": np.zeros(D, np.float32), "xb": np.zeros(D, np.float32),
                     "moe_router": np.zeros(E, np.float32), "moe_out_acc": np.zeros(D, np.float32),

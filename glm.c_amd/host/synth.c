@@ -103,6 +103,12 @@ static void fill_normal(uint64_t key, size_t n, double mean, double sd, float *o
     for (long long i = 0; i < (long long)n; i++) out[i] = (float)(mean + sd * synth_normal_at(key, (uint64_t)i));
 }
 
+void synth_normal_fill(uint64_t key, size_t n, double mean, double sd, float *out) { fill_normal(key, n, mean, sd, out); }
+
+void synth_q8_matrix(uint64_t kq, uint64_t ks, int rows, int cols, int gs, int scale_mode, int8_t *q, float *s) {
+    fill_q8_matrix(kq, ks, rows, cols, gs, scale_mode == SYNTH_SCALES_FP32, q, s);
+}
+
 int synth_layer(const synth_spec *sp, int layer, int e_begin, int e_end, const synth_layer_buffers *b) {
     if (!sp || !b) return -1;
     const int D = sp->dim, F = sp->moe_ffn_dim, E = sp->n_routed_experts, gs = sp->group_size;

@@ -66,6 +66,13 @@ void synth_activations(uint64_t seed, int stream, int n_tokens, int dim, float *
 /* Nearest fp16 value of f (round to nearest even, subnormals kept), as a float. */
 float synth_round_fp16(float f);
 
+/* x[i] = mean + sd * N(0,1) from stream `key` (synth_key), n values. */
+void synth_normal_fill(uint64_t key, size_t n, double mean, double sd, float *out);
+
+/* A Q8 matrix drawn as the experts' are: int8 [rows][cols] from stream kq, scales
+ * [rows][cols/gs] from ks in the form scale_mode (SYNTH_SCALES_*); NULL q or s is skipped. */
+void synth_q8_matrix(uint64_t kq, uint64_t ks, int rows, int cols, int gs, int scale_mode, int8_t *q, float *s);
+
 /* Raw stream access, for tests of the generator itself. */
 uint64_t synth_key(uint64_t seed, int layer, int tensor, int expert);
 uint64_t synth_draw(uint64_t key, uint64_t n);

@@ -177,3 +177,57 @@ int ref_moe_layer_timed(const oracle_dims *d, const oracle_layer *w, int T, cons
     runstate_free(&st);
     return 0;
 }
+
+/* glm.c's own loader on a checkpoint file (runtime_open, infer.c:357-744; it exits the
+ * process on a file it rejects, so callers run this in a child process): the header and
+ * every tensor pointer as its file offset (0 for none), in the order of glm_ckpt_layout
+ * (include/glm_ckpt.h). Returns the number of offsets. */
+int ref_ckpt_layout(const char *path, uint64_t *out, int max, void *cfg_out) {
+    Runtime rt;
+    runtime_open(&rt, path);
+    int n = 0;
+#define PUT(p) do { if (n < max) out[n] = (p) ? (uint64_t)((const unsigned char *)(p) - rt.data) : 0u; n++; } while (0)
+    PUT(rt.output_norm);
+    PUT(rt.tok_q);
+    PUT(rt.tok_s);
+    PUT(rt.out_q);
+    PUT(rt.out_s);
+    const void *l0f[7] = {rt.l0_ffn_norm, rt.l0_ffn_gate_q, rt.l0_ffn_gate_s, rt.l0_ffn_up_q,
+                          rt.l0_ffn_up_s, rt.l0_ffn_down_q, rt.l0_ffn_down_s};
+    for (int i = 0; i < 7; i++) PUT(rt.has_l0_ffn ? l0f[i] : NULL);
+    const void *l0a[15] = {rt.l0_attn_norm, rt.l0_q_a_norm, rt.l0_kv_a_norm, rt.l0_q_a_q, rt.l0_q_a_s,
+                           rt.l0_q_b_q, rt.l0_q_b_s, rt.l0_kv_a_q, rt.l0_kv_a_s, rt.l0_k_b_q, rt.l0_k_b_s,
+                           rt.l0_v_b_q, rt.l0_v_b_s, rt.l0_attn_out_q, rt.l0_attn_out_s};
+    for (int i = 0; i < 15; i++) PUT(rt.has_l0_attn ? l0a[i] : NULL);
+    for (int l = 0; l < rt.cfg.n_layers; l++) {
+        const LayerAttnWeights *w = rt.has_all_attn ? &rt.attn_layers[l] : NULL;
+        const void *a[15] = {0};
+        if (w) {
+            const void *t[15] = {w->attn_norm, w->q_a_norm, w->kv_a_norm, w->q_a_q, w->q_a_s, w->q_b_q, w->q_b_s,
+                                 w->kv_a_q, w->kv_a_s, w->k_b_q, w->k_b_s, w->v_b_q, w->v_b_s, w->attn_out_q,
+                                 w->attn_out_s};
+            memcpy(a, t, sizeof(t));
+        }
+        for (int i = 0; i < 15; i++) PUT(a[i]);
+    }
+    for (int l = 1; l < rt.cfg.n_layers; l++) {
+        const void *s[9] = {0}, *r[6] = {0};
+        if (rt.has_moe_shared) {
+            const LayerMoeShared *w = &rt.moe_layers[l];
+            const void *t[9] = {w->ffn_norm, w->gate_inp, w->exp_probs_b, w->gate_sh_q, w->gate_sh_s,
+                                w->up_sh_q, w->up_sh_s, w->down_sh_q, w->down_sh_s};
+            memcpy(s, t, sizeof(t));
+        }
+        if (rt.has_moe_routed) {
+            const LayerMoeRouted *w = &rt.moe_routed_layers[l];
+            const void *t[6] = {w->gate_q, w->gate_s, w->up_q, w->up_s, w->down_q, w->down_s};
+            memcpy(r, t, sizeof(t));
+        }
+        for (int i = 0; i < 9; i++) PUT(s[i]);
+        for (int i = 0; i < 6; i++) PUT(r[i]);
+    }
+#undef PUT
+    if (cfg_out) memcpy(cfg_out, &rt.cfg, sizeof(rt.cfg));
+    runtime_close(&rt);
+    return n;
+}

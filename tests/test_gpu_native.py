@@ -121,3 +121,41 @@ def test_backend_takes_exporter_checkpoints(shape):
             assert_close(b["x"], want["x_out"][0], f"layer {l} x")
     finally:
         model.free()
+
+
+@pytest.mark.parametrize("gs,scale_mode", [(16, gmoe.SYNTH_SCALES_FP32), (32, gmoe.SYNTH_SCALES_FP16)],
+                         ids=["gs16_native", "gs32_tiled"])
+def test_backend_runs_a_checkpoint_file(tmp_path, gs, scale_mode):
+    """A v4 .bin written by glm_ckpt_write_synth and mapped by glm_ckpt_open (the Runtime
+    glm.c's runtime_open would fill) goes to glm_backend_init(BACKEND_HIP); each MoE layer
+    then runs on the GPU against the oracle on the same layer, regenerated from the seed."""
+    spec = glm_model.CkptSpec(dim=512, hidden_dim=1024, n_layers=3, n_heads=4, n_kv_heads=4, vocab_size=200,
+                              seq_len=64, rope_dim=16, q_lora_rank=128, kv_lora_rank=64, n_routed_experts=16,
+                              n_experts_used=4, bos_id=1, eos_id=2, qk_nope_dim=32, v_head_dim=32, moe_ffn_dim=256,
+                              group_size=gs, seed=61, norm_mode=gmoe.SYNTH_NORM_RANDOM,
+                              bias_mode=gmoe.SYNTH_BIAS_NORMAL, scale_mode=scale_mode)
+    path = tmp_path / "model.bin"
+    glm_model.write_synth_checkpoint(path, spec)
+    shape = gmoe.Shape(dim=spec.dim, moe_ffn_dim=spec.moe_ffn_dim, n_routed_experts=spec.n_routed_experts,
+                       n_experts_used=spec.n_experts_used, group_size=gs)
+    ck = glm_model.Checkpoint(path)
+    model = glm_model.GlmModel(shape, checkpoint=ck)
+    print(f"[case] backend on a checkpoint file, gs={gs}", flush=True)
+    assert model.init() == glm_model.BACKEND_HIP
+    orc = oracle.Oracle("port")
+    try:
+        model.buf["x"][:] = gmoe.activations(61, 0, 1, shape.D)[0]
+        for l in range(1, spec.n_layers):
+            hl = gmoe.HostLayer(shape, seed=spec.seed, layer=l, norm_mode=spec.norm_mode, scale_mode=scale_mode)
+            x_in = model.buf["x"].copy()
+            want = orc.layer(shape, hl, x_in[None, :])
+            assert model.try_moe(l) == 0
+            b = model.buf
+            np.testing.assert_array_equal(b["moe_topk_idx"], want["topk_idx"][0], err_msg=f"layer {l} moe_topk_idx")
+            assert np.array_equal(b["xn"].view(np.uint32), want["xn"][0].view(np.uint32)), f"layer {l} xn"
+            assert_close(b["xb"], want["shared_out"][0], f"layer {l} xb")
+            assert_close(b["moe_out_acc"], want["routed_out"][0], f"layer {l} moe_out_acc")
+            assert_close(b["x"], want["x_out"][0], f"layer {l} x")
+    finally:
+        model.free()
+        ck.close()
