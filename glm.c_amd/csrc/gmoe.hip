@@ -130,6 +130,12 @@ struct gmoe_ctx {
     unsigned *sk_ctr = nullptr;  // [GM_STACK_COUNTERS]
     int *sk_error = nullptr;
     int *sk_error_host = nullptr;      // pinned host word a failing launch sets (hipHostMalloc)
+    // The host-visible outputs (x for the host-buffer forward, xn, shared_out, routed_out,
+    // router_prob, topk_w, topk_idx: the pointers above are slices of it, in this order)
+    // in one device block, and its pinned host image: gmoe_forward_host moves a layer's
+    // input and all of its outputs with one copy each way.
+    uint8_t *obs = nullptr, *obs_host = nullptr;
+    size_t obs_bytes = 0;
     int *sk_error_host_dev = nullptr;  // its device address
     unsigned sk_spin_limit = SK_SPIN_LIMIT;
     StackLayer *sk_layers = nullptr;  // [L], device
@@ -202,13 +208,14 @@ static void free_ctx(gmoe_ctx *c) {
         }
         delete[] c->layers;
     }
-    void *bufs[] = {c->xn, c->router_prob, c->topk_w, c->topk_ws, c->h, c->y, c->shared_out, c->routed_out,
-                    c->stage, c->topk_idx, c->tok_counter, c->panel_counter, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
-                    c->stats_dev, c->x_host_io, c->staging, c->sk_ws, c->sk_ctr, c->sk_error,
+    void *bufs[] = {c->obs, c->topk_ws, c->h, c->y,
+                    c->stage, c->tok_counter, c->panel_counter, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
+                    c->stats_dev, c->staging, c->sk_ws, c->sk_ctr, c->sk_error,
                     c->sk_layers, c->sk_trace, c->xspl, c->hspl, c->xexp, c->hexp, c->pair_row, c->n_tiles,
                     c->hbuf, c->ybuf, c->tiles, c->rt_t, c->rt_sp, c->rt_sa};
     for (void *b : bufs) dev_free(b);
     if (c->sk_error_host) (void)hipHostFree(c->sk_error_host);
+    if (c->obs_host) (void)hipHostFree(c->obs_host);
     delete c;
 }
 
@@ -299,21 +306,36 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
 
     const size_t T = c->Tmax, D = c->D, F = c->F, E = c->E, K = c->K, NS = c->K + c->S;
     int rc = GMOE_OK;
-    rc |= dev_alloc(&c->xn, T * D);
-    rc |= dev_alloc(&c->router_prob, T * E);
+    {
+        // obs: x_host_io, xn, shared_out, routed_out [T][D]; router_prob [T][E]; topk_w,
+        // topk_idx [T][K] -- 4-byte elements, in this order (obs_slice)
+        c->obs_bytes = (4 * T * D + T * E + 2 * T * K + 1) * sizeof(float);
+        rc |= dev_alloc(&c->obs, c->obs_bytes);
+        if (!rc && hipHostMalloc((void **)&c->obs_host, c->obs_bytes, hipHostMallocDefault) != hipSuccess) {
+            c->obs_host = nullptr;
+            set_err("hipHostMalloc of %zu bytes failed", c->obs_bytes);
+            rc |= GMOE_ERR_NOMEM;
+        }
+        if (!rc) {
+            float *o = (float *)c->obs;
+            c->x_host_io = o;
+            c->xn = o + T * D;
+            c->shared_out = o + 2 * T * D;
+            c->routed_out = o + 3 * T * D;
+            c->router_prob = o + 4 * T * D;
+            c->topk_w = c->router_prob + T * E;
+            c->topk_idx = (int *)(c->topk_w + T * K);
+        }
+    }
     if (E <= 64) {
         rc |= dev_alloc(&c->rt_t, T * 4 * E);
         rc |= dev_alloc(&c->rt_sp, T * 4 * E);
         rc |= dev_alloc(&c->rt_sa, T * 4 * E);
     }
-    rc |= dev_alloc(&c->topk_w, T * K);
     rc |= dev_alloc(&c->topk_ws, T * K);
     rc |= dev_alloc(&c->h, T * NS * F);
     rc |= dev_alloc(&c->y, T * NS * D);
-    rc |= dev_alloc(&c->shared_out, T * D);
-    rc |= dev_alloc(&c->routed_out, T * D);
     rc |= dev_alloc(&c->stage, T * E);
-    rc |= dev_alloc(&c->topk_idx, T * K);
     rc |= dev_alloc(&c->tok_counter, T);
     rc |= dev_alloc(&c->panel_counter, T * (D / 16));
     rc |= dev_alloc(&c->offsets, E + 1);
@@ -335,7 +357,6 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     rc |= dev_alloc(&c->hist_idx, (size_t)c->L * T * K);
     rc |= dev_alloc(&c->hist_w, (size_t)c->L * T * K);
     rc |= dev_alloc(&c->stats_dev, GM_STAT_COUNT);
-    rc |= dev_alloc(&c->x_host_io, T * D);
     // The persistent decode kernels hold one panel's chunks per wave in registers and xn in
     // shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots. k_moe_stack
     // stages a combine chunk's partials, F/16 x (K+1) x 8 floats, in the slice buffer;
@@ -1122,14 +1143,51 @@ extern "C" int gmoe_forward_host(gmoe_ctx *c, int layer, int T, const float *x_i
         return GMOE_ERR_INVALID;
     }
     HIP_OK(hipSetDevice(c->device));
-    const size_t bytes = (size_t)T * c->D * sizeof(float);
-    HIP_OK(hipMemcpy(c->x_host_io, x_in, bytes, hipMemcpyHostToDevice));
+    const size_t T_ = (size_t)T, TM = (size_t)c->Tmax, D = c->D, E = c->E, K = c->K;
+    const size_t bytes = T_ * D * sizeof(float);
+    // in: through the pinned image, one copy
+    float *h = (float *)c->obs_host;
+    memcpy(h, x_in, bytes);
+    HIP_OK(hipMemcpyAsync(c->x_host_io, h, bytes, hipMemcpyHostToDevice, nullptr));
     int rc = gmoe_forward(c, layer, T, c->x_host_io, c->x_host_io, flags, nullptr);
     if (rc) return rc;
+    // out: x and the observables in one copy of the block (its used parts when T < max_tokens),
+    // and the launch's device error word, then one synchronisation
+    int *err_h = (int *)(c->obs_host + c->obs_bytes - sizeof(int));
+    *err_h = 0;
+    if (T_ == TM) {
+        HIP_OK(hipMemcpyAsync(c->obs_host, c->obs, c->obs_bytes - sizeof(int), hipMemcpyDeviceToHost, nullptr));
+    } else {
+        const size_t parts[][2] = {{0, T_ * D}, {TM * D, T_ * D}, {2 * TM * D, T_ * D}, {3 * TM * D, T_ * D},
+                                   {4 * TM * D, T_ * E}, {4 * TM * D + TM * E, T_ * K}, {4 * TM * D + TM * E + TM * K, T_ * K}};
+        for (const auto &pt : parts)
+            HIP_OK(hipMemcpyAsync(c->obs_host + pt[0] * 4, c->obs + pt[0] * 4, pt[1] * 4, hipMemcpyDeviceToHost, nullptr));
+    }
+    if (c->stack_launched && c->stack_last)
+        HIP_OK(hipMemcpyAsync(err_h, c->stack_error_dev, sizeof(int), hipMemcpyDeviceToHost, nullptr));
+    HIP_OK(hipStreamSynchronize(nullptr));
     // a timed-out launch leaves x_out untouched, so a caller may rerun the layer from it
-    if ((rc = check_stack_error(c))) return rc;
-    HIP_OK(hipMemcpy(x_out, c->x_host_io, bytes, hipMemcpyDeviceToHost));
-    if (state) return gmoe_read_layer_state(c, state, nullptr);
+    if (take_launch_error(c) || *err_h) {
+        set_err("%s", k_timeout_msg);
+        return GMOE_ERR_HIP;
+    }
+    memcpy(x_out, h, bytes);
+    if (!state) return GMOE_OK;
+    const float *ho = (const float *)c->obs_host;
+    if (state->xn) memcpy(state->xn, ho + TM * D, bytes);
+    if (state->shared_out) memcpy(state->shared_out, ho + 2 * TM * D, bytes);
+    if (state->routed_out) memcpy(state->routed_out, ho + 3 * TM * D, bytes);
+    if (state->router_prob) memcpy(state->router_prob, ho + 4 * TM * D, T_ * E * sizeof(float));
+    if (state->topk_w) memcpy(state->topk_w, ho + 4 * TM * D + TM * E, T_ * K * sizeof(float));
+    if (state->topk_idx) memcpy(state->topk_idx, ho + 4 * TM * D + TM * E + TM * K, T_ * K * sizeof(int));
+    if (state->expert_offsets || state->expert_tokens) {
+        // the per-expert lists (dispatched on demand at T=1) take the general read-back
+        gmoe_layer_state lists;
+        memset(&lists, 0, sizeof(lists));
+        lists.expert_offsets = state->expert_offsets;
+        lists.expert_tokens = state->expert_tokens;
+        return gmoe_read_layer_state(c, &lists, nullptr);
+    }
     return GMOE_OK;
 }
 
