@@ -1220,6 +1220,12 @@ extern "C" int gmoe_read_layer_state(gmoe_ctx *c, gmoe_layer_state *o, void *str
     if (o->expert_tokens) {
         int total = 0;
         if (hipMemcpy(&total, c->offsets + E, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return GMOE_ERR_HIP;
+        // the caller's list holds T*K entries: a total outside that is device state gone
+        // wrong, reported rather than copied past the end of the caller's buffer
+        if (total < 0 || (size_t)total > T * K) {
+            set_err("gmoe_read_layer_state: per-expert lists hold %d entries, more than n_tokens * K = %zu", total, T * K);
+            return GMOE_ERR_HIP;
+        }
         rc |= copy_out(o->expert_tokens, c->tokens, (size_t)total * sizeof(int));
     }
     return rc ? GMOE_ERR_HIP : GMOE_OK;

@@ -26,6 +26,8 @@
 // once at the end. Errors are ~2^-22 of each element, fp32-like.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 #include "dispatch.h"
 #include "experts.h"
@@ -102,36 +104,41 @@ typedef __attribute__((address_space(3))) void gp_lds_void;
 typedef _Float16 gp_h8 __attribute__((ext_vector_type(8)));
 typedef float gp_f4 __attribute__((ext_vector_type(4)));
 
-// Staging of a tile's GP_TOK inputs, chunk by chunk, into [GP_TOK * 2 rows][GP_KC]
-// fp16 of shared memory, row r = 2 (input) + plane (hi, lo). The 16-byte groups of row
-// r are stored XOR-swizzled by input % 16, so the A-operand reads (16 inputs, 16 bytes
-// each) hit 16 different bank groups. Each thread fills GP_STAGE_ITERS slots per chunk;
-// their source addresses are fixed per tile (the row's start plus the slot's logical
-// group), so a chunk costs exactly GP_STAGE_ITERS loads per thread.
+// Staging of a tile's inputs, chunk by chunk, into [GP_TOK * 2 rows][GP_KC] fp16 of
+// shared memory, row r = 2 (input) + plane (hi, lo). The 16-byte groups of row r are
+// stored XOR-swizzled by input % 16, so the A-operand reads (16 inputs, 16 bytes each)
+// hit 16 different bank groups. A tile body for NA A tiles (16 NA inputs) stages rows
+// 0 .. 32 NA - 1 only: each thread fills gp_stage_iters(NA) slots per chunk, whose source
+// addresses are fixed per tile (the row's start plus the slot's logical group), so a
+// chunk costs exactly that many loads per thread.
 #define GP_RB (GP_KC * 2)            // bytes per staged row
 #define GP_RG (GP_RB / 16)           // 16-byte groups per staged row
-#define GP_STAGE_ITERS (GP_TOK * 2 * GP_RG / GP_BLOCK)  // 16-byte staging loads per thread and chunk
+#define GP_NA_MAX (GP_TOK / 16)      // A tiles (16 inputs each) per tile
+static_assert(16 * 2 * GP_RG == 2 * GP_BLOCK, "an A tile's staged rows take two slots per thread");
+__host__ __device__ constexpr int gp_stage_iters(int na) { return 2 * na; }
+template <int NA>
 struct GpStage {
-    const __half *src[GP_STAGE_ITERS];
+    const __half *src[gp_stage_iters(NA)];
 };
 
 // src_row(i): the activation row of input i (clamped to a valid row past the count).
-template <typename RowOf>
-__device__ static inline GpStage gp_stage_init(const __half *spl, int cols, RowOf src_row) {
+template <int NA, typename RowOf>
+__device__ static inline GpStage<NA> gp_stage_init(const __half *spl, int cols, RowOf src_row) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    GpStage g;
+    GpStage<NA> g;
 #pragma unroll
-    for (int it = 0; it < GP_STAGE_ITERS; it++) {
+    for (int it = 0; it < gp_stage_iters(NA); it++) {
         const int s = 64 * w + GP_BLOCK * it + lane, r = s / GP_RG, p = s % GP_RG, j = p ^ ((r >> 1) & 15);
         g.src[it] = spl + ((size_t)src_row(r >> 1) * 2 + (r & 1)) * cols + 8 * j;
     }
     return g;
 }
 
-__device__ static inline void gp_stage(const GpStage &g, uint8_t *buf, int c0) {
+template <int NA>
+__device__ static inline void gp_stage(const GpStage<NA> &g, uint8_t *buf, int c0) {
     const int w = threadIdx.x >> 6;
 #pragma unroll
-    for (int it = 0; it < GP_STAGE_ITERS; it++)
+    for (int it = 0; it < gp_stage_iters(NA); it++)
         __builtin_amdgcn_global_load_lds((const GM_GLOBAL void *)gbl(g.src[it] + c0),
                                          (gp_lds_void *)(buf + 16 * (64 * w + GP_BLOCK * it)), 16, 0, 0);
 }
@@ -166,16 +173,34 @@ __device__ static inline gp_h8 gp_i8_to_h8(unsigned lo, unsigned hi) {
     return r;
 }
 
-// acc[i][0..3] += the block dots of the lane's four inputs of A tile i, times scale s.
+// acc[i][0..3] += the block dots of the lane's four inputs of A tile i (i < NA), times
+// scale s. NA is a compile-time count: a data-dependent exit between these MFMAs and the
+// accumulation would put the accumulation in a join block, where the compiler's wait
+// states before reading an MFMA result only cover the fall-through path (seen on gfx950:
+// the first reads after the branch got the registers' old contents).
+template <int NA>
 __device__ static inline void gp_block(const uint8_t *buf, int b, gp_h8 B, float s, float (*acc)[4]) {
     const gp_f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < GP_TOK / 16; i++) {
+    for (int i = 0; i < NA; i++) {
         gp_f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(gp_a(buf, i, 0, b), B, zero, 0, 0, 0);
         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(gp_a(buf, i, 1, b), B, d, 0, 0, 0);
 #pragma unroll
         for (int k = 0; k < 4; k++) acc[i][k] = fmaf(d[k], s, acc[i][k]);
     }
+}
+
+// f(NA) for the tile's A-tile count na (1 .. GP_NA_MAX, block-uniform) as a compile-time
+// constant: one branch per block, before any of the tile's work.
+template <int N, typename Body>
+__device__ __attribute__((always_inline)) static inline void gp_with_na(int na, Body &&f) {
+    if constexpr (N > 1) {
+        if (na < N) {
+            gp_with_na<N - 1>(na, f);
+            return;
+        }
+    }
+    f(std::integral_constant<int, N>{});
 }
 
 // Chunk pipeline shared by the grouped GEMMs. A chunk's weights are requested into one of
@@ -186,20 +211,21 @@ __device__ static inline void gp_block(const uint8_t *buf, int b, gp_h8 B, float
 // prefetch included, which would serialise the pipeline.
 __device__ static inline void gp_barrier() { __builtin_amdgcn_s_barrier(); }
 
-// grid (F/64, max tiles). Wave w computes rows 64 p + 16 w .. +16 of F, gate and up, for
-// the tile's GP_TOK tokens, and from them h = silu(g) * u.
+typedef uint8_t gp_abuf_t[2][GP_TOK * 2 * GP_RB];
+
+// k_group_gu: grid (F/64, max tiles). Wave w computes rows 64 p + 16 w .. +16 of F, gate
+// and up, for the tile's inputs, and from them h = silu(g) * u.
 typedef unsigned gp_sw __attribute__((ext_vector_type(GP_NB / 2)));  // a chunk's GP_NB fp16 block scales
 struct GuRegs {
     u32x4 q[2][GP_NB / 2];  // gate, up: the chunk's 64-column pieces
     gp_sw s[2];             // gate, up: the chunk's block scales
 };
-#define GU_LOADS (2 * (GP_NB / 2) + 2 + GP_STAGE_ITERS)  // loads per chunk and thread
+// loads per chunk and thread
+__host__ __device__ constexpr int gp_gu_loads(int na) { return 2 * (GP_NB / 2) + 2 + gp_stage_iters(na); }
 
-__global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
-    __shared__ __align__(16) uint8_t abuf[2][GP_TOK * 2 * GP_RB];
-    const int p = blockIdx.x, ti = blockIdx.y;
-    if (ti >= *a.n_tiles) return;
-    const GpTile tl = a.tiles[ti];
+template <int NA>
+__device__ __attribute__((always_inline)) static inline void gp_gu_tile(const GroupArgs &a, const GpTile &tl, gp_abuf_t &abuf) {
+    const int p = blockIdx.x;
     const int D = a.D, F = a.F, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int nchunks = D >> 6, nblocks = D >> 5;
     const uint8_t *base = a.experts + (size_t)tl.e * a.stride;
@@ -211,15 +237,15 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
     const GM_GLOBAL gp_sw *sg = gbl((const gp_sw *)(base + a.off_gs + (size_t)row * nblocks * 2));
     const GM_GLOBAL gp_sw *su = gbl((const gp_sw *)(base + a.off_us + (size_t)row * nblocks * 2));
     auto src_row = [&](int i) { return gp_token(a, tl.row + (i < tl.count ? i : 0)); };
-    const GpStage stg = gp_stage_init(a.aspl, D, src_row);
+    const GpStage<NA> stg = gp_stage_init<NA>(a.aspl, D, src_row);
     const int nkc = D / GP_KC;  // K chunks
 
-    float ag[GP_TOK / 16][4], au[GP_TOK / 16][4];
+    float ag[NA][4], au[NA][4];
 #pragma unroll
-    for (int i = 0; i < GP_TOK / 16; i++)
+    for (int i = 0; i < NA; i++)
 #pragma unroll
         for (int k = 0; k < 4; k++) ag[i][k] = au[i][k] = 0.0f;
-    auto issue = [&](GuRegs &r, int kc) {  // GU_LOADS loads
+    auto issue = [&](GuRegs &r, int kc) {  // gp_gu_loads(NA) loads
 #pragma unroll
         for (int u = 0; u < GP_NB / 2; u++) {
             r.q[0][u] = qg[(size_t)((GP_NB / 2) * kc + u) * 64];
@@ -227,7 +253,7 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
         }
         r.s[0] = sg[kc];
         r.s[1] = su[kc];
-        gp_stage(stg, abuf[kc & 1], kc * GP_KC);
+        gp_stage<NA>(stg, abuf[kc & 1], kc * GP_KC);
     };
     auto compute = [&](const GuRegs &r, int kc) {
         const uint8_t *buf = abuf[kc & 1];
@@ -239,7 +265,7 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
                 const gp_h8 B = (b & 1) ? gp_i8_to_h8(c.z, c.w) : gp_i8_to_h8(c.x, c.y);
                 const unsigned s2 = r.s[m][b >> 1];
                 const float sc = __half2float(__ushort_as_half((unsigned short)((b & 1) ? s2 >> 16 : s2 & 0xffffu)));
-                gp_block(buf, b, B, sc, m ? au : ag);
+                gp_block<NA>(buf, b, B, sc, m ? au : ag);
             }
         }
     };
@@ -247,7 +273,7 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
     // (every full step issues the same loads, so the compiler's own wait counts agree)
     auto step = [&](GuRegs &r, GuRegs &rn, int kc) {
         issue(rn, kc + 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(GU_LOADS) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gp_gu_loads(NA)) : "memory");
         gp_barrier();  // every wave's part of chunk kc's activations is in shared memory
         compute(r, kc);
         gp_barrier();  // every wave is done with buffer kc&1 before it is refilled
@@ -273,7 +299,7 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
     // lane l holds inputs 16i + 4(l/16) + k, row l % 16 of the wave's panel
     const int f = 16 * P + (lane & 15);
 #pragma unroll
-    for (int i = 0; i < GP_TOK / 16; i++)
+    for (int i = 0; i < NA; i++)
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int in = 16 * i + 4 * (lane >> 4) + k;
@@ -285,19 +311,26 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
         }
 }
 
-// grid (D/64, max tiles). Wave w computes D rows 64 p + 16 w .. +16 for the tile's
-// inputs (list rows), from h's split form; down is in the column-slice layout.
+__global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
+    __shared__ __align__(16) gp_abuf_t abuf;
+    if ((int)blockIdx.y >= *a.n_tiles) return;
+    const GpTile tl = a.tiles[blockIdx.y];
+    gp_with_na<GP_NA_MAX>(__builtin_amdgcn_readfirstlane((tl.count + 15) >> 4),
+                          [&](auto NA) { gp_gu_tile<decltype(NA)::value>(a, tl, abuf); });
+}
+
+// k_group_down: grid (D/64, max tiles). Wave w computes D rows 64 p + 16 w .. +16 for the
+// tile's inputs (list rows), from h's split form; down is in the column-slice layout.
 struct DnRegs {
     unsigned long long q[GP_NB];  // the chunk's blocks: 8 bytes of the row each
     unsigned short s[GP_NB];
 };
-#define DN_LOADS (2 * GP_NB + GP_STAGE_ITERS)  // loads per chunk and thread
+// loads per chunk and thread
+__host__ __device__ constexpr int gp_dn_loads(int na) { return 2 * GP_NB + gp_stage_iters(na); }
 
-__global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_down(GroupArgs a) {
-    __shared__ __align__(16) uint8_t abuf[2][GP_TOK * 2 * GP_RB];
-    const int p = blockIdx.x, ti = blockIdx.y;
-    if (ti >= *a.n_tiles) return;
-    const GpTile tl = a.tiles[ti];
+template <int NA>
+__device__ __attribute__((always_inline)) static inline void gp_down_tile(const GroupArgs &a, const GpTile &tl, gp_abuf_t &abuf) {
+    const int p = blockIdx.x;
     const int D = a.D, F = a.F, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const uint8_t *base = a.experts + (size_t)tl.e * a.stride;
     const int row = 64 * p + 16 * w + (lane & 15), qh = lane >> 4;
@@ -305,31 +338,32 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_down(GroupArgs a) {
     const GM_GLOBAL uint8_t *qd = gbl(base + a.off_dq) + (size_t)row * 16 + 8 * (qh & 1);
     const GM_GLOBAL unsigned short *sd = gbl((const unsigned short *)(base + a.off_ds)) + row;
     auto src_row = [&](int i) { return tl.row + (i < tl.count ? i : 0); };
-    const GpStage stg = gp_stage_init(a.aspl, F, src_row);
+    const GpStage<NA> stg = gp_stage_init<NA>(a.aspl, F, src_row);
     const int nkc = F / GP_KC;
-    float acc[GP_TOK / 16][4];
+    float acc[NA][4];
 #pragma unroll
-    for (int i = 0; i < GP_TOK / 16; i++)
+    for (int i = 0; i < NA; i++)
 #pragma unroll
         for (int k = 0; k < 4; k++) acc[i][k] = 0.0f;
-    auto issue = [&](DnRegs &r, int kc) {  // DN_LOADS loads
+    auto issue = [&](DnRegs &r, int kc) {  // gp_dn_loads(NA) loads
 #pragma unroll
         for (int b = 0; b < GP_NB; b++) {
             const int blk = GP_NB * kc + b;
             r.q[b] = *(const GM_GLOBAL unsigned long long *)(qd + ((size_t)(2 * blk + (qh >> 1)) * D) * 16);
             r.s[b] = sd[(size_t)blk * D];
         }
-        gp_stage(stg, abuf[kc & 1], kc * GP_KC);
+        gp_stage<NA>(stg, abuf[kc & 1], kc * GP_KC);
     };
     auto compute = [&](const DnRegs &r, int kc) {
         const uint8_t *buf = abuf[kc & 1];
 #pragma unroll
         for (int b = 0; b < GP_NB; b++)
-            gp_block(buf, b, gp_i8_to_h8((unsigned)r.q[b], (unsigned)(r.q[b] >> 32)), __half2float(__ushort_as_half(r.s[b])), acc);
+            gp_block<NA>(buf, b, gp_i8_to_h8((unsigned)r.q[b], (unsigned)(r.q[b] >> 32)), __half2float(__ushort_as_half(r.s[b])),
+                         acc);
     };
     auto step = [&](DnRegs &r, DnRegs &rn, int kc) {
         issue(rn, kc + 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DN_LOADS) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gp_dn_loads(NA)) : "memory");
         gp_barrier();
         compute(r, kc);
         gp_barrier();
@@ -353,7 +387,7 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_down(GroupArgs a) {
         last(r0, kc);
     }
 #pragma unroll
-    for (int i = 0; i < GP_TOK / 16; i++)
+    for (int i = 0; i < NA; i++)
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const int in = 16 * i + 4 * (lane >> 4) + k;
@@ -362,6 +396,14 @@ __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_down(GroupArgs a) {
                 a.out[(size_t)r * D + row] = ldexpf(acc[i][k], a.aexp[r]);
             }
         }
+}
+
+__global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_down(GroupArgs a) {
+    __shared__ __align__(16) gp_abuf_t abuf;
+    if ((int)blockIdx.y >= *a.n_tiles) return;
+    const GpTile tl = a.tiles[blockIdx.y];
+    gp_with_na<GP_NA_MAX>(__builtin_amdgcn_readfirstlane((tl.count + 15) >> 4),
+                          [&](auto NA) { gp_down_tile<decltype(NA)::value>(a, tl, abuf); });
 }
 
 struct TokenCombineArgs {
