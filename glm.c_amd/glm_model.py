@@ -200,3 +200,76 @@ class GlmModel:
 
     def free(self, backend=BACKEND_HIP):
         backend_lib().glm_backend_free(backend)
+
+
+def forward_lib():
+    """libglm_hip.so's token forward (include/glm_forward.h)."""
+    lib = backend_lib()
+    if not getattr(lib, "_forward_typed", False):
+        RP, SP, FP, IP = C.POINTER(Runtime), C.POINTER(RunState), C.POINTER(C.c_float), C.POINTER(C.c_int)
+        lib.glm_runstate_build.argtypes = [SP, RP, C.c_int]
+        lib.glm_runstate_build.restype = C.c_int
+        lib.glm_runstate_free.argtypes = [SP]
+        lib.glm_runstate_free.restype = None
+        lib.glm_hip_forward_token.argtypes = [RP, SP, C.c_int, C.c_int, C.c_int]
+        lib.glm_hip_forward_token.restype = C.c_int
+        lib.glm_hip_forward_token_dual_checkpoints.argtypes = [RP, SP, C.c_int, C.c_int, C.c_int, FP, C.c_int, C.c_int,
+                                                               IP, FP, C.c_int, C.c_int, IP]
+        lib.glm_hip_forward_token_dual_checkpoints.restype = C.c_int
+        lib.glm_argmax.argtypes = [FP, C.c_int]
+        lib.glm_argmax.restype = C.c_int
+        lib._forward_typed = True
+    return lib
+
+
+class Decoder:
+    """glm.c's decode state on a Checkpoint: a RunState from glm_runstate_build with a
+    latent cache of cache_cap positions, advanced one token at a time by
+    glm_hip_forward_token (the MoE layers on the GPU after glm_backend_init(BACKEND_HIP),
+    which a checkpoint without MoE layers does not need)."""
+
+    def __init__(self, checkpoint, cache_cap):
+        self.lib = forward_lib()
+        self.ckpt = checkpoint
+        self.rt = checkpoint.rt
+        self.st = RunState()
+        if self.lib.glm_runstate_build(C.byref(self.st), C.byref(self.rt), cache_cap) != 0:
+            raise RuntimeError("glm_runstate_build failed")
+        c = self.rt.cfg
+        self.L, self.D, self.V = c.n_layers, c.dim, c.vocab_size
+        self.backend = BACKEND_CPU
+        if self.rt.has_moe_shared and c.n_layers > 1:
+            self.backend = self.lib.glm_backend_init(BACKEND_HIP, C.byref(self.rt), C.byref(self.st))
+
+    def logits(self):
+        return np.ctypeslib.as_array(C.cast(self.st.logits, C.POINTER(C.c_float)), shape=(self.V,)).copy()
+
+    def step(self, token, pos, checkpoints=False):
+        """One token at position pos; returns the logits, and with checkpoints also x after
+        each layer's attention and after its FFN ([n_layers][dim] each) from
+        glm_hip_forward_token_dual_checkpoints on the state before the step."""
+        FP = C.POINTER(C.c_float)
+        attn = layer = None
+        if checkpoints:
+            attn = np.zeros((self.L, self.D), np.float32)
+            layer = np.zeros((self.L, self.D), np.float32)
+            na, nl = C.c_int(), C.c_int()
+            rc = self.lib.glm_hip_forward_token_dual_checkpoints(
+                C.byref(self.rt), C.byref(self.st), token, pos, 0, attn.ctypes.data_as(FP), self.D, self.L,
+                C.byref(na), layer.ctypes.data_as(FP), self.D, self.L, C.byref(nl))
+            if rc != 0:
+                raise RuntimeError(f"glm_hip_forward_token_dual_checkpoints failed at pos {pos}")
+        if self.lib.glm_hip_forward_token(C.byref(self.rt), C.byref(self.st), token, pos, 0) != 0:
+            raise RuntimeError(f"glm_hip_forward_token failed at pos {pos}")
+        out = self.logits()
+        return (out, attn, layer) if checkpoints else out
+
+    def argmax(self):
+        return self.lib.glm_argmax(C.cast(self.st.logits, C.POINTER(C.c_float)), self.V)
+
+    def free(self):
+        if self.backend == BACKEND_HIP:
+            self.lib.glm_backend_free(BACKEND_HIP)
+            self.backend = BACKEND_CPU
+        if self.st.x:
+            self.lib.glm_runstate_free(C.byref(self.st))

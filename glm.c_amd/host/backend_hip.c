@@ -2,10 +2,11 @@
  * backend_hip.c -- the --backend hip drop-in for glm.c's backend layer (backend.c).
  *
  * glm.c selects a backend once (glm_backend_init, infer.c:2174) and then runs every
- * token through glm_backend_forward_token (infer.c:2195). This backend keeps glm.c's
- * CPU forward for embedding, attention, the dense layer 0 and the LM head, and takes
- * over each MoE FFN layer (apply_moe_shared_ffn_layer, infer.c:1087-1216) through
- * glm_backend_try_hip_moe, called from the layer loop (infer.c:1844-1845). Expert
+ * token through glm_backend_forward_token (infer.c:2195). With BACKEND_HIP that is
+ * glm_hip_forward_token (forward.c): glm.c's forward with every MoE FFN layer
+ * (apply_moe_shared_ffn_layer, infer.c:1087-1216) on the GPU. A glm.c that keeps its
+ * own forward can instead offload the MoE layers one at a time through
+ * glm_backend_try_hip_moe, called from its layer loop (infer.c:1844-1845). Expert
  * weights are uploaded once, at init, into device memory by libgmoe.so.
  *
  * Messages use the "[glm-hip]" prefix, like backend.c's "[glm-metal]".
@@ -19,6 +20,7 @@
 #include <string.h>
 
 #include "glm_backend.h"
+#include "glm_forward.h"
 #include "gmoe.h"
 
 _Static_assert(sizeof(int) == sizeof(int32_t), "RunState.moe_topk_idx is int; the ABI uses int32_t");
@@ -216,7 +218,8 @@ int glm_backend_init(BackendType backend, const Runtime *rt, RunState *st) {
 }
 
 int glm_backend_forward_token(int use_gpu, const Runtime *rt, RunState *st, int token, int pos, int debug_mode) {
-    (void)use_gpu; /* the HIP backend runs inside the CPU forward, one MoE layer at a time */
+    if (use_gpu == (int)BACKEND_HIP) return glm_hip_forward_token(rt, st, token, pos, debug_mode);
+    /* the CPU backend: glm.c's own forward (backend.c:88-91) */
     if (!glm_cpu_forward_token) {
         fprintf(stderr, "[glm-hip] glm_cpu_forward_token is not linked in\n");
         return -1;

@@ -5,7 +5,9 @@
  *   glm_backend_init     returns the "use gpu" handle (0 = CPU, BACKEND_HIP = HIP) and
  *                        exits the process when the requested backend cannot start,
  *                        as backend.c:73-86 does for Metal;
- *   glm_backend_forward_token  0 on success, nonzero on failure (backend.c:88-91);
+ *   glm_backend_forward_token  0 on success, nonzero on failure (backend.c:88-91); with
+ *                        BACKEND_HIP it runs glm_hip_forward_token (glm_forward.h), with
+ *                        0 glm.c's own glm_cpu_forward_token when that is linked in;
  *   glm_backend_free.
  * glm_backend_try_hip_moe is the HIP counterpart of the per-op offload hook
  * glm_backend_try_metal_matvec (backend.h:13, called at infer.c:793): it runs one

@@ -231,3 +231,29 @@ int ref_ckpt_layout(const char *path, uint64_t *out, int max, void *cfg_out) {
     runtime_close(&rt);
     return n;
 }
+
+/* glm.c's own token forward on the checkpoint at `path` (runtime_open, runstate_build,
+ * infer.c:357-744, 827-860; a child process, as for ref_ckpt_layout): tokens[i] at
+ * position i for i < n, teacher-forced. Per position, glm_cpu_forward_token_dual_checkpoints
+ * (infer.c:1940-1983) gives x after each layer's attention and after its FFN, into
+ * attn_out and layer_out ([n][n_layers][dim]), and glm_cpu_forward_token (infer.c:1903)
+ * then advances the state, whose logits go to logits ([n][vocab]). 0, or -1. */
+int ref_decode(const char *path, const int *tokens, int n, int cache_cap, float *attn_out, float *layer_out,
+               float *logits) {
+    Runtime rt;
+    runtime_open(&rt, path);
+    RunState st;
+    runstate_build(&st, &rt, cache_cap);
+    const int L = rt.cfg.n_layers, dim = rt.cfg.dim, V = rt.cfg.vocab_size;
+    int rc = 0;
+    for (int i = 0; i < n && !rc; i++) {
+        int wa = 0, wl = 0;
+        rc = glm_cpu_forward_token_dual_checkpoints(&rt, &st, tokens[i], i, 0, attn_out + (size_t)i * L * dim, dim, L,
+                                                    &wa, layer_out + (size_t)i * L * dim, dim, L, &wl);
+        if (!rc) rc = glm_cpu_forward_token(&rt, &st, tokens[i], i, 0);
+        if (!rc) memcpy(logits + (size_t)i * V, st.logits, (size_t)V * sizeof(float));
+    }
+    runstate_free(&st);
+    runtime_close(&rt);
+    return rc;
+}

@@ -1,0 +1,115 @@
+"""glm.c's token forward with the MoE layers on the GPU (glm_hip_forward_token, what
+glm_backend_forward_token runs for BACKEND_HIP) against glm.c's own forward
+(infer.c:1767-1901, compiled into oracle/_ref) on synthetic v4 checkpoints.
+
+Teacher-forced: the same tokens at the same positions on both sides, with glm.c's dual
+checkpoints (infer.c:1940-1983) per position. Layer 0 (attention and dense FFN) never
+sees a GPU result, so its x after attention and after the FFN equals glm.c's bit for
+bit at every position. From layer 1 on, x carries the GPU MoE layers' rounding: every
+later checkpoint and the logits are held to the FFN bar, max-abs 1e-2 and rel-L2 1e-3,
+and each position's argmax equals glm.c's.
+
+Greedy: the decoder picks each next token itself (argmax, with infer.c:2213-2219's
+bos/eos skips), and glm.c, fed the same sequence, picks the same token at every step."""
+import numpy as np
+import pytest
+
+import glm_model
+import gmoe
+import ref_decode
+from conftest import assert_close
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not ref_decode.available(), reason="oracle/_ref not built (needs the reference sources)")]
+
+
+def small(gs, scale_mode, n_layers=4, seed=21):
+    return glm_model.CkptSpec(dim=256, hidden_dim=512, n_layers=n_layers, n_heads=4, n_kv_heads=4, vocab_size=300,
+                              seq_len=64, rope_dim=16, q_lora_rank=64, kv_lora_rank=64, n_routed_experts=8,
+                              n_experts_used=2, bos_id=1, eos_id=2, qk_nope_dim=32, v_head_dim=32, moe_ffn_dim=256,
+                              group_size=gs, seed=seed, norm_mode=gmoe.SYNTH_NORM_RANDOM,
+                              bias_mode=gmoe.SYNTH_BIAS_NORMAL, scale_mode=scale_mode)
+
+
+def glm_dims(seed=22):
+    """GLM-4.7-Flash's MoE dimensions (D 2048, F 1536, 64 experts, top-4, group size 32),
+    with a small vocabulary, four heads and two MoE layers."""
+    return glm_model.CkptSpec(dim=2048, hidden_dim=1024, n_layers=3, n_heads=4, n_kv_heads=4, vocab_size=1000,
+                              seq_len=64, rope_dim=64, q_lora_rank=256, kv_lora_rank=512, n_routed_experts=64,
+                              n_experts_used=4, bos_id=1, eos_id=2, qk_nope_dim=192, v_head_dim=256, moe_ffn_dim=1536,
+                              group_size=32, seed=seed, norm_mode=gmoe.SYNTH_NORM_RANDOM,
+                              bias_mode=gmoe.SYNTH_BIAS_NORMAL, scale_mode=gmoe.SYNTH_SCALES_FP16)
+
+
+CASES = {"gs16_native": lambda: small(16, gmoe.SYNTH_SCALES_FP32), "gs32_tiled": lambda: small(32, gmoe.SYNTH_SCALES_FP16),
+         "glm_dims": glm_dims}
+TOKENS = [1, 5, 17, 299, 42, 0, 17, 123, 7, 250]
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def open_decoder(tmp_path, sp, cap):
+    path = tmp_path / "model.bin"
+    glm_model.write_synth_checkpoint(path, sp)
+    ck = glm_model.Checkpoint(path)
+    dec = glm_model.Decoder(ck, cap)
+    assert dec.backend == glm_model.BACKEND_HIP
+    return path, ck, dec
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_teacher_forced_positions_match_glm(tmp_path, case):
+    sp = CASES[case]()
+    tokens = [t % sp.vocab_size for t in TOKENS]
+    cap = len(tokens) + 2
+    path, ck, dec = open_decoder(tmp_path, sp, cap)
+    try:
+        ref = ref_decode.reference_decode(path, tokens, cap, dec.L, dec.D, dec.V, tmp_path / "ref")
+        for pos, tok in enumerate(tokens):
+            print(f"[case] forward {case} pos {pos} token {tok}", flush=True)
+            logits, attn, layer = dec.step(tok, pos, checkpoints=True)
+            assert np.array_equal(bits(attn[0]), bits(ref["attn"][pos][0])), f"pos {pos}: layer 0 attention"
+            assert np.array_equal(bits(layer[0]), bits(ref["layer"][pos][0])), f"pos {pos}: layer 0 FFN"
+            for l in range(1, dec.L):
+                assert_close(attn[l], ref["attn"][pos][l], f"pos {pos} layer {l} attention")
+                assert_close(layer[l], ref["layer"][pos][l], f"pos {pos} layer {l} MoE")
+            assert_close(logits, ref["logits"][pos], f"pos {pos} logits")
+            assert int(np.argmax(logits)) == int(np.argmax(ref["logits"][pos])), f"pos {pos}: argmax"
+    finally:
+        dec.free()
+        ck.close()
+
+
+def next_token(logits, sp):
+    """infer.c:2212-2219 at temperature 0 (bench mode: eos is skipped, not a stop)."""
+    t = int(np.argmax(logits))
+    if t == sp.bos_id:
+        t = (t + 1) % sp.vocab_size
+    if t == sp.eos_id:
+        t = (t + 1) % sp.vocab_size
+    return t
+
+
+@pytest.mark.parametrize("case", ["gs32_tiled", "glm_dims"])
+def test_greedy_decode_picks_glms_tokens(tmp_path, case):
+    sp = CASES[case]()
+    prompt, n_new = [1, 5, 17], 8
+    cap = len(prompt) + n_new + 1
+    path, ck, dec = open_decoder(tmp_path, sp, cap)
+    try:
+        seq, picked = list(prompt), []
+        for pos in range(len(prompt) + n_new - 1):
+            logits = dec.step(seq[pos], pos)
+            if pos + 1 >= len(prompt):
+                picked.append(next_token(logits, sp))
+                seq.append(picked[-1])
+        print(f"[case] greedy {case}: {seq}", flush=True)
+        ref = ref_decode.reference_decode(path, seq, cap, dec.L, dec.D, dec.V, tmp_path / "ref")
+        for i, t in enumerate(picked):
+            pos = len(prompt) - 1 + i
+            assert next_token(ref["logits"][pos], sp) == t, f"step {i} (pos {pos})"
+    finally:
+        dec.free()
+        ck.close()
