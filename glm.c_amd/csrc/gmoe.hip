@@ -62,6 +62,14 @@ static void set_err(const char *fmt, ...) {
     va_end(ap);
 }
 
+// The same message slot for the library's other translation units (model.hip).
+__attribute__((visibility("hidden"))) void gm_set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
 #define HIP_OK(expr)                                                                     \
     do {                                                                                 \
         hipError_t err_ = (expr);                                                        \
@@ -819,6 +827,10 @@ static int take_launch_error(gmoe_ctx *c) {
     set_err("%s", k_timeout_msg);
     return GMOE_ERR_HIP;
 }
+
+// take_launch_error for the library's other translation units (model.hip), called after
+// they have synchronised the stream of their launches.
+__attribute__((visibility("hidden"))) int gm_take_launch_error(gmoe_ctx *c) { return c ? take_launch_error(c) : GMOE_OK; }
 
 // 0, or GMOE_ERR_HIP if the most recent persistent launch timed out (synchronises).
 static int check_stack_error(gmoe_ctx *c) {

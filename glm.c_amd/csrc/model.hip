@@ -1,0 +1,460 @@
+// model.hip -- gmoe_model (include/gmoe_model.h): glm.c's decode forward (infer.c:1767-1901)
+// with every weight, the latent cache and x in device memory. Per token, on one stream:
+//
+//   k_embed                      x = the token's embedding row
+//   per attention layer (infer.c:978-1065):
+//     k_gemv                     q_a = q_a . rmsnorm(x), kv_a = kv_a . rmsnorm(x)
+//     k_gemv                     q = q_b . rmsnorm(q_a)
+//     k_attn_prep                the position's cache entry (normalised kv, rotated rope
+//                                part) and every head's rotated query part
+//     k_gemv (per head)          q_abs = k_b_h . q_nope_h
+//     k_attn_part, k_attn_combine  softmax over the cache, weighted sum of entries
+//     k_gemv (per head)          concat_h = v_b_h . ctx_h
+//     k_gemv (residual)          x += attn_out . concat
+//   layer 0: k_gemv (SwiGLU pair), k_gemv (residual): the dense FFN (infer.c:1067-1085)
+//   layers 1..: gmoe_forward of the MoE context, in place on x
+//   k_gemv                       logits = out . rmsnorm(x)
+//
+// The rope angles' cosines and sines are computed once on the host with libm, as glm.c
+// computes them (infer.c:964-976), so the rotations are glm.c's to the bit.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "gmoe_model.h"
+#include "common.h"
+#include "dense.h"
+
+// gmoe.hip
+void gm_set_err(const char *fmt, ...);
+int gm_take_launch_error(gmoe_ctx *c);
+
+#define MH_OK(expr)                                                                                  \
+    do {                                                                                             \
+        hipError_t e_ = (expr);                                                                      \
+        if (e_ != hipSuccess) {                                                                      \
+            gm_set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+            return GMOE_ERR_HIP;                                                                     \
+        }                                                                                            \
+    } while (0)
+
+namespace {
+
+struct AttnDev {
+    float *attn_norm = nullptr, *q_a_norm = nullptr, *kv_a_norm = nullptr;
+    int8_t *q_a_q = nullptr, *q_b_q = nullptr, *kv_a_q = nullptr, *k_b_q = nullptr, *v_b_q = nullptr, *out_q = nullptr;
+    float *q_a_s = nullptr, *q_b_s = nullptr, *kv_a_s = nullptr, *k_b_s = nullptr, *v_b_s = nullptr, *out_s = nullptr;
+    bool set = false;
+};
+
+}  // namespace
+
+struct gmoe_model {
+    int device = 0;
+    gmoe_model_config c{};
+    gmoe_ctx *moe = nullptr;
+    std::vector<uint8_t> moe_on;
+    int moe_flags = 0;
+    // model-wide tensors
+    float *output_norm = nullptr, *tok_s = nullptr, *out_s = nullptr;
+    int8_t *tok_q = nullptr, *out_q = nullptr;
+    float *l0_norm = nullptr, *l0_gate_s = nullptr, *l0_up_s = nullptr, *l0_down_s = nullptr;
+    int8_t *l0_gate_q = nullptr, *l0_up_q = nullptr, *l0_down_q = nullptr;
+    bool globals = false;
+    std::vector<AttnDev> attn;
+    // the latent cache [attn_layers][cap][kv], [..][rope] and the rope table [cap][rope/2][2]
+    float *comp = nullptr, *pe = nullptr, *rope_cs = nullptr;
+    // activations
+    float *x = nullptr, *q_a = nullptr, *q_full = nullptr, *kv_a = nullptr, *q_pe = nullptr, *q_abs = nullptr,
+          *ctx = nullptr, *concat = nullptr, *ffh = nullptr, *logits = nullptr, *part_ctx = nullptr,
+          *part_ml = nullptr, *saved = nullptr;
+    std::vector<void *> allocs;  // every device allocation, freed by gmoe_model_destroy
+};
+
+namespace {
+
+template <typename T>
+int mdalloc(gmoe_model *m, T **p, size_t n) {
+    *p = nullptr;
+    if (n == 0) n = 1;
+    const hipError_t e = hipMalloc((void **)p, n * sizeof(T));
+    if (e != hipSuccess) {
+        gm_set_err("gmoe_model: hipMalloc of %zu bytes failed: %s", n * sizeof(T), hipGetErrorString(e));
+        *p = nullptr;
+        return GMOE_ERR_NOMEM;
+    }
+    m->allocs.push_back(*p);
+    return GMOE_OK;
+}
+
+// Device copy of n elements from host src into *dst (allocated on first use).
+template <typename T>
+int upload(gmoe_model *m, T **dst, const T *src, size_t n, const char *what) {
+    if (!src) {
+        gm_set_err("gmoe_model: %s is missing", what);
+        return GMOE_ERR_INVALID;
+    }
+    if (!*dst) {
+        if (int rc = mdalloc(m, dst, n)) return rc;
+    }
+    MH_OK(hipMemcpy(*dst, src, n * sizeof(T), hipMemcpyHostToDevice));
+    return GMOE_OK;
+}
+
+// The k_gemv instance for cols columns: 16 lanes per row up to 64 units of 16 columns,
+// a whole wave per row beyond (at most 640 units).
+template <int MODE>
+int launch_gemv_mode(const GemvArgs &a, hipStream_t st) {
+    const int units = a.cols >> 4;
+    const int lpr = units <= 64 ? 16 : 64;
+    const int rpw = 64 / lpr, nrg = (a.rows + rpw - 1) / rpw;
+    const dim3 grid((unsigned)std::min((nrg + 3) / 4, 2048)), block(DM_BLOCK);
+    if (lpr == 16) {
+        switch ((units + 15) / 16) {
+        case 1: hipLaunchKernelGGL((k_gemv<16, 1, MODE>), grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL((k_gemv<16, 2, MODE>), grid, block, 0, st, a); break;
+        case 3: hipLaunchKernelGGL((k_gemv<16, 3, MODE>), grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL((k_gemv<16, 4, MODE>), grid, block, 0, st, a); break;
+        }
+    } else {
+        switch ((units + 63) / 64) {
+        case 2: hipLaunchKernelGGL((k_gemv<64, 2, MODE>), grid, block, 0, st, a); break;
+        case 3: hipLaunchKernelGGL((k_gemv<64, 3, MODE>), grid, block, 0, st, a); break;
+        case 4: hipLaunchKernelGGL((k_gemv<64, 4, MODE>), grid, block, 0, st, a); break;
+        case 5: hipLaunchKernelGGL((k_gemv<64, 5, MODE>), grid, block, 0, st, a); break;
+        case 6: hipLaunchKernelGGL((k_gemv<64, 6, MODE>), grid, block, 0, st, a); break;
+        case 7:
+        case 8: hipLaunchKernelGGL((k_gemv<64, 8, MODE>), grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL((k_gemv<64, 10, MODE>), grid, block, 0, st, a); break;
+        }
+    }
+    return GMOE_OK;
+}
+
+int launch_gemv(const GemvArgs &a, int mode, hipStream_t st) {
+    if (mode == GV_RESID) return launch_gemv_mode<GV_RESID>(a, st);
+    if (mode == GV_PAIR) return launch_gemv_mode<GV_PAIR>(a, st);
+    return launch_gemv_mode<GV_PLAIN>(a, st);
+}
+
+// y = q . x for one shared input (normalised by norm when given).
+GemvArgs gemv(const int8_t *q, const float *s, const float *x, const float *norm, float *y, int rows, int cols, int gs) {
+    GemvArgs a{};
+    a.q = q;
+    a.s = s;
+    a.x = x;
+    a.norm = norm;
+    a.y = y;
+    a.rows = rows;
+    a.cols = cols;
+    a.gs = gs;
+    a.x_rows = 1 << 30;
+    a.x_stride = 0;
+    return a;
+}
+
+constexpr int kMaxCols = 16 * 64 * 10;  // the widest k_gemv instance
+
+int check_config(const gmoe_model_config &c) {
+    const int gs = c.group_size;
+    auto cols_ok = [&](int n) { return n > 0 && n % 16 == 0 && n % gs == 0 && n <= kMaxCols; };
+    if (gs < 16 || gs % 16 || c.dim <= 0 || c.n_layers < 1 || c.vocab_size < 1) {
+        gm_set_err("gmoe_model_create: need group_size a multiple of 16 and positive dim, n_layers, vocab_size");
+        return GMOE_ERR_INVALID;
+    }
+    if (!cols_ok(c.dim)) {
+        gm_set_err("gmoe_model_create: dim %d must be a multiple of 16 and of group_size, at most %d", c.dim, kMaxCols);
+        return GMOE_ERR_INVALID;
+    }
+    if (c.has_l0_ffn && !cols_ok(c.hidden_dim)) {
+        gm_set_err("gmoe_model_create: hidden_dim %d must be a multiple of 16 and of group_size, at most %d", c.hidden_dim,
+                   kMaxCols);
+        return GMOE_ERR_INVALID;
+    }
+    if (c.attn_layers != 0 && c.attn_layers != 1 && c.attn_layers != c.n_layers) {
+        gm_set_err("gmoe_model_create: attn_layers must be 0, 1 or n_layers (got %d)", c.attn_layers);
+        return GMOE_ERR_INVALID;
+    }
+    if (c.cache_cap < 1 || c.cache_cap > 65536) {
+        gm_set_err("gmoe_model_create: cache_cap %d outside 1..65536", c.cache_cap);
+        return GMOE_ERR_INVALID;
+    }
+    if (c.attn_layers > 0) {
+        const int H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim;
+        if (H < 1 || kv < 64 || kv % 64 || kv > AT_KV_MAX || rope < 2 || rope % 2 || rope > AT_ROPE_MAX ||
+            c.head_k_dim != c.qk_nope_dim + rope || c.head_k_dim % 4 || c.v_head_dim < 4 || c.v_head_dim % 4 ||
+            !cols_ok(c.q_lora_rank) || !cols_ok(c.qk_nope_dim) || !cols_ok(kv) || !cols_ok(H * c.v_head_dim)) {
+            gm_set_err("gmoe_model_create: attention shape not supported (heads %d, q_lora %d, kv_lora %d, rope %d, "
+                       "nope %d, head_k %d, v_head %d, group %d): kv_lora a multiple of 64 up to %d, rope even up to %d, "
+                       "head_k = nope + rope, every product's columns multiples of 16 and of the group",
+                       H, c.q_lora_rank, kv, rope, c.qk_nope_dim, c.head_k_dim, c.v_head_dim, gs, AT_KV_MAX, AT_ROPE_MAX);
+            return GMOE_ERR_INVALID;
+        }
+    }
+    return GMOE_OK;
+}
+
+int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
+    const gmoe_model_config &c = m->c;
+    const AttnDev &A = m->attn[l];
+    const int gs = c.group_size, H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim;
+    launch_gemv(gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, c.q_lora_rank, c.dim, gs), GV_PLAIN, st);
+    launch_gemv(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, c.dim, gs), GV_PLAIN, st);
+    launch_gemv(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * c.head_k_dim, c.q_lora_rank, gs), GV_PLAIN, st);
+    AttnArgs aa{};
+    aa.kv_a = m->kv_a;
+    aa.kv_norm = A.kv_a_norm;
+    aa.q_full = m->q_full;
+    aa.rope_cs = m->rope_cs;
+    aa.comp = m->comp + (size_t)l * c.cache_cap * kv;
+    aa.pe = m->pe + (size_t)l * c.cache_cap * rope;
+    aa.q_pe = m->q_pe;
+    aa.q_abs = m->q_abs;
+    aa.part_ctx = m->part_ctx;
+    aa.part_ml = m->part_ml;
+    aa.ctx = m->ctx;
+    aa.H = H;
+    aa.kv = kv;
+    aa.rope = rope;
+    aa.head_k = c.head_k_dim;
+    aa.nope = c.qk_nope_dim;
+    aa.pos = pos;
+    aa.kq_scale = 1.0f / sqrtf((float)c.head_k_dim);  // infer.c:992
+    hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(DM_BLOCK), 0, st, aa);
+    // the query absorbed into the latent space, per head: k_b_h [kv][nope] . q_nope_h
+    GemvArgs kb = gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs);
+    kb.x_rows = kv;
+    kb.x_stride = c.head_k_dim;
+    launch_gemv(kb, GV_PLAIN, st);
+    const int chunks = pos / AT_CH + 1;
+    hipLaunchKernelGGL(k_attn_part, dim3(chunks, (H + AT_HG - 1) / AT_HG), dim3(DM_BLOCK), 0, st, aa);
+    hipLaunchKernelGGL(k_attn_combine, dim3(H), dim3(DM_BLOCK), 0, st, aa);
+    // back out of the latent space, per head: v_b_h [v_head][kv] . ctx_h
+    GemvArgs vb = gemv(A.v_b_q, A.v_b_s, m->ctx, nullptr, m->concat, H * c.v_head_dim, kv, gs);
+    vb.x_rows = c.v_head_dim;
+    vb.x_stride = kv;
+    launch_gemv(vb, GV_PLAIN, st);
+    GemvArgs ao = gemv(A.out_q, A.out_s, m->concat, nullptr, m->x, c.dim, H * c.v_head_dim, gs);
+    ao.resid = m->x;
+    launch_gemv(ao, GV_RESID, st);
+    return GMOE_OK;
+}
+
+int dense_ffn(gmoe_model *m, hipStream_t st) {
+    const gmoe_model_config &c = m->c;
+    GemvArgs gu = gemv(m->l0_gate_q, m->l0_gate_s, m->x, m->l0_norm, m->ffh, c.hidden_dim, c.dim, c.group_size);
+    gu.q2 = m->l0_up_q;
+    gu.s2 = m->l0_up_s;
+    launch_gemv(gu, GV_PAIR, st);
+    GemvArgs dn = gemv(m->l0_down_q, m->l0_down_s, m->ffh, nullptr, m->x, c.dim, c.hidden_dim, c.group_size);
+    dn.resid = m->x;
+    launch_gemv(dn, GV_RESID, st);
+    return GMOE_OK;
+}
+
+}  // namespace
+
+extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_config *cfg) {
+    if (!out || !cfg) {
+        gm_set_err("gmoe_model_create: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    *out = nullptr;
+    if (int rc = check_config(*cfg)) return rc;
+    MH_OK(hipSetDevice(device));
+    gmoe_model *m = new gmoe_model();
+    m->device = device;
+    m->c = *cfg;
+    const gmoe_model_config &c = m->c;
+    const size_t L = (size_t)c.n_layers, A = (size_t)c.attn_layers, cap = (size_t)c.cache_cap;
+    const size_t H = (size_t)c.n_heads, kv = (size_t)c.kv_lora_rank, rope = (size_t)c.rope_dim;
+    const size_t chunks = (cap + AT_CH - 1) / AT_CH;
+    m->attn.resize(A);
+    m->moe_on.assign(L, 0);
+    int rc = GMOE_OK;
+    rc |= mdalloc(m, &m->x, (size_t)c.dim);
+    rc |= mdalloc(m, &m->logits, (size_t)c.vocab_size);
+    if (c.has_l0_ffn) rc |= mdalloc(m, &m->ffh, (size_t)c.hidden_dim);
+    if (A > 0) {
+        rc |= mdalloc(m, &m->comp, A * cap * kv);
+        rc |= mdalloc(m, &m->pe, A * cap * rope);
+        rc |= mdalloc(m, &m->rope_cs, cap * rope);
+        rc |= mdalloc(m, &m->q_a, (size_t)c.q_lora_rank);
+        rc |= mdalloc(m, &m->q_full, H * (size_t)c.head_k_dim);
+        rc |= mdalloc(m, &m->kv_a, kv + rope);
+        rc |= mdalloc(m, &m->q_pe, H * rope);
+        rc |= mdalloc(m, &m->q_abs, H * kv);
+        rc |= mdalloc(m, &m->ctx, H * kv);
+        rc |= mdalloc(m, &m->concat, H * (size_t)c.v_head_dim);
+        rc |= mdalloc(m, &m->part_ctx, chunks * H * kv);
+        rc |= mdalloc(m, &m->part_ml, chunks * H * 2);
+        rc |= mdalloc(m, &m->saved, A * (kv + rope));
+    }
+    if (!rc && A > 0) {
+        // glm.c's angles (infer.c:964-976): pair i of position p turns by p * 1e6^(-2i / rope)
+        std::vector<float> cs(cap * rope);
+        for (size_t p = 0; p < cap; p++)
+            for (size_t i = 0; i + 1 < rope; i += 2) {
+                const float freq = powf(1000000.0f, -((float)i / (float)rope));
+                const float ang = (float)p * freq;
+                cs[p * rope + i] = cosf(ang);
+                cs[p * rope + i + 1] = sinf(ang);
+            }
+        if (hipMemcpy(m->rope_cs, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+            gm_set_err("gmoe_model_create: copy of the rope table failed");
+            rc = GMOE_ERR_HIP;
+        }
+        if (!rc && (hipMemset(m->comp, 0, A * cap * kv * sizeof(float)) != hipSuccess ||
+                    hipMemset(m->pe, 0, A * cap * rope * sizeof(float)) != hipSuccess)) {
+            gm_set_err("gmoe_model_create: clearing the cache failed");
+            rc = GMOE_ERR_HIP;
+        }
+    }
+    if (rc) {
+        gmoe_model_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return GMOE_OK;
+}
+
+extern "C" void gmoe_model_destroy(gmoe_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    for (void *p : m->allocs) (void)hipFree(p);
+    delete m;
+}
+
+extern "C" int gmoe_model_upload(gmoe_model *m, const gmoe_model_weights *w) {
+    if (!m || !w) {
+        gm_set_err("gmoe_model_upload: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    MH_OK(hipSetDevice(m->device));
+    const gmoe_model_config &c = m->c;
+    const size_t D = (size_t)c.dim, V = (size_t)c.vocab_size, gs = (size_t)c.group_size, F = (size_t)c.hidden_dim;
+    int rc = GMOE_OK;
+    if (!rc) rc = upload(m, &m->output_norm, w->output_norm, D, "output_norm");
+    if (!rc) rc = upload(m, &m->tok_q, w->tok_q, V * D, "tok_q");
+    if (!rc) rc = upload(m, &m->tok_s, w->tok_s, V * D / gs, "tok_s");
+    if (!rc) rc = upload(m, &m->out_q, w->out_q, V * D, "out_q");
+    if (!rc) rc = upload(m, &m->out_s, w->out_s, V * D / gs, "out_s");
+    if (c.has_l0_ffn) {
+        if (!rc) rc = upload(m, &m->l0_norm, w->l0_ffn_norm, D, "l0_ffn_norm");
+        if (!rc) rc = upload(m, &m->l0_gate_q, w->l0_ffn_gate_q, F * D, "l0_ffn_gate_q");
+        if (!rc) rc = upload(m, &m->l0_gate_s, w->l0_ffn_gate_s, F * D / gs, "l0_ffn_gate_s");
+        if (!rc) rc = upload(m, &m->l0_up_q, w->l0_ffn_up_q, F * D, "l0_ffn_up_q");
+        if (!rc) rc = upload(m, &m->l0_up_s, w->l0_ffn_up_s, F * D / gs, "l0_ffn_up_s");
+        if (!rc) rc = upload(m, &m->l0_down_q, w->l0_ffn_down_q, D * F, "l0_ffn_down_q");
+        if (!rc) rc = upload(m, &m->l0_down_s, w->l0_ffn_down_s, D * F / gs, "l0_ffn_down_s");
+    }
+    m->globals = rc == GMOE_OK;
+    return rc;
+}
+
+extern "C" int gmoe_model_upload_attn(gmoe_model *m, int layer, const gmoe_attn_weights *w) {
+    if (!m || !w || layer < 0 || layer >= m->c.attn_layers) {
+        gm_set_err("gmoe_model_upload_attn: bad arguments (layer %d of %d attention layers)", layer, m ? m->c.attn_layers : 0);
+        return GMOE_ERR_INVALID;
+    }
+    MH_OK(hipSetDevice(m->device));
+    const gmoe_model_config &c = m->c;
+    const size_t D = (size_t)c.dim, gs = (size_t)c.group_size, H = (size_t)c.n_heads, ql = (size_t)c.q_lora_rank;
+    const size_t kv = (size_t)c.kv_lora_rank, rope = (size_t)c.rope_dim, hk = (size_t)c.head_k_dim;
+    const size_t nope = (size_t)c.qk_nope_dim, vh = (size_t)c.v_head_dim;
+    AttnDev &A = m->attn[layer];
+    int rc = GMOE_OK;
+    if (!rc) rc = upload(m, &A.attn_norm, w->attn_norm, D, "attn_norm");
+    if (!rc) rc = upload(m, &A.q_a_norm, w->q_a_norm, ql, "q_a_norm");
+    if (!rc) rc = upload(m, &A.kv_a_norm, w->kv_a_norm, kv, "kv_a_norm");
+    if (!rc) rc = upload(m, &A.q_a_q, w->q_a_q, ql * D, "q_a_q");
+    if (!rc) rc = upload(m, &A.q_a_s, w->q_a_s, ql * D / gs, "q_a_s");
+    if (!rc) rc = upload(m, &A.q_b_q, w->q_b_q, H * hk * ql, "q_b_q");
+    if (!rc) rc = upload(m, &A.q_b_s, w->q_b_s, H * hk * ql / gs, "q_b_s");
+    if (!rc) rc = upload(m, &A.kv_a_q, w->kv_a_q, (kv + rope) * D, "kv_a_q");
+    if (!rc) rc = upload(m, &A.kv_a_s, w->kv_a_s, (kv + rope) * D / gs, "kv_a_s");
+    if (!rc) rc = upload(m, &A.k_b_q, w->k_b_q, H * kv * nope, "k_b_q");
+    if (!rc) rc = upload(m, &A.k_b_s, w->k_b_s, H * kv * nope / gs, "k_b_s");
+    if (!rc) rc = upload(m, &A.v_b_q, w->v_b_q, H * vh * kv, "v_b_q");
+    if (!rc) rc = upload(m, &A.v_b_s, w->v_b_s, H * vh * kv / gs, "v_b_s");
+    if (!rc) rc = upload(m, &A.out_q, w->attn_out_q, D * H * vh, "attn_out_q");
+    if (!rc) rc = upload(m, &A.out_s, w->attn_out_s, D * H * vh / gs, "attn_out_s");
+    A.set = rc == GMOE_OK;
+    return rc;
+}
+
+extern "C" int gmoe_model_set_moe(gmoe_model *m, gmoe_ctx *moe, const uint8_t *layers, int moe_flags) {
+    if (!m) {
+        gm_set_err("gmoe_model_set_moe: null model");
+        return GMOE_ERR_INVALID;
+    }
+    m->moe = moe;
+    m->moe_flags = moe_flags;
+    for (int l = 0; l < m->c.n_layers; l++) m->moe_on[l] = moe && layers && l > 0 ? layers[l] : 0;
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, float *x_out,
+                                        float *attn_ckpt, float *layer_ckpt, void *stream) {
+    if (!m || !logits) {
+        gm_set_err("gmoe_model_forward_token: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    const gmoe_model_config &c = m->c;
+    if (!m->globals) {
+        gm_set_err("gmoe_model_forward_token: gmoe_model_upload has not succeeded");
+        return GMOE_ERR_INVALID;
+    }
+    for (int l = 0; l < c.attn_layers; l++)
+        if (!m->attn[l].set) {
+            gm_set_err("gmoe_model_forward_token: attention layer %d is not uploaded", l);
+            return GMOE_ERR_INVALID;
+        }
+    if (c.attn_layers > 0 && (pos < 0 || pos >= c.cache_cap)) {
+        gm_set_err("gmoe_model_forward_token: position %d outside the cache (%d positions)", pos, c.cache_cap);
+        return GMOE_ERR_INVALID;
+    }
+    if (token < 0 || token >= c.vocab_size) token = 0;  // infer.c:1781
+    MH_OK(hipSetDevice(m->device));
+    hipStream_t st = (hipStream_t)stream;
+    const size_t D = (size_t)c.dim, kv = (size_t)c.kv_lora_rank, rope = (size_t)c.rope_dim, cap = (size_t)c.cache_cap;
+    const size_t A = (size_t)c.attn_layers;
+    const bool keep = (flags & GMOE_MODEL_KEEP_CACHE) && A > 0;
+    if (keep) {
+        // the entries this position is about to overwrite, one per attention layer
+        MH_OK(hipMemcpy2DAsync(m->saved, kv * sizeof(float), m->comp + pos * kv, cap * kv * sizeof(float),
+                               kv * sizeof(float), A, hipMemcpyDeviceToDevice, st));
+        MH_OK(hipMemcpy2DAsync(m->saved + A * kv, rope * sizeof(float), m->pe + pos * rope, cap * rope * sizeof(float),
+                               rope * sizeof(float), A, hipMemcpyDeviceToDevice, st));
+    }
+    hipLaunchKernelGGL(k_embed, dim3((unsigned)((D + DM_BLOCK - 1) / DM_BLOCK)), dim3(DM_BLOCK), 0, st, m->tok_q, m->tok_s,
+                       token, c.dim, c.group_size, m->x);
+    // the three model forms of infer.c:1817-1881
+    const int n_run = c.attn_layers == c.n_layers ? c.n_layers : 1;
+    int rc = GMOE_OK;
+    for (int l = 0; l < n_run && !rc; l++) {
+        if (A > 0) rc = attention(m, l, pos, st);
+        if (!rc && attn_ckpt) MH_OK(hipMemcpyAsync(attn_ckpt + l * D, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
+        if (!rc && l == 0 && c.has_l0_ffn) rc = dense_ffn(m, st);
+        if (!rc && l > 0 && m->moe_on[l]) rc = gmoe_forward(m->moe, l, 1, m->x, m->x, m->moe_flags, st);
+        if (!rc && layer_ckpt) MH_OK(hipMemcpyAsync(layer_ckpt + l * D, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
+    }
+    if (rc) return rc;
+    launch_gemv(gemv(m->out_q, m->out_s, m->x, m->output_norm, m->logits, c.vocab_size, c.dim, c.group_size), GV_PLAIN, st);
+    MH_OK(hipGetLastError());
+    MH_OK(hipMemcpyAsync(logits, m->logits, (size_t)c.vocab_size * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (x_out) MH_OK(hipMemcpyAsync(x_out, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (keep) {
+        MH_OK(hipMemcpy2DAsync(m->comp + pos * kv, cap * kv * sizeof(float), m->saved, kv * sizeof(float),
+                               kv * sizeof(float), A, hipMemcpyDeviceToDevice, st));
+        MH_OK(hipMemcpy2DAsync(m->pe + pos * rope, cap * rope * sizeof(float), m->saved + A * kv, rope * sizeof(float),
+                               rope * sizeof(float), A, hipMemcpyDeviceToDevice, st));
+    }
+    MH_OK(hipStreamSynchronize(st));
+    if (m->moe && gm_take_launch_error(m->moe)) return GMOE_ERR_HIP;
+    return GMOE_OK;
+}

@@ -218,6 +218,8 @@ def forward_lib():
         lib.glm_hip_forward_token_dual_checkpoints.restype = C.c_int
         lib.glm_argmax.argtypes = [FP, C.c_int]
         lib.glm_argmax.restype = C.c_int
+        lib.glm_hip_model_active.argtypes = []
+        lib.glm_hip_model_active.restype = C.c_int
         lib._forward_typed = True
     return lib
 
@@ -263,6 +265,10 @@ class Decoder:
             raise RuntimeError(f"glm_hip_forward_token failed at pos {pos}")
         out = self.logits()
         return (out, attn, layer) if checkpoints else out
+
+    def on_gpu(self):
+        """True when every step of the forward runs on the GPU model (gmoe_model.h)."""
+        return self.backend == BACKEND_HIP and bool(self.lib.glm_hip_model_active())
 
     def argmax(self):
         return self.lib.glm_argmax(C.cast(self.st.logits, C.POINTER(C.c_float)), self.V)

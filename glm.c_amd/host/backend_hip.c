@@ -12,6 +12,8 @@
  * Messages use the "[glm-hip]" prefix, like backend.c's "[glm-metal]".
  * Environment:
  *   GLM_HIP_DEVICE          HIP device index (default 0)
+ *   GLM_HIP_HOST_ATTN       keep embedding, attention, layer 0 and the LM head on the host
+ *                           (glm.c's own arithmetic, forward.c) instead of the GPU model
  *   GLM_HIP_STRICT          exit(1) when a GPU layer fails instead of returning -1
  *   GLM_DISABLE_MOE_ROUTED  skip routed experts, as infer.c:1161-1166 does
  */
@@ -22,6 +24,7 @@
 #include "glm_backend.h"
 #include "glm_forward.h"
 #include "gmoe.h"
+#include "gmoe_model.h"
 
 _Static_assert(sizeof(int) == sizeof(int32_t), "RunState.moe_topk_idx is int; the ABI uses int32_t");
 
@@ -29,9 +32,13 @@ _Static_assert(sizeof(int) == sizeof(int32_t), "RunState.moe_topk_idx is int; th
 int glm_cpu_forward_token(const Runtime *rt, RunState *st, int token, int pos, int debug_mode) __attribute__((weak));
 
 static gmoe_ctx *g_ctx = NULL;
+static gmoe_model *g_model = NULL; /* the whole forward on the GPU (gmoe_model.h), when built */
 static int g_active = 0;
 static gmoe_config g_cfg;  /* the context's config, kept to re-create it in the native form */
 static int g_device = 0;
+
+static int prepare_model(const Runtime *rt, const RunState *st);
+static int routed_disabled(void);
 
 /* "0"/"false" (any case of the first letter, as backend.c:48-55 accepts) mean off. */
 static int env_on(const char *name, int fallback) {
@@ -83,7 +90,6 @@ int glm_hip_init(const Runtime *rt, RunState *st) {
 }
 
 int glm_hip_prepare(const Runtime *rt, RunState *st) {
-    (void)st;
     if (!g_ctx || !rt) return -1;
     for (int l = 1; l < rt->cfg.n_layers; l++) {
         const LayerMoeShared *s = &rt->moe_layers[l];
@@ -130,6 +136,98 @@ int glm_hip_prepare(const Runtime *rt, RunState *st) {
         }
     }
     g_active = 1;
+    if (!env_on("GLM_HIP_HOST_ATTN", 0)) (void)prepare_model(rt, st);
+    return 0;
+}
+
+/* The device model for rt with a cache of st->cache_cap positions: every tensor outside the
+ * MoE layers uploaded, the MoE layers taken from g_ctx. 0, or -1 (and no model) when the
+ * checkpoint's shape is one the model's kernels do not take or the GPU refuses it. */
+static int prepare_model(const Runtime *rt, const RunState *st) {
+    const RuntimeConfig *c = &rt->cfg;
+    gmoe_model_config mc;
+    memset(&mc, 0, sizeof(mc));
+    mc.dim = c->dim;
+    mc.hidden_dim = c->hidden_dim;
+    mc.n_layers = c->n_layers;
+    mc.n_heads = c->n_heads;
+    mc.vocab_size = c->vocab_size;
+    mc.q_lora_rank = c->q_lora_rank;
+    mc.kv_lora_rank = c->kv_lora_rank;
+    mc.rope_dim = c->rope_dim;
+    mc.qk_nope_dim = c->l0_qk_nope_dim;
+    mc.head_k_dim = c->l0_head_k_dim;
+    mc.v_head_dim = c->l0_v_head_dim;
+    mc.group_size = (int32_t)c->group_size;
+    mc.cache_cap = st ? st->cache_cap : 0;
+    mc.attn_layers = rt->has_all_attn ? c->n_layers : (rt->has_l0_attn ? 1 : 0);
+    mc.has_l0_ffn = rt->has_l0_ffn;
+    gmoe_model *m = NULL;
+    if (gmoe_model_create(&m, g_device, &mc) != GMOE_OK) {
+        fprintf(stderr, "[glm-hip] %s; attention, layer 0 and the LM head stay on the host\n", gmoe_last_error());
+        return -1;
+    }
+    gmoe_model_weights w;
+    memset(&w, 0, sizeof(w));
+    w.output_norm = rt->output_norm;
+    w.tok_q = rt->tok_q;
+    w.tok_s = rt->tok_s;
+    w.out_q = rt->out_q;
+    w.out_s = rt->out_s;
+    w.l0_ffn_norm = rt->l0_ffn_norm;
+    w.l0_ffn_gate_q = rt->l0_ffn_gate_q;
+    w.l0_ffn_gate_s = rt->l0_ffn_gate_s;
+    w.l0_ffn_up_q = rt->l0_ffn_up_q;
+    w.l0_ffn_up_s = rt->l0_ffn_up_s;
+    w.l0_ffn_down_q = rt->l0_ffn_down_q;
+    w.l0_ffn_down_s = rt->l0_ffn_down_s;
+    int rc = gmoe_model_upload(m, &w);
+    for (int l = 0; l < mc.attn_layers && rc == GMOE_OK; l++) {
+        /* LayerAttnWeights and gmoe_attn_weights list the same tensors in the same order */
+        const LayerAttnWeights l0 = {rt->l0_attn_norm, rt->l0_q_a_norm, rt->l0_kv_a_norm, rt->l0_q_a_q, rt->l0_q_a_s,
+                                     rt->l0_q_b_q,     rt->l0_q_b_s,    rt->l0_kv_a_q,    rt->l0_kv_a_s, rt->l0_k_b_q,
+                                     rt->l0_k_b_s,     rt->l0_v_b_q,    rt->l0_v_b_s,     rt->l0_attn_out_q,
+                                     rt->l0_attn_out_s};
+        const LayerAttnWeights *a = rt->has_all_attn ? &rt->attn_layers[l] : &l0;
+        const gmoe_attn_weights aw = {a->attn_norm, a->q_a_norm, a->kv_a_norm, a->q_a_q,  a->q_a_s,
+                                      a->q_b_q,     a->q_b_s,    a->kv_a_q,    a->kv_a_s, a->k_b_q,
+                                      a->k_b_s,     a->v_b_q,    a->v_b_s,     a->attn_out_q, a->attn_out_s};
+        rc = gmoe_model_upload_attn(m, l, &aw);
+    }
+    if (rc == GMOE_OK) {
+        uint8_t *on = (uint8_t *)calloc((size_t)c->n_layers, 1);
+        if (!on) {
+            rc = GMOE_ERR_NOMEM;
+        } else {
+            for (int l = 1; l < c->n_layers; l++)
+                on[l] = (uint8_t)(rt->has_moe_shared && rt->moe_layers && rt->moe_layers[l].ffn_norm != NULL);
+            rc = gmoe_model_set_moe(m, g_ctx, on, routed_disabled() ? GMOE_FLAG_NO_ROUTED : 0);
+            free(on);
+        }
+    }
+    if (rc != GMOE_OK) {
+        fprintf(stderr, "[glm-hip] model upload failed: %s; attention, layer 0 and the LM head stay on the host\n",
+                gmoe_last_error());
+        gmoe_model_destroy(m);
+        return -1;
+    }
+    g_model = m;
+    return 0;
+}
+
+int glm_hip_model_active(void) { return g_model != NULL; }
+
+int glm_hip_model_forward(const Runtime *rt, RunState *st, int token, int pos, int keep_state, float *logits,
+                          float *attn_ckpt, float *layer_ckpt) {
+    (void)rt;
+    if (!g_model || !st) return -1;
+    const int rc = gmoe_model_forward_token(g_model, token, pos, keep_state ? GMOE_MODEL_KEEP_CACHE : 0,
+                                            logits ? logits : st->logits, keep_state ? NULL : st->x, attn_ckpt,
+                                            layer_ckpt, NULL);
+    if (rc != GMOE_OK) {
+        fprintf(stderr, "[glm-hip] forward at position %d failed: %s\n", pos, gmoe_last_error());
+        return -1;
+    }
     return 0;
 }
 
@@ -169,6 +267,8 @@ int glm_hip_moe_layer(const Runtime *rt, RunState *st, int layer_idx, int debug_
 }
 
 void glm_hip_free(void) {
+    if (g_model) gmoe_model_destroy(g_model);
+    g_model = NULL;
     if (g_ctx) gmoe_destroy(g_ctx);
     g_ctx = NULL;
     g_active = 0;

@@ -2,9 +2,12 @@
  * forward.c -- glm.c's token forward (infer.c:1767-1901) for the --backend hip drop-in.
  *
  * One token at one position: embedding (infer.c:1807-1810), then per layer the MLA
- * attention (infer.c:978-1065) and the FFN -- layer 0's dense FFN (infer.c:1067-1085)
- * on the host, every MoE layer (infer.c:1087-1216) on the GPU through
- * glm_hip_moe_layer -- then the final rmsnorm and the LM head (infer.c:1886-1893).
+ * attention (infer.c:978-1065) and the FFN -- layer 0's dense FFN (infer.c:1067-1085),
+ * every MoE layer (infer.c:1087-1216) -- then the final rmsnorm and the LM head
+ * (infer.c:1886-1893). When glm_hip_prepare built the GPU model (gmoe_model.h), all of it
+ * runs there, with x and the latent cache in device memory. Otherwise (GLM_HIP_HOST_ATTN,
+ * or a shape the model's kernels do not take) the steps below run on the host and each
+ * MoE layer on the GPU through glm_hip_moe_layer.
  *
  * The host operations repeat glm.c's arithmetic operation for operation: the same
  * accumulation types and orders, the same parallel-rows / SIMD-reduction loop shape in
@@ -240,9 +243,45 @@ static int fw_forward(const Runtime *rt, RunState *s, int token, int pos, int de
     return 0;
 }
 
+/* The forward on the GPU model (glm_hip_model_forward), with the per-layer copies of x
+ * placed at the caller's strides. keep: leave the model's cache and s as they were. */
+static int fw_forward_device(const Runtime *rt, RunState *s, int token, int pos, int keep, float *attn_out,
+                             int attn_stride, int max_attn, int *n_attn, float *layer_out, int layer_stride,
+                             int max_layers, int *n_layers) {
+    const RuntimeConfig *c = &rt->cfg;
+    const int L = c->n_layers, dim = c->dim;
+    const int n_run = rt->has_all_attn ? L : 1, n_att = (rt->has_all_attn || rt->has_l0_attn) ? n_run : 0;
+    const int keep_attn = attn_out && attn_stride >= dim && max_attn > 0 && n_att > 0;
+    const int keep_layer = layer_out && layer_stride >= dim && max_layers > 0;
+    float *ab = keep_attn ? (float *)malloc((size_t)L * dim * sizeof(float)) : NULL;
+    float *lb = keep_layer ? (float *)malloc((size_t)L * dim * sizeof(float)) : NULL;
+    float *logits = keep ? (float *)malloc((size_t)c->vocab_size * sizeof(float)) : NULL;
+    int rc = -1;
+    if ((!keep_attn || ab) && (!keep_layer || lb) && (!keep || logits))
+        rc = glm_hip_model_forward(rt, s, token, pos, keep, logits, ab, lb);
+    else
+        fprintf(stderr, "[glm-hip] out of memory for the forward's checkpoints\n");
+    if (n_attn) *n_attn = 0;
+    if (n_layers) *n_layers = 0;
+    if (rc == 0) {
+        const int na = keep_attn ? (n_att < max_attn ? n_att : max_attn) : 0;
+        const int nl = keep_layer ? (n_run < max_layers ? n_run : max_layers) : 0;
+        for (int l = 0; l < na; l++) memcpy(attn_out + (size_t)l * attn_stride, ab + (size_t)l * dim, (size_t)dim * sizeof(float));
+        for (int l = 0; l < nl; l++) memcpy(layer_out + (size_t)l * layer_stride, lb + (size_t)l * dim, (size_t)dim * sizeof(float));
+        if (n_attn) *n_attn = na;
+        if (n_layers) *n_layers = nl;
+    }
+    free(ab);
+    free(lb);
+    free(logits);
+    return rc;
+}
+
 /* ---- public ----------------------------------------------------------------------- */
 
 int glm_hip_forward_token(const Runtime *rt, RunState *st, int token, int pos, int debug_mode) {
+    if (rt && st && glm_hip_model_active())
+        return fw_forward_device(rt, st, token, pos, 0, NULL, 0, 0, NULL, NULL, 0, 0, NULL);
     return fw_forward(rt, st, token, pos, debug_mode, NULL, 0, 0, NULL, NULL, 0, 0, NULL);
 }
 
@@ -253,6 +292,9 @@ int glm_hip_forward_token_dual_checkpoints(const Runtime *rt, const RunState *sr
     if (!rt || !src || src->cache_cap <= 0) return -1;
     if (attn_layer_out && (attn_layer_stride < rt->cfg.dim || max_attn_layers <= 0)) return -1;
     if (layer_out && (layer_stride < rt->cfg.dim || max_layers <= 0)) return -1;
+    if (glm_hip_model_active())  // the GPU model restores what the token writes: no copy of src needed
+        return fw_forward_device(rt, (RunState *)src, token, pos, 1, attn_layer_out, attn_layer_stride, max_attn_layers,
+                                 written_attn_layers, layer_out, layer_stride, max_layers, written_layers);
     RunState tmp;
     if (glm_runstate_build(&tmp, rt, src->cache_cap) != 0) return -1;
     glm_runstate_copy(rt, src, &tmp);

@@ -46,6 +46,14 @@ int glm_backend_try_hip_moe(const Runtime *rt, RunState *st, int layer_idx, int 
 int glm_hip_init(const Runtime *rt, RunState *st);      /* 0 ok, -1 failure; idempotent */
 int glm_hip_prepare(const Runtime *rt, RunState *st);   /* uploads MoE layers 1..n_layers-1; 0 ok */
 int glm_hip_moe_layer(const Runtime *rt, RunState *st, int layer_idx, int debug_mode); /* 0 ok, -1 error */
+/* 1 when glm_hip_prepare built the whole forward on the GPU (gmoe_model.h; not with
+ * GLM_HIP_HOST_ATTN set). glm_hip_model_forward then runs a token through it: logits into
+ * `logits` (st->logits when NULL) and the final x into st->x; with keep_state the model's
+ * cache and st are left as they were (the dual-checkpoint form); attn_ckpt / layer_ckpt,
+ * when given, receive x after each layer's attention / FFN ([n_layers][dim]). 0 ok, -1 error. */
+int glm_hip_model_active(void);
+int glm_hip_model_forward(const Runtime *rt, RunState *st, int token, int pos, int keep_state, float *logits,
+                          float *attn_ckpt, float *layer_ckpt);
 void glm_hip_free(void);
 
 #ifdef __cplusplus

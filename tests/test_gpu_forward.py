@@ -1,16 +1,21 @@
-"""glm.c's token forward with the MoE layers on the GPU (glm_hip_forward_token, what
+"""glm.c's token forward through the HIP backend (glm_hip_forward_token, what
 glm_backend_forward_token runs for BACKEND_HIP) against glm.c's own forward
-(infer.c:1767-1901, compiled into oracle/_ref) on synthetic v4 checkpoints.
+(infer.c:1767-1901, compiled into oracle/_ref) on synthetic v4 checkpoints, in both forms
+the backend takes:
+
+* "gpu": the whole forward on the GPU model (gmoe_model.h): embedding, MLA attention over
+  the device-resident latent cache, dense layer 0, the MoE layers, LM head;
+* "host_attn" (GLM_HIP_HOST_ATTN=1): glm.c's host steps around the GPU MoE layers.
 
 Teacher-forced: the same tokens at the same positions on both sides, with glm.c's dual
-checkpoints (infer.c:1940-1983) per position. Layer 0 (attention and dense FFN) never
-sees a GPU result, so its x after attention and after the FFN equals glm.c's bit for
-bit at every position. From layer 1 on, x carries the GPU MoE layers' rounding: every
-later checkpoint and the logits are held to the FFN bar, max-abs 1e-2 and rel-L2 1e-3,
-and each position's argmax equals glm.c's.
+checkpoints (infer.c:1940-1983) per position. Every checkpoint and the logits are held to
+the FFN bar, max-abs 1e-2 and rel-L2 1e-3, and each position's argmax equals glm.c's. In
+the host form layer 0 (attention and dense FFN) never sees a GPU result, so its
+checkpoints equal glm.c's bit for bit at every position.
 
 Greedy: the decoder picks each next token itself (argmax, with infer.c:2213-2219's
-bos/eos skips), and glm.c, fed the same sequence, picks the same token at every step."""
+bos/eos skips), and glm.c, fed the same sequence, picks the same token at every step.
+A 150-position run takes the GPU attention over several 64-position chunks."""
 import numpy as np
 import pytest
 
@@ -23,17 +28,18 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not ref_decode.available(), reason="oracle/_ref not built (needs the reference sources)")]
 
 
-def small(gs, scale_mode, n_layers=4, seed=21):
+def small(gs, scale_mode, n_layers=4, seed=21, seq_len=64):
     return glm_model.CkptSpec(dim=256, hidden_dim=512, n_layers=n_layers, n_heads=4, n_kv_heads=4, vocab_size=300,
-                              seq_len=64, rope_dim=16, q_lora_rank=64, kv_lora_rank=64, n_routed_experts=8,
+                              seq_len=seq_len, rope_dim=16, q_lora_rank=64, kv_lora_rank=64, n_routed_experts=8,
                               n_experts_used=2, bos_id=1, eos_id=2, qk_nope_dim=32, v_head_dim=32, moe_ffn_dim=256,
                               group_size=gs, seed=seed, norm_mode=gmoe.SYNTH_NORM_RANDOM,
                               bias_mode=gmoe.SYNTH_BIAS_NORMAL, scale_mode=scale_mode)
 
 
 def glm_dims(seed=22):
-    """GLM-4.7-Flash's MoE dimensions (D 2048, F 1536, 64 experts, top-4, group size 32),
-    with a small vocabulary, four heads and two MoE layers."""
+    """GLM-4.7-Flash's MoE dimensions (D 2048, F 1536, 64 experts, top-4, group size 32)
+    and attention ranks (kv_lora 512, rope 64, nope 192, v_head 256), with a small
+    vocabulary, four heads and two MoE layers."""
     return glm_model.CkptSpec(dim=2048, hidden_dim=1024, n_layers=3, n_heads=4, n_kv_heads=4, vocab_size=1000,
                               seq_len=64, rope_dim=64, q_lora_rank=256, kv_lora_rank=512, n_routed_experts=64,
                               n_experts_used=4, bos_id=1, eos_id=2, qk_nope_dim=192, v_head_dim=256, moe_ffn_dim=1536,
@@ -44,39 +50,77 @@ def glm_dims(seed=22):
 CASES = {"gs16_native": lambda: small(16, gmoe.SYNTH_SCALES_FP32), "gs32_tiled": lambda: small(32, gmoe.SYNTH_SCALES_FP16),
          "glm_dims": glm_dims}
 TOKENS = [1, 5, 17, 299, 42, 0, 17, 123, 7, 250]
+MODES = ["gpu", "host_attn"]
 
 
 def bits(a):
     return np.ascontiguousarray(a).view(np.uint32)
 
 
-def open_decoder(tmp_path, sp, cap):
+@pytest.fixture(params=MODES)
+def mode(request, monkeypatch):
+    if request.param == "host_attn":
+        monkeypatch.setenv("GLM_HIP_HOST_ATTN", "1")
+    else:
+        monkeypatch.delenv("GLM_HIP_HOST_ATTN", raising=False)
+    return request.param
+
+
+def open_decoder(tmp_path, sp, cap, mode):
     path = tmp_path / "model.bin"
     glm_model.write_synth_checkpoint(path, sp)
     ck = glm_model.Checkpoint(path)
     dec = glm_model.Decoder(ck, cap)
     assert dec.backend == glm_model.BACKEND_HIP
+    assert dec.on_gpu() == (mode == "gpu"), "the forward runs where the mode says"
     return path, ck, dec
 
 
+def check_position(dec, ref, pos, logits, attn, layer, mode, what):
+    if mode == "host_attn":
+        assert np.array_equal(bits(attn[0]), bits(ref["attn"][pos][0])), f"{what}: layer 0 attention"
+        assert np.array_equal(bits(layer[0]), bits(ref["layer"][pos][0])), f"{what}: layer 0 FFN"
+    for l in range(dec.L):
+        assert_close(attn[l], ref["attn"][pos][l], f"{what} layer {l} attention")
+        assert_close(layer[l], ref["layer"][pos][l], f"{what} layer {l} FFN")
+    assert_close(logits, ref["logits"][pos], f"{what} logits")
+    assert int(np.argmax(logits)) == int(np.argmax(ref["logits"][pos])), f"{what}: argmax"
+
+
 @pytest.mark.parametrize("case", list(CASES))
-def test_teacher_forced_positions_match_glm(tmp_path, case):
+def test_teacher_forced_positions_match_glm(tmp_path, case, mode):
     sp = CASES[case]()
     tokens = [t % sp.vocab_size for t in TOKENS]
     cap = len(tokens) + 2
-    path, ck, dec = open_decoder(tmp_path, sp, cap)
+    path, ck, dec = open_decoder(tmp_path, sp, cap, mode)
     try:
         ref = ref_decode.reference_decode(path, tokens, cap, dec.L, dec.D, dec.V, tmp_path / "ref")
         for pos, tok in enumerate(tokens):
-            print(f"[case] forward {case} pos {pos} token {tok}", flush=True)
+            print(f"[case] forward {case} {mode} pos {pos} token {tok}", flush=True)
             logits, attn, layer = dec.step(tok, pos, checkpoints=True)
-            assert np.array_equal(bits(attn[0]), bits(ref["attn"][pos][0])), f"pos {pos}: layer 0 attention"
-            assert np.array_equal(bits(layer[0]), bits(ref["layer"][pos][0])), f"pos {pos}: layer 0 FFN"
-            for l in range(1, dec.L):
-                assert_close(attn[l], ref["attn"][pos][l], f"pos {pos} layer {l} attention")
-                assert_close(layer[l], ref["layer"][pos][l], f"pos {pos} layer {l} MoE")
-            assert_close(logits, ref["logits"][pos], f"pos {pos} logits")
-            assert int(np.argmax(logits)) == int(np.argmax(ref["logits"][pos])), f"pos {pos}: argmax"
+            check_position(dec, ref, pos, logits, attn, layer, mode, f"pos {pos}")
+    finally:
+        dec.free()
+        ck.close()
+
+
+def test_long_context_over_several_attention_chunks(tmp_path, mode):
+    sp = small(32, gmoe.SYNTH_SCALES_FP16, n_layers=3, seed=23, seq_len=256)
+    rng = np.random.default_rng(23)
+    tokens = [1] + [int(t) for t in rng.integers(3, sp.vocab_size, 149)]
+    cap = len(tokens) + 1
+    path, ck, dec = open_decoder(tmp_path, sp, cap, mode)
+    try:
+        ref = ref_decode.reference_decode(path, tokens, cap, dec.L, dec.D, dec.V, tmp_path / "ref")
+        print(f"[case] long context {mode}: {len(tokens)} positions", flush=True)
+        for pos, tok in enumerate(tokens):
+            full = pos in (0, 63, 64, 65, 127, 128, len(tokens) - 1)
+            if full:
+                logits, attn, layer = dec.step(tok, pos, checkpoints=True)
+                check_position(dec, ref, pos, logits, attn, layer, mode, f"pos {pos}")
+            else:
+                logits = dec.step(tok, pos)
+                assert_close(logits, ref["logits"][pos], f"pos {pos} logits")
     finally:
         dec.free()
         ck.close()
@@ -93,11 +137,11 @@ def next_token(logits, sp):
 
 
 @pytest.mark.parametrize("case", ["gs32_tiled", "glm_dims"])
-def test_greedy_decode_picks_glms_tokens(tmp_path, case):
+def test_greedy_decode_picks_glms_tokens(tmp_path, case, mode):
     sp = CASES[case]()
     prompt, n_new = [1, 5, 17], 8
     cap = len(prompt) + n_new + 1
-    path, ck, dec = open_decoder(tmp_path, sp, cap)
+    path, ck, dec = open_decoder(tmp_path, sp, cap, mode)
     try:
         seq, picked = list(prompt), []
         for pos in range(len(prompt) + n_new - 1):
@@ -105,7 +149,7 @@ def test_greedy_decode_picks_glms_tokens(tmp_path, case):
             if pos + 1 >= len(prompt):
                 picked.append(next_token(logits, sp))
                 seq.append(picked[-1])
-        print(f"[case] greedy {case}: {seq}", flush=True)
+        print(f"[case] greedy {case} {mode}: {seq}", flush=True)
         ref = ref_decode.reference_decode(path, seq, cap, dec.L, dec.D, dec.V, tmp_path / "ref")
         for i, t in enumerate(picked):
             pos = len(prompt) - 1 + i
