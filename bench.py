@@ -332,7 +332,7 @@ def main():
     K1 = shape.K + 1
     mat = shape.F * shape.D * 34 // 32
     kernel_bytes = {"gate_up": K1 * 2 * mat, "down": K1 * mat, "k_moe_stack": bytes_per_token,
-                    "k_moe_decode": bytes_per_token}
+                    "k_moe_decode": bytes_per_token, "k_moe_relay": bytes_per_token}
     dom = max(prof, key=lambda k: prof[k][1])
     kernels = {k: {"launches": n, "avg_us": ms * 1e3 / n} for k, (n, ms) in prof.items()}
     for k in kernels:

@@ -19,6 +19,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 #include <stdlib.h>
@@ -30,6 +31,7 @@
 #include "experts.h"
 #include "grouped.h"
 #include "native.h"
+#include "relay.h"
 #include "repack.h"
 #include "router.h"
 #include "stack.h"
@@ -44,6 +46,15 @@ static __device__ __align__(256) unsigned char scratch[GMOE_NOALLOC_SCRATCH_BYTE
 #define GM_MAX_DEVICES 64
 static void *g_scratch_dev[GM_MAX_DEVICES];
 static std::mutex g_scratch_mu;
+
+// The k_moe_relay instance of a shape: D == 2048 or narrower; experts per lane in its selection.
+typedef void (*relay_fn)(StackArgs);
+static relay_fn relay_kernel(int D, int E) {
+    const bool full = D == GM_MAX_COLS;
+    if (E <= 64) return full ? k_moe_relay<true, 1> : k_moe_relay<false, 1>;
+    if (E <= 128) return full ? k_moe_relay<true, 2> : k_moe_relay<false, 2>;
+    return full ? k_moe_relay<true, 4> : k_moe_relay<false, 4>;
+}
 
 // Router blocks of the persistent kernel: the largest power of two <= min(E, 64), so
 // that every block holds at most GM_MAX_E / 64 experts.
@@ -131,6 +142,8 @@ struct gmoe_ctx {
     int stack_ok = 0;            // shape fits k_moe_stack
     int stack_grid = 0;          // co-resident blocks
     int decode_rows = 0;         // T=1 runs k_moe_decode (decode.h) rather than k_moe_stack
+    int relay = 0;               // T=1 runs k_moe_relay (relay.h) rather than k_moe_stack
+    unsigned long long *sk_par_dev = nullptr;  // k_moe_relay: its workspace layers' parities (StackArgs::par_dev)
     int native = 0;              // GMOE_Q8_NATIVE: checkpoint layout, fp32 scales, native.h kernels
     uint8_t *sk_ws = nullptr;    // per-layer workspace, L regions of sk_ws_layer bytes
     size_t sk_ws_layer = 0;
@@ -218,7 +231,7 @@ static void free_ctx(gmoe_ctx *c) {
     }
     void *bufs[] = {c->obs, c->topk_ws, c->h, c->y,
                     c->stage, c->tok_counter, c->panel_counter, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
-                    c->stats_dev, c->staging, c->sk_ws, c->sk_ctr, c->sk_error,
+                    c->stats_dev, c->staging, c->sk_ws, c->sk_ctr, c->sk_error, c->sk_par_dev,
                     c->sk_layers, c->sk_trace, c->xspl, c->hspl, c->xexp, c->hexp, c->pair_row, c->n_tiles,
                     c->hbuf, c->ybuf, c->tiles, c->rt_t, c->rt_sp, c->rt_sa};
     for (void *b : bufs) dev_free(b);
@@ -387,10 +400,16 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
             // roles: the router blocks, at least one shared-expert and one routed block
             if (c->stack_grid < stack_routers(c->E) + 2) c->stack_ok = 0;
             const char *dk_env = getenv("GMOE_DECODE_KERNEL");
-            // the row-owner kernel is opted into (GMOE_DECODE_KERNEL=1): k_moe_stack is the default
+            // k_moe_relay is the default where the shape fits it; GMOE_DECODE_KERNEL=0 asks for
+            // k_moe_stack, 1 for the row-owner k_moe_decode
             c->decode_rows = c->stack_ok && dk_env && dk_env[0] == '1' &&
                              hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_dk, k_moe_decode, SK_BLOCK, 0) == hipSuccess &&
                              per_cu_dk >= want && dk_fits(c->stack_grid, c->D, c->F, c->E, c->K);
+            int per_cu_rl = 0;
+            c->relay = c->stack_ok && !c->decode_rows && !(dk_env && dk_env[0] == '0') &&
+                       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rl, relay_kernel(c->D, c->E), SK_BLOCK, 0) ==
+                           hipSuccess &&
+                       per_cu_rl >= want && rl_fits(c->stack_grid, c->D, c->F, c->E, c->K);
         }
     }
     if (c->decode_rows) {
@@ -416,11 +435,14 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         // k_moe_stack's partial sums, or k_moe_decode's h records and router records
         c->sk_o.ypart = take(c->decode_rows ? 0 : NS * (F / 16) * D * sizeof(float));
         c->sk_o.h = take(c->decode_rows ? NS * (F / 16) * DK_HREC : 0);
-        c->sk_o.rec = take(c->decode_rows ? (D / DK_ROWS) * E * sizeof(DkRec) : 0);
-        c->sk_o.xsq = take(c->decode_rows ? (D / DK_ROWS) * sizeof(double) : 0);
+        // router records: k_moe_decode's per owner of DK_ROWS rows, k_moe_relay's per chunk of RL_ROWS
+        const size_t rec_pieces = c->decode_rows ? D / DK_ROWS : c->relay ? D / RL_ROWS : 0;
+        c->sk_o.rec = take(rec_pieces * E * sizeof(DkRec));
+        c->sk_o.xsq = take(rec_pieces * sizeof(double));
         c->sk_ws_layer = off;
         rc |= dev_alloc(&c->sk_ws, (size_t)c->L * off);
     }
+    rc |= dev_alloc(&c->sk_par_dev, SK_MAX_LAYERS / 64);
     rc |= dev_alloc(&c->sk_ctr, GM_STACK_COUNTERS);
     rc |= dev_alloc(&c->sk_error, 1);
     rc |= dev_alloc(&c->sk_layers, (size_t)c->L);
@@ -447,6 +469,8 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     hipError_t e4 = hipMemset(c->hist_idx, 0xff, (size_t)c->L * T * K * sizeof(int));
     hipError_t e6 = hipMemset(c->sk_error, 0, sizeof(int));
     hipError_t e7 = hipMemset(c->sk_layers, 0, (size_t)c->L * sizeof(StackLayer));
+    if (!e7) e7 = hipMemset(c->sk_ws, 0, (size_t)c->L * c->sk_ws_layer);
+    if (!e7) e7 = hipMemset(c->sk_par_dev, 0, SK_MAX_LAYERS / 64 * sizeof(unsigned long long));
     hipError_t e5 = hipDeviceSynchronize();
     if (e0 || e1 || e3 || e4 || e5 || e6 || e7) {
         set_err("gmoe_create: initialising device buffers failed");
@@ -712,13 +736,14 @@ struct StackSpace {
     uint8_t *ws;   // n_layers regions of ws_layer bytes
     unsigned *ctr; // SK_CTR_WORDS(n_layers)
     int *error;
+    unsigned long long *par;  // k_moe_relay's parities (SK_MAX_LAYERS / 64 words)
 };
 
 // T=1 through layers first..first+n-1 with the persistent kernel. With `space` the launch
 // uses that workspace and records neither trace nor profile (both may allocate).
 static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float *x_out, int flags, hipStream_t st,
                         const StackSpace *space = nullptr) {
-    const StackSpace own = {c->sk_ws, c->sk_ctr, c->sk_error};
+    const StackSpace own = {c->sk_ws, c->sk_ctr, c->sk_error, c->sk_par_dev};
     const StackSpace &sp = space ? *space : own;
     StackArgs a;
     a.layers = c->sk_layers + first;
@@ -775,10 +800,26 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         a.shared_blocks = nsb;
     }
     a.h_words = c->decode_rows ? (c->K + 1) * (c->F / 16) * DK_HREC / 8 : 0;
+    a.par_dev = c->relay ? sp.par : nullptr;
+    a.rl_cb0 = 0;
+    a.rl_poll = 0;
+    if (const char *pm = getenv("GMOE_RELAY_POLL")) a.rl_poll = atoi(pm);
+    if (c->relay) {
+        a.rl_cb0 = rl_roles(c->stack_grid, c->D, c->F, c->E, c->K).cb0;
+        // diagnostic: another first combine block (a routed block; its chunks must stay routed)
+        if (const char *cb = getenv("GMOE_RELAY_CB0")) {
+            const RlRoles rr = rl_roles(c->stack_grid, c->D, c->F, c->E, c->K);
+            const int v = atoi(cb);
+            if (v >= 0 && v + rr.nch <= rr.nri) a.rl_cb0 = v;
+        }
+    }
     if (c->sk_trace_on && !space) {
-        // k_moe_stack: its work items; k_moe_decode: one item per (layer, block)
+        // k_moe_stack: its work items; k_moe_decode: one item per (layer, block); k_moe_relay:
+        // routed and shared items, combine chunks and finisher blocks
+        const RlRoles rr = rl_roles(c->stack_grid, c->D, c->F, c->E, c->K);
         const size_t items = c->decode_rows ? (size_t)c->stack_grid * n
-                                            : (size_t)(stack_routers(c->E) + c->D / SK_CROWS + (c->K + 1) * (c->F / 16)) * n;
+                             : c->relay    ? (size_t)(rr.nri + rr.nsi + rr.nch + rr.nfb) * n
+                                           : (size_t)(stack_routers(c->E) + c->D / SK_CROWS + (c->K + 1) * (c->F / 16)) * n;
         if (items > c->sk_trace_items) {
             dev_free(c->sk_trace);
             c->sk_trace = nullptr;
@@ -791,10 +832,20 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         HIP_OK(hipMemsetAsync(c->sk_trace, 0, SK_TRACE_STAMPS * items * sizeof(uint64_t), st));
     }
     const int n_ctr = SK_CTR_WORDS(n);
+    if (c->relay && space) {
+        // the fixed array's previous user may have been another context or kernel: its
+        // workspace layers and their parities start from zeros
+        const size_t n16 = (size_t)n * c->sk_ws_layer / 16;
+        hipLaunchKernelGGL(k_relay_zero, dim3(1024), dim3(256), 0, st, (u32x4 *)sp.ws, n16);
+        hipLaunchKernelGGL(k_relay_zero, dim3(1), dim3(256), 0, st, (u32x4 *)sp.par, (size_t)(SK_MAX_LAYERS / 64 * 8 / 16));
+    }
     hipLaunchKernelGGL(k_stack_reset, dim3(n + 1), dim3(SK_BLOCK), 0, st, sp.ctr, n_ctr, sp.error, a);
-    ProfRecord *pr = space ? nullptr : prof_begin(c, st, c->decode_rows ? GMOE_KERNEL_DECODE : GMOE_KERNEL_STACK);
+    ProfRecord *pr = space ? nullptr
+                           : prof_begin(c, st, c->decode_rows ? GMOE_KERNEL_DECODE : c->relay ? GMOE_KERNEL_RELAY : GMOE_KERNEL_STACK);
     if (c->decode_rows)
         hipLaunchKernelGGL(k_moe_decode, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+    else if (c->relay)
+        hipLaunchKernelGGL(relay_kernel(c->D, c->E), dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
     else
         hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
     prof_end(pr, st);
@@ -820,10 +871,22 @@ static const char k_timeout_msg[] =
 // Without synchronising: GMOE_ERR_HIP if a persistent launch that has already ended gave up
 // on a wait since the last report (the failing block sets the pinned host word). The
 // report clears the word, so the next launch starts clean.
+// After a launch of k_moe_relay that gave up: words of its workspace layers may hold the
+// parity of an older launch, so the context's workspace goes back to zeros, and its
+// parities with it (the fixed array of the no-alloc call is cleared before each use).
+static void relay_reset(gmoe_ctx *c) {
+    if (!c->relay) return;
+    (void)hipDeviceSynchronize();
+    (void)hipMemset(c->sk_ws, 0, (size_t)c->L * c->sk_ws_layer);
+    (void)hipMemset(c->sk_par_dev, 0, SK_MAX_LAYERS / 64 * sizeof(unsigned long long));
+    (void)hipDeviceSynchronize();
+}
+
 static int take_launch_error(gmoe_ctx *c) {
     volatile int *w = c->sk_error_host;
     if (!c->stack_launched || !w || *w == 0) return GMOE_OK;
     *w = 0;
+    relay_reset(c);
     set_err("%s", k_timeout_msg);
     return GMOE_ERR_HIP;
 }
@@ -840,6 +903,7 @@ static int check_stack_error(gmoe_ctx *c) {
     if (c->stack_last) HIP_OK(hipMemcpy(&err, c->stack_error_dev, sizeof(int), hipMemcpyDeviceToHost));
     const int host_rc = take_launch_error(c);
     if (err || host_rc) {
+        if (!host_rc) relay_reset(c);
         set_err("%s", k_timeout_msg);
         return GMOE_ERR_HIP;
     }
@@ -1089,7 +1153,7 @@ extern "C" int gmoe_forward_layers(gmoe_ctx *c, int first, int n, int T, const f
 // (on 256-byte lines) and the error word.
 static size_t noalloc_bytes(const gmoe_ctx *c, int n) {
     const size_t ctr = ((size_t)SK_CTR_WORDS(n) * sizeof(unsigned) + 255) & ~(size_t)255;
-    return (size_t)n * c->sk_ws_layer + ctr + 256;
+    return (size_t)n * c->sk_ws_layer + ctr + 256 + 256;  // + the error word's line + the parities' line
 }
 
 extern "C" int gmoe_forward_layers_noalloc(gmoe_ctx *c, int first, int n, const float *x_in, float *x_out, int flags,
@@ -1128,11 +1192,12 @@ extern "C" int gmoe_forward_layers_noalloc(gmoe_ctx *c, int first, int n, const 
         base = (uint8_t *)g_scratch_dev[c->device];  // set by gmoe_create on this device
     }
     const size_t ws_bytes = (size_t)n * c->sk_ws_layer;
-    const size_t ctr_bytes = noalloc_bytes(c, n) - ws_bytes - 256;
+    const size_t ctr_bytes = noalloc_bytes(c, n) - ws_bytes - 512;
     StackSpace sp;
     sp.ws = base;
     sp.ctr = (unsigned *)(base + ws_bytes);
     sp.error = (int *)(base + ws_bytes + ctr_bytes);
+    sp.par = (unsigned long long *)(base + ws_bytes + ctr_bytes + 256);
     return launch_stack(c, first, n, x_in, x_out, flags, (hipStream_t)stream, &sp);
 }
 
@@ -1179,7 +1244,9 @@ extern "C" int gmoe_forward_host(gmoe_ctx *c, int layer, int T, const float *x_i
         HIP_OK(hipMemcpyAsync(err_h, c->stack_error_dev, sizeof(int), hipMemcpyDeviceToHost, nullptr));
     HIP_OK(hipStreamSynchronize(nullptr));
     // a timed-out launch leaves x_out untouched, so a caller may rerun the layer from it
-    if (take_launch_error(c) || *err_h) {
+    const int launch_rc = take_launch_error(c);
+    if (launch_rc || *err_h) {
+        if (!launch_rc) relay_reset(c);
         set_err("%s", k_timeout_msg);
         return GMOE_ERR_HIP;
     }

@@ -134,6 +134,10 @@ struct StackArgs {
     int n_router;              // router blocks: a power of two, <= min(E, 64)
     int shared_blocks;         // blocks in the shared-expert role
     int h_words;               // 8-byte words of each layer's h records, zeroed before the launch (decode.h; 0 otherwise)
+    unsigned long long *par_dev;  // relay.h: [SK_MAX_LAYERS / 64] words, bit li = the parity of workspace layer li;
+                                  // k_stack_reset flips the launch's layers before the kernel reads them
+    int rl_cb0;                // relay.h: the routed block that runs combine chunk 0
+    int rl_poll;               // relay.h: polling policy (rl_spin)
 };
 
 template <typename T>
@@ -213,6 +217,7 @@ struct SkShared {
     int xe_local;   // exponent of a routed block's own digits of xn (sk_local_digits)
     unsigned spin_limit;
     float xr4[4];   // the row-owner kernel's (decode.h): an owner's new rows of x
+    float xres[16]; // relay.h: a combine chunk's residual rows
     unsigned long long hrec[8];  // and an item's h record
     int idx[GM_MAX_K];
     float wk[GM_MAX_K], ws[GM_MAX_K];
@@ -412,7 +417,7 @@ __device__ static void sk_exact_select(const StackArgs &a, const StackLayer &L, 
 // Observables of layer `layer` (top-k, weights, router probabilities), written through
 // by the block that selected the top-k.
 __device__ static void sk_write_routing(const StackArgs &a, int layer, SkShared &sh) {
-    const int tid = threadIdx.x;
+    const int tid = phase_tid();
     if (tid < a.K) {
         st_i(a.topk_idx + tid, sh.idx[tid]);
         st_f(a.topk_w + tid, sh.wk[tid]);
@@ -703,7 +708,7 @@ __device__ static inline bool sk_read_topk(const StackArgs &a, int li, SkShared 
 // into sh.wk / sh.ws.
 __device__ static inline bool sk_read_weights(const StackArgs &a, int li, SkShared &sh) {
     if (!wait_ge(&a.ctr[SKF(li, SKF_SELW)], 1u, a.error, sh)) return false;
-    const int tid = threadIdx.x;
+    const int tid = phase_tid();
     if (tid < a.K) {
         const float wk = ws_at<float>(a, li, a.o.ex_w)[tid];
         sh.wk[tid] = wk;
@@ -1100,6 +1105,11 @@ __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, 
     if (li == a.n_layers) {
         for (int i = tid; i < n; i += SK_BLOCK) ctr[i] = 0u;
         if (tid == 0) *error = 0;
+        // relay.h: this launch writes the other parity into each of its workspace layers
+        if (a.par_dev && tid < SK_MAX_LAYERS / 64) {
+            const int lo = 64 * tid, cnt = a.n_layers - lo;
+            if (cnt > 0) a.par_dev[tid] ^= cnt >= 64 ? ~0ull : (1ull << cnt) - 1ull;
+        }
         return;
     }
     unsigned long long *stage = ws_at<unsigned long long>(a, li, a.o.stage);

@@ -57,11 +57,12 @@ class GmoeLayerState(C.Structure):
 # gmoe_profile buckets (GMOE_KERNEL_*): gate_up is k_gate_up (T=1) or k_group_gu (grouped
 # prefill), down is k_down_combine or k_group_down
 KERNEL_NAMES = {0: "k_router_tok", 1: "gate_up", 2: "down", 3: "k_dispatch", 4: "k_moe_stack", 5: "k_act_split",
-                6: "k_token_combine", 7: "k_moe_decode"}
+                6: "k_token_combine", 7: "k_moe_decode", 8: "k_moe_relay"}
+N_KERNEL_IDS = 9
 
 
 class GmoeKernelTimes(C.Structure):
-    _fields_ = [("launches", C.c_int64 * 8), ("ms", C.c_double * 8)]
+    _fields_ = [("launches", C.c_int64 * N_KERNEL_IDS), ("ms", C.c_double * N_KERNEL_IDS)]
 
 
 class GmoeStats(C.Structure):
@@ -276,7 +277,7 @@ class Context:
         """{kernel name: (launches, total ms)} from the HIP events of the profiled calls."""
         kt = GmoeKernelTimes()
         check(self.lib.gmoe_profile_read(self.h, C.byref(kt)), "gmoe_profile_read")
-        return {KERNEL_NAMES.get(i, str(i)): (int(kt.launches[i]), float(kt.ms[i])) for i in range(8)
+        return {KERNEL_NAMES.get(i, str(i)): (int(kt.launches[i]), float(kt.ms[i])) for i in range(N_KERNEL_IDS)
                 if kt.launches[i] > 0}
 
     def expert_bytes_last(self):

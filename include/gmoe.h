@@ -180,7 +180,9 @@ int gmoe_get_stats(gmoe_ctx *ctx, gmoe_stats *out);
 #define GMOE_KERNEL_COMBINE 6    /* prefill: per-token combine + residual */
 #define GMOE_KERNEL_DECODE 7     /* row-owner persistent decode kernel (T=1, all requested layers), opted into
                                   * with GMOE_DECODE_KERNEL=1 where the shape fits it */
-#define GMOE_KERNEL_COUNT 8
+#define GMOE_KERNEL_RELAY 8      /* persistent decode kernel whose phases poll each other's tagged results (T=1,
+                                  * all requested layers) */
+#define GMOE_KERNEL_COUNT 9
 typedef struct gmoe_kernel_times {
     int64_t launches[GMOE_KERNEL_COUNT];
     double ms[GMOE_KERNEL_COUNT];

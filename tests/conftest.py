@@ -34,15 +34,25 @@ def assert_close(got, want, what, max_abs=MAX_ABS, rel_l2=REL_L2):
     return err.max(), rel
 
 
-# The two persistent T=1 kernels, chosen when a context is created: k_moe_stack (the
-# default) and the row-owner k_moe_decode (GMOE_DECODE_KERNEL=1).
-DECODE_KERNELS = {"stack": "0", "rows": "1"}
-DECODE_KERNEL_NAMES = {"stack": "k_moe_stack", "rows": "k_moe_decode"}
+# The persistent T=1 kernels, chosen when a context is created: k_moe_relay (the default,
+# GMOE_DECODE_KERNEL=2 or unset), k_moe_stack (0) and the row-owner k_moe_decode (1).
+DECODE_KERNELS = {"stack": "0", "rows": "1", "relay": "2"}
+DECODE_KERNEL_NAMES = {"stack": "k_moe_stack", "rows": "k_moe_decode", "relay": "k_moe_relay"}
+DEFAULT_DECODE_KERNEL = "relay"
+
+
+def current_decode_kernel():
+    """The persistent kernel that a context created now runs its T=1 launches on."""
+    env = os.environ.get("GMOE_DECODE_KERNEL")
+    for kind, val in DECODE_KERNELS.items():
+        if env == val:
+            return kind
+    return DEFAULT_DECODE_KERNEL
 
 
 @contextlib.contextmanager
 def decode_kernel(kind):
-    """Contexts created inside run their T=1 launches on `kind` ("stack" or "rows")."""
+    """Contexts created inside run their T=1 launches on `kind` (a key of DECODE_KERNELS)."""
     old = os.environ.get("GMOE_DECODE_KERNEL")
     os.environ["GMOE_DECODE_KERNEL"] = DECODE_KERNELS[kind]
     try:

@@ -11,7 +11,7 @@ import pytest
 
 import gmoe
 import oracle
-from conftest import DECODE_KERNELS, assert_close, assert_decode_kernel, decode_kernel, launched
+from conftest import DECODE_KERNELS, assert_close, assert_decode_kernel, current_decode_kernel, decode_kernel, launched
 
 pytestmark = pytest.mark.gpu
 
@@ -35,8 +35,7 @@ def run_case(shape, seed, T, norm_mode=gmoe.SYNTH_NORM_ONES, flags=0, layer=1):
         ran = launched(ctx, lambda: out.update(r=gmoe.forward_host(ctx, layer, x, flags=flags)))
         got, st = out["r"]
         if T == 1:  # the persistent kernel the environment asks for
-            kind = "rows" if os.environ.get("GMOE_DECODE_KERNEL") == DECODE_KERNELS["rows"] else "stack"
-            assert_decode_kernel(ran, kind)
+            assert_decode_kernel(ran, current_decode_kernel())
         stats = ctx.stats()
     finally:
         ctx.close()
@@ -75,13 +74,13 @@ def test_glm_shape_batch8():
     check(*run_case(gmoe.GLM47_FLASH, seed=5, T=8, norm_mode=gmoe.SYNTH_NORM_RANDOM))
 
 
-@pytest.mark.parametrize("T,kind", [(1, "stack"), (1, "rows"), (8, "stack")])
+@pytest.mark.parametrize("T,kind", [(1, "stack"), (1, "rows"), (1, "relay"), (8, "stack")])
 def test_wide_expert_count(T, kind):
     with decode_kernel(kind):
         check(*run_case(WIDE, seed=6, T=T, norm_mode=gmoe.SYNTH_NORM_RANDOM))
 
 
-@pytest.mark.parametrize("T,kind", [(1, "stack"), (1, "rows"), (8, "stack")])
+@pytest.mark.parametrize("T,kind", [(1, "stack"), (1, "rows"), (1, "relay"), (8, "stack")])
 def test_widest_expert_count(T, kind):
     with decode_kernel(kind):
         check(*run_case(WIDEST, seed=7, T=T))
