@@ -29,6 +29,7 @@ struct GemvArgs {
     const float *resid;    // GV_RESID: y = resid + dot (infer.c:1061, 1083)
     float *y;              // GV_PAIR: y = silu(dot) * dot2 (infer.c:1078-1080)
     int rows, cols, gs, x_rows, x_stride;
+    int bx, by, br;        // a batch (grid y): token t's x, y and resid start t*bx, t*by, t*br floats in
 };
 
 // Sum over each 16-lane row of a wave in fp64, to every lane of the row.
@@ -121,6 +122,12 @@ __device__ static inline float gv_reduce(float v) {
 template <int LPR, int U, int MODE>
 __global__ __launch_bounds__(DM_BLOCK) void k_gemv(GemvArgs a) {
     constexpr int RPW = 64 / LPR;  // rows per wave at a time
+    {
+        const size_t t = blockIdx.y;  // the token of a batch
+        a.x += t * (size_t)a.bx;
+        a.y += t * (size_t)a.by;
+        if (MODE == GV_RESID) a.resid += t * (size_t)a.br;
+    }
     const int lane = threadIdx.x & 63, sub = lane / LPR, sl = lane % LPR;
     const int wave = blockIdx.x * (DM_BLOCK / 64) + (threadIdx.x >> 6), nwaves = gridDim.x * (DM_BLOCK / 64);
     const int nrg = (a.rows + RPW - 1) / RPW;
@@ -156,6 +163,18 @@ __global__ __launch_bounds__(DM_BLOCK) void k_embed(const int8_t *__restrict__ t
     x[i] = __fmul_rn((float)tq[(size_t)token * dim + i], ts[(size_t)token * (dim / gs) + i / gs]);
 }
 
+// The embedding rows of a batch: token blockIdx.y's row into x + blockIdx.y * dim; a token
+// outside the vocabulary takes row 0, as infer.c:1781 does.
+__global__ __launch_bounds__(DM_BLOCK) void k_embed_batch(const int8_t *__restrict__ tq, const float *__restrict__ ts,
+                                                          const int32_t *__restrict__ tokens, int vocab, int dim, int gs,
+                                                          float *__restrict__ x) {
+    const int i = blockIdx.x * DM_BLOCK + threadIdx.x;
+    if (i >= dim) return;
+    int token = tokens[blockIdx.y];
+    if (token < 0 || token >= vocab) token = 0;
+    x[(size_t)blockIdx.y * dim + i] = __fmul_rn((float)tq[(size_t)token * dim + i], ts[(size_t)token * (dim / gs) + i / gs]);
+}
+
 // ---- MLA attention over the latent cache ------------------------------------------
 
 #define AT_CH 64   // cache positions per chunk of k_attn_part (one per lane in its softmax)
@@ -180,10 +199,18 @@ struct AttnArgs {
 
 // The position's cache entry and the heads' rotated queries (infer.c:1000-1016): the
 // compressed kv normalised (rmsnorm over kv values), the rope part of kv_a and of every
-// head's query rotated by the position's angles. One block.
+// head's query rotated by the position's angles. One block per token: block t of a batch
+// takes token t at position pos + t (its kv_a, q_full and q_pe t token strides on).
 __global__ __launch_bounds__(DM_BLOCK) void k_attn_prep(AttnArgs a) {
     __shared__ double red[DM_BLOCK / 64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    {
+        const int t = blockIdx.x;
+        a.kv_a += (size_t)t * (a.kv + a.rope);
+        a.q_full += (size_t)t * a.H * a.head_k;
+        a.q_pe += (size_t)t * a.H * a.rope;
+        a.pos += t;
+    }
     double ss = 0.0;
     for (int i = tid; i < a.kv; i += DM_BLOCK) ss += (double)a.kv_a[i] * (double)a.kv_a[i];
     ss = wave_sum_dpp(ss);

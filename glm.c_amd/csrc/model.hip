@@ -1,5 +1,8 @@
 // model.hip -- gmoe_model (include/gmoe_model.h): glm.c's decode forward (infer.c:1767-1901)
-// with every weight, the latent cache and x in device memory. Per token, on one stream:
+// with every weight, the latent cache and x in device memory. A prefill runs the same steps
+// over a batch of tokens, each product launched once for the batch (grid y = token), the
+// attention over the cache once per token, and each MoE layer as one grouped call.
+// Per token, on one stream:
 //
 //   k_embed                      x = the token's embedding row
 //   per attention layer (infer.c:978-1065):
@@ -69,9 +72,11 @@ struct gmoe_model {
     // the latent cache [attn_layers][cap][kv], [..][rope] and the rope table [cap][rope/2][2]
     float *comp = nullptr, *pe = nullptr, *rope_cs = nullptr;
     // activations
+    // activations, each [max_batch][..] (a single token uses the first row)
     float *x = nullptr, *q_a = nullptr, *q_full = nullptr, *kv_a = nullptr, *q_pe = nullptr, *q_abs = nullptr,
           *ctx = nullptr, *concat = nullptr, *ffh = nullptr, *logits = nullptr, *part_ctx = nullptr,
           *part_ml = nullptr, *saved = nullptr;
+    int32_t *tokens = nullptr;  // [max_batch] a prefill's token ids
     std::vector<void *> allocs;  // every device allocation, freed by gmoe_model_destroy
 };
 
@@ -108,11 +113,11 @@ int upload(gmoe_model *m, T **dst, const T *src, size_t n, const char *what) {
 // The k_gemv instance for cols columns: 16 lanes per row up to 64 units of 16 columns,
 // a whole wave per row beyond (at most 640 units).
 template <int MODE>
-int launch_gemv_mode(const GemvArgs &a, hipStream_t st) {
+int launch_gemv_mode(const GemvArgs &a, hipStream_t st, int nb) {
     const int units = a.cols >> 4;
     const int lpr = units <= 64 ? 16 : 64;
     const int rpw = 64 / lpr, nrg = (a.rows + rpw - 1) / rpw;
-    const dim3 grid((unsigned)std::min((nrg + 3) / 4, 2048)), block(DM_BLOCK);
+    const dim3 grid((unsigned)std::min((nrg + 3) / 4, 2048), (unsigned)nb), block(DM_BLOCK);
     if (lpr == 16) {
         switch ((units + 15) / 16) {
         case 1: hipLaunchKernelGGL((k_gemv<16, 1, MODE>), grid, block, 0, st, a); break;
@@ -135,10 +140,18 @@ int launch_gemv_mode(const GemvArgs &a, hipStream_t st) {
     return GMOE_OK;
 }
 
-int launch_gemv(const GemvArgs &a, int mode, hipStream_t st) {
-    if (mode == GV_RESID) return launch_gemv_mode<GV_RESID>(a, st);
-    if (mode == GV_PAIR) return launch_gemv_mode<GV_PAIR>(a, st);
-    return launch_gemv_mode<GV_PLAIN>(a, st);
+// One launch for nb tokens (a.bx, a.by, a.br apart).
+int launch_gemv(const GemvArgs &a, int mode, hipStream_t st, int nb = 1) {
+    if (mode == GV_RESID) return launch_gemv_mode<GV_RESID>(a, st, nb);
+    if (mode == GV_PAIR) return launch_gemv_mode<GV_PAIR>(a, st, nb);
+    return launch_gemv_mode<GV_PLAIN>(a, st, nb);
+}
+
+// gemv() over a batch: token t's input x + t bx, output y + t by.
+GemvArgs batched(GemvArgs a, int bx, int by) {
+    a.bx = bx;
+    a.by = by;
+    return a;
 }
 
 // y = q . x for one shared input (normalised by norm when given).
@@ -154,6 +167,7 @@ GemvArgs gemv(const int8_t *q, const float *s, const float *x, const float *norm
     a.gs = gs;
     a.x_rows = 1 << 30;
     a.x_stride = 0;
+    a.bx = a.by = a.br = 0;
     return a;
 }
 
@@ -177,6 +191,10 @@ int check_config(const gmoe_model_config &c) {
     }
     if (c.attn_layers != 0 && c.attn_layers != 1 && c.attn_layers != c.n_layers) {
         gm_set_err("gmoe_model_create: attn_layers must be 0, 1 or n_layers (got %d)", c.attn_layers);
+        return GMOE_ERR_INVALID;
+    }
+    if (c.max_batch < 0 || c.max_batch > 65536) {
+        gm_set_err("gmoe_model_create: max_batch %d outside 0..65536", c.max_batch);
         return GMOE_ERR_INVALID;
     }
     if (c.cache_cap < 1 || c.cache_cap > 65536) {
@@ -256,6 +274,79 @@ int dense_ffn(gmoe_model *m, hipStream_t st) {
     return GMOE_OK;
 }
 
+// attention() over a batch: n tokens of x at positions pos0 .. pos0+n-1. Every product is one
+// launch for the batch; every token's cache entry is written before any token's scores
+// (token t reads positions up to pos0 + t only), then the attention over the cache runs
+// per token, since its length differs.
+int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
+    const gmoe_model_config &c = m->c;
+    const AttnDev &A = m->attn[l];
+    const int gs = c.group_size, H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim, D = c.dim;
+    const int ql = c.q_lora_rank, hk = c.head_k_dim, vh = c.v_head_dim;
+    launch_gemv(batched(gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, ql, D, gs), D, ql), GV_PLAIN, st, n);
+    launch_gemv(batched(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, D, gs), D, kv + rope), GV_PLAIN, st,
+                n);
+    launch_gemv(batched(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * hk, ql, gs), ql, H * hk), GV_PLAIN, st, n);
+    AttnArgs aa{};
+    aa.kv_a = m->kv_a;
+    aa.kv_norm = A.kv_a_norm;
+    aa.q_full = m->q_full;
+    aa.rope_cs = m->rope_cs;
+    aa.comp = m->comp + (size_t)l * c.cache_cap * kv;
+    aa.pe = m->pe + (size_t)l * c.cache_cap * rope;
+    aa.q_pe = m->q_pe;
+    aa.q_abs = m->q_abs;
+    aa.part_ctx = m->part_ctx;
+    aa.part_ml = m->part_ml;
+    aa.ctx = m->ctx;
+    aa.H = H;
+    aa.kv = kv;
+    aa.rope = rope;
+    aa.head_k = hk;
+    aa.nope = c.qk_nope_dim;
+    aa.pos = pos0;
+    aa.kq_scale = 1.0f / sqrtf((float)hk);  // infer.c:992
+    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)n), dim3(DM_BLOCK), 0, st, aa);
+    GemvArgs kb = batched(gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs), H * hk, H * kv);
+    kb.x_rows = kv;
+    kb.x_stride = hk;
+    launch_gemv(kb, GV_PLAIN, st, n);
+    for (int t = 0; t < n; t++) {
+        AttnArgs at = aa;
+        at.q_pe = m->q_pe + (size_t)t * H * rope;
+        at.q_abs = m->q_abs + (size_t)t * H * kv;
+        at.ctx = m->ctx + (size_t)t * H * kv;
+        at.pos = pos0 + t;
+        const int chunks = at.pos / AT_CH + 1;
+        hipLaunchKernelGGL(k_attn_part, dim3(chunks, (H + AT_HG - 1) / AT_HG), dim3(DM_BLOCK), 0, st, at);
+        hipLaunchKernelGGL(k_attn_combine, dim3(H), dim3(DM_BLOCK), 0, st, at);
+    }
+    GemvArgs vb = batched(gemv(A.v_b_q, A.v_b_s, m->ctx, nullptr, m->concat, H * vh, kv, gs), H * kv, H * vh);
+    vb.x_rows = vh;
+    vb.x_stride = kv;
+    launch_gemv(vb, GV_PLAIN, st, n);
+    GemvArgs ao = batched(gemv(A.out_q, A.out_s, m->concat, nullptr, m->x, D, H * vh, gs), H * vh, D);
+    ao.resid = m->x;
+    ao.br = D;
+    launch_gemv(ao, GV_RESID, st, n);
+    return GMOE_OK;
+}
+
+// dense_ffn() over a batch of n tokens of x.
+int dense_ffn_batch(gmoe_model *m, int n, hipStream_t st) {
+    const gmoe_model_config &c = m->c;
+    const int D = c.dim, F = c.hidden_dim;
+    GemvArgs gu = batched(gemv(m->l0_gate_q, m->l0_gate_s, m->x, m->l0_norm, m->ffh, F, D, c.group_size), D, F);
+    gu.q2 = m->l0_up_q;
+    gu.s2 = m->l0_up_s;
+    launch_gemv(gu, GV_PAIR, st, n);
+    GemvArgs dn = batched(gemv(m->l0_down_q, m->l0_down_s, m->ffh, nullptr, m->x, D, F, c.group_size), F, D);
+    dn.resid = m->x;
+    dn.br = D;
+    launch_gemv(dn, GV_RESID, st, n);
+    return GMOE_OK;
+}
+
 }  // namespace
 
 extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_config *cfg) {
@@ -276,20 +367,22 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
     m->attn.resize(A);
     m->moe_on.assign(L, 0);
     int rc = GMOE_OK;
-    rc |= mdalloc(m, &m->x, (size_t)c.dim);
+    const size_t B = (size_t)(c.max_batch > 1 ? c.max_batch : 1);
+    rc |= mdalloc(m, &m->x, B * c.dim);
+    rc |= mdalloc(m, &m->tokens, B);
     rc |= mdalloc(m, &m->logits, (size_t)c.vocab_size);
-    if (c.has_l0_ffn) rc |= mdalloc(m, &m->ffh, (size_t)c.hidden_dim);
+    if (c.has_l0_ffn) rc |= mdalloc(m, &m->ffh, B * c.hidden_dim);
     if (A > 0) {
         rc |= mdalloc(m, &m->comp, A * cap * kv);
         rc |= mdalloc(m, &m->pe, A * cap * rope);
         rc |= mdalloc(m, &m->rope_cs, cap * rope);
-        rc |= mdalloc(m, &m->q_a, (size_t)c.q_lora_rank);
-        rc |= mdalloc(m, &m->q_full, H * (size_t)c.head_k_dim);
-        rc |= mdalloc(m, &m->kv_a, kv + rope);
-        rc |= mdalloc(m, &m->q_pe, H * rope);
-        rc |= mdalloc(m, &m->q_abs, H * kv);
-        rc |= mdalloc(m, &m->ctx, H * kv);
-        rc |= mdalloc(m, &m->concat, H * (size_t)c.v_head_dim);
+        rc |= mdalloc(m, &m->q_a, B * c.q_lora_rank);
+        rc |= mdalloc(m, &m->q_full, B * H * c.head_k_dim);
+        rc |= mdalloc(m, &m->kv_a, B * (kv + rope));
+        rc |= mdalloc(m, &m->q_pe, B * H * rope);
+        rc |= mdalloc(m, &m->q_abs, B * H * kv);
+        rc |= mdalloc(m, &m->ctx, B * H * kv);
+        rc |= mdalloc(m, &m->concat, B * H * c.v_head_dim);
         rc |= mdalloc(m, &m->part_ctx, chunks * H * kv);
         rc |= mdalloc(m, &m->part_ml, chunks * H * 2);
         rc |= mdalloc(m, &m->saved, A * (kv + rope));
@@ -454,6 +547,56 @@ extern "C" int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int f
         MH_OK(hipMemcpy2DAsync(m->pe + pos * rope, cap * rope * sizeof(float), m->saved + A * kv, rope * sizeof(float),
                                rope * sizeof(float), A, hipMemcpyDeviceToDevice, st));
     }
+    MH_OK(hipStreamSynchronize(st));
+    if (m->moe && gm_take_launch_error(m->moe)) return GMOE_ERR_HIP;
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_model_prefill(gmoe_model *m, const int32_t *tokens, int n, int pos0, float *logits, float *x_out,
+                                  void *stream) {
+    if (!m || !tokens || !logits) {
+        gm_set_err("gmoe_model_prefill: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    const gmoe_model_config &c = m->c;
+    const int B = c.max_batch > 1 ? c.max_batch : 1;
+    if (n < 1 || n > B) {
+        gm_set_err("gmoe_model_prefill: %d tokens outside 1..%d (the model's max_batch)", n, B);
+        return GMOE_ERR_INVALID;
+    }
+    if (!m->globals) {
+        gm_set_err("gmoe_model_prefill: gmoe_model_upload has not succeeded");
+        return GMOE_ERR_INVALID;
+    }
+    for (int l = 0; l < c.attn_layers; l++)
+        if (!m->attn[l].set) {
+            gm_set_err("gmoe_model_prefill: attention layer %d is not uploaded", l);
+            return GMOE_ERR_INVALID;
+        }
+    if (c.attn_layers > 0 && (pos0 < 0 || pos0 + n > c.cache_cap)) {
+        gm_set_err("gmoe_model_prefill: positions %d..%d outside the cache (%d positions)", pos0, pos0 + n - 1, c.cache_cap);
+        return GMOE_ERR_INVALID;
+    }
+    MH_OK(hipSetDevice(m->device));
+    hipStream_t st = (hipStream_t)stream;
+    const size_t D = (size_t)c.dim;
+    MH_OK(hipMemcpyAsync(m->tokens, tokens, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice, st));
+    hipLaunchKernelGGL(k_embed_batch, dim3((unsigned)((D + DM_BLOCK - 1) / DM_BLOCK), (unsigned)n), dim3(DM_BLOCK), 0, st,
+                       m->tok_q, m->tok_s, m->tokens, c.vocab_size, c.dim, c.group_size, m->x);
+    // the three model forms of infer.c:1817-1881, layer by layer over the batch
+    const int n_run = c.attn_layers == c.n_layers ? c.n_layers : 1;
+    int rc = GMOE_OK;
+    for (int l = 0; l < n_run && !rc; l++) {
+        if (c.attn_layers > 0) rc = attention_batch(m, l, pos0, n, st);
+        if (!rc && l == 0 && c.has_l0_ffn) rc = dense_ffn_batch(m, n, st);
+        if (!rc && l > 0 && m->moe_on[l]) rc = gmoe_forward(m->moe, l, n, m->x, m->x, m->moe_flags, st);
+    }
+    if (rc) return rc;
+    const float *xl = m->x + (size_t)(n - 1) * D;  // the last token
+    launch_gemv(gemv(m->out_q, m->out_s, xl, m->output_norm, m->logits, c.vocab_size, c.dim, c.group_size), GV_PLAIN, st);
+    MH_OK(hipGetLastError());
+    MH_OK(hipMemcpyAsync(logits, m->logits, (size_t)c.vocab_size * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (x_out) MH_OK(hipMemcpyAsync(x_out, xl, D * sizeof(float), hipMemcpyDeviceToHost, st));
     MH_OK(hipStreamSynchronize(st));
     if (m->moe && gm_take_launch_error(m->moe)) return GMOE_ERR_HIP;
     return GMOE_OK;

@@ -220,6 +220,8 @@ def forward_lib():
         lib.glm_argmax.restype = C.c_int
         lib.glm_hip_model_active.argtypes = []
         lib.glm_hip_model_active.restype = C.c_int
+        lib.glm_hip_prefill.argtypes = [RP, SP, IP, C.c_int, C.c_int, C.c_int]
+        lib.glm_hip_prefill.restype = C.c_int
         lib._forward_typed = True
     return lib
 
@@ -265,6 +267,18 @@ class Decoder:
             raise RuntimeError(f"glm_hip_forward_token failed at pos {pos}")
         out = self.logits()
         return (out, attn, layer) if checkpoints else out
+
+    def prefill(self, tokens, pos0=0):
+        """The prompt tokens at positions pos0.. (glm_hip_prefill: batches through the GPU
+        model when it is active); returns the last token's logits."""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        if toks.ndim != 1 or toks.size == 0:
+            raise ValueError("prefill takes a non-empty 1-d sequence of tokens")
+        rc = self.lib.glm_hip_prefill(C.byref(self.rt), C.byref(self.st), toks.ctypes.data_as(C.POINTER(C.c_int)),
+                                      int(toks.size), int(pos0), 0)
+        if rc != 0:
+            raise RuntimeError(f"glm_hip_prefill failed at positions {pos0}..{pos0 + toks.size - 1}")
+        return self.logits()
 
     def on_gpu(self):
         """True when every step of the forward runs on the GPU model (gmoe_model.h)."""

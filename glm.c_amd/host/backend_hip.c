@@ -14,6 +14,8 @@
  *   GLM_HIP_DEVICE          HIP device index (default 0)
  *   GLM_HIP_HOST_ATTN       keep embedding, attention, layer 0 and the LM head on the host
  *                           (glm.c's own arithmetic, forward.c) instead of the GPU model
+ *   GLM_HIP_PREFILL_BATCH   most prompt tokens of one batched prefill step (glm_hip_prefill;
+ *                           default 512, 1 turns batching off)
  *   GLM_HIP_STRICT          exit(1) when a GPU layer fails instead of returning -1
  *   GLM_DISABLE_MOE_ROUTED  skip routed experts, as infer.c:1161-1166 does
  */
@@ -73,7 +75,9 @@ int glm_hip_init(const Runtime *rt, RunState *st) {
     cfg.n_shared_experts = 1; /* infer.c:1197-1206 always runs one shared expert */
     cfg.group_size = (int32_t)c->group_size;
     cfg.n_layers = c->n_layers;
-    cfg.max_tokens = 1; /* the decode loop feeds one token at a time */
+    /* the decode loop feeds one token at a time, glm_hip_prefill up to a batch of prompt tokens */
+    const char *pb = getenv("GLM_HIP_PREFILL_BATCH");
+    cfg.max_tokens = pb && atoi(pb) > 0 ? atoi(pb) : 512;
     cfg.routed_scale = 1.8f; /* infer.c:1171 */
     cfg.norm_eps = 1e-5f;    /* infer.c:750 */
     cfg.q8_form = GMOE_Q8_AUTO; /* tiled at group size 32, glm.c's own layout otherwise */
@@ -162,6 +166,7 @@ static int prepare_model(const Runtime *rt, const RunState *st) {
     mc.cache_cap = st ? st->cache_cap : 0;
     mc.attn_layers = rt->has_all_attn ? c->n_layers : (rt->has_l0_attn ? 1 : 0);
     mc.has_l0_ffn = rt->has_l0_ffn;
+    mc.max_batch = g_cfg.max_tokens;
     gmoe_model *m = NULL;
     if (gmoe_model_create(&m, g_device, &mc) != GMOE_OK) {
         fprintf(stderr, "[glm-hip] %s; attention, layer 0 and the LM head stay on the host\n", gmoe_last_error());
@@ -227,6 +232,21 @@ int glm_hip_model_forward(const Runtime *rt, RunState *st, int token, int pos, i
     if (rc != GMOE_OK) {
         fprintf(stderr, "[glm-hip] forward at position %d failed: %s\n", pos, gmoe_last_error());
         return -1;
+    }
+    return 0;
+}
+
+int glm_hip_model_prefill(const Runtime *rt, RunState *st, const int *tokens, int n, int pos0) {
+    (void)rt;
+    if (!g_model || !st || !tokens || n < 1) return -1;
+    const int B = g_cfg.max_tokens;
+    for (int i = 0; i < n; i += B) {
+        const int k = n - i < B ? n - i : B;
+        if (gmoe_model_prefill(g_model, (const int32_t *)tokens + i, k, pos0 + i, st->logits, st->x, NULL) != GMOE_OK) {
+            fprintf(stderr, "[glm-hip] prefill at positions %d..%d failed: %s\n", pos0 + i, pos0 + i + k - 1,
+                    gmoe_last_error());
+            return -1;
+        }
     }
     return 0;
 }

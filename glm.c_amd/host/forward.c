@@ -285,6 +285,22 @@ int glm_hip_forward_token(const Runtime *rt, RunState *st, int token, int pos, i
     return fw_forward(rt, st, token, pos, debug_mode, NULL, 0, 0, NULL, NULL, 0, 0, NULL);
 }
 
+int glm_hip_prefill(const Runtime *rt, RunState *st, const int *tokens, int n, int pos0, int debug_mode) {
+    if (!rt || !st || !tokens || n < 1 || pos0 < 0) return -1;
+    if (pos0 + n > st->cache_cap) {
+        fprintf(stderr, "[glm-hip] prefill of positions %d..%d past the cache (%d positions)\n", pos0, pos0 + n - 1,
+                st->cache_cap);
+        return -1;
+    }
+    if (glm_hip_model_active()) return glm_hip_model_prefill(rt, st, tokens, n, pos0);
+    for (int i = 0; i < n; i++) {
+        int tok = tokens[i];
+        if (tok < 0 || tok >= rt->cfg.vocab_size) tok = 0;  // infer.c:2220
+        if (glm_hip_forward_token(rt, st, tok, pos0 + i, debug_mode) != 0) return -1;
+    }
+    return 0;
+}
+
 int glm_hip_forward_token_dual_checkpoints(const Runtime *rt, const RunState *src, int token, int pos, int debug_mode,
                                            float *attn_layer_out, int attn_layer_stride, int max_attn_layers,
                                            int *written_attn_layers, float *layer_out, int layer_stride, int max_layers,

@@ -54,6 +54,10 @@ int glm_hip_moe_layer(const Runtime *rt, RunState *st, int layer_idx, int debug_
 int glm_hip_model_active(void);
 int glm_hip_model_forward(const Runtime *rt, RunState *st, int token, int pos, int keep_state, float *logits,
                           float *attn_ckpt, float *layer_ckpt);
+/* n prompt tokens at positions pos0.. through the GPU model in batches of GLM_HIP_PREFILL_BATCH
+ * (gmoe_model_prefill): the last token's logits into st->logits and its final x into st->x.
+ * 0 ok, -1 error (glm_hip_prefill in glm_forward.h is the form that also works without the model). */
+int glm_hip_model_prefill(const Runtime *rt, RunState *st, const int *tokens, int n, int pos0);
 void glm_hip_free(void);
 
 #ifdef __cplusplus

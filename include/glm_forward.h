@@ -34,6 +34,14 @@ void glm_runstate_copy(const Runtime *rt, const RunState *src, RunState *dst);
 /* glm_cpu_forward_token (infer.c:1903-1905). */
 int glm_hip_forward_token(const Runtime *rt, RunState *st, int token, int pos, int debug_mode);
 
+/* The prompt loop of infer.c:2190-2219 for n prompt tokens at positions pos0 .. pos0+n-1:
+ * the same state as n glm_hip_forward_token calls in order (the cache gains the n
+ * positions, st->logits and st->x are the last token's; a token outside the vocabulary is
+ * taken as 0, infer.c:2220). With the GPU model the tokens go through it in batches
+ * (gmoe_model_prefill, GLM_HIP_PREFILL_BATCH tokens at a time), every layer's products and
+ * MoE experts over the whole batch; otherwise token by token. 0, or -1. */
+int glm_hip_prefill(const Runtime *rt, RunState *st, const int *tokens, int n, int pos0, int debug_mode);
+
 /* glm_cpu_forward_token_checkpoints (infer.c:1907-1938): the forward on a copy of src
  * (src is left as it was), writing x after each layer's FFN to layer_out + l*layer_stride
  * for l < max_layers. */

@@ -30,6 +30,7 @@ typedef struct gmoe_model_config {
     int32_t cache_cap;      /* latent-cache positions per attention layer, <= 65536 */
     int32_t attn_layers;    /* layers with attention: n_layers (has_all_attn), 1 (layer 0 only) or 0 */
     int32_t has_l0_ffn;     /* layer 0's dense FFN is present */
+    int32_t max_batch;      /* most tokens of one gmoe_model_prefill call (0 or 1: one) */
 } gmoe_model_config;
 
 /* One layer's attention tensors, in LayerAttnWeights order (model.h:47-63). */
@@ -87,6 +88,17 @@ int gmoe_model_set_moe(gmoe_model *m, gmoe_ctx *moe, const uint8_t *layers, int 
 #define GMOE_MODEL_KEEP_CACHE 1
 int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, float *x_out,
                              float *attn_ckpt, float *layer_ckpt, void *stream);
+
+/* n tokens at positions pos0 .. pos0+n-1 (n <= max_batch, pos0 + n <= cache_cap) through the
+ * model at once, layer by layer, then a synchronisation: the same result as n calls of
+ * gmoe_model_forward_token in order (the latent cache gains the n positions), but every
+ * product over the batch in one launch, and each MoE layer one gmoe_forward over the n
+ * tokens (the grouped expert GEMMs over per-expert token lists). glm.c prefills a prompt
+ * token by token (infer.c:2190-2233); this is the batched form of that loop. logits (host,
+ * vocab_size floats) are the last token's, and optionally x_out (host, dim floats) its x
+ * after the final layer. The MoE context must take n tokens (gmoe_config.max_tokens >= n). */
+int gmoe_model_prefill(gmoe_model *m, const int32_t *tokens, int n, int pos0, float *logits, float *x_out,
+                       void *stream);
 
 #ifdef __cplusplus
 }

@@ -96,3 +96,31 @@ def test_checkpoints_leave_the_state_alone_and_bad_positions_fail(tmp_path):
     finally:
         dec.free()
         ck.close()
+
+
+def test_prefill_without_the_gpu_model_is_the_token_loop(tmp_path):
+    """glm_hip_prefill on a checkpoint the host forward runs: the same logits, x and cache
+    as glm_hip_forward_token position by position; out-of-vocabulary tokens read as 0
+    (infer.c:2220); a prefill past the cache fails and leaves the process running."""
+    path = tmp_path / "dense.bin"
+    glm_model.write_synth_checkpoint(path, spec(1, 32, gmoe.SYNTH_SCALES_FP16))
+    ck = glm_model.Checkpoint(path)
+    toks = [1, 5, 17, 299, 42, 0, 17, 123]
+    a, b = glm_model.Decoder(ck, 12), glm_model.Decoder(ck, 12)
+    try:
+        c = ck.rt.cfg
+        for pos, tok in enumerate(toks):
+            a.step(tok, pos)
+        got = b.prefill([1, 5, 17, 299, 42, -3, 17, 123])  # -3 is read as token 0
+        assert np.array_equal(bits(got), bits(a.logits()))
+        x = [np.ctypeslib.as_array(C.cast(d.st.x, C.POINTER(C.c_float)), shape=(c.dim,)) for d in (a, b)]
+        assert np.array_equal(bits(x[0]), bits(x[1]))
+        n = len(toks) * c.kv_lora_rank
+        comp = [np.ctypeslib.as_array(C.cast(d.st.k_cache_comp, C.POINTER(C.c_float)), shape=(n,)) for d in (a, b)]
+        assert np.array_equal(bits(comp[0]), bits(comp[1]))
+        with pytest.raises(RuntimeError):
+            b.prefill([3, 4, 5, 6, 7], pos0=len(toks))  # positions 8..12 of a 12-position cache
+    finally:
+        a.free()
+        b.free()
+        ck.close()
