@@ -13,8 +13,10 @@ time against MI355X's 8 TB/s) and the reference CPU path timed on this host (glm
 own infer.c built from source, OpenMP bound to cores as glm.c's Makefile runs it, same
 weights). Extra keys time the other workloads on the same resident layers: one MoE
 layer per launch (rotating over the 46), prefill batches of T=512 (near-uniform
-routing) and T=128 (Zipf(1.2)-skewed routing) on the grouped expert GEMMs, and the
-glm.c drop-in hook (glm_backend_try_hip_moe on a RunState in host memory).
+routing) and T=128 (Zipf(1.2)-skewed routing) on the grouped expert GEMMs, the
+glm.c drop-in hook (glm_backend_try_hip_moe on a RunState in host memory), and the whole
+GLM-4.7-Flash-shaped model on the GPU: a 4096-token prompt by batched prefill, then 128
+tokens decoded one at a time.
 """
 import os
 
@@ -230,6 +232,48 @@ def backend_hook_us(gmoe, np, shape, host_layers, x0, tokens=2):
             "note": "per-layer wall time of glm_backend_try_hip_moe, host RunState in and out (PCIe-inclusive)"}
 
 
+def e2e_decode(gmoe, np, ctx, context=4096, new=128, seed=0):
+    """The whole GLM-4.7-Flash-shaped model on the GPU (gmoe_model): random-init dense side
+    (47 layers of MLA attention, dense layer 0, vocabulary 154880, all Q8_0) around the MoE
+    layers 1..46 already resident in ctx. A `context`-token prompt goes in by batched
+    prefill, then `new` tokens are decoded one at a time, each picked greedily on the host
+    from the logits of the step before (as glm.c's loop samples, infer.c:2190-2231)."""
+    cfg = dict(gmoe.GLM47_FLASH_MODEL, cache_cap=context + new, attn_layers=47, has_l0_ffn=1, max_batch=ctx.max_tokens)
+    t0 = time.perf_counter()
+    g, layers = gmoe.synth_model_weights(cfg, seed)
+    model = gmoe.Model(cfg)
+    try:
+        model.upload(g)
+        for l, a in enumerate(layers):
+            model.upload_attn(l, a)
+        del g, layers
+        model.set_moe(ctx, range(1, cfg["n_layers"]))
+        log(f"e2e model: dense side generated and uploaded in {time.perf_counter() - t0:.1f}s")
+        rng = np.random.default_rng(seed)
+        prompt = rng.integers(3, cfg["vocab_size"], context).astype(np.int32)
+        B = ctx.max_tokens
+        model.prefill(prompt[:B], 0)  # warm-up, rewritten below
+        t0 = time.perf_counter()
+        for i in range(0, context, B):
+            logits = model.prefill(prompt[i:i + B], i)
+        prefill_s = time.perf_counter() - t0
+        tok = int(np.argmax(logits))
+        for _ in range(2):  # warm-up steps that leave the cache as it was
+            model.forward_token(tok, context, flags=1)
+        t0 = time.perf_counter()
+        for i in range(new):
+            tok = int(np.argmax(model.forward_token(tok, context + i)))
+        decode_s = time.perf_counter() - t0
+    finally:
+        model.close()
+    return {"workload": f"GLM-4.7-Flash-shaped model (47 layers, vocab {cfg['vocab_size']}), {new} new tokens "
+                        f"decoded greedily after a {context}-token prompt; random-init Q8_0 weights",
+            "decode_tokens_s": round(new / decode_s, 2), "decode_ms_per_token": round(decode_s * 1e3 / new, 3),
+            "prefill_tokens_s": round(context / prefill_s, 1), "prefill_batch": B, "context": context, "new_tokens": new,
+            "note": "wall clock around gmoe_model_forward_token (each a synchronised step with its logits copied "
+                    "to the host) and gmoe_model_prefill; no CPU baseline (glm.c's CPU forward would take hours)"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -396,6 +440,10 @@ def main():
         # the glm.c drop-in hook on host memory (uploads its own copy of the layers)
         extra["backend_hook"] = backend_hook_us(gmoe, np, shape, host_layers, x0)
         log(f"backend hook: {extra['backend_hook']['layer_us']} us/layer")
+        if L == N_MOE_LAYERS:
+            extra["e2e_decode"] = e2e_decode(gmoe, np, ctx)
+            log(f"e2e: {extra['e2e_decode']['decode_tokens_s']} tok/s decode, "
+                f"{extra['e2e_decode']['prefill_tokens_s']} tok/s prefill")
 
     cpu = None
     if not args.no_cpu:

@@ -177,10 +177,13 @@ __global__ __launch_bounds__(DM_BLOCK) void k_embed_batch(const int8_t *__restri
 
 // ---- MLA attention over the latent cache ------------------------------------------
 
-#define AT_CH 64   // cache positions per chunk of k_attn_part (one per lane in its softmax)
-#define AT_HG 8    // heads per block of k_attn_part
+#define AT_TILE 36   // cache positions staged at a time by k_attn_chunk
+#define AT_HG 16     // most heads per block of k_attn_chunk
 #define AT_KV_MAX 512
 #define AT_ROPE_MAX 64
+#define AT_KS (AT_KV_MAX + AT_ROPE_MAX + 4)  // LDS row stride of a staged entry at the largest shape
+#define AT_MAX_PARTS 1024                   // most position ranges (partial results) per head
+#define AT_BLOCK 1024                       // threads of k_attn_chunk
 
 struct AttnArgs {
     const float *kv_a;     // [kv + rope]: the kv_a product of this position
@@ -190,10 +193,12 @@ struct AttnArgs {
     float *comp, *pe;      // this layer's latent cache, [cap][kv] and [cap][rope]
     float *q_pe;           // [H][rope]
     const float *q_abs;    // [H][kv]
-    float *part_ctx;       // [chunks][H][kv]
-    float *part_ml;        // [chunks][H][2]: chunk maximum and its sum of exponentials
+    float *part_ctx;       // [nblk][H][kv]
+    float *part_ml;        // [nblk][H][2]: a range's maximum score and its sum of exponentials
     float *ctx;            // [H][kv]
     int H, kv, rope, head_k, nope, pos;
+    int hg;                // heads per block of k_attn_chunk (<= AT_HG)
+    int nblk;              // position ranges of k_attn_chunk (blocks per head group), <= AT_MAX_PARTS
     float kq_scale;
 };
 
@@ -234,84 +239,214 @@ __global__ __launch_bounds__(DM_BLOCK) void k_attn_prep(AttnArgs a) {
     }
 }
 
-// Chunk c (AT_CH positions) of heads AT_HG * blockIdx.y ..: every score (the absorbed
-// query against the compressed entry plus the rotated parts, times 1/sqrt(head_k)), the
-// chunk's maximum and sum of exponentials per head, and its exponential-weighted sum of
-// compressed entries (infer.c:1017-1051, split into chunks and merged by k_attn_combine).
-__global__ __launch_bounds__(DM_BLOCK) void k_attn_part(AttnArgs a) {
-    __shared__ float qs[AT_HG][AT_KV_MAX + AT_ROPE_MAX];
-    __shared__ float sc[AT_HG][AT_CH];
+// Position range blockIdx.x of nblk (an even split of 0 .. pos) for heads hg * blockIdx.y ..
+// (infer.c:1029-1051, split into ranges and merged by k_attn_merge). The heads' queries are
+// staged in LDS once, the range's cache entries AT_TILE at a time, each with one round of
+// loads; each score is the absorbed query against the compressed entry plus the rotated
+// parts, times 1/sqrt(head_k). Per head the block keeps the range's running maximum and sum
+// of exponentials and the exponential-weighted sum of compressed entries, rescaled when the
+// maximum grows. The LDS holds one block per CU, so the block is 16 waves wide, and the
+// host sizes nblk so that a head group's ranges fill the CUs once.
+__global__ __launch_bounds__(AT_BLOCK) void k_attn_chunk(AttnArgs a) {
+    __shared__ __align__(16) float ks[AT_TILE * AT_KS];
+    __shared__ __align__(16) float qs[AT_HG * (AT_KV_MAX + AT_ROPE_MAX)];
+    __shared__ float sc[AT_HG][AT_TILE];
+    __shared__ float run_m[AT_HG], run_l[AT_HG], corr[AT_HG];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int c = blockIdx.x, h0 = AT_HG * blockIdx.y, nh = min(AT_HG, a.H - h0);
-    const int t0 = c * AT_CH, nt = min(AT_CH, a.pos + 1 - t0), KQ = a.kv + a.rope;
-    for (int j = tid; j < nh * KQ; j += DM_BLOCK) {
-        const int h = j / KQ, i = j % KQ;
-        qs[h][i] = i < a.kv ? a.q_abs[(size_t)(h0 + h) * a.kv + i] : a.q_pe[(size_t)(h0 + h) * a.rope + (i - a.kv)];
-    }
-    __syncthreads();
-    // scores: a wave per position, lane l holding entries l, l + 64, .. of it
-    const int nk = a.kv >> 6;
-    for (int t = w; t < nt; t += DM_BLOCK / 64) {
-        const float *kc = a.comp + (size_t)(t0 + t) * a.kv, *kp = a.pe + (size_t)(t0 + t) * a.rope;
-        float cv[AT_KV_MAX / 64];
+    const int b = blockIdx.x, h0 = a.hg * blockIdx.y, nh = min(a.hg, a.H - h0);
+    const int P = a.pos + 1;
+    const int r0 = (int)((long long)b * P / a.nblk), r1 = (int)((long long)(b + 1) * P / a.nblk);
+    const int kv = a.kv, rope = a.rope, KQ = kv + rope;
+    const int qsd = (KQ + 3) & ~3;          // a row of either, rounded up to whole float4s
+    const int ksd = ((KQ + 31) & ~31) + 4;  // entry row stride: 4 mod 32 keeps row-wise b128 reads apart
+    const int kv4 = kv >> 2, r2 = rope >> 1;
+    {
+        constexpr int NQ = (AT_HG * AT_KV_MAX / 4 + AT_BLOCK - 1) / AT_BLOCK;    // float4s of absorbed queries
+        constexpr int NR = (AT_HG * AT_ROPE_MAX / 2 + AT_BLOCK - 1) / AT_BLOCK;  // float2s of rotated queries
+        const float4 *gq = reinterpret_cast<const float4 *>(a.q_abs + (size_t)h0 * kv);
+        const float2 *gr = reinterpret_cast<const float2 *>(a.q_pe + (size_t)h0 * rope);
+        float4 vq[NQ];
+        float2 vr[NR];
 #pragma unroll
-        for (int k = 0; k < AT_KV_MAX / 64; k++) cv[k] = k < nk ? kc[lane + 64 * k] : 0.0f;
-        const float pv = lane < a.rope ? kp[lane] : 0.0f;
-        for (int h = 0; h < nh; h++) {
-            float part = lane < a.rope ? __fmul_rn(qs[h][a.kv + lane], pv) : 0.0f;
+        for (int k = 0; k < NQ; k++) {
+            const int i = tid + AT_BLOCK * k;
+            vq[k] = i < nh * kv4 ? gq[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
 #pragma unroll
-            for (int k = 0; k < AT_KV_MAX / 64; k++)
-                if (k < nk) part = fmaf(qs[h][lane + 64 * k], cv[k], part);
-            const float sum = gv_reduce<64>(part);
-            if (lane == 0) sc[h][t] = __fmul_rn(sum, a.kq_scale);
+        for (int k = 0; k < NR; k++) {
+            const int i = tid + AT_BLOCK * k;
+            vr[k] = i < nh * r2 ? gr[i] : make_float2(0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < NQ; k++) {
+            const int i = tid + AT_BLOCK * k;
+            if (i < nh * kv4) *reinterpret_cast<float4 *>(&qs[(i / kv4) * qsd + 4 * (i % kv4)]) = vq[k];
+        }
+#pragma unroll
+        for (int k = 0; k < NR; k++) {
+            const int i = tid + AT_BLOCK * k;
+            if (i < nh * r2) *reinterpret_cast<float2 *>(&qs[(i / r2) * qsd + kv + 2 * (i % r2)]) = vr[k];
+        }
+        if (qsd > KQ && tid < nh) {  // zeros up to the float4 boundary (rope % 4 == 2)
+            qs[tid * qsd + KQ] = 0.0f;
+            qs[tid * qsd + KQ + 1] = 0.0f;
+        }
+        if (tid < AT_HG) {
+            run_m[tid] = -INFINITY;
+            run_l[tid] = 0.0f;
         }
     }
-    __syncthreads();
-    // per head: the chunk's maximum, exp(score - max) and their sum (lane = position)
-    for (int h = w; h < nh; h += DM_BLOCK / 64) {
-        const float v = lane < nt ? sc[h][lane] : -INFINITY;
-        const float m = wave_max_dpp_f(v);
-        const float e = lane < nt ? expf(__fsub_rn(v, m)) : 0.0f;
-        const float l = gv_reduce<64>(e);
-        sc[h][lane] = e;
-        if (lane == 0) {
-            a.part_ml[((size_t)c * a.H + h0 + h) * 2] = m;
-            a.part_ml[((size_t)c * a.H + h0 + h) * 2 + 1] = l;
+    // the weighted sum's threads: (entry quad q, heads hs + HS j), each staged entry read
+    // once per thread for all of its heads
+    const int nq = kv4, HS = AT_BLOCK / nq;  // nq <= 128: HS >= 8
+    constexpr int NH = (AT_HG + AT_BLOCK / (AT_KV_MAX / 4) - 1) / (AT_BLOCK / (AT_KV_MAX / 4));
+    const bool summer = tid < nq * HS;
+    const int q = tid % nq, hs = tid / nq;
+    float4 acc[NH];
+#pragma unroll
+    for (int j = 0; j < NH; j++) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int t0 = r0; t0 < r1; t0 += AT_TILE) {
+        const int nt = min(AT_TILE, r1 - t0);
+        {
+            // every load of the tile first (one round trip), then the LDS stores
+            constexpr int NC = (AT_TILE * AT_KV_MAX / 4 + AT_BLOCK - 1) / AT_BLOCK;    // float4s of entries
+            constexpr int NP = (AT_TILE * AT_ROPE_MAX / 2 + AT_BLOCK - 1) / AT_BLOCK;  // float2s of rope parts
+            const float4 *gc = reinterpret_cast<const float4 *>(a.comp + (size_t)t0 * kv);
+            const float2 *gp = reinterpret_cast<const float2 *>(a.pe + (size_t)t0 * rope);
+            float4 vc[NC];
+            float2 vp[NP];
+#pragma unroll
+            for (int k = 0; k < NC; k++) {
+                const int i = tid + AT_BLOCK * k;
+                vc[k] = i < nt * kv4 ? gc[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int k = 0; k < NP; k++) {
+                const int i = tid + AT_BLOCK * k;
+                vp[k] = i < nt * r2 ? gp[i] : make_float2(0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int k = 0; k < NC; k++) {
+                const int i = tid + AT_BLOCK * k;
+                if (i < nt * kv4) *reinterpret_cast<float4 *>(&ks[(i / kv4) * ksd + 4 * (i % kv4)]) = vc[k];
+            }
+#pragma unroll
+            for (int k = 0; k < NP; k++) {
+                const int i = tid + AT_BLOCK * k;
+                if (i < nt * r2) *reinterpret_cast<float2 *>(&ks[(i / r2) * ksd + kv + 2 * (i % r2)]) = vp[k];
+            }
+            if (qsd > KQ && tid < nt) {
+                ks[tid * ksd + KQ] = 0.0f;
+                ks[tid * ksd + KQ + 1] = 0.0f;
+            }
+        }
+        __syncthreads();
+        // scores: lane pair (2p, 2p + 1) takes position p % AT_TILE of head p / AT_TILE, the
+        // two halves of the dot product, summed across the pair
+#pragma unroll
+        for (int k = 0; k < (AT_HG * AT_TILE + AT_BLOCK / 2 - 1) / (AT_BLOCK / 2); k++) {
+            const int p = (tid >> 1) + (AT_BLOCK / 2) * k, half = tid & 1, t = p % AT_TILE, h = p / AT_TILE;
+            const int n4 = qsd >> 2, n4a = (n4 + 1) >> 1;  // float4s of the dot, of its first half
+            const bool on = h < nh && t < nt;
+            float d0 = 0.0f, d1 = 0.0f;
+            if (on) {
+                const float4 *kr = reinterpret_cast<const float4 *>(ks + t * ksd);
+                const float4 *qr = reinterpret_cast<const float4 *>(qs + h * qsd);
+                const int j1 = half ? n4 : n4a;
+                int j = half ? n4a : 0;
+                for (; j + 1 < j1; j += 2) {
+                    const float4 k4 = kr[j], q4 = qr[j], k5 = kr[j + 1], q5 = qr[j + 1];
+                    d0 = fmaf(q4.x, k4.x, d0);
+                    d0 = fmaf(q4.y, k4.y, d0);
+                    d0 = fmaf(q4.z, k4.z, d0);
+                    d0 = fmaf(q4.w, k4.w, d0);
+                    d1 = fmaf(q5.x, k5.x, d1);
+                    d1 = fmaf(q5.y, k5.y, d1);
+                    d1 = fmaf(q5.z, k5.z, d1);
+                    d1 = fmaf(q5.w, k5.w, d1);
+                }
+                if (j < j1) {
+                    const float4 k4 = kr[j], q4 = qr[j];
+                    d0 = fmaf(q4.x, k4.x, d0);
+                    d0 = fmaf(q4.y, k4.y, d0);
+                    d0 = fmaf(q4.z, k4.z, d0);
+                    d0 = fmaf(q4.w, k4.w, d0);
+                }
+            }
+            float v = __fadd_rn(d0, d1);
+            v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_QUAD_1032, 0xF, 0xF,
+                                                                        false)));  // + the pair's other half
+            if (half == 0 && on) sc[h][t] = __fmul_rn(v, a.kq_scale);
+        }
+        __syncthreads();
+        // per head (a wave each): the tile's maximum, the running maximum and sum of
+        // exponentials, exp(score - running maximum) for the tile (lane = position)
+        for (int h = w; h < nh; h += AT_BLOCK / 64) {
+            const float v = lane < nt ? sc[h][lane] : -INFINITY;
+            const float mo = run_m[h], mn = fmaxf(mo, wave_max_dpp_f(v));
+            const float e = lane < nt ? expf(__fsub_rn(v, mn)) : 0.0f;
+            const float l = gv_reduce<64>(e);
+            const float cr = mo == -INFINITY ? 0.0f : expf(__fsub_rn(mo, mn));  // the earlier tiles' rescale
+            if (lane < AT_TILE) sc[h][lane] = e;
+            if (lane == 0) {
+                run_m[h] = mn;
+                run_l[h] = fmaf(run_l[h], cr, l);
+                corr[h] = cr;
+            }
+        }
+        __syncthreads();
+        if (summer) {
+#pragma unroll
+            for (int j = 0; j < NH; j++) {
+                const int h = hs + HS * j;
+                if (h < nh) {
+                    const float cr = corr[h];
+                    acc[j].x = __fmul_rn(acc[j].x, cr);
+                    acc[j].y = __fmul_rn(acc[j].y, cr);
+                    acc[j].z = __fmul_rn(acc[j].z, cr);
+                    acc[j].w = __fmul_rn(acc[j].w, cr);
+                }
+            }
+            for (int t = 0; t < nt; t++) {
+                const float4 k4 = *reinterpret_cast<const float4 *>(&ks[t * ksd + 4 * q]);
+#pragma unroll
+                for (int j = 0; j < NH; j++) {
+                    const int h = hs + HS * j;
+                    if (h < nh) {
+                        const float p = sc[h][t];
+                        acc[j].x = fmaf(p, k4.x, acc[j].x);
+                        acc[j].y = fmaf(p, k4.y, acc[j].y);
+                        acc[j].z = fmaf(p, k4.z, acc[j].z);
+                        acc[j].w = fmaf(p, k4.w, acc[j].w);
+                    }
+                }
+            }
+        }
+        __syncthreads();  // the next tile overwrites ks and sc
+    }
+    if (summer) {
+#pragma unroll
+        for (int j = 0; j < NH; j++) {
+            const int h = hs + HS * j;
+            if (h < nh) *reinterpret_cast<float4 *>(&a.part_ctx[((size_t)b * a.H + h0 + h) * kv + 4 * q]) = acc[j];
         }
     }
-    __syncthreads();
-    // the chunk's weighted sum of compressed entries: thread j owns entries j and j + 256
-    float acc[AT_HG][AT_KV_MAX / DM_BLOCK];
-#pragma unroll
-    for (int h = 0; h < AT_HG; h++)
-#pragma unroll
-        for (int k = 0; k < AT_KV_MAX / DM_BLOCK; k++) acc[h][k] = 0.0f;
-    for (int t = 0; t < nt; t++) {
-        const float *kc = a.comp + (size_t)(t0 + t) * a.kv;
-        float cv[AT_KV_MAX / DM_BLOCK];
-#pragma unroll
-        for (int k = 0; k < AT_KV_MAX / DM_BLOCK; k++) cv[k] = tid + DM_BLOCK * k < a.kv ? kc[tid + DM_BLOCK * k] : 0.0f;
-#pragma unroll
-        for (int h = 0; h < AT_HG; h++)
-            if (h < nh)
-#pragma unroll
-                for (int k = 0; k < AT_KV_MAX / DM_BLOCK; k++) acc[h][k] = fmaf(sc[h][t], cv[k], acc[h][k]);
+    if (tid < nh) {
+        a.part_ml[((size_t)b * a.H + h0 + tid) * 2] = run_m[tid];
+        a.part_ml[((size_t)b * a.H + h0 + tid) * 2 + 1] = run_l[tid];
     }
-#pragma unroll
-    for (int h = 0; h < AT_HG; h++)
-        if (h < nh)
-#pragma unroll
-            for (int k = 0; k < AT_KV_MAX / DM_BLOCK; k++)
-                if (tid + DM_BLOCK * k < a.kv) a.part_ctx[((size_t)c * a.H + h0 + h) * a.kv + tid + DM_BLOCK * k] = acc[h][k];
 }
 
-// Head blockIdx.x: the chunks merged (each weighted by exp(its max - the overall max)) and
-// divided by the total sum of exponentials: the softmax-weighted sum of compressed entries.
-__global__ __launch_bounds__(DM_BLOCK) void k_attn_combine(AttnArgs a) {
-    __shared__ float wgt[1024];
+// Head blockIdx.x, entries 64 * blockIdx.y ..: the ranges' partial sums merged (each
+// weighted by exp(its max - the overall max)) and divided by the total sum of exponentials,
+// the softmax-weighted sum of compressed entries (infer.c:1038-1051). The block's four
+// waves take every fourth range, eight loads in flight each.
+__global__ __launch_bounds__(DM_BLOCK) void k_attn_merge(AttnArgs a) {
+    __shared__ float wgt[AT_MAX_PARTS];
     __shared__ float red[DM_BLOCK / 64];
+    __shared__ float part[DM_BLOCK / 64][64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = blockIdx.x;
-    const int nc = (a.pos + AT_CH) / AT_CH;  // chunks over positions 0 .. pos
+    const int nc = a.nblk;  // the position ranges of k_attn_chunk
     float m = -INFINITY;
     for (int c = tid; c < nc; c += DM_BLOCK) m = fmaxf(m, a.part_ml[((size_t)c * a.H + h) * 2]);
     m = wave_max_dpp_f(m);
@@ -329,10 +464,23 @@ __global__ __launch_bounds__(DM_BLOCK) void k_attn_combine(AttnArgs a) {
     if (lane == 0) red[w] = l;
     __syncthreads();
     l = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = __fdiv_rn(1.0f, l);
-    for (int d = tid; d < a.kv; d += DM_BLOCK) {
-        float s = 0.0f;
-        for (int c = 0; c < nc; c++) s = fmaf(wgt[c], a.part_ctx[((size_t)c * a.H + h) * a.kv + d], s);
-        a.ctx[(size_t)h * a.kv + d] = __fmul_rn(s, inv);
+    const int d = 64 * blockIdx.y + lane;
+    const float *pc = a.part_ctx + (size_t)h * a.kv + d;
+    const size_t cs = (size_t)a.H * a.kv;  // one chunk's stride
+    float s = 0.0f;
+    int c = w;
+    for (; c + 28 < nc; c += 32) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = pc[(size_t)(c + 4 * k) * cs];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s = fmaf(wgt[c + 4 * k], v[k], s);
+    }
+    for (; c < nc; c += 4) s = fmaf(wgt[c], pc[(size_t)c * cs], s);
+    part[w][lane] = s;
+    __syncthreads();
+    if (w == 0) {
+        const float t = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+        a.ctx[(size_t)h * a.kv + d] = __fmul_rn(t, __fdiv_rn(1.0f, l));
     }
 }

@@ -11,7 +11,7 @@
 //     k_attn_prep                the position's cache entry (normalised kv, rotated rope
 //                                part) and every head's rotated query part
 //     k_gemv (per head)          q_abs = k_b_h . q_nope_h
-//     k_attn_part, k_attn_combine  softmax over the cache, weighted sum of entries
+//     k_attn_chunk, k_attn_merge   softmax over the cache, weighted sum of entries
 //     k_gemv (per head)          concat_h = v_b_h . ctx_h
 //     k_gemv (residual)          x += attn_out . concat
 //   layer 0: k_gemv (SwiGLU pair), k_gemv (residual): the dense FFN (infer.c:1067-1085)
@@ -58,6 +58,7 @@ struct AttnDev {
 
 struct gmoe_model {
     int device = 0;
+    int n_cu = 256;  // compute units of the device: k_attn_chunk fills them once per head group
     gmoe_model_config c{};
     gmoe_ctx *moe = nullptr;
     std::vector<uint8_t> moe_on;
@@ -71,7 +72,6 @@ struct gmoe_model {
     std::vector<AttnDev> attn;
     // the latent cache [attn_layers][cap][kv], [..][rope] and the rope table [cap][rope/2][2]
     float *comp = nullptr, *pe = nullptr, *rope_cs = nullptr;
-    // activations
     // activations, each [max_batch][..] (a single token uses the first row)
     float *x = nullptr, *q_a = nullptr, *q_full = nullptr, *kv_a = nullptr, *q_pe = nullptr, *q_abs = nullptr,
           *ctx = nullptr, *concat = nullptr, *ffh = nullptr, *logits = nullptr, *part_ctx = nullptr,
@@ -216,16 +216,13 @@ int check_config(const gmoe_model_config &c) {
     return GMOE_OK;
 }
 
-int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
+// The arguments of layer l's attention kernels for a token at position pos.
+AttnArgs attn_args(gmoe_model *m, int l, int pos) {
     const gmoe_model_config &c = m->c;
-    const AttnDev &A = m->attn[l];
-    const int gs = c.group_size, H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim;
-    launch_gemv(gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, c.q_lora_rank, c.dim, gs), GV_PLAIN, st);
-    launch_gemv(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, c.dim, gs), GV_PLAIN, st);
-    launch_gemv(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * c.head_k_dim, c.q_lora_rank, gs), GV_PLAIN, st);
+    const int H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim;
     AttnArgs aa{};
     aa.kv_a = m->kv_a;
-    aa.kv_norm = A.kv_a_norm;
+    aa.kv_norm = m->attn[l].kv_a_norm;
     aa.q_full = m->q_full;
     aa.rope_cs = m->rope_cs;
     aa.comp = m->comp + (size_t)l * c.cache_cap * kv;
@@ -241,16 +238,43 @@ int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
     aa.head_k = c.head_k_dim;
     aa.nope = c.qk_nope_dim;
     aa.pos = pos;
+    const int groups = (H + AT_HG - 1) / AT_HG;  // blocks per chunk, heads spread evenly over them
+    aa.hg = (H + groups - 1) / groups;
     aa.kq_scale = 1.0f / sqrtf((float)c.head_k_dim);  // infer.c:992
+    return aa;
+}
+
+// Position ranges of the attention over pos + 1 positions: about 32 positions each (a tile's
+// worth), at most one block per CU over all head groups.
+int attn_ranges(int n_cu, int groups, int positions) {
+    const int by_len = (positions + 31) / 32, by_cu = std::max(1, n_cu / groups);
+    return std::min(std::min(by_len, by_cu), AT_MAX_PARTS);
+}
+
+// The attention over the cache for one token (q_abs, q_pe of aa.pos into ctx): the ranges,
+// then their merge.
+void launch_attn_cache(gmoe_model *m, AttnArgs aa, hipStream_t st) {
+    const int groups = (aa.H + aa.hg - 1) / aa.hg;
+    aa.nblk = attn_ranges(m->n_cu, groups, aa.pos + 1);
+    hipLaunchKernelGGL(k_attn_chunk, dim3(aa.nblk, groups), dim3(AT_BLOCK), 0, st, aa);
+    hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64), dim3(DM_BLOCK), 0, st, aa);
+}
+
+int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
+    const gmoe_model_config &c = m->c;
+    const AttnDev &A = m->attn[l];
+    const int gs = c.group_size, H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim;
+    launch_gemv(gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, c.q_lora_rank, c.dim, gs), GV_PLAIN, st);
+    launch_gemv(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, c.dim, gs), GV_PLAIN, st);
+    launch_gemv(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * c.head_k_dim, c.q_lora_rank, gs), GV_PLAIN, st);
+    const AttnArgs aa = attn_args(m, l, pos);
     hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(DM_BLOCK), 0, st, aa);
     // the query absorbed into the latent space, per head: k_b_h [kv][nope] . q_nope_h
     GemvArgs kb = gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs);
     kb.x_rows = kv;
     kb.x_stride = c.head_k_dim;
     launch_gemv(kb, GV_PLAIN, st);
-    const int chunks = pos / AT_CH + 1;
-    hipLaunchKernelGGL(k_attn_part, dim3(chunks, (H + AT_HG - 1) / AT_HG), dim3(DM_BLOCK), 0, st, aa);
-    hipLaunchKernelGGL(k_attn_combine, dim3(H), dim3(DM_BLOCK), 0, st, aa);
+    launch_attn_cache(m, aa, st);
     // back out of the latent space, per head: v_b_h [v_head][kv] . ctx_h
     GemvArgs vb = gemv(A.v_b_q, A.v_b_s, m->ctx, nullptr, m->concat, H * c.v_head_dim, kv, gs);
     vb.x_rows = c.v_head_dim;
@@ -287,25 +311,7 @@ int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
     launch_gemv(batched(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, D, gs), D, kv + rope), GV_PLAIN, st,
                 n);
     launch_gemv(batched(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * hk, ql, gs), ql, H * hk), GV_PLAIN, st, n);
-    AttnArgs aa{};
-    aa.kv_a = m->kv_a;
-    aa.kv_norm = A.kv_a_norm;
-    aa.q_full = m->q_full;
-    aa.rope_cs = m->rope_cs;
-    aa.comp = m->comp + (size_t)l * c.cache_cap * kv;
-    aa.pe = m->pe + (size_t)l * c.cache_cap * rope;
-    aa.q_pe = m->q_pe;
-    aa.q_abs = m->q_abs;
-    aa.part_ctx = m->part_ctx;
-    aa.part_ml = m->part_ml;
-    aa.ctx = m->ctx;
-    aa.H = H;
-    aa.kv = kv;
-    aa.rope = rope;
-    aa.head_k = hk;
-    aa.nope = c.qk_nope_dim;
-    aa.pos = pos0;
-    aa.kq_scale = 1.0f / sqrtf((float)hk);  // infer.c:992
+    const AttnArgs aa = attn_args(m, l, pos0);
     hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)n), dim3(DM_BLOCK), 0, st, aa);
     GemvArgs kb = batched(gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs), H * hk, H * kv);
     kb.x_rows = kv;
@@ -317,9 +323,7 @@ int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
         at.q_abs = m->q_abs + (size_t)t * H * kv;
         at.ctx = m->ctx + (size_t)t * H * kv;
         at.pos = pos0 + t;
-        const int chunks = at.pos / AT_CH + 1;
-        hipLaunchKernelGGL(k_attn_part, dim3(chunks, (H + AT_HG - 1) / AT_HG), dim3(DM_BLOCK), 0, st, at);
-        hipLaunchKernelGGL(k_attn_combine, dim3(H), dim3(DM_BLOCK), 0, st, at);
+        launch_attn_cache(m, at, st);
     }
     GemvArgs vb = batched(gemv(A.v_b_q, A.v_b_s, m->ctx, nullptr, m->concat, H * vh, kv, gs), H * kv, H * vh);
     vb.x_rows = vh;
@@ -357,13 +361,16 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
     *out = nullptr;
     if (int rc = check_config(*cfg)) return rc;
     MH_OK(hipSetDevice(device));
+    int n_cu = 0;
+    MH_OK(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device));
     gmoe_model *m = new gmoe_model();
     m->device = device;
+    m->n_cu = std::max(1, n_cu);
     m->c = *cfg;
     const gmoe_model_config &c = m->c;
     const size_t L = (size_t)c.n_layers, A = (size_t)c.attn_layers, cap = (size_t)c.cache_cap;
     const size_t H = (size_t)c.n_heads, kv = (size_t)c.kv_lora_rank, rope = (size_t)c.rope_dim;
-    const size_t chunks = (cap + AT_CH - 1) / AT_CH;
+    const size_t ranges = (size_t)attn_ranges(m->n_cu, 1, (int)cap);  // the most any launch uses
     m->attn.resize(A);
     m->moe_on.assign(L, 0);
     int rc = GMOE_OK;
@@ -383,8 +390,8 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
         rc |= mdalloc(m, &m->q_abs, B * H * kv);
         rc |= mdalloc(m, &m->ctx, B * H * kv);
         rc |= mdalloc(m, &m->concat, B * H * c.v_head_dim);
-        rc |= mdalloc(m, &m->part_ctx, chunks * H * kv);
-        rc |= mdalloc(m, &m->part_ml, chunks * H * 2);
+        rc |= mdalloc(m, &m->part_ctx, ranges * H * kv);
+        rc |= mdalloc(m, &m->part_ml, ranges * H * 2);
         rc |= mdalloc(m, &m->saved, A * (kv + rope));
     }
     if (!rc && A > 0) {

@@ -107,6 +107,11 @@ def host_lib():
         lib.synth_q8_at.restype = C.c_int
         lib.synth_normal_at.argtypes = [C.c_uint64, C.c_uint64]
         lib.synth_normal_at.restype = C.c_double
+        lib.synth_q8_matrix.argtypes = [C.c_uint64, C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                        C.c_void_p]
+        lib.synth_q8_matrix.restype = None
+        lib.synth_normal_fill.argtypes = [C.c_uint64, C.c_size_t, C.c_double, C.c_double, C.c_void_p]
+        lib.synth_normal_fill.restype = None
         lib._typed = True
     return lib
 
@@ -286,6 +291,145 @@ class Context:
     def close(self):
         if self.h:
             self.lib.gmoe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- the whole model (gmoe_model.h)
+_MODEL_CFG = ["dim", "hidden_dim", "n_layers", "n_heads", "vocab_size", "q_lora_rank", "kv_lora_rank", "rope_dim",
+              "qk_nope_dim", "head_k_dim", "v_head_dim", "group_size", "cache_cap", "attn_layers", "has_l0_ffn",
+              "max_batch"]
+_ATTN_FIELDS = ["attn_norm", "q_a_norm", "kv_a_norm", "q_a_q", "q_a_s", "q_b_q", "q_b_s", "kv_a_q", "kv_a_s", "k_b_q",
+                "k_b_s", "v_b_q", "v_b_s", "attn_out_q", "attn_out_s"]
+_MODEL_FIELDS = ["output_norm", "tok_q", "tok_s", "out_q", "out_s", "l0_ffn_norm", "l0_ffn_gate_q", "l0_ffn_gate_s",
+                 "l0_ffn_up_q", "l0_ffn_up_s", "l0_ffn_down_q", "l0_ffn_down_s"]
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in _MODEL_CFG]
+
+
+class AttnWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _ATTN_FIELDS]
+
+
+class ModelWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _MODEL_FIELDS]
+
+
+# GLM-4.7-Flash's dense side (47 layers, MLA attention on every layer, dense layer 0)
+GLM47_FLASH_MODEL = dict(dim=2048, hidden_dim=10240, n_layers=47, n_heads=20, vocab_size=154880, q_lora_rank=768,
+                         kv_lora_rank=512, rope_dim=64, qk_nope_dim=192, head_k_dim=256, v_head_dim=256, group_size=32)
+
+
+def synth_model_weights(cfg, seed):
+    """Seeded random-init weights for gmoe_model_upload ({name: array}) and for every
+    attention layer's gmoe_model_upload_attn ([{name: array}]), from the counter-based
+    generator of the MoE layers (synth.c): Q8_0 values uniform in [-127, 127], fp32 scales
+    |N(0,1)| * 0.002, norm weights N(1, 0.1). Tensor t of layer l draws from
+    synth_key(seed, l, 100 + t, 0) (model-wide tensors: layer -1), apart from every MoE stream."""
+    h = host_lib()
+    D, gs, H = cfg["dim"], cfg["group_size"], cfg["n_heads"]
+    kv, rope, nope, hk, vh = cfg["kv_lora_rank"], cfg["rope_dim"], cfg["qk_nope_dim"], cfg["head_k_dim"], cfg["v_head_dim"]
+    where = {"layer": -1, "t": 100}
+
+    def key():
+        where["t"] += 1
+        return h.synth_key(seed, where["layer"], where["t"], 0)
+
+    def norm(n):
+        out = np.empty(n, np.float32)
+        h.synth_normal_fill(key(), n, 1.0, 0.1, ptr(out))
+        return out
+
+    def q8(rows, cols):
+        q = np.empty((rows, cols), np.int8)
+        s = np.empty((rows, cols // gs), np.float32)
+        h.synth_q8_matrix(key(), key(), rows, cols, gs, SYNTH_SCALES_FP32, ptr(q), ptr(s))
+        return q, s
+
+    g = {"output_norm": norm(D)}
+    g["tok_q"], g["tok_s"] = q8(cfg["vocab_size"], D)
+    g["out_q"], g["out_s"] = q8(cfg["vocab_size"], D)
+    if cfg.get("has_l0_ffn", 1):
+        F = cfg["hidden_dim"]
+        g["l0_ffn_norm"] = norm(D)
+        g["l0_ffn_gate_q"], g["l0_ffn_gate_s"] = q8(F, D)
+        g["l0_ffn_up_q"], g["l0_ffn_up_s"] = q8(F, D)
+        g["l0_ffn_down_q"], g["l0_ffn_down_s"] = q8(D, F)
+    layers = []
+    for layer in range(cfg.get("attn_layers", cfg["n_layers"])):
+        where["layer"], where["t"] = layer, 100
+        a = {"attn_norm": norm(D), "q_a_norm": norm(cfg["q_lora_rank"]), "kv_a_norm": norm(kv)}
+        a["q_a_q"], a["q_a_s"] = q8(cfg["q_lora_rank"], D)
+        a["q_b_q"], a["q_b_s"] = q8(H * hk, cfg["q_lora_rank"])
+        a["kv_a_q"], a["kv_a_s"] = q8(kv + rope, D)
+        a["k_b_q"], a["k_b_s"] = q8(H * kv, nope)
+        a["v_b_q"], a["v_b_s"] = q8(H * vh, kv)
+        a["attn_out_q"], a["attn_out_s"] = q8(D, H * vh)
+        layers.append(a)
+    return g, layers
+
+
+class Model:
+    """A gmoe_model: the whole decode forward on one device (embedding, MLA attention over
+    a device-resident latent cache, dense layer 0, the MoE layers of a Context, LM head)."""
+
+    def __init__(self, cfg, device=0):
+        self.lib = gmoe_lib()
+        if not getattr(self.lib, "_model_typed", False):
+            P = C.c_void_p
+            self.lib.gmoe_model_create.argtypes = [C.POINTER(P), C.c_int, C.POINTER(ModelConfig)]
+            self.lib.gmoe_model_upload.argtypes = [P, C.POINTER(ModelWeights)]
+            self.lib.gmoe_model_upload_attn.argtypes = [P, C.c_int, C.POINTER(AttnWeights)]
+            self.lib.gmoe_model_set_moe.argtypes = [P, P, P, C.c_int]
+            self.lib.gmoe_model_forward_token.argtypes = [P, C.c_int, C.c_int, C.c_int, P, P, P, P, P]
+            self.lib.gmoe_model_prefill.argtypes = [P, P, C.c_int, C.c_int, P, P, P]
+            for f in ("gmoe_model_create", "gmoe_model_upload", "gmoe_model_upload_attn", "gmoe_model_set_moe",
+                      "gmoe_model_forward_token", "gmoe_model_prefill"):
+                getattr(self.lib, f).restype = C.c_int
+            self.lib.gmoe_model_destroy.argtypes = [P]
+            self.lib.gmoe_model_destroy.restype = None
+            self.lib._model_typed = True
+        self.cfg = dict(cfg)
+        mc = ModelConfig(*[int(self.cfg.get(n, 0)) for n in _MODEL_CFG])
+        h = C.c_void_p()
+        check(self.lib.gmoe_model_create(C.byref(h), device, C.byref(mc)), "gmoe_model_create")
+        self.h = h
+        self.logits = np.zeros(self.cfg["vocab_size"], np.float32)
+
+    def upload(self, weights):
+        w = ModelWeights(*[ptr(weights.get(n)) for n in _MODEL_FIELDS])
+        check(self.lib.gmoe_model_upload(self.h, C.byref(w)), "gmoe_model_upload")
+
+    def upload_attn(self, layer, weights):
+        w = AttnWeights(*[ptr(weights[n]) for n in _ATTN_FIELDS])
+        check(self.lib.gmoe_model_upload_attn(self.h, layer, C.byref(w)), "gmoe_model_upload_attn")
+
+    def set_moe(self, ctx, layers, flags=0):
+        on = np.zeros(self.cfg["n_layers"], np.uint8)
+        on[list(layers)] = 1
+        check(self.lib.gmoe_model_set_moe(self.h, ctx.h, ptr(on), flags), "gmoe_model_set_moe")
+
+    def forward_token(self, token, pos, flags=0, stream=None):
+        check(self.lib.gmoe_model_forward_token(self.h, int(token), int(pos), flags, ptr(self.logits), None, None, None,
+                                                stream), "gmoe_model_forward_token")
+        return self.logits
+
+    def prefill(self, tokens, pos0=0, stream=None):
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        check(self.lib.gmoe_model_prefill(self.h, ptr(toks), int(toks.size), int(pos0), ptr(self.logits), None, stream),
+              "gmoe_model_prefill")
+        return self.logits
+
+    def close(self):
+        if self.h:
+            self.lib.gmoe_model_destroy(self.h)
             self.h = None
 
     def __del__(self):

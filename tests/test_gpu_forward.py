@@ -15,7 +15,7 @@ checkpoints equal glm.c's bit for bit at every position.
 
 Greedy: the decoder picks each next token itself (argmax, with infer.c:2213-2219's
 bos/eos skips), and glm.c, fed the same sequence, picks the same token at every step.
-A 150-position run takes the GPU attention over several 64-position chunks."""
+A 150-position run takes the GPU attention over several 32-position chunks."""
 import numpy as np
 import pytest
 
@@ -47,8 +47,16 @@ def glm_dims(seed=22):
                               bias_mode=gmoe.SYNTH_BIAS_NORMAL, scale_mode=gmoe.SYNTH_SCALES_FP16)
 
 
+def glm_heads(seed=25):
+    """glm_dims with GLM-4.7-Flash's 20 heads: the attention spreads them over two blocks of
+    10 per cache chunk."""
+    sp = glm_dims(seed)
+    sp.n_heads = sp.n_kv_heads = 20
+    return sp
+
+
 CASES = {"gs16_native": lambda: small(16, gmoe.SYNTH_SCALES_FP32), "gs32_tiled": lambda: small(32, gmoe.SYNTH_SCALES_FP16),
-         "glm_dims": glm_dims}
+         "glm_dims": glm_dims, "glm_heads": glm_heads}
 TOKENS = [1, 5, 17, 299, 42, 0, 17, 123, 7, 250]
 MODES = ["gpu", "host_attn"]
 

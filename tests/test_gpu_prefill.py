@@ -10,7 +10,7 @@ at a time on the cache the prefill wrote, must match glm.c's logits at every lat
 position, which checks every cache entry the prefill wrote (every attention layer reads all
 of them). Batches of 1, 4 and the default 512 take the prompt whole, in ragged pieces
 and one token at a time; a 150-token prompt in 64-token batches crosses attention's
-64-position chunks inside a batch."""
+32-position chunks inside a batch."""
 import ctypes as C
 
 import numpy as np
