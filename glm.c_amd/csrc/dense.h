@@ -30,6 +30,12 @@ struct GemvArgs {
     float *y;              // GV_PAIR: y = silu(dot) * dot2 (infer.c:1078-1080)
     int rows, cols, gs, x_rows, x_stride;
     int bx, by, br;        // a batch (grid y): token t's x, y and resid start t*bx, t*by, t*br floats in
+    // GV_PLAIN only: a second matrix over the same input, its rows after the first's
+    // (rows a multiple of the kernel's rows per wave): yb = qb . x
+    const int8_t *qb;
+    const float *sb;
+    float *yb;
+    int rows_b, by_b;
 };
 
 // Sum over each 16-lane row of a wave in fp64, to every lane of the row.
@@ -87,26 +93,36 @@ __device__ static inline void gv_load_x(const GemvArgs &a, int g, float (&xv)[U]
     }
 }
 
-// The lane's share of row r's dot product with its units.
+// The lane's units of row r of a matrix: 16 int8 values and their group's scale each.
+template <int U>
+struct GvRow {
+    u32x4 q[U];
+    float s[U];
+};
+
 template <int LPR, int U>
-__device__ static inline float gv_dot(const int8_t *q, const float *s, int r, const GemvArgs &a, const float (&xv)[U][16]) {
+__device__ static inline void gv_fetch(const int8_t *q, const float *s, int r, const GemvArgs &a, GvRow<U> &w) {
     const int sl = (threadIdx.x & 63) % LPR, nunits = a.cols >> 4, ng = a.cols / a.gs;
-    u32x4 qv[U];
-    float sv[U];
 #pragma unroll
     for (int m = 0; m < U; m++) {
         const int u = sl + LPR * m, uc = u < nunits ? u : 0;
-        qv[m] = *gbl((const u32x4 *)(q + (size_t)r * a.cols + 16 * (size_t)uc));
-        sv[m] = *gbl(s + (size_t)r * ng + (16 * uc) / a.gs);
+        w.q[m] = *gbl((const u32x4 *)(q + (size_t)r * a.cols + 16 * (size_t)uc));
+        w.s[m] = *gbl(s + (size_t)r * ng + (16 * uc) / a.gs);
     }
+}
+
+// The lane's share of a fetched row's dot product with its units.
+template <int LPR, int U>
+__device__ static inline float gv_dot(const GvRow<U> &w, const GemvArgs &a, const float (&xv)[U][16]) {
+    const int sl = (threadIdx.x & 63) % LPR, nunits = a.cols >> 4;
     float acc = 0.0f;
 #pragma unroll
     for (int m = 0; m < U; m++) {
-        const unsigned wd[4] = {qv[m].x, qv[m].y, qv[m].z, qv[m].w};
+        const unsigned wd[4] = {w.q[m].x, w.q[m].y, w.q[m].z, w.q[m].w};
         float part = 0.0f;
 #pragma unroll
         for (int k = 0; k < 16; k++) part = fmaf((float)(int8_t)(wd[k >> 2] >> (8 * (k & 3))), xv[m][k], part);
-        if (sl + LPR * m < nunits) acc = fmaf(part, sv[m], acc);
+        if (sl + LPR * m < nunits) acc = fmaf(part, w.s[m], acc);
     }
     return acc;
 }
@@ -128,27 +144,44 @@ __global__ __launch_bounds__(DM_BLOCK) void k_gemv(GemvArgs a) {
         a.y += t * (size_t)a.by;
         if (MODE == GV_RESID) a.resid += t * (size_t)a.br;
     }
+    if (MODE == GV_PLAIN && a.rows_b) a.yb += blockIdx.y * (size_t)a.by_b;
     const int lane = threadIdx.x & 63, sub = lane / LPR, sl = lane % LPR;
     const int wave = blockIdx.x * (DM_BLOCK / 64) + (threadIdx.x >> 6), nwaves = gridDim.x * (DM_BLOCK / 64);
-    const int nrg = (a.rows + RPW - 1) / RPW;
+    const int rows_all = a.rows + (MODE == GV_PLAIN ? a.rows_b : 0);
+    const int nrg = (rows_all + RPW - 1) / RPW;
     float xv[U][16];
     int xg = -1;  // the input group xv holds
     for (int rg = wave; rg < nrg; rg += nwaves) {
+        // the row group's weights are requested before the input is loaded and normalised
+        int r = rg * RPW + sub, n = a.rows;
+        const int8_t *q = a.q;
+        const float *s = a.s;
+        float *y = a.y;
+        if (MODE == GV_PLAIN && r >= a.rows) {  // the second matrix (whole row groups)
+            r -= a.rows;
+            n = a.rows_b;
+            q = a.qb;
+            s = a.sb;
+            y = a.yb;
+        }
+        const int rc = r < n ? r : n - 1;
+        GvRow<U> w, w2;
+        gv_fetch<LPR, U>(q, s, rc, a, w);
+        if (MODE == GV_PAIR) gv_fetch<LPR, U>(a.q2, a.s2, rc, a, w2);
         const int g = (rg * RPW) / a.x_rows;  // x_rows is a multiple of RPW: one group per row group
         if (g != xg) {
             gv_load_x<LPR, U>(a, g, xv);
             xg = g;
         }
-        const int r = rg * RPW + sub, rc = r < a.rows ? r : a.rows - 1;
-        const float d = gv_reduce<LPR>(gv_dot<LPR, U>(a.q, a.s, rc, a, xv));
+        const float d = gv_reduce<LPR>(gv_dot<LPR, U>(w, a, xv));
         float out = d;
         if (MODE == GV_PAIR) {
-            const float d2 = gv_reduce<LPR>(gv_dot<LPR, U>(a.q2, a.s2, rc, a, xv));
+            const float d2 = gv_reduce<LPR>(gv_dot<LPR, U>(w2, a, xv));
             out = __fmul_rn(__fdiv_rn(d, __fadd_rn(1.0f, expf(-d))), d2);
         }
-        if (sl == 0 && r < a.rows) {
+        if (sl == 0 && r < n) {
             if (MODE == GV_RESID) out = __fadd_rn(a.resid[r], d);
-            a.y[r] = out;
+            y[r] = out;
         }
     }
 }

@@ -116,7 +116,7 @@ template <int MODE>
 int launch_gemv_mode(const GemvArgs &a, hipStream_t st, int nb) {
     const int units = a.cols >> 4;
     const int lpr = units <= 64 ? 16 : 64;
-    const int rpw = 64 / lpr, nrg = (a.rows + rpw - 1) / rpw;
+    const int rpw = 64 / lpr, nrg = (a.rows + a.rows_b + rpw - 1) / rpw;
     const dim3 grid((unsigned)std::min((nrg + 3) / 4, 2048), (unsigned)nb), block(DM_BLOCK);
     if (lpr == 16) {
         switch ((units + 15) / 16) {
@@ -139,6 +139,9 @@ int launch_gemv_mode(const GemvArgs &a, hipStream_t st, int nb) {
     }
     return GMOE_OK;
 }
+
+// The rows per wave of k_gemv for cols columns (a second matrix's rows start on a multiple).
+int gemv_rows_per_wave(int cols) { return (cols >> 4) <= 64 ? 4 : 1; }
 
 // One launch for nb tokens (a.bx, a.by, a.br apart).
 int launch_gemv(const GemvArgs &a, int mode, hipStream_t st, int nb = 1) {
@@ -168,7 +171,23 @@ GemvArgs gemv(const int8_t *q, const float *s, const float *x, const float *norm
     a.x_rows = 1 << 30;
     a.x_stride = 0;
     a.bx = a.by = a.br = 0;
+    a.qb = nullptr;
+    a.sb = nullptr;
+    a.yb = nullptr;
+    a.rows_b = a.by_b = 0;
     return a;
+}
+
+// a (GV_PLAIN) and b, two products of the same input and norm, in one launch when a's rows
+// end on a row group of the kernel (else b is left for its own launch: returns false).
+bool fuse_second(GemvArgs &a, const GemvArgs &b) {
+    if (a.rows % gemv_rows_per_wave(a.cols) || b.cols != a.cols) return false;
+    a.qb = b.q;
+    a.sb = b.s;
+    a.yb = b.y;
+    a.rows_b = b.rows;
+    a.by_b = b.by;
+    return true;
 }
 
 constexpr int kMaxCols = 16 * 64 * 10;  // the widest k_gemv instance
@@ -264,8 +283,12 @@ int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
     const gmoe_model_config &c = m->c;
     const AttnDev &A = m->attn[l];
     const int gs = c.group_size, H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim;
-    launch_gemv(gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, c.q_lora_rank, c.dim, gs), GV_PLAIN, st);
-    launch_gemv(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, c.dim, gs), GV_PLAIN, st);
+    {
+        GemvArgs qa = gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, c.q_lora_rank, c.dim, gs);
+        const GemvArgs kva = gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, c.dim, gs);
+        if (!fuse_second(qa, kva)) launch_gemv(kva, GV_PLAIN, st);
+        launch_gemv(qa, GV_PLAIN, st);
+    }
     launch_gemv(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * c.head_k_dim, c.q_lora_rank, gs), GV_PLAIN, st);
     const AttnArgs aa = attn_args(m, l, pos);
     hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(DM_BLOCK), 0, st, aa);
@@ -307,9 +330,12 @@ int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
     const AttnDev &A = m->attn[l];
     const int gs = c.group_size, H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim, D = c.dim;
     const int ql = c.q_lora_rank, hk = c.head_k_dim, vh = c.v_head_dim;
-    launch_gemv(batched(gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, ql, D, gs), D, ql), GV_PLAIN, st, n);
-    launch_gemv(batched(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, D, gs), D, kv + rope), GV_PLAIN, st,
-                n);
+    {
+        GemvArgs qa = batched(gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, ql, D, gs), D, ql);
+        const GemvArgs kva = batched(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, D, gs), D, kv + rope);
+        if (!fuse_second(qa, kva)) launch_gemv(kva, GV_PLAIN, st, n);
+        launch_gemv(qa, GV_PLAIN, st, n);
+    }
     launch_gemv(batched(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * hk, ql, gs), ql, H * hk), GV_PLAIN, st, n);
     const AttnArgs aa = attn_args(m, l, pos0);
     hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)n), dim3(DM_BLOCK), 0, st, aa);
