@@ -135,8 +135,9 @@ __device__ static inline float gv_reduce(float v) {
     return v;
 }
 
+// The product over blocks bx of nbx (grid x) and token blockIdx.y of a batch.
 template <int LPR, int U, int MODE>
-__global__ __launch_bounds__(DM_BLOCK) void k_gemv(GemvArgs a) {
+__device__ __attribute__((always_inline)) static void gemv_run(GemvArgs a, int bx, int nbx) {
     constexpr int RPW = 64 / LPR;  // rows per wave at a time
     {
         const size_t t = blockIdx.y;  // the token of a batch
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(DM_BLOCK) void k_gemv(GemvArgs a) {
     }
     if (MODE == GV_PLAIN && a.rows_b) a.yb += blockIdx.y * (size_t)a.by_b;
     const int lane = threadIdx.x & 63, sub = lane / LPR, sl = lane % LPR;
-    const int wave = blockIdx.x * (DM_BLOCK / 64) + (threadIdx.x >> 6), nwaves = gridDim.x * (DM_BLOCK / 64);
+    const int wave = bx * (DM_BLOCK / 64) + (threadIdx.x >> 6), nwaves = nbx * (DM_BLOCK / 64);
     const int rows_all = a.rows + (MODE == GV_PLAIN ? a.rows_b : 0);
     const int nrg = (rows_all + RPW - 1) / RPW;
     float xv[U][16];
@@ -184,6 +185,11 @@ __global__ __launch_bounds__(DM_BLOCK) void k_gemv(GemvArgs a) {
             y[r] = out;
         }
     }
+}
+
+template <int LPR, int U, int MODE>
+__global__ __launch_bounds__(DM_BLOCK) void k_gemv(GemvArgs a) {
+    gemv_run<LPR, U, MODE>(a, blockIdx.x, gridDim.x);
 }
 
 // ---- embedding --------------------------------------------------------------------
@@ -237,13 +243,12 @@ struct AttnArgs {
 
 // The position's cache entry and the heads' rotated queries (infer.c:1000-1016): the
 // compressed kv normalised (rmsnorm over kv values), the rope part of kv_a and of every
-// head's query rotated by the position's angles. One block per token: block t of a batch
-// takes token t at position pos + t (its kv_a, q_full and q_pe t token strides on).
-__global__ __launch_bounds__(DM_BLOCK) void k_attn_prep(AttnArgs a) {
+// head's query rotated by the position's angles. One block for token t of a batch, at
+// position pos + t (its kv_a, q_full and q_pe t token strides on).
+__device__ __attribute__((always_inline)) static void attn_prep_run(AttnArgs a, int t) {
     __shared__ double red[DM_BLOCK / 64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     {
-        const int t = blockIdx.x;
         a.kv_a += (size_t)t * (a.kv + a.rope);
         a.q_full += (size_t)t * a.H * a.head_k;
         a.q_pe += (size_t)t * a.H * a.rope;
@@ -270,6 +275,17 @@ __global__ __launch_bounds__(DM_BLOCK) void k_attn_prep(AttnArgs a) {
         dst[2 * i] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
         dst[2 * i + 1] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
     }
+}
+
+// The query side of a token's attention in one launch: the absorbed queries q_abs = k_b_h .
+// q_nope_h (the k_b product, blocks 0 .. gridDim.x - 2) and, on the last block of the
+// row, k_attn_prep's cache entry and rotated queries. The two read q_full and kv_a only.
+template <int LPR, int U>
+__global__ __launch_bounds__(DM_BLOCK) void k_attn_query(GemvArgs kb, AttnArgs aa) {
+    if (blockIdx.x + 1 < gridDim.x)
+        gemv_run<LPR, U, GV_PLAIN>(kb, blockIdx.x, gridDim.x - 1);
+    else
+        attn_prep_run(aa, blockIdx.y);
 }
 
 // Position range blockIdx.x of nblk (an even split of 0 .. pos) for heads hg * blockIdx.y ..

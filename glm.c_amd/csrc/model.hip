@@ -8,9 +8,9 @@
 //   per attention layer (infer.c:978-1065):
 //     k_gemv                     q_a = q_a . rmsnorm(x), kv_a = kv_a . rmsnorm(x)
 //     k_gemv                     q = q_b . rmsnorm(q_a)
-//     k_attn_prep                the position's cache entry (normalised kv, rotated rope
-//                                part) and every head's rotated query part
-//     k_gemv (per head)          q_abs = k_b_h . q_nope_h
+//     k_attn_query               q_abs = k_b_h . q_nope_h per head, and on one more block the
+//                                position's cache entry (normalised kv, rotated rope part)
+//                                and every head's rotated query part
 //     k_attn_chunk, k_attn_merge   softmax over the cache, weighted sum of entries
 //     k_gemv (per head)          concat_h = v_b_h . ctx_h
 //     k_gemv (residual)          x += attn_out . concat
@@ -135,6 +135,39 @@ int launch_gemv_mode(const GemvArgs &a, hipStream_t st, int nb) {
         case 7:
         case 8: hipLaunchKernelGGL((k_gemv<64, 8, MODE>), grid, block, 0, st, a); break;
         default: hipLaunchKernelGGL((k_gemv<64, 10, MODE>), grid, block, 0, st, a); break;
+        }
+    }
+    return GMOE_OK;
+}
+
+// k_attn_query for nb tokens: kb (the k_b product, batched) and one prep block per token.
+template <int LPR, int U>
+void launch_query_lu(const GemvArgs &kb, const AttnArgs &aa, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((k_attn_query<LPR, U>), grid, dim3(DM_BLOCK), 0, st, kb, aa);
+}
+
+int launch_query(const GemvArgs &kb, const AttnArgs &aa, hipStream_t st, int nb) {
+    const int units = kb.cols >> 4;
+    const int lpr = units <= 64 ? 16 : 64;
+    const int rpw = 64 / lpr, nrg = (kb.rows + rpw - 1) / rpw;
+    const dim3 grid((unsigned)std::min((nrg + 3) / 4, 2048) + 1, (unsigned)nb);
+    if (lpr == 16) {
+        switch ((units + 15) / 16) {
+        case 1: launch_query_lu<16, 1>(kb, aa, grid, st); break;
+        case 2: launch_query_lu<16, 2>(kb, aa, grid, st); break;
+        case 3: launch_query_lu<16, 3>(kb, aa, grid, st); break;
+        default: launch_query_lu<16, 4>(kb, aa, grid, st); break;
+        }
+    } else {
+        switch ((units + 63) / 64) {
+        case 2: launch_query_lu<64, 2>(kb, aa, grid, st); break;
+        case 3: launch_query_lu<64, 3>(kb, aa, grid, st); break;
+        case 4: launch_query_lu<64, 4>(kb, aa, grid, st); break;
+        case 5: launch_query_lu<64, 5>(kb, aa, grid, st); break;
+        case 6: launch_query_lu<64, 6>(kb, aa, grid, st); break;
+        case 7:
+        case 8: launch_query_lu<64, 8>(kb, aa, grid, st); break;
+        default: launch_query_lu<64, 10>(kb, aa, grid, st); break;
         }
     }
     return GMOE_OK;
@@ -291,12 +324,12 @@ int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
     }
     launch_gemv(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * c.head_k_dim, c.q_lora_rank, gs), GV_PLAIN, st);
     const AttnArgs aa = attn_args(m, l, pos);
-    hipLaunchKernelGGL(k_attn_prep, dim3(1), dim3(DM_BLOCK), 0, st, aa);
-    // the query absorbed into the latent space, per head: k_b_h [kv][nope] . q_nope_h
+    // the query absorbed into the latent space, per head: k_b_h [kv][nope] . q_nope_h, with
+    // the cache entry and the rotated queries in the same launch
     GemvArgs kb = gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs);
     kb.x_rows = kv;
     kb.x_stride = c.head_k_dim;
-    launch_gemv(kb, GV_PLAIN, st);
+    launch_query(kb, aa, st, 1);
     launch_attn_cache(m, aa, st);
     // back out of the latent space, per head: v_b_h [v_head][kv] . ctx_h
     GemvArgs vb = gemv(A.v_b_q, A.v_b_s, m->ctx, nullptr, m->concat, H * c.v_head_dim, kv, gs);
@@ -338,11 +371,10 @@ int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
     }
     launch_gemv(batched(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * hk, ql, gs), ql, H * hk), GV_PLAIN, st, n);
     const AttnArgs aa = attn_args(m, l, pos0);
-    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)n), dim3(DM_BLOCK), 0, st, aa);
     GemvArgs kb = batched(gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs), H * hk, H * kv);
     kb.x_rows = kv;
     kb.x_stride = hk;
-    launch_gemv(kb, GV_PLAIN, st, n);
+    launch_query(kb, aa, st, n);  // every token's cache entry before any token's attention
     for (int t = 0; t < n; t++) {
         AttnArgs at = aa;
         at.q_pe = m->q_pe + (size_t)t * H * rope;

@@ -841,6 +841,7 @@ __device__ __attribute__((always_inline)) static bool rl_finish_expert(const Sta
     const float arg = lane == 0 ? f32_rd(S - B) : lane == 1 ? f32_ru(S + B) : (float)S;
     const float sgm = 1.0f / (1.0f + expf(-arg));
     const float plo = readlane_f(sgm, 0), phi = readlane_f(sgm, 1), pv = readlane_f(sgm, 2);
+    sk_stamp(sh, 21);
     if (lane < SK_STAGE_COPIES) {
         double lo, hi;
         selection_bounds((double)plo, (double)phi, bias, &lo, &hi);
@@ -853,6 +854,7 @@ __device__ __attribute__((always_inline)) static bool rl_finish_expert(const Sta
         st_u64(stage_plane(a, li, lane, 0) + e,
                (unsigned long long)__float_as_uint(lo_f) | ((unsigned long long)__float_as_uint(hi_f) << 32));
     }
+    sk_stamp(sh, 22);
     return true;
 }
 
