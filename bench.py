@@ -271,7 +271,8 @@ def e2e_decode(gmoe, np, ctx, context=4096, new=128, seed=0):
             "decode_tokens_s": round(new / decode_s, 2), "decode_ms_per_token": round(decode_s * 1e3 / new, 3),
             "prefill_tokens_s": round(context / prefill_s, 1), "prefill_batch": B, "context": context, "new_tokens": new,
             "note": "wall clock around gmoe_model_forward_token (each a synchronised step with its logits copied "
-                    "to the host) and gmoe_model_prefill; no CPU baseline (glm.c's CPU forward would take hours)"}
+                    "to the host) and gmoe_model_prefill; glm.c's CPU forward at the same position: "
+                    "python3 bench.py --e2e --e2e-cpu"}
 
 
 def main():
@@ -295,6 +296,9 @@ def main():
                     help="only the whole-model decode (a --context-token prompt by batched prefill, then --new tokens)")
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--new", type=int, default=128)
+    ap.add_argument("--e2e-cpu", action="store_true",
+                    help="with --e2e: also time glm.c's CPU forward at the same position (writes a ~33 GB checkpoint "
+                         "to a RAM-backed temporary file for the run)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -486,6 +490,64 @@ def main():
     ctx.close()
 
 
+E2E_CPU_SCRIPT = r"""
+import ctypes as C, json, sys
+lib = C.CDLL(sys.argv[1])
+lib.ref_forward_timed.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
+lib.ref_forward_timed.restype = C.c_int
+pos, cap, n, threads = (int(v) for v in sys.argv[3:7])
+ms = (C.c_double * n)()
+rc = lib.ref_forward_timed(sys.argv[2].encode(), 5, pos, cap, n, threads, ms)
+print(json.dumps({"rc": rc, "token_ms": list(ms)}))
+"""
+
+
+def e2e_cpu_baseline(gmoe, context, tokens=2):
+    """glm.c's own CPU forward (oracle/_ref: infer.c's glm_cpu_forward_token, its Makefile's
+    flags, OpenMP bound to cores) on a synthetic v4 checkpoint of the same GLM-4.7-Flash
+    shape, `tokens` tokens at position `context` of a zeroed cache (the attention reads
+    every earlier position either way), in a child process since glm.c's loader exits on
+    a file it rejects. The checkpoint (~33 GB) lives in a RAM-backed temporary file for
+    the run only."""
+    import tempfile
+    import glm_model
+    import oracle
+    if not oracle.available("reference"):
+        return None
+    m = gmoe.GLM47_FLASH_MODEL
+    sp = glm_model.CkptSpec(dim=m["dim"], hidden_dim=m["hidden_dim"], n_layers=m["n_layers"], n_heads=m["n_heads"],
+                            n_kv_heads=m["n_heads"], vocab_size=m["vocab_size"], seq_len=context + tokens + 8,
+                            rope_dim=m["rope_dim"], q_lora_rank=m["q_lora_rank"], kv_lora_rank=m["kv_lora_rank"],
+                            n_routed_experts=64, n_experts_used=4, bos_id=1, eos_id=2, qk_nope_dim=m["qk_nope_dim"],
+                            v_head_dim=m["v_head_dim"], moe_ffn_dim=1536, group_size=m["group_size"], seed=0,
+                            norm_mode=gmoe.SYNTH_NORM_RANDOM, bias_mode=gmoe.SYNTH_BIAS_NORMAL,
+                            scale_mode=gmoe.SYNTH_SCALES_FP16)
+    tmp_dir = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    fd, path = tempfile.mkstemp(prefix="glm_e2e_", suffix=".bin", dir=tmp_dir)
+    os.close(fd)
+    try:
+        t0 = time.perf_counter()
+        glm_model.write_synth_checkpoint(path, sp)
+        log(f"e2e CPU: wrote a {os.path.getsize(path) / 1e9:.1f} GB checkpoint in {time.perf_counter() - t0:.1f}s")
+        threads = omp_threads()
+        r = subprocess.run([sys.executable, "-c", E2E_CPU_SCRIPT, oracle.PATHS["reference"], path, str(context),
+                            str(context + tokens + 1), str(tokens), str(threads)], capture_output=True, text=True,
+                           timeout=900)
+        if r.returncode != 0:
+            raise SystemExit(f"glm.c's CPU forward failed: {r.stdout[-2000:]} {r.stderr[-2000:]}")
+        res = json.loads(r.stdout.strip().splitlines()[-1])
+        if res["rc"] != 0:
+            raise SystemExit("glm.c's CPU forward returned an error")
+    finally:
+        os.unlink(path)
+    ms = median(res["token_ms"])
+    return {"value": round(1e3 / ms, 4), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{tokens} decode tokens at position {context} of glm.c's CPU forward (infer.c built with its "
+                      f"Makefile flags, OpenMP threads bound to cores) on a synthetic checkpoint of the same shape; "
+                      f"median per-token time",
+            "ms_per_token": round(ms, 1), "token_ms": [round(v, 1) for v in res["token_ms"]]}
+
+
 def e2e_only(args, gmoe, np):
     """--e2e: the whole-model decode alone, on 46 freshly uploaded MoE layers."""
     shape = gmoe.GLM47_FLASH
@@ -496,6 +558,10 @@ def e2e_only(args, gmoe, np):
     log(f"generated and uploaded {N_MOE_LAYERS} layers in {time.perf_counter() - t0:.1f}s")
     res = e2e_decode(gmoe, np, ctx, context=args.context, new=args.new)
     ctx.close()
+    cpu = None
+    if args.e2e_cpu:
+        log(f"timing glm.c's CPU forward at position {args.context}")
+        cpu = e2e_cpu_baseline(gmoe, args.context)
     out = {
         "metric": "GLM-4.7-Flash-shaped model decode tokens/s (47 layers, Q8_0, whole forward on the GPU)",
         "value": res["decode_tokens_s"],
@@ -511,6 +577,7 @@ def e2e_only(args, gmoe, np):
         "data": "synthetic (seeded random-init Q8_0 weights, random prompt tokens)",
         "config": {"workload": res["workload"], "context": args.context, "new_tokens": args.new},
         **{k: v for k, v in res.items() if k not in ("workload", "decode_tokens_s", "decode_ms_per_token")},
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
 

@@ -257,3 +257,29 @@ int ref_decode(const char *path, const int *tokens, int n, int cache_cap, float 
     runtime_close(&rt);
     return rc;
 }
+
+/* CPU baseline timing of the whole forward (bench.py --e2e-cpu): glm.c's
+ * glm_cpu_forward_token (infer.c:1903) on the checkpoint at `path` for n_tokens tokens at
+ * positions pos, pos + 1, ... of a cache of cache_cap positions, each timed with glm.c's
+ * monotonic_ms (infer.c:1426-1430) into token_ms. The cache below pos holds runstate_build's
+ * zeros instead of a prompt's entries: the attention reads every position up to its own
+ * either way (infer.c:1029-1051), so the work per token is that of a pos-token context.
+ * n_threads > 0 sets the OpenMP team. A child process, as for ref_ckpt_layout. 0, or -1. */
+int ref_forward_timed(const char *path, int token, int pos, int cache_cap, int n_tokens, int n_threads,
+                      double *token_ms) {
+    if (!path || !token_ms || pos < 0 || n_tokens < 1 || pos + n_tokens > cache_cap) return -1;
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+    Runtime rt;
+    runtime_open(&rt, path);
+    RunState st;
+    runstate_build(&st, &rt, cache_cap);
+    int rc = 0;
+    for (int i = 0; i < n_tokens && !rc; i++) {
+        const double t0 = monotonic_ms();
+        rc = glm_cpu_forward_token(&rt, &st, token, pos + i, 0);
+        token_ms[i] = monotonic_ms() - t0;
+    }
+    runstate_free(&st);
+    runtime_close(&rt);
+    return rc;
+}
