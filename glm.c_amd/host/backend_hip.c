@@ -149,6 +149,8 @@ int glm_hip_prepare(const Runtime *rt, RunState *st) {
  * checkpoint's shape is one the model's kernels do not take or the GPU refuses it. */
 static int prepare_model(const Runtime *rt, const RunState *st) {
     const RuntimeConfig *c = &rt->cfg;
+    /* a Runtime that carries only MoE layers (the per-layer hook's callers) has no forward */
+    if (!rt->tok_q || !rt->out_q || !rt->output_norm || c->vocab_size <= 0) return -1;
     gmoe_model_config mc;
     memset(&mc, 0, sizeof(mc));
     mc.dim = c->dim;
