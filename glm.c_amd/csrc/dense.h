@@ -222,6 +222,7 @@ __global__ __launch_bounds__(DM_BLOCK) void k_embed_batch(const int8_t *__restri
 #define AT_ROPE_MAX 64
 #define AT_KS (AT_KV_MAX + AT_ROPE_MAX + 4)  // LDS row stride of a staged entry at the largest shape
 #define AT_MAX_PARTS 1024                   // most position ranges (partial results) per head
+#define AT_PREFILL_RANGES 8                 // position ranges per token of a batch
 #define AT_BLOCK 1024                       // threads of k_attn_chunk
 
 struct AttnArgs {
@@ -288,6 +289,18 @@ __global__ __launch_bounds__(DM_BLOCK) void k_attn_query(GemvArgs kb, AttnArgs a
         attn_prep_run(aa, blockIdx.y);
 }
 
+// Token t of a batch (grid z) at position pos + t: its queries, context and partial results
+// t token strides on (nblk ranges of partials per token).
+__device__ __attribute__((always_inline)) static void attn_token(AttnArgs &a, int t) {
+    if (t == 0) return;
+    a.pos += t;
+    a.q_abs += (size_t)t * a.H * a.kv;
+    a.q_pe += (size_t)t * a.H * a.rope;
+    a.ctx += (size_t)t * a.H * a.kv;
+    a.part_ctx += (size_t)t * a.nblk * a.H * a.kv;
+    a.part_ml += (size_t)t * a.nblk * a.H * 2;
+}
+
 // Position range blockIdx.x of nblk (an even split of 0 .. pos) for heads hg * blockIdx.y ..
 // (infer.c:1029-1051, split into ranges and merged by k_attn_merge). The heads' queries are
 // staged in LDS once, the range's cache entries AT_TILE at a time, each with one round of
@@ -295,16 +308,19 @@ __global__ __launch_bounds__(DM_BLOCK) void k_attn_query(GemvArgs kb, AttnArgs a
 // parts, times 1/sqrt(head_k). Per head the block keeps the range's running maximum and sum
 // of exponentials and the exponential-weighted sum of compressed entries, rescaled when the
 // maximum grows. The LDS holds one block per CU, so the block is 16 waves wide, and the
-// host sizes nblk so that a head group's ranges fill the CUs once.
+// host sizes nblk so that a head group's ranges fill the CUs once. A batch of tokens takes
+// grid z (attn_token), each token min(nblk, its positions) ranges.
 __global__ __launch_bounds__(AT_BLOCK) void k_attn_chunk(AttnArgs a) {
     __shared__ __align__(16) float ks[AT_TILE * AT_KS];
     __shared__ __align__(16) float qs[AT_HG * (AT_KV_MAX + AT_ROPE_MAX)];
     __shared__ float sc[AT_HG][AT_TILE];
     __shared__ float run_m[AT_HG], run_l[AT_HG], corr[AT_HG];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    attn_token(a, blockIdx.z);
     const int b = blockIdx.x, h0 = a.hg * blockIdx.y, nh = min(a.hg, a.H - h0);
-    const int P = a.pos + 1;
-    const int r0 = (int)((long long)b * P / a.nblk), r1 = (int)((long long)(b + 1) * P / a.nblk);
+    const int P = a.pos + 1, nb = min(a.nblk, P);
+    if (b >= nb) return;  // a prefill token with fewer positions than ranges
+    const int r0 = (int)((long long)b * P / nb), r1 = (int)((long long)(b + 1) * P / nb);
     const int kv = a.kv, rope = a.rope, KQ = kv + rope;
     const int qsd = (KQ + 3) & ~3;          // a row of either, rounded up to whole float4s
     const int ksd = ((KQ + 31) & ~31) + 4;  // entry row stride: 4 mod 32 keeps row-wise b128 reads apart
@@ -495,7 +511,8 @@ __global__ __launch_bounds__(DM_BLOCK) void k_attn_merge(AttnArgs a) {
     __shared__ float red[DM_BLOCK / 64];
     __shared__ float part[DM_BLOCK / 64][64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = blockIdx.x;
-    const int nc = a.nblk;  // the position ranges of k_attn_chunk
+    attn_token(a, blockIdx.z);
+    const int nc = min(a.nblk, a.pos + 1);  // the position ranges of k_attn_chunk
     float m = -INFINITY;
     for (int c = tid; c < nc; c += DM_BLOCK) m = fmaxf(m, a.part_ml[((size_t)c * a.H + h) * 2]);
     m = wave_max_dpp_f(m);

@@ -312,6 +312,17 @@ void launch_attn_cache(gmoe_model *m, AttnArgs aa, hipStream_t st) {
     hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64), dim3(DM_BLOCK), 0, st, aa);
 }
 
+// The attention over the cache for n tokens at positions aa.pos .. aa.pos + n - 1 (their
+// cache entries already written): one launch of ranges for the whole batch (grid z = token,
+// up to AT_PREFILL_RANGES ranges each, so that the tokens' blocks share the CUs), then one
+// merge.
+void launch_attn_cache_batch(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) {
+    const int groups = (aa.H + aa.hg - 1) / aa.hg;
+    aa.nblk = std::min(AT_PREFILL_RANGES, std::max(1, m->n_cu / groups));
+    hipLaunchKernelGGL(k_attn_chunk, dim3(aa.nblk, groups, (unsigned)n), dim3(AT_BLOCK), 0, st, aa);
+    hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64, (unsigned)n), dim3(DM_BLOCK), 0, st, aa);
+}
+
 int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
     const gmoe_model_config &c = m->c;
     const AttnDev &A = m->attn[l];
@@ -375,14 +386,7 @@ int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
     kb.x_rows = kv;
     kb.x_stride = hk;
     launch_query(kb, aa, st, n);  // every token's cache entry before any token's attention
-    for (int t = 0; t < n; t++) {
-        AttnArgs at = aa;
-        at.q_pe = m->q_pe + (size_t)t * H * rope;
-        at.q_abs = m->q_abs + (size_t)t * H * kv;
-        at.ctx = m->ctx + (size_t)t * H * kv;
-        at.pos = pos0 + t;
-        launch_attn_cache(m, at, st);
-    }
+    launch_attn_cache_batch(m, aa, n, st);
     GemvArgs vb = batched(gemv(A.v_b_q, A.v_b_s, m->ctx, nullptr, m->concat, H * vh, kv, gs), H * kv, H * vh);
     vb.x_rows = vh;
     vb.x_stride = kv;
@@ -428,11 +432,12 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
     const gmoe_model_config &c = m->c;
     const size_t L = (size_t)c.n_layers, A = (size_t)c.attn_layers, cap = (size_t)c.cache_cap;
     const size_t H = (size_t)c.n_heads, kv = (size_t)c.kv_lora_rank, rope = (size_t)c.rope_dim;
-    const size_t ranges = (size_t)attn_ranges(m->n_cu, 1, (int)cap);  // the most any launch uses
     m->attn.resize(A);
     m->moe_on.assign(L, 0);
     int rc = GMOE_OK;
     const size_t B = (size_t)(c.max_batch > 1 ? c.max_batch : 1);
+    // partial results: the most a token's launch uses, or AT_PREFILL_RANGES per token of a batch
+    const size_t ranges = std::max((size_t)attn_ranges(m->n_cu, 1, (int)cap), B * AT_PREFILL_RANGES);
     rc |= mdalloc(m, &m->x, B * c.dim);
     rc |= mdalloc(m, &m->tokens, B);
     rc |= mdalloc(m, &m->logits, (size_t)c.vocab_size);
