@@ -143,6 +143,7 @@ struct gmoe_ctx {
     int stack_grid = 0;          // co-resident blocks
     int decode_rows = 0;         // T=1 runs k_moe_decode (decode.h) rather than k_moe_stack
     int relay = 0;               // T=1 runs k_moe_relay (relay.h) rather than k_moe_stack
+    int coop = 0;                // the persistent kernels go out as cooperative launches (GMOE_COOPERATIVE=1)
     unsigned long long *sk_par_dev = nullptr;  // k_moe_relay: its workspace layers' parities (StackArgs::par_dev)
     int native = 0;              // GMOE_Q8_NATIVE: checkpoint layout, fp32 scales, native.h kernels
     uint8_t *sk_ws = nullptr;    // per-layer workspace, L regions of sk_ws_layer bytes
@@ -410,6 +411,12 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
                        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rl, relay_kernel(c->D, c->E), SK_BLOCK, 0) ==
                            hipSuccess &&
                        per_cu_rl >= want && rl_fits(c->stack_grid, c->D, c->F, c->E, c->K);
+            int coop_ok = 0;
+            const char *co_env = getenv("GMOE_COOPERATIVE");
+            // opt-in: a cooperative launch costs ~18 us per launch on MI355X (2 % of a 46-layer
+            // decode step, far more on one-layer launches)
+            c->coop = c->stack_ok && co_env && co_env[0] == '1' &&
+                      hipDeviceGetAttribute(&coop_ok, hipDeviceAttributeCooperativeLaunch, device) == hipSuccess && coop_ok;
         }
     }
     if (c->decode_rows) {
@@ -842,12 +849,28 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     hipLaunchKernelGGL(k_stack_reset, dim3(n + 1), dim3(SK_BLOCK), 0, st, sp.ctr, n_ctr, sp.error, a);
     ProfRecord *pr = space ? nullptr
                            : prof_begin(c, st, c->decode_rows ? GMOE_KERNEL_DECODE : c->relay ? GMOE_KERNEL_RELAY : GMOE_KERNEL_STACK);
-    if (c->decode_rows)
-        hipLaunchKernelGGL(k_moe_decode, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
-    else if (c->relay)
-        hipLaunchKernelGGL(relay_kernel(c->D, c->E), dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
-    else
-        hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+    {
+        const void *fn = c->decode_rows ? (const void *)k_moe_decode
+                         : c->relay     ? (const void *)relay_kernel(c->D, c->E)
+                                        : (const void *)k_moe_stack;
+        // Every block waits on others' results, so the grid must be resident at once: a
+        // cooperative launch has the runtime guarantee it (or refuse the launch), where an
+        // ordinary one relies on the GPU being otherwise idle and the bounded waits turn a
+        // grid that does not fit into a timeout error. Graph capture takes the ordinary form.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (c->coop) HIP_OK(hipStreamIsCapturing(st, &cap));
+        if (c->coop && cap == hipStreamCaptureStatusNone) {
+            void *args[] = {&a};
+            HIP_OK(hipLaunchCooperativeKernel(fn, dim3(c->stack_grid), dim3(SK_BLOCK), args, 0, st));
+        } else {
+            if (c->decode_rows)
+                hipLaunchKernelGGL(k_moe_decode, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+            else if (c->relay)
+                hipLaunchKernelGGL(relay_kernel(c->D, c->E), dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+            else
+                hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+        }
+    }
     prof_end(pr, st);
     HIP_OK(hipGetLastError());
     for (int l = first; l < first + n; l++) {
