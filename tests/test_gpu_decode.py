@@ -22,7 +22,7 @@ WIDE = gmoe.Shape(dim=512, moe_ffn_dim=256, n_routed_experts=128, n_experts_used
 WIDEST = gmoe.Shape(dim=256, moe_ffn_dim=256, n_routed_experts=256, n_experts_used=8)
 
 
-def run_case(shape, seed, T, norm_mode=gmoe.SYNTH_NORM_ONES, flags=0, layer=1):
+def run_case(shape, seed, T, norm_mode=gmoe.SYNTH_NORM_ONES, flags=0, layer=1, expect=None):
     print(f"[case] D={shape.D} F={shape.F} E={shape.E} K={shape.K} seed={seed} T={T} norm={norm_mode} flags={flags}",
           flush=True)
     L = gmoe.HostLayer(shape, seed=seed, layer=layer, norm_mode=norm_mode)
@@ -34,7 +34,9 @@ def run_case(shape, seed, T, norm_mode=gmoe.SYNTH_NORM_ONES, flags=0, layer=1):
         out = {}
         ran = launched(ctx, lambda: out.update(r=gmoe.forward_host(ctx, layer, x, flags=flags)))
         got, st = out["r"]
-        if T == 1:  # the persistent kernel the environment asks for
+        if expect is not None:  # the kernels the case must have run
+            assert expect <= ran, ran
+        elif T == 1:  # the persistent kernel the environment asks for
             assert_decode_kernel(ran, current_decode_kernel())
         stats = ctx.stats()
     finally:
@@ -72,6 +74,18 @@ def test_glm_shape_t1(dkernel):
 
 def test_glm_shape_batch8():
     check(*run_case(gmoe.GLM47_FLASH, seed=5, T=8, norm_mode=gmoe.SYNTH_NORM_RANDOM))
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_per_token_kernels_against_oracle(monkeypatch, T):
+    """The per-token kernels (the router, k_gate_up, k_down_combine) on their own: with the
+    persistent kernels off (GMOE_STACK_KERNEL=0) a T=1 call takes them, and with
+    GMOE_GROUPED_MIN_T above T so does a batch."""
+    monkeypatch.setenv("GMOE_STACK_KERNEL", "0")
+    monkeypatch.setenv("GMOE_GROUPED_MIN_T", "64")
+    want, got, st, stats = run_case(gmoe.GLM47_FLASH, seed=6, T=T, norm_mode=gmoe.SYNTH_NORM_RANDOM,
+                                    expect={"gate_up", "down"})
+    check(want, got, st, stats)
 
 
 @pytest.mark.parametrize("T,kind", [(1, "stack"), (1, "rows"), (1, "relay"), (8, "stack")])
