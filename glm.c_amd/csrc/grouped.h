@@ -203,15 +203,19 @@ __device__ __attribute__((always_inline)) static inline void gp_with_na(int na, 
     f(std::integral_constant<int, N>{});
 }
 
-// Chunk pipeline shared by the grouped GEMMs. A chunk's weights are requested into one of
-// two register sets and its activations into one of two shared-memory buffers while the
-// previous chunk is multiplied; the chunk loop is unrolled by two so that the register
-// sets alternate without copies. Barriers are plain s_barrier after an exact vmcnt wait:
+// Chunk pipeline of the grouped GEMMs. A chunk's weights are requested into one of the
+// register sets and its activations into one of the shared-memory buffers while earlier
+// chunks are multiplied: k_group_down keeps one chunk in flight (two sets, the loop
+// unrolled by two), k_group_gu two (three sets and buffers, unrolled by three; its
+// gate and up weights make it the larger stream: 162 -> 151 us at T=512, while a third set
+// in k_group_down, at 159 VGPRs and three blocks per CU, was slower), so that the register
+// sets rotate without copies. Barriers are plain s_barrier after an exact vmcnt wait:
 // __syncthreads() carries a release fence that waits for every outstanding load, the
 // prefetch included, which would serialise the pipeline.
 __device__ static inline void gp_barrier() { __builtin_amdgcn_s_barrier(); }
 
 typedef uint8_t gp_abuf_t[2][GP_TOK * 2 * GP_RB];
+typedef uint8_t gp_abuf3_t[3][GP_TOK * 2 * GP_RB];  // k_group_gu: two chunks in flight
 
 // k_group_gu: grid (F/64, max tiles). Wave w computes rows 64 p + 16 w .. +16 of F, gate
 // and up, for the tile's inputs, and from them h = silu(g) * u.
@@ -224,7 +228,7 @@ struct GuRegs {
 __host__ __device__ constexpr int gp_gu_loads(int na) { return 2 * (GP_NB / 2) + 2 + gp_stage_iters(na); }
 
 template <int NA>
-__device__ __attribute__((always_inline)) static inline void gp_gu_tile(const GroupArgs &a, const GpTile &tl, gp_abuf_t &abuf) {
+__device__ __attribute__((always_inline)) static inline void gp_gu_tile(const GroupArgs &a, const GpTile &tl, gp_abuf3_t &abuf) {
     const int p = blockIdx.x;
     const int D = a.D, F = a.F, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int nchunks = D >> 6, nblocks = D >> 5;
@@ -253,10 +257,10 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
         }
         r.s[0] = sg[kc];
         r.s[1] = su[kc];
-        gp_stage<NA>(stg, abuf[kc & 1], kc * GP_KC);
+        gp_stage<NA>(stg, abuf[kc % 3], kc * GP_KC);
     };
     auto compute = [&](const GuRegs &r, int kc) {
-        const uint8_t *buf = abuf[kc & 1];
+        const uint8_t *buf = abuf[kc % 3];
 #pragma unroll
         for (int b = 0; b < GP_NB; b++) {
 #pragma unroll
@@ -269,32 +273,29 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
             }
         }
     };
-    // one step: chunk kc's data is in (r, buffer kc&1); chunk kc+1's is requested into rn
-    // (every full step issues the same loads, so the compiler's own wait counts agree)
+    // one step: chunk kc's data is in (r, buffer kc % 3); chunk kc + 2's is requested into rn
+    // (into the registers and buffer chunk kc - 1 used), so that two chunks are in flight
+    // while one is multiplied; the wait leaves the later chunks' loads outstanding
     auto step = [&](GuRegs &r, GuRegs &rn, int kc) {
-        issue(rn, kc + 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gp_gu_loads(NA)) : "memory");
+        if (kc + 2 < nkc) {
+            issue(rn, kc + 2);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * gp_gu_loads(NA)) : "memory");
+        } else if (kc + 1 < nkc) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gp_gu_loads(NA)) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
         gp_barrier();  // every wave's part of chunk kc's activations is in shared memory
         compute(r, kc);
-        gp_barrier();  // every wave is done with buffer kc&1 before it is refilled
+        gp_barrier();  // every wave is done with buffer kc % 3 before it is refilled
     };
-    auto last = [&](GuRegs &r, int kc) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        gp_barrier();
-        compute(r, kc);
-    };
-    GuRegs r0, r1;
+    GuRegs r0, r1, r2;
     issue(r0, 0);
-    int kc = 0;
-    for (; kc + 2 < nkc; kc += 2) {
-        step(r0, r1, kc);
-        step(r1, r0, kc + 1);
-    }
-    if (nkc - kc == 2) {
-        step(r0, r1, kc);
-        last(r1, kc + 1);
-    } else {
-        last(r0, kc);
+    if (nkc > 1) issue(r1, 1);
+    for (int kc = 0; kc < nkc; kc += 3) {
+        step(r0, r2, kc);
+        if (kc + 1 < nkc) step(r1, r0, kc + 1);
+        if (kc + 2 < nkc) step(r2, r1, kc + 2);
     }
     // lane l holds inputs 16i + 4(l/16) + k, row l % 16 of the wave's panel
     const int f = 16 * P + (lane & 15);
@@ -312,7 +313,7 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
 }
 
 __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
-    __shared__ __align__(16) gp_abuf_t abuf;
+    __shared__ __align__(16) gp_abuf3_t abuf;
     if ((int)blockIdx.y >= *a.n_tiles) return;
     const GpTile tl = a.tiles[blockIdx.y];
     gp_with_na<GP_NA_MAX>(__builtin_amdgcn_readfirstlane((tl.count + 15) >> 4),
