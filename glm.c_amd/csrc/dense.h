@@ -301,19 +301,56 @@ __device__ __attribute__((always_inline)) static void attn_token(AttnArgs &a, in
     a.part_ml += (size_t)t * a.nblk * a.H * 2;
 }
 
+// Float DPP move within a row (bound_ctrl off: an inactive source lane gives 0).
+template <int CTRL>
+__device__ static inline float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Reduce-scatter over each 16-lane row: every lane holds v[0..7]; afterwards lanes s and
+// s ^ 1 of the row hold the row's sum of v[s >> 1]. Each step pairs a lane with one whose
+// index differs in the next bit down (across the row, then within each half, then within
+// quads), keeps the half of its values whose index has its own bit and adds the partner's
+// copy of that half; the last step adds the pair's two sums. 8 adds and DPP moves per lane
+// instead of 8 row sums of 4 steps each.
+__device__ static inline float row_reduce_scatter8(const float (&v)[8], int s) {
+    const bool b3 = (s & 8) != 0, b2 = (s & 4) != 0, b1 = (s & 2) != 0;
+    float u[4], x[2];
+#pragma unroll
+    for (int m = 0; m < 4; m++) u[m] = (b3 ? v[m + 4] : v[m]) + dpp_f<DPP_ROW_MIRROR>(b3 ? v[m] : v[m + 4]);
+#pragma unroll
+    for (int m = 0; m < 2; m++) x[m] = (b2 ? u[m + 2] : u[m]) + dpp_f<DPP_ROW_HALF_MIRROR>(b2 ? u[m] : u[m + 2]);
+    const float y = (b1 ? x[1] : x[0]) + dpp_f<DPP_QUAD_2301>(b1 ? x[0] : x[1]);
+    return y + dpp_f<DPP_QUAD_1032>(y);
+}
+
+// A block barrier after this wave's shared-memory accesses only: global loads still in
+// flight (the next tile's) are not waited for, as __syncthreads()'s release fence would.
+__device__ static inline void at_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+#define AT_HB 2  // heads per thread in k_attn_chunk's scores and weighted sum
+#define AT_TB 4  // cache positions per thread in its scores
+static_assert(AT_HB * AT_TB == 8, "row_reduce_scatter8 takes eight scores per lane");
+
 // Position range blockIdx.x of nblk (an even split of 0 .. pos) for heads hg * blockIdx.y ..
 // (infer.c:1029-1051, split into ranges and merged by k_attn_merge). The heads' queries are
-// staged in LDS once, the range's cache entries AT_TILE at a time, each with one round of
-// loads; each score is the absorbed query against the compressed entry plus the rotated
-// parts, times 1/sqrt(head_k). Per head the block keeps the range's running maximum and sum
-// of exponentials and the exponential-weighted sum of compressed entries, rescaled when the
-// maximum grows. The LDS holds one block per CU, so the block is 16 waves wide, and the
-// host sizes nblk so that a head group's ranges fill the CUs once. A batch of tokens takes
-// grid z (attn_token), each token min(nblk, its positions) ranges.
+// staged in LDS once and the range's cache entries AT_TILE at a time; the loads of the
+// first tile go out with the queries' and each later tile's while the one before it is
+// scored, so a range waits on memory once. Each score is the absorbed query against the
+// compressed entry plus the rotated parts, times 1/sqrt(head_k): a 16-lane row takes
+// AT_HB heads x AT_TB positions, each lane a sixteenth of the columns, so every value it
+// reads from LDS serves two or four products, and a reduce-scatter leaves one score per
+// lane pair. Pairs of heads spread the work over 10 of the 16 waves at 10 heads. Per
+// head the block keeps the range's running maximum and sum of exponentials and the
+// exponential-weighted sum of compressed entries, rescaled when the maximum grows; a
+// thread of that sum takes one float4 of the entry for AT_HB heads, four positions per
+// step. The LDS holds one block per CU, so the block is 16 waves wide, and the host sizes
+// nblk so that a head group's ranges fill the CUs once. A batch of tokens takes grid z
+// (attn_token), each token min(nblk, its positions) ranges.
 __global__ __launch_bounds__(AT_BLOCK) void k_attn_chunk(AttnArgs a) {
     __shared__ __align__(16) float ks[AT_TILE * AT_KS];
     __shared__ __align__(16) float qs[AT_HG * (AT_KV_MAX + AT_ROPE_MAX)];
-    __shared__ float sc[AT_HG][AT_TILE];
+    __shared__ __align__(16) float sc[AT_HG][AT_TILE];
     __shared__ float run_m[AT_HG], run_l[AT_HG], corr[AT_HG];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     attn_token(a, blockIdx.z);
@@ -324,10 +361,29 @@ __global__ __launch_bounds__(AT_BLOCK) void k_attn_chunk(AttnArgs a) {
     const int kv = a.kv, rope = a.rope, KQ = kv + rope;
     const int qsd = (KQ + 3) & ~3;          // a row of either, rounded up to whole float4s
     const int ksd = ((KQ + 31) & ~31) + 4;  // entry row stride: 4 mod 32 keeps row-wise b128 reads apart
-    const int kv4 = kv >> 2, r2 = rope >> 1;
+    const int kv4 = kv >> 2, r2 = rope >> 1, n4 = qsd >> 2;
+    constexpr int NQ = (AT_HG * AT_KV_MAX / 4 + AT_BLOCK - 1) / AT_BLOCK;      // float4s of absorbed queries
+    constexpr int NR = (AT_HG * AT_ROPE_MAX / 2 + AT_BLOCK - 1) / AT_BLOCK;    // float2s of rotated queries
+    constexpr int NC = (AT_TILE * AT_KV_MAX / 4 + AT_BLOCK - 1) / AT_BLOCK;    // float4s of a tile's entries
+    constexpr int NP = (AT_TILE * AT_ROPE_MAX / 2 + AT_BLOCK - 1) / AT_BLOCK;  // float2s of its rope parts
+    float4 vc[NC];
+    float2 vp[NP];
+    auto fetch = [&](int t0) {  // a tile's loads into vc, vp
+        const int nt = min(AT_TILE, r1 - t0);
+        const float4 *gc = reinterpret_cast<const float4 *>(a.comp + (size_t)t0 * kv);
+        const float2 *gp = reinterpret_cast<const float2 *>(a.pe + (size_t)t0 * rope);
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            const int i = tid + AT_BLOCK * k;
+            vc[k] = i < nt * kv4 ? gc[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            const int i = tid + AT_BLOCK * k;
+            vp[k] = i < nt * r2 ? gp[i] : make_float2(0.0f, 0.0f);
+        }
+    };
     {
-        constexpr int NQ = (AT_HG * AT_KV_MAX / 4 + AT_BLOCK - 1) / AT_BLOCK;    // float4s of absorbed queries
-        constexpr int NR = (AT_HG * AT_ROPE_MAX / 2 + AT_BLOCK - 1) / AT_BLOCK;  // float2s of rotated queries
         const float4 *gq = reinterpret_cast<const float4 *>(a.q_abs + (size_t)h0 * kv);
         const float2 *gr = reinterpret_cast<const float2 *>(a.q_pe + (size_t)h0 * rope);
         float4 vq[NQ];
@@ -342,6 +398,7 @@ __global__ __launch_bounds__(AT_BLOCK) void k_attn_chunk(AttnArgs a) {
             const int i = tid + AT_BLOCK * k;
             vr[k] = i < nh * r2 ? gr[i] : make_float2(0.0f, 0.0f);
         }
+        fetch(r0);
 #pragma unroll
         for (int k = 0; k < NQ; k++) {
             const int i = tid + AT_BLOCK * k;
@@ -361,91 +418,65 @@ __global__ __launch_bounds__(AT_BLOCK) void k_attn_chunk(AttnArgs a) {
             run_l[tid] = 0.0f;
         }
     }
-    // the weighted sum's threads: (entry quad q, heads hs + HS j), each staged entry read
-    // once per thread for all of its heads
-    const int nq = kv4, HS = AT_BLOCK / nq;  // nq <= 128: HS >= 8
-    constexpr int NH = (AT_HG + AT_BLOCK / (AT_KV_MAX / 4) - 1) / (AT_BLOCK / (AT_KV_MAX / 4));
-    const bool summer = tid < nq * HS;
-    const int q = tid % nq, hs = tid / nq;
-    float4 acc[NH];
+    const int ngh = (nh + AT_HB - 1) / AT_HB;  // head groups of AT_HB
+    const int sg = tid >> 4, sl = tid & 15;    // scores: the thread's 16-lane row and its lane in it
+    const int wq = tid % kv4, wh = tid / kv4;  // weighted sum: the entry's float4 and the head group
+    const bool summer = wh < ngh;
+    float4 acc[AT_HB];
 #pragma unroll
-    for (int j = 0; j < NH; j++) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int x = 0; x < AT_HB; x++) acc[x] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int t0 = r0; t0 < r1; t0 += AT_TILE) {
         const int nt = min(AT_TILE, r1 - t0);
-        {
-            // every load of the tile first (one round trip), then the LDS stores
-            constexpr int NC = (AT_TILE * AT_KV_MAX / 4 + AT_BLOCK - 1) / AT_BLOCK;    // float4s of entries
-            constexpr int NP = (AT_TILE * AT_ROPE_MAX / 2 + AT_BLOCK - 1) / AT_BLOCK;  // float2s of rope parts
-            const float4 *gc = reinterpret_cast<const float4 *>(a.comp + (size_t)t0 * kv);
-            const float2 *gp = reinterpret_cast<const float2 *>(a.pe + (size_t)t0 * rope);
-            float4 vc[NC];
-            float2 vp[NP];
 #pragma unroll
-            for (int k = 0; k < NC; k++) {
-                const int i = tid + AT_BLOCK * k;
-                vc[k] = i < nt * kv4 ? gc[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-#pragma unroll
-            for (int k = 0; k < NP; k++) {
-                const int i = tid + AT_BLOCK * k;
-                vp[k] = i < nt * r2 ? gp[i] : make_float2(0.0f, 0.0f);
-            }
-#pragma unroll
-            for (int k = 0; k < NC; k++) {
-                const int i = tid + AT_BLOCK * k;
-                if (i < nt * kv4) *reinterpret_cast<float4 *>(&ks[(i / kv4) * ksd + 4 * (i % kv4)]) = vc[k];
-            }
-#pragma unroll
-            for (int k = 0; k < NP; k++) {
-                const int i = tid + AT_BLOCK * k;
-                if (i < nt * r2) *reinterpret_cast<float2 *>(&ks[(i / r2) * ksd + kv + 2 * (i % r2)]) = vp[k];
-            }
-            if (qsd > KQ && tid < nt) {
-                ks[tid * ksd + KQ] = 0.0f;
-                ks[tid * ksd + KQ + 1] = 0.0f;
-            }
+        for (int k = 0; k < NC; k++) {
+            const int i = tid + AT_BLOCK * k;
+            if (i < nt * kv4) *reinterpret_cast<float4 *>(&ks[(i / kv4) * ksd + 4 * (i % kv4)]) = vc[k];
         }
-        __syncthreads();
-        // scores: lane pair (2p, 2p + 1) takes position p % AT_TILE of head p / AT_TILE, the
-        // two halves of the dot product, summed across the pair
 #pragma unroll
-        for (int k = 0; k < (AT_HG * AT_TILE + AT_BLOCK / 2 - 1) / (AT_BLOCK / 2); k++) {
-            const int p = (tid >> 1) + (AT_BLOCK / 2) * k, half = tid & 1, t = p % AT_TILE, h = p / AT_TILE;
-            const int n4 = qsd >> 2, n4a = (n4 + 1) >> 1;  // float4s of the dot, of its first half
-            const bool on = h < nh && t < nt;
-            float d0 = 0.0f, d1 = 0.0f;
-            if (on) {
-                const float4 *kr = reinterpret_cast<const float4 *>(ks + t * ksd);
-                const float4 *qr = reinterpret_cast<const float4 *>(qs + h * qsd);
-                const int j1 = half ? n4 : n4a;
-                int j = half ? n4a : 0;
-                for (; j + 1 < j1; j += 2) {
-                    const float4 k4 = kr[j], q4 = qr[j], k5 = kr[j + 1], q5 = qr[j + 1];
-                    d0 = fmaf(q4.x, k4.x, d0);
-                    d0 = fmaf(q4.y, k4.y, d0);
-                    d0 = fmaf(q4.z, k4.z, d0);
-                    d0 = fmaf(q4.w, k4.w, d0);
-                    d1 = fmaf(q5.x, k5.x, d1);
-                    d1 = fmaf(q5.y, k5.y, d1);
-                    d1 = fmaf(q5.z, k5.z, d1);
-                    d1 = fmaf(q5.w, k5.w, d1);
-                }
-                if (j < j1) {
-                    const float4 k4 = kr[j], q4 = qr[j];
-                    d0 = fmaf(q4.x, k4.x, d0);
-                    d0 = fmaf(q4.y, k4.y, d0);
-                    d0 = fmaf(q4.z, k4.z, d0);
-                    d0 = fmaf(q4.w, k4.w, d0);
+        for (int k = 0; k < NP; k++) {
+            const int i = tid + AT_BLOCK * k;
+            if (i < nt * r2) *reinterpret_cast<float2 *>(&ks[(i / r2) * ksd + kv + 2 * (i % r2)]) = vp[k];
+        }
+        if (qsd > KQ && tid < nt) {
+            ks[tid * ksd + KQ] = 0.0f;
+            ks[tid * ksd + KQ + 1] = 0.0f;
+        }
+        at_barrier();
+        if (t0 + AT_TILE < r1) fetch(t0 + AT_TILE);  // in flight while this tile is used
+        // scores: row sg takes heads AT_HB gh .. and positions AT_TB gt .. (rows past nh or nt
+        // read LDS rows inside the buffers and are not written)
+        const int ngt = (nt + AT_TB - 1) / AT_TB;
+        for (int g = sg; g < ngh * ngt; g += AT_BLOCK / 16) {
+            const int gh = g % ngh, gt = g / ngh;
+            const float *qr = qs + AT_HB * gh * qsd, *kr = ks + AT_TB * gt * ksd;
+            float d[AT_HB * AT_TB];
+#pragma unroll
+            for (int i = 0; i < AT_HB * AT_TB; i++) d[i] = 0.0f;
+            for (int j = sl; j < n4; j += 16) {
+                float4 q4[AT_HB];
+#pragma unroll
+                for (int x = 0; x < AT_HB; x++) q4[x] = *reinterpret_cast<const float4 *>(qr + x * qsd + 4 * j);
+#pragma unroll
+                for (int y = 0; y < AT_TB; y++) {  // one entry at a time: fewer live registers
+                    const float4 k4 = *reinterpret_cast<const float4 *>(kr + y * ksd + 4 * j);
+#pragma unroll
+                    for (int x = 0; x < AT_HB; x++) {
+                        float s = d[AT_TB * x + y];
+                        s = fmaf(q4[x].x, k4.x, s);
+                        s = fmaf(q4[x].y, k4.y, s);
+                        s = fmaf(q4[x].z, k4.z, s);
+                        d[AT_TB * x + y] = fmaf(q4[x].w, k4.w, s);
+                    }
                 }
             }
-            float v = __fadd_rn(d0, d1);
-            v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), DPP_QUAD_1032, 0xF, 0xF,
-                                                                        false)));  // + the pair's other half
-            if (half == 0 && on) sc[h][t] = __fmul_rn(v, a.kq_scale);
+            const float v = row_reduce_scatter8(d, sl);
+            const int h = AT_HB * gh + (sl >> 3), t = AT_TB * gt + ((sl >> 1) & 3);
+            if ((sl & 1) == 0 && h < nh && t < nt) sc[h][t] = __fmul_rn(v, a.kq_scale);
         }
-        __syncthreads();
+        at_barrier();
         // per head (a wave each): the tile's maximum, the running maximum and sum of
-        // exponentials, exp(score - running maximum) for the tile (lane = position)
+        // exponentials, exp(score - running maximum) for the tile (lane = position; zeros
+        // past nt, which the weighted sum reads in its last step)
         for (int h = w; h < nh; h += AT_BLOCK / 64) {
             const float v = lane < nt ? sc[h][lane] : -INFINITY;
             const float mo = run_m[h], mn = fmaxf(mo, wave_max_dpp_f(v));
@@ -459,41 +490,43 @@ __global__ __launch_bounds__(AT_BLOCK) void k_attn_chunk(AttnArgs a) {
                 corr[h] = cr;
             }
         }
-        __syncthreads();
+        at_barrier();
         if (summer) {
 #pragma unroll
-            for (int j = 0; j < NH; j++) {
-                const int h = hs + HS * j;
-                if (h < nh) {
-                    const float cr = corr[h];
-                    acc[j].x = __fmul_rn(acc[j].x, cr);
-                    acc[j].y = __fmul_rn(acc[j].y, cr);
-                    acc[j].z = __fmul_rn(acc[j].z, cr);
-                    acc[j].w = __fmul_rn(acc[j].w, cr);
-                }
+            for (int x = 0; x < AT_HB; x++) {  // head groups past nh rescale rows that are not stored
+                const float cr = corr[AT_HB * wh + x];
+                acc[x].x = __fmul_rn(acc[x].x, cr);
+                acc[x].y = __fmul_rn(acc[x].y, cr);
+                acc[x].z = __fmul_rn(acc[x].z, cr);
+                acc[x].w = __fmul_rn(acc[x].w, cr);
             }
-            for (int t = 0; t < nt; t++) {
-                const float4 k4 = *reinterpret_cast<const float4 *>(&ks[t * ksd + 4 * q]);
+            for (int t = 0; t < nt; t += 4) {
+                float4 k4[4];
 #pragma unroll
-                for (int j = 0; j < NH; j++) {
-                    const int h = hs + HS * j;
-                    if (h < nh) {
-                        const float p = sc[h][t];
-                        acc[j].x = fmaf(p, k4.x, acc[j].x);
-                        acc[j].y = fmaf(p, k4.y, acc[j].y);
-                        acc[j].z = fmaf(p, k4.z, acc[j].z);
-                        acc[j].w = fmaf(p, k4.w, acc[j].w);
+                for (int y = 0; y < 4; y++)
+                    k4[y] = t + y < nt ? *reinterpret_cast<const float4 *>(&ks[(t + y) * ksd + 4 * wq])
+                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                for (int x = 0; x < AT_HB; x++) {
+                    const float4 p = *reinterpret_cast<const float4 *>(&sc[AT_HB * wh + x][t]);
+                    const float pv[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+                    for (int y = 0; y < 4; y++) {
+                        acc[x].x = fmaf(pv[y], k4[y].x, acc[x].x);
+                        acc[x].y = fmaf(pv[y], k4[y].y, acc[x].y);
+                        acc[x].z = fmaf(pv[y], k4[y].z, acc[x].z);
+                        acc[x].w = fmaf(pv[y], k4[y].w, acc[x].w);
                     }
                 }
             }
         }
-        __syncthreads();  // the next tile overwrites ks and sc
+        at_barrier();  // the next tile overwrites ks and sc
     }
     if (summer) {
 #pragma unroll
-        for (int j = 0; j < NH; j++) {
-            const int h = hs + HS * j;
-            if (h < nh) *reinterpret_cast<float4 *>(&a.part_ctx[((size_t)b * a.H + h0 + h) * kv + 4 * q]) = acc[j];
+        for (int x = 0; x < AT_HB; x++) {
+            const int h = AT_HB * wh + x;
+            if (h < nh) *reinterpret_cast<float4 *>(&a.part_ctx[((size_t)b * a.H + h0 + h) * kv + 4 * wq]) = acc[x];
         }
     }
     if (tid < nh) {
