@@ -55,8 +55,15 @@ def glm_heads(seed=25):
     return sp
 
 
+def odd_heads(seed=26):
+    """Five heads, so that the attention's last pair of heads has one member."""
+    sp = small(32, gmoe.SYNTH_SCALES_FP16, n_layers=3, seed=seed)
+    sp.n_heads = sp.n_kv_heads = 5
+    return sp
+
+
 CASES = {"gs16_native": lambda: small(16, gmoe.SYNTH_SCALES_FP32), "gs32_tiled": lambda: small(32, gmoe.SYNTH_SCALES_FP16),
-         "glm_dims": glm_dims, "glm_heads": glm_heads}
+         "glm_dims": glm_dims, "glm_heads": glm_heads, "odd_heads": odd_heads}
 TOKENS = [1, 5, 17, 299, 42, 0, 17, 123, 7, 250]
 MODES = ["gpu", "host_attn"]
 
