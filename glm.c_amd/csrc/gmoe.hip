@@ -746,10 +746,16 @@ struct StackSpace {
     unsigned long long *par;  // k_moe_relay's parities (SK_MAX_LAYERS / 64 words)
 };
 
+// What launch_stack launches: the reset kernel and then the persistent kernel over
+// workspace layers 0..n-1 (SP_BOTH), the reset alone (SP_RESET), or k_moe_relay alone on
+// workspace layers ws_base.. that an earlier SP_RESET of at least ws_base + n layers
+// prepared (SP_KERNEL).
+enum StackPart { SP_BOTH, SP_RESET, SP_KERNEL };
+
 // T=1 through layers first..first+n-1 with the persistent kernel. With `space` the launch
 // uses that workspace and records neither trace nor profile (both may allocate).
 static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float *x_out, int flags, hipStream_t st,
-                        const StackSpace *space = nullptr) {
+                        const StackSpace *space = nullptr, StackPart part = SP_BOTH, int ws_base = 0) {
     const StackSpace own = {c->sk_ws, c->sk_ctr, c->sk_error, c->sk_par_dev};
     const StackSpace &sp = space ? *space : own;
     StackArgs a;
@@ -808,6 +814,14 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     }
     a.h_words = c->decode_rows ? (c->K + 1) * (c->F / 16) * DK_HREC / 8 : 0;
     a.par_dev = c->relay ? sp.par : nullptr;
+    a.par_base = 0;
+    if (part == SP_KERNEL) {
+        // workspace layer ws_base on: its region, its per-layer flags (k_moe_relay uses no
+        // launch-wide counter) and its parity bit
+        a.ws = sp.ws + (size_t)ws_base * c->sk_ws_layer;
+        a.ctr = sp.ctr + (size_t)SKF_PER_LAYER * SKC_PAD * ws_base;
+        a.par_base = ws_base;
+    }
     a.rl_cb0 = 0;
     a.rl_poll = 0;
     if (const char *pm = getenv("GMOE_RELAY_POLL")) a.rl_poll = atoi(pm);
@@ -820,7 +834,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
             if (v >= 0 && v + rr.nch <= rr.nri) a.rl_cb0 = v;
         }
     }
-    if (c->sk_trace_on && !space) {
+    if (c->sk_trace_on && !space && part == SP_BOTH) {
         // k_moe_stack: its work items; k_moe_decode: one item per (layer, block); k_moe_relay:
         // routed and shared items, combine chunks and finisher blocks
         const RlRoles rr = rl_roles(c->stack_grid, c->D, c->F, c->E, c->K);
@@ -846,7 +860,11 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         hipLaunchKernelGGL(k_relay_zero, dim3(1024), dim3(256), 0, st, (u32x4 *)sp.ws, n16);
         hipLaunchKernelGGL(k_relay_zero, dim3(1), dim3(256), 0, st, (u32x4 *)sp.par, (size_t)(SK_MAX_LAYERS / 64 * 8 / 16));
     }
-    hipLaunchKernelGGL(k_stack_reset, dim3(n + 1), dim3(SK_BLOCK), 0, st, sp.ctr, n_ctr, sp.error, a);
+    if (part != SP_KERNEL) hipLaunchKernelGGL(k_stack_reset, dim3(n + 1), dim3(SK_BLOCK), 0, st, sp.ctr, n_ctr, sp.error, a);
+    if (part == SP_RESET) {
+        HIP_OK(hipGetLastError());
+        return GMOE_OK;
+    }
     ProfRecord *pr = space ? nullptr
                            : prof_begin(c, st, c->decode_rows ? GMOE_KERNEL_DECODE : c->relay ? GMOE_KERNEL_RELAY : GMOE_KERNEL_STACK);
     {
@@ -917,6 +935,30 @@ static int take_launch_error(gmoe_ctx *c) {
 // take_launch_error for the library's other translation units (model.hip), called after
 // they have synchronised the stream of their launches.
 __attribute__((visibility("hidden"))) int gm_take_launch_error(gmoe_ctx *c) { return c ? take_launch_error(c) : GMOE_OK; }
+
+// One token's MoE layers through k_moe_relay, each in a launch of its own (model.hip puts
+// attention between them), with one reset kernel for all of them: the token's w-th MoE
+// layer runs on workspace layer w, so its launch needs no reset of its own.
+// gm_decode_begin resets n workspace layers and sets *on when the context decodes with
+// k_moe_relay (else the caller takes gmoe_forward per layer); gm_decode_layer then runs
+// `layer` (uploaded, 1 <= layer < L) on workspace layer w < n, as gmoe_forward(layer, T=1).
+__attribute__((visibility("hidden"))) int gm_decode_begin(gmoe_ctx *c, int n, hipStream_t st, int *on) {
+    *on = 0;
+    if (!c || !c->relay || !c->stack_ok || c->sk_trace_on || n < 1 || n >= c->L) return GMOE_OK;
+    HIP_OK(hipSetDevice(c->device));
+    if (int erc = take_launch_error(c)) return erc;
+    if (int rc = launch_stack(c, 1, n, nullptr, nullptr, 0, st, nullptr, SP_RESET)) return rc;
+    *on = 1;
+    return GMOE_OK;
+}
+__attribute__((visibility("hidden"))) int gm_decode_layer(gmoe_ctx *c, int layer, int w, const float *x_in, float *x_out,
+                                                          int flags, hipStream_t st) {
+    if (layer < 1 || layer >= c->L || !c->layers[layer].uploaded || w < 0 || w >= c->L) {
+        set_err("gmoe_model: MoE layer %d (workspace %d) cannot run", layer, w);
+        return GMOE_ERR_INVALID;
+    }
+    return launch_stack(c, layer, 1, x_in, x_out, flags, st, nullptr, SP_KERNEL, w);
+}
 
 // 0, or GMOE_ERR_HIP if the most recent persistent launch timed out (synchronises).
 static int check_stack_error(gmoe_ctx *c) {

@@ -35,6 +35,8 @@
 // gmoe.hip
 void gm_set_err(const char *fmt, ...);
 int gm_take_launch_error(gmoe_ctx *c);
+int gm_decode_begin(gmoe_ctx *c, int n, hipStream_t st, int *on);
+int gm_decode_layer(gmoe_ctx *c, int layer, int w, const float *x_in, float *x_out, int flags, hipStream_t st);
 
 #define MH_OK(expr)                                                                                  \
     do {                                                                                             \
@@ -599,11 +601,18 @@ extern "C" int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int f
     // the three model forms of infer.c:1817-1881
     const int n_run = c.attn_layers == c.n_layers ? c.n_layers : 1;
     int rc = GMOE_OK;
+    // the token's MoE layers on k_moe_relay share one reset launch (workspace layer w for
+    // the w-th of them); other decode kernels take gmoe_forward per layer
+    int n_moe = 0, relay = 0, w = 0;
+    for (int l = 1; l < n_run; l++) n_moe += m->moe_on[l] ? 1 : 0;
+    if (n_moe > 0) rc = gm_decode_begin(m->moe, n_moe, st, &relay);
     for (int l = 0; l < n_run && !rc; l++) {
         if (A > 0) rc = attention(m, l, pos, st);
         if (!rc && attn_ckpt) MH_OK(hipMemcpyAsync(attn_ckpt + l * D, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
         if (!rc && l == 0 && c.has_l0_ffn) rc = dense_ffn(m, st);
-        if (!rc && l > 0 && m->moe_on[l]) rc = gmoe_forward(m->moe, l, 1, m->x, m->x, m->moe_flags, st);
+        if (!rc && l > 0 && m->moe_on[l])
+            rc = relay ? gm_decode_layer(m->moe, l, w++, m->x, m->x, m->moe_flags, st)
+                       : gmoe_forward(m->moe, l, 1, m->x, m->x, m->moe_flags, st);
         if (!rc && layer_ckpt) MH_OK(hipMemcpyAsync(layer_ckpt + l * D, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
     }
     if (rc) return rc;

@@ -60,8 +60,8 @@
 // The launch's parities (StackArgs::par_dev, as k_stack_reset left them), read once per block.
 static __shared__ unsigned long long rl_par_sh[SK_MAX_LAYERS / 64];
 __device__ static inline unsigned rl_par(const StackArgs &a, int li) {
-    (void)a;
-    return (unsigned)(rl_par_sh[li >> 6] >> (li & 63)) & 1u;
+    const int q = a.par_base + li;
+    return (unsigned)(rl_par_sh[q >> 6] >> (q & 63)) & 1u;
 }
 __device__ static inline unsigned rl_tag(float v, unsigned p) { return (__float_as_uint(v) & ~1u) | p; }
 __device__ static inline float rl_untag(unsigned b) { return __uint_as_float(b & ~1u); }

@@ -138,6 +138,7 @@ struct StackArgs {
                                   // k_stack_reset flips the launch's layers before the kernel reads them
     int rl_cb0;                // relay.h: the routed block that runs combine chunk 0
     int rl_poll;               // relay.h: polling policy (rl_spin)
+    int par_base;              // relay.h: parity bit of the launch's first workspace layer (ws and ctr point at it)
 };
 
 template <typename T>
