@@ -76,7 +76,9 @@ int gmoe_model_upload_attn(gmoe_model *m, int layer, const gmoe_attn_weights *w)
 
 /* The MoE layers: layer l (1 <= l < n_layers) runs through `moe` (created for the same
  * dim and n_layers, its layer l uploaded) when layers[l] is nonzero. moe_flags as in
- * gmoe_forward. The context stays the caller's. */
+ * gmoe_forward. The context stays the caller's; the model's calls use its workspace (a
+ * token's MoE layers on k_moe_relay share one reset, each on a workspace layer of its
+ * own), so they must not overlap the caller's own calls on the context. */
 int gmoe_model_set_moe(gmoe_model *m, gmoe_ctx *moe, const uint8_t *layers, int moe_flags);
 
 /* One token at position pos (< cache_cap) through the model, on `stream`, then a
