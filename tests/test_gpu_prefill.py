@@ -10,7 +10,7 @@ at a time on the cache the prefill wrote, must match glm.c's logits at every lat
 position, which checks every cache entry the prefill wrote (every attention layer reads all
 of them). Batches of 1, 4 and the default 512 take the prompt whole, in ragged pieces
 and one token at a time; a 150-token prompt in 64-token batches crosses attention's
-32-position chunks inside a batch."""
+32-position chunks inside a batch, and a 400-token prompt gives ranges of several tiles."""
 import ctypes as C
 
 import numpy as np
@@ -77,6 +77,18 @@ def test_long_prompt_in_batches_across_attention_chunks(tmp_path, monkeypatch):
     rng = np.random.default_rng(24)
     tokens = [1] + [int(t) for t in rng.integers(3, sp.vocab_size, 153)]
     prefill_then_decode(tmp_path, sp, tokens, 150, "long prompt batch 64")
+
+
+def test_prefill_ranges_of_several_tiles(tmp_path, monkeypatch):
+    """A 400-token prompt in one batch: a token's attention splits its positions into 8
+    ranges, so past position 288 a range holds more than one 36-position tile and the
+    next tile's loads are in flight while the current one is scored."""
+    monkeypatch.setenv("GLM_HIP_PREFILL_BATCH", "512")
+    monkeypatch.delenv("GLM_HIP_HOST_ATTN", raising=False)
+    sp = small(32, gmoe.SYNTH_SCALES_FP16, n_layers=3, seed=27, seq_len=512)
+    rng = np.random.default_rng(27)
+    tokens = [1] + [int(t) for t in rng.integers(3, sp.vocab_size, 402)]
+    prefill_then_decode(tmp_path, sp, tokens, 400, "400-token prompt")
 
 
 def test_prefill_at_an_offset_and_past_the_cache(tmp_path, monkeypatch):
