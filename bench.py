@@ -87,6 +87,24 @@ def median(v):
     return v[len(v) // 2]
 
 
+def latency_stats(ms):
+    """Per-token latencies as glm.c's bench mode reports them (infer.c:1452-1462,
+    1564-1581): the mean, and p50 and p95 interpolated linearly between the sorted times
+    at rank q/100 * (n - 1)."""
+    v = sorted(ms)
+    n = len(v)
+
+    def pct(q):
+        r = q / 100.0 * (n - 1)
+        lo = int(r)
+        if lo + 1 >= n:
+            return v[-1]
+        return v[lo] * (1.0 - (r - lo)) + v[lo + 1] * (r - lo)
+
+    return {"tokens": n, "mean_ms": round(sum(v) / n, 4), "p50_ms": round(pct(50), 4), "p95_ms": round(pct(95), 4),
+            "min_ms": round(v[0], 4), "max_ms": round(v[-1], 4)}
+
+
 def cpu_baseline(shape, host_layers, x0, seconds):
     """glm.c's CPU MoE path (infer.c, OpenMP) on the same layers: decode tokens through the
     46-layer stack, every layer call timed with glm.c's monotonic clock (infer.c:1426-1430).
@@ -261,14 +279,18 @@ def e2e_decode(gmoe, np, ctx, context=4096, new=128, seed=0):
         for _ in range(2):  # warm-up steps that leave the cache as it was
             model.forward_token(tok, context, flags=1)
         t0 = time.perf_counter()
+        tok_ms = []
         for i in range(new):
+            t1 = time.perf_counter()
             tok = int(np.argmax(model.forward_token(tok, context + i)))
+            tok_ms.append((time.perf_counter() - t1) * 1e3)
         decode_s = time.perf_counter() - t0
     finally:
         model.close()
     return {"workload": f"GLM-4.7-Flash-shaped model (47 layers, vocab {cfg['vocab_size']}), {new} new tokens "
                         f"decoded greedily after a {context}-token prompt; random-init Q8_0 weights",
             "decode_tokens_s": round(new / decode_s, 2), "decode_ms_per_token": round(decode_s * 1e3 / new, 3),
+            "decode_per_token": latency_stats(tok_ms),
             "prefill_tokens_s": round(context / prefill_s, 1), "prefill_batch": B, "context": context, "new_tokens": new,
             "note": "wall clock around gmoe_model_forward_token (each a synchronised step with its logits copied "
                     "to the host) and gmoe_model_prefill; glm.c's CPU forward at the same position: "
@@ -374,6 +396,17 @@ def main():
     stack_gbs = bytes_per_token / (ms_per_step * 1e-3) / 1e9
     log(f"{tokens_per_s:.1f} tok/s, {layer_us:.2f} us/layer, {stack_gbs:.0f} GB/s on expert bytes")
 
+    # per-token latencies (glm.c's bench-mode p50/p95): each step of a separate pass of
+    # args.steps steps between HIP events on the stream, with no host synchronisation inside
+    ev = [gmoe.Event() for _ in range(args.steps + 1)]
+    ev[0].record(stream)
+    for i in range(args.steps):
+        step()
+        ev[i + 1].record(stream)
+    stream.sync()
+    per_token = latency_stats([ev[i].elapsed_ms(ev[i + 1]) for i in range(args.steps)])
+    per_token["note"] = "HIP events between consecutive steps of a second pass of the same steps"
+
     # per-kernel HIP-event timing over a separate pass of the same steps
     ctx.profile(True)
     for _ in range(args.profile_steps):
@@ -386,7 +419,7 @@ def main():
     K1 = shape.K + 1
     mat = shape.F * shape.D * 34 // 32
     kernel_bytes = {"gate_up": K1 * 2 * mat, "down": K1 * mat, "k_moe_stack": bytes_per_token,
-                    "k_moe_decode": bytes_per_token, "k_moe_relay": bytes_per_token}
+                    "k_moe_relay": bytes_per_token}
     dom = max(prof, key=lambda k: prof[k][1])
     kernels = {k: {"launches": n, "avg_us": ms * 1e3 / n} for k, (n, ms) in prof.items()}
     for k in kernels:
@@ -454,6 +487,9 @@ def main():
             extra["e2e_decode"] = e2e_decode(gmoe, np, ctx)
             log(f"e2e: {extra['e2e_decode']['decode_tokens_s']} tok/s decode, "
                 f"{extra['e2e_decode']['prefill_tokens_s']} tok/s prefill")
+            if not args.no_cpu:
+                log("e2e: timing glm.c's CPU forward at position 4096")
+                extra["e2e_decode"]["cpu_baseline"] = e2e_cpu_baseline(gmoe, 4096)
 
     cpu = None
     if not args.no_cpu:
@@ -477,6 +513,7 @@ def main():
                    "dim": shape.D, "moe_ffn_dim": shape.F, "experts": shape.E, "top_k": shape.K, "shared_experts": 1,
                    "quant": "Q8_0 (32 x int8 + fp16 scale)", "seed": 0},
         "layer_us": round(layer_us, 3),
+        "per_token": per_token,
         "expert_bytes_per_token": bytes_per_token,
         "hbm_gbps_expert_bytes": round(stack_gbs, 1),
         "hbm_frac_expert_bytes": round(stack_gbs / HBM_PEAK_GBS, 4),

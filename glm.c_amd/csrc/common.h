@@ -80,19 +80,6 @@ __host__ __device__ static inline size_t gm_ds_offset(int r, int b, int rows) {
     return (size_t)b * (size_t)rows + (size_t)r;
 }
 
-// The row-owner decode kernel (decode.h) reads down matrices in the row-group layout, kept
-// beside the column-slice copy when that kernel is chosen: rows in groups of 4, and for each
-// group its 16-column slices in order, 4 rows x 16 bytes each; scales [D/4][F/32][4]. The
-// owner of rows 4g..4g+3 then reads its share of a matrix as one run of 4 F bytes (and 8 F/32
-// bytes of scales), where the slice layout scatters it in 64-byte pieces 16 D bytes apart.
-#define GM_LAYOUT_ROWGROUPS 2
-__host__ __device__ static inline size_t gm_drq_offset(int r, int c, int cols) {
-    return ((size_t)(r >> 2) * (size_t)(cols >> 4) + (size_t)(c >> 4)) * 64 + (size_t)(r & 3) * 16 + (size_t)(c & 15);
-}
-__host__ __device__ static inline size_t gm_drs_offset(int r, int b, int cols) {
-    return ((size_t)(r >> 2) * (size_t)(cols >> 5) + (size_t)b) * 4 + (size_t)(r & 3);
-}
-
 // Correctly rounded fp32 square root. The fp32 intrinsic lowers to v_sqrt_f32, which is
 // not always correctly rounded; the fp64 lowering is (Newton-refined), and rounding a
 // correctly rounded fp64 root to fp32 is exact-rounding since 53 >= 2*24 + 2.

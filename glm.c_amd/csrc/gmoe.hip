@@ -26,7 +26,6 @@
 #include <string.h>
 
 #include "common.h"
-#include "decode.h"
 #include "dispatch.h"
 #include "experts.h"
 #include "grouped.h"
@@ -115,7 +114,6 @@ struct gmoe_ctx {
     gmoe_config cfg{};
     int D = 0, F = 0, E = 0, K = 0, S = 0, L = 0, Tmax = 0;
     size_t stride = 0, off_gq = 0, off_uq = 0, off_dq = 0, off_gs = 0, off_us = 0, off_ds = 0;
-    size_t off_rq = 0, off_rs = 0;  // down in the row-group layout (decode_rows only)
     LayerDev *layers = nullptr;
 
     float *xn = nullptr, *router_prob = nullptr, *topk_w = nullptr, *topk_ws = nullptr;
@@ -141,7 +139,6 @@ struct gmoe_ctx {
     int grouped_min_t = 2;       // T from which batches take the grouped GEMMs (GMOE_GROUPED_MIN_T)
     int stack_ok = 0;            // shape fits k_moe_stack
     int stack_grid = 0;          // co-resident blocks
-    int decode_rows = 0;         // T=1 runs k_moe_decode (decode.h) rather than k_moe_stack
     int relay = 0;               // T=1 runs k_moe_relay (relay.h) rather than k_moe_stack
     int coop = 0;                // the persistent kernels go out as cooperative launches (GMOE_COOPERATIVE=1)
     unsigned long long *sk_par_dev = nullptr;  // k_moe_relay: its workspace layers' parities (StackArgs::par_dev)
@@ -381,15 +378,14 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     rc |= dev_alloc(&c->stats_dev, GM_STAT_COUNT);
     // The persistent decode kernels hold one panel's chunks per wave in registers and xn in
     // shared memory: D, F <= 2048, D a multiple of 256, at most 8 routed slots. k_moe_stack
-    // stages a combine chunk's partials, F/16 x (K+1) x 8 floats, in the slice buffer;
-    // k_moe_decode (decode.h) runs shapes whose expert items and router finishers fit its grid.
+    // stages a combine chunk's partials, F/16 x (K+1) x 8 floats, in the slice buffer.
     c->stack_ok = !c->native && c->L <= SK_MAX_LAYERS &&
                   (size_t)(F / 16) * (K + 1) * SK_CROWS * sizeof(float) <= sizeof(SkShared::dslice);
     if (const char *g_env = getenv("GMOE_GROUPED_MIN_T")) c->grouped_min_t = atoi(g_env) > 1 ? atoi(g_env) : 2;
     const char *env = getenv("GMOE_STACK_KERNEL");
     if (env && env[0] == '0') c->stack_ok = 0;
     if (c->stack_ok) {
-        int per_cu = 0, per_cu_dk = 0, cus = 0;
+        int per_cu = 0, cus = 0;
         hipDeviceProp_t prop;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_stack, SK_BLOCK, 0) != hipSuccess ||
             hipGetDeviceProperties(&prop, device) != hipSuccess || per_cu < 1) {
@@ -402,12 +398,9 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
             if (c->stack_grid < stack_routers(c->E) + 2) c->stack_ok = 0;
             const char *dk_env = getenv("GMOE_DECODE_KERNEL");
             // k_moe_relay is the default where the shape fits it; GMOE_DECODE_KERNEL=0 asks for
-            // k_moe_stack, 1 for the row-owner k_moe_decode
-            c->decode_rows = c->stack_ok && dk_env && dk_env[0] == '1' &&
-                             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_dk, k_moe_decode, SK_BLOCK, 0) == hipSuccess &&
-                             per_cu_dk >= want && dk_fits(c->stack_grid, c->D, c->F, c->E, c->K);
+            // k_moe_stack
             int per_cu_rl = 0;
-            c->relay = c->stack_ok && !c->decode_rows && !(dk_env && dk_env[0] == '0') &&
+            c->relay = c->stack_ok && !(dk_env && dk_env[0] == '0') &&
                        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rl, relay_kernel(c->D, c->E), SK_BLOCK, 0) ==
                            hipSuccess &&
                        per_cu_rl >= want && rl_fits(c->stack_grid, c->D, c->F, c->E, c->K);
@@ -418,12 +411,6 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
             c->coop = c->stack_ok && co_env && co_env[0] == '1' &&
                       hipDeviceGetAttribute(&coop_ok, hipDeviceAttributeCooperativeLaunch, device) == hipSuccess && coop_ok;
         }
-    }
-    if (c->decode_rows) {
-        // each expert also holds its down matrix in the row-group layout, after the rest
-        c->off_rq = c->stride;
-        c->off_rs = c->off_rq + qb;
-        c->stride = (c->off_rs + sb + 255) & ~(size_t)255;
     }
     {
         // per-layer regions of the persistent kernel, each buffer on its own 256-byte lines
@@ -439,12 +426,11 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         c->sk_o.dexp = take(D / 32 * sizeof(int));
         c->sk_o.stage = take(SK_STAGE_COPIES * SK_STAGE_COPY_WORDS * sizeof(unsigned long long));
         c->sk_o.ex_w = take(K * sizeof(float));
-        // k_moe_stack's partial sums, or k_moe_decode's h records and router records
-        c->sk_o.ypart = take(c->decode_rows ? 0 : NS * (F / 16) * D * sizeof(float));
-        c->sk_o.h = take(c->decode_rows ? NS * (F / 16) * DK_HREC : 0);
-        // router records: k_moe_decode's per owner of DK_ROWS rows, k_moe_relay's per chunk of RL_ROWS
-        const size_t rec_pieces = c->decode_rows ? D / DK_ROWS : c->relay ? D / RL_ROWS : 0;
-        c->sk_o.rec = take(rec_pieces * E * sizeof(DkRec));
+        // the expert items' partial sums
+        c->sk_o.ypart = take(NS * (F / 16) * D * sizeof(float));
+        // k_moe_relay's router records, one per chunk of RL_ROWS rows and expert
+        const size_t rec_pieces = c->relay ? D / RL_ROWS : 0;
+        c->sk_o.rec = take(rec_pieces * E * sizeof(RlRec));
         c->sk_o.xsq = take(rec_pieces * sizeof(double));
         c->sk_ws_layer = off;
         rc |= dev_alloc(&c->sk_ws, (size_t)c->L * off);
@@ -512,8 +498,7 @@ static void repack_staged(gmoe_ctx *c, int n_mat, int rows, int cols, uint8_t *d
 // Copies n_mat matrices to the staging buffer and repacks them into `layout`; with
 // layout2 >= 0 also into layout2 at off_q2 / off_s2 (scales counted once).
 static int upload_matrices(gmoe_ctx *c, const int8_t *q, const float *s, int n_mat, int rows, int cols, uint8_t *dst,
-                           size_t dst_stride, size_t off_q, size_t off_s, int layout, unsigned long long *inexact_dev,
-                           int layout2 = -1, size_t off_q2 = 0, size_t off_s2 = 0) {
+                           size_t dst_stride, size_t off_q, size_t off_s, int layout, unsigned long long *inexact_dev) {
     const size_t qbytes = (size_t)n_mat * rows * cols;
     const size_t sbytes = (size_t)n_mat * rows * (cols / GM_QBLOCK) * sizeof(float);
     if (qbytes + sbytes > c->staging_bytes) {
@@ -528,7 +513,6 @@ static int upload_matrices(gmoe_ctx *c, const int8_t *q, const float *s, int n_m
     rc = copy_in(c->staging + qbytes, s, sbytes);
     if (rc) return rc;
     repack_staged(c, n_mat, rows, cols, dst, dst_stride, off_q, off_s, layout, inexact_dev);
-    if (layout2 >= 0) repack_staged(c, n_mat, rows, cols, dst, dst_stride, off_q2, off_s2, layout2, nullptr);
     HIP_OK(hipGetLastError());
     HIP_OK(hipDeviceSynchronize());
     return GMOE_OK;
@@ -564,7 +548,7 @@ extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weight
     if ((rc = copy_in(L.bias, w->exp_probs_b, (size_t)E * sizeof(float)))) return rc;
     {
         // nu_e = sum_i |gate_inp[e][i]| (|ffn_norm[i]| + 1), rounded up: bounds what underflow in
-        // xn's two fp32 roundings can add to expert e's router logit (decode.h)
+        // xn's two fp32 roundings can add to expert e's router logit (relay.h)
         std::vector<double> nu((size_t)E);
         for (int e = 0; e < E; e++) {
             double s = 0.0;
@@ -609,15 +593,12 @@ extern "C" int gmoe_upload_layer(gmoe_ctx *c, int layer, const gmoe_layer_weight
     const int P = GM_LAYOUT_PANELS, S = GM_LAYOUT_SLICES;  // gate/up in row panels, down in column slices
     rc = upload_matrices(c, w->gate_sh_q, w->gate_sh_s, 1, F, D, sh, c->stride, c->off_gq, c->off_gs, P, inexact);
     if (!rc) rc = upload_matrices(c, w->up_sh_q, w->up_sh_s, 1, F, D, sh, c->stride, c->off_uq, c->off_us, P, inexact);
-    const int R = c->decode_rows ? GM_LAYOUT_ROWGROUPS : -1;
-    if (!rc) rc = upload_matrices(c, w->down_sh_q, w->down_sh_s, 1, D, F, sh, c->stride, c->off_dq, c->off_ds, S, inexact,
-                                  R, c->off_rq, c->off_rs);
+    if (!rc) rc = upload_matrices(c, w->down_sh_q, w->down_sh_s, 1, D, F, sh, c->stride, c->off_dq, c->off_ds, S, inexact);
     if (has_routed) {
         uint8_t *ex = L.experts;
         if (!rc) rc = upload_matrices(c, w->gate_q, w->gate_s, E, F, D, ex, c->stride, c->off_gq, c->off_gs, P, inexact);
         if (!rc) rc = upload_matrices(c, w->up_q, w->up_s, E, F, D, ex, c->stride, c->off_uq, c->off_us, P, inexact);
-        if (!rc) rc = upload_matrices(c, w->down_q, w->down_s, E, D, F, ex, c->stride, c->off_dq, c->off_ds, S, inexact,
-                                      R, c->off_rq, c->off_rs);
+        if (!rc) rc = upload_matrices(c, w->down_q, w->down_s, E, D, F, ex, c->stride, c->off_dq, c->off_ds, S, inexact);
     }
     unsigned long long n_inexact = 0;
     if (!rc && hipMemcpy(&n_inexact, inexact, sizeof(n_inexact), hipMemcpyDeviceToHost) != hipSuccess) {
@@ -778,8 +759,6 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     a.off_gs = c->off_gs;
     a.off_us = c->off_us;
     a.off_ds = c->off_ds;
-    a.off_rq = c->off_rq;
-    a.off_rs = c->off_rs;
     a.ws = sp.ws;
     a.ws_layer_bytes = c->sk_ws_layer;
     a.o = c->sk_o;
@@ -809,10 +788,9 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
             nwb = avail - nsb;
         }
         if (nsb > npf) nsb = npf;
-        a.n_router = c->decode_rows ? dk_finishers(c->stack_grid, c->E, c->K, c->F) : nr;
+        a.n_router = nr;
         a.shared_blocks = nsb;
     }
-    a.h_words = c->decode_rows ? (c->K + 1) * (c->F / 16) * DK_HREC / 8 : 0;
     a.par_dev = c->relay ? sp.par : nullptr;
     a.par_base = 0;
     if (part == SP_KERNEL) {
@@ -835,12 +813,11 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         }
     }
     if (c->sk_trace_on && !space && part == SP_BOTH) {
-        // k_moe_stack: its work items; k_moe_decode: one item per (layer, block); k_moe_relay:
-        // routed and shared items, combine chunks and finisher blocks
+        // k_moe_stack: its work items; k_moe_relay: routed and shared items, combine chunks
+        // and finisher blocks
         const RlRoles rr = rl_roles(c->stack_grid, c->D, c->F, c->E, c->K);
-        const size_t items = c->decode_rows ? (size_t)c->stack_grid * n
-                             : c->relay    ? (size_t)(rr.nri + rr.nsi + rr.nch + rr.nfb) * n
-                                           : (size_t)(stack_routers(c->E) + c->D / SK_CROWS + (c->K + 1) * (c->F / 16)) * n;
+        const size_t items = c->relay ? (size_t)(rr.nri + rr.nsi + rr.nch + rr.nfb) * n
+                                      : (size_t)(stack_routers(c->E) + c->D / SK_CROWS + (c->K + 1) * (c->F / 16)) * n;
         if (items > c->sk_trace_items) {
             dev_free(c->sk_trace);
             c->sk_trace = nullptr;
@@ -866,11 +843,9 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
         return GMOE_OK;
     }
     ProfRecord *pr = space ? nullptr
-                           : prof_begin(c, st, c->decode_rows ? GMOE_KERNEL_DECODE : c->relay ? GMOE_KERNEL_RELAY : GMOE_KERNEL_STACK);
+                           : prof_begin(c, st, c->relay ? GMOE_KERNEL_RELAY : GMOE_KERNEL_STACK);
     {
-        const void *fn = c->decode_rows ? (const void *)k_moe_decode
-                         : c->relay     ? (const void *)relay_kernel(c->D, c->E)
-                                        : (const void *)k_moe_stack;
+        const void *fn = c->relay ? (const void *)relay_kernel(c->D, c->E) : (const void *)k_moe_stack;
         // Every block waits on others' results, so the grid must be resident at once: a
         // cooperative launch has the runtime guarantee it (or refuse the launch), where an
         // ordinary one relies on the GPU being otherwise idle and the bounded waits turn a
@@ -881,9 +856,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
             void *args[] = {&a};
             HIP_OK(hipLaunchCooperativeKernel(fn, dim3(c->stack_grid), dim3(SK_BLOCK), args, 0, st));
         } else {
-            if (c->decode_rows)
-                hipLaunchKernelGGL(k_moe_decode, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
-            else if (c->relay)
+            if (c->relay)
                 hipLaunchKernelGGL(relay_kernel(c->D, c->E), dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
             else
                 hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
@@ -950,6 +923,22 @@ __attribute__((visibility("hidden"))) int gm_decode_begin(gmoe_ctx *c, int n, hi
     if (int rc = launch_stack(c, 1, n, nullptr, nullptr, 0, st, nullptr, SP_RESET)) return rc;
     *on = 1;
     return GMOE_OK;
+}
+// The device rows of the last T=1 call's shared-expert output and routed combine
+// (infer.c:1206, 1192), which each launch's last layer writes.
+__attribute__((visibility("hidden"))) void gm_layer_outputs(const gmoe_ctx *c, const float **shared, const float **routed) {
+    *shared = c ? c->shared_out : nullptr;
+    *routed = c ? c->routed_out : nullptr;
+}
+// Whether `layer` is an uploaded MoE layer of c (what gmoe_forward accepts).
+__attribute__((visibility("hidden"))) int gm_layer_ready(const gmoe_ctx *c, int layer) {
+    return c && layer >= 1 && layer < c->L && c->layers[layer].uploaded;
+}
+// After gm_decode_begin, a token that fails before all n of its layers ran leaves some
+// workspace layers with the reset's flipped parity but none of this token's data: the next
+// token's flip would make their older words look current. Back to zeros, parities included.
+__attribute__((visibility("hidden"))) void gm_decode_abort(gmoe_ctx *c) {
+    if (c) relay_reset(c);
 }
 __attribute__((visibility("hidden"))) int gm_decode_layer(gmoe_ctx *c, int layer, int w, const float *x_in, float *x_out,
                                                           int flags, hipStream_t st) {

@@ -37,6 +37,9 @@ void gm_set_err(const char *fmt, ...);
 int gm_take_launch_error(gmoe_ctx *c);
 int gm_decode_begin(gmoe_ctx *c, int n, hipStream_t st, int *on);
 int gm_decode_layer(gmoe_ctx *c, int layer, int w, const float *x_in, float *x_out, int flags, hipStream_t st);
+int gm_layer_ready(const gmoe_ctx *c, int layer);
+void gm_layer_outputs(const gmoe_ctx *c, const float **shared, const float **routed);
+void gm_decode_abort(gmoe_ctx *c);
 
 #define MH_OK(expr)                                                                                  \
     do {                                                                                             \
@@ -44,6 +47,16 @@ int gm_decode_layer(gmoe_ctx *c, int layer, int w, const float *x_in, float *x_o
         if (e_ != hipSuccess) {                                                                      \
             gm_set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
             return GMOE_ERR_HIP;                                                                     \
+        }                                                                                            \
+    } while (0)
+
+// MH_OK's check without the return: the error into rc (for loops that must clean up)
+#define MH_RC(rc, expr)                                                                              \
+    do {                                                                                             \
+        hipError_t e_ = (expr);                                                                      \
+        if (e_ != hipSuccess) {                                                                      \
+            gm_set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+            rc = GMOE_ERR_HIP;                                                                       \
         }                                                                                            \
     } while (0)
 
@@ -563,8 +576,35 @@ extern "C" int gmoe_model_set_moe(gmoe_model *m, gmoe_ctx *moe, const uint8_t *l
     return GMOE_OK;
 }
 
+namespace {
+// Host buffers of the debug form ([n_layers][..] each; any may be null).
+struct DebugOut {
+    float *kv = nullptr, *concat = nullptr, *shexp = nullptr, *moe = nullptr;
+};
+
+int forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, float *x_out, float *attn_ckpt,
+                  float *layer_ckpt, const DebugOut *dbg, void *stream);
+}  // namespace
+
 extern "C" int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, float *x_out,
                                         float *attn_ckpt, float *layer_ckpt, void *stream) {
+    return forward_token(m, token, pos, flags, logits, x_out, attn_ckpt, layer_ckpt, nullptr, stream);
+}
+
+extern "C" int gmoe_model_forward_token_debug(gmoe_model *m, int token, int pos, int flags, float *logits,
+                                              float *x_out, float *attn_ckpt, float *layer_ckpt, float *kv_out,
+                                              float *concat_out, float *shexp_out, float *moe_out, void *stream) {
+    DebugOut d;
+    d.kv = kv_out;
+    d.concat = concat_out;
+    d.shexp = shexp_out;
+    d.moe = moe_out;
+    return forward_token(m, token, pos, flags, logits, x_out, attn_ckpt, layer_ckpt, &d, stream);
+}
+
+namespace {
+int forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, float *x_out, float *attn_ckpt,
+                  float *layer_ckpt, const DebugOut *dbg, void *stream) {
     if (!m || !logits) {
         gm_set_err("gmoe_model_forward_token: null argument");
         return GMOE_ERR_INVALID;
@@ -604,18 +644,48 @@ extern "C" int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int f
     // the token's MoE layers on k_moe_relay share one reset launch (workspace layer w for
     // the w-th of them); other decode kernels take gmoe_forward per layer
     int n_moe = 0, relay = 0, w = 0;
-    for (int l = 1; l < n_run; l++) n_moe += m->moe_on[l] ? 1 : 0;
+    for (int l = 1; l < n_run; l++) {
+        if (!m->moe_on[l]) continue;
+        // every MoE layer must be able to run before the reset below: a token that stops
+        // after it would leave workspace layers flipped but unwritten
+        if (!gm_layer_ready(m->moe, l)) {
+            gm_set_err("gmoe_model_forward_token: MoE layer %d is not uploaded to the model's context", l);
+            return GMOE_ERR_INVALID;
+        }
+        n_moe++;
+    }
     if (n_moe > 0) rc = gm_decode_begin(m->moe, n_moe, st, &relay);
+    const size_t HV = (size_t)c.n_heads * c.v_head_dim;
     for (int l = 0; l < n_run && !rc; l++) {
         if (A > 0) rc = attention(m, l, pos, st);
-        if (!rc && attn_ckpt) MH_OK(hipMemcpyAsync(attn_ckpt + l * D, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
+        if (!rc && attn_ckpt) MH_RC(rc, hipMemcpyAsync(attn_ckpt + l * D, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
+        if (!rc && dbg && A > 0) {
+            // the position's normalised kv entry (glm.c's kv_a, infer.c:1001-1003) and the heads' concat
+            if (dbg->kv)
+                MH_RC(rc, hipMemcpyAsync(dbg->kv + l * kv, m->comp + ((size_t)l * cap + pos) * kv, kv * sizeof(float),
+                                         hipMemcpyDeviceToHost, st));
+            if (!rc && dbg->concat)
+                MH_RC(rc, hipMemcpyAsync(dbg->concat + l * HV, m->concat, HV * sizeof(float), hipMemcpyDeviceToHost, st));
+        }
         if (!rc && l == 0 && c.has_l0_ffn) rc = dense_ffn(m, st);
-        if (!rc && l > 0 && m->moe_on[l])
+        if (!rc && l > 0 && m->moe_on[l]) {
             rc = relay ? gm_decode_layer(m->moe, l, w++, m->x, m->x, m->moe_flags, st)
                        : gmoe_forward(m->moe, l, 1, m->x, m->x, m->moe_flags, st);
-        if (!rc && layer_ckpt) MH_OK(hipMemcpyAsync(layer_ckpt + l * D, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
+            if (!rc && dbg && (dbg->shexp || dbg->moe)) {
+                const float *sh = nullptr, *ro = nullptr;
+                gm_layer_outputs(m->moe, &sh, &ro);
+                if (dbg->shexp && sh)
+                    MH_RC(rc, hipMemcpyAsync(dbg->shexp + l * D, sh, D * sizeof(float), hipMemcpyDeviceToHost, st));
+                if (!rc && dbg->moe && ro)
+                    MH_RC(rc, hipMemcpyAsync(dbg->moe + l * D, ro, D * sizeof(float), hipMemcpyDeviceToHost, st));
+            }
+        }
+        if (!rc && layer_ckpt) MH_RC(rc, hipMemcpyAsync(layer_ckpt + l * D, m->x, D * sizeof(float), hipMemcpyDeviceToHost, st));
     }
-    if (rc) return rc;
+    if (rc) {
+        if (relay) gm_decode_abort(m->moe);
+        return rc;
+    }
     launch_gemv(gemv(m->out_q, m->out_s, m->x, m->output_norm, m->logits, c.vocab_size, c.dim, c.group_size), GV_PLAIN, st);
     MH_OK(hipGetLastError());
     MH_OK(hipMemcpyAsync(logits, m->logits, (size_t)c.vocab_size * sizeof(float), hipMemcpyDeviceToHost, st));
@@ -630,6 +700,7 @@ extern "C" int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int f
     if (m->moe && gm_take_launch_error(m->moe)) return GMOE_ERR_HIP;
     return GMOE_OK;
 }
+}  // namespace
 
 extern "C" int gmoe_model_prefill(gmoe_model *m, const int32_t *tokens, int n, int pos0, float *logits, float *x_out,
                                   void *stream) {
@@ -678,5 +749,28 @@ extern "C" int gmoe_model_prefill(gmoe_model *m, const int32_t *tokens, int n, i
     if (x_out) MH_OK(hipMemcpyAsync(x_out, xl, D * sizeof(float), hipMemcpyDeviceToHost, st));
     MH_OK(hipStreamSynchronize(st));
     if (m->moe && gm_take_launch_error(m->moe)) return GMOE_ERR_HIP;
+    return GMOE_OK;
+}
+
+extern "C" int gmoe_model_read_cache(gmoe_model *m, int layer, int pos0, int n, float *comp_out, float *pe_out,
+                                     void *stream) {
+    if (!m || (!comp_out && !pe_out)) {
+        gm_set_err("gmoe_model_read_cache: null argument");
+        return GMOE_ERR_INVALID;
+    }
+    const gmoe_model_config &c = m->c;
+    if (layer < 0 || layer >= c.attn_layers || pos0 < 0 || n < 1 || pos0 + n > c.cache_cap) {
+        gm_set_err("gmoe_model_read_cache: layer %d, positions %d..%d outside %d attention layers x %d positions", layer,
+                   pos0, pos0 + n - 1, c.attn_layers, c.cache_cap);
+        return GMOE_ERR_INVALID;
+    }
+    MH_OK(hipSetDevice(m->device));
+    hipStream_t st = (hipStream_t)stream;
+    const size_t kv = (size_t)c.kv_lora_rank, rope = (size_t)c.rope_dim, row0 = (size_t)layer * c.cache_cap + pos0;
+    if (comp_out)
+        MH_OK(hipMemcpyAsync(comp_out, m->comp + row0 * kv, (size_t)n * kv * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (pe_out)
+        MH_OK(hipMemcpyAsync(pe_out, m->pe + row0 * rope, (size_t)n * rope * sizeof(float), hipMemcpyDeviceToHost, st));
+    MH_OK(hipStreamSynchronize(st));
     return GMOE_OK;
 }

@@ -49,11 +49,36 @@
 // all blocks are resident, so the schedule cannot deadlock.
 #pragma once
 
-#include "decode.h"
+#include "stack.h"
 
 #define RL_ROWS 16       // rows of D per combine chunk and router record
 #define RL_FIN_MAX 16    // finisher blocks (four experts at a time each)
 #define RL_PPL 2         // combine chunks (router records) per lane of a finisher wave: D <= 64 * 2 * 16
+
+// Router record of one chunk and expert (16 bytes): the fp64 sum of t_i over the chunk's
+// rows, and upper bounds of the sums of |partial sums| and |t_i|, rounded up to fp32.
+struct RlRec {
+    double sigma;
+    float lam, mu;
+};
+
+// Entry li of the launch's layer table, read through the constant address space: the host
+// writes the table before the launch and the kernel never does, so scalar loads may read it
+// and its pointers live in scalar registers. (Loaded by vector loads, their first use after
+// a burst of weight requests would wait for the whole burst: the memory counter retires
+// loads in order.)
+__device__ static inline StackLayer rl_layer(const StackArgs &a, int li) {
+    const __attribute__((address_space(4))) StackLayer *t = (const __attribute__((address_space(4))) StackLayer *)a.layers + li;
+    StackLayer L;
+    L.experts = t->experts;
+    L.norm = t->norm;
+    L.gate_inp = t->gate_inp;
+    L.bias = t->bias;
+    L.nu = t->nu;
+    L.has_routed = t->has_routed;
+    L.pad = 0;
+    return L;
+}
 
 // ---------------------------------------------------------------- tags
 
@@ -593,7 +618,7 @@ __device__ __attribute__((always_inline)) static void rl_records(const StackArgs
     const int tid = phase_tid(), q = tid & 3, eq = tid >> 2, E = a.E, NCH = a.D / RL_ROWS;
     const unsigned p = rl_par(a, li);
     const double x0 = xc[4 * q], x1 = xc[4 * q + 1], x2 = xc[4 * q + 2], x3 = xc[4 * q + 3];
-    DkRec *rec = ws_at<DkRec>(a, li, a.o.rec);  // [E][D/16]: an expert's chunks contiguous
+    RlRec *rec = ws_at<RlRec>(a, li, a.o.rec);  // [E][D/16]: an expert's chunks contiguous
 #pragma unroll
     for (int m = 0; m < GM_MAX_E / 64; m++) {
         const int e = eq + 64 * m;
@@ -619,7 +644,7 @@ __device__ __attribute__((always_inline)) static void rl_records(const StackArgs
             const double sig = dpp_d<0xFF>(incl, 0.0);  // quad_perm [3,3,3,3]
             if (q == 0 && e < E) {
                 const float lf = f32_ru(lam * (1.0 + 0x1p-50)), mf = f32_ru(mu * (1.0 + 0x1p-50));
-                DkRec *re = rec + (size_t)e * NCH + c;
+                RlRec *re = rec + (size_t)e * NCH + c;
                 st_u64((unsigned long long *)&re->sigma, rl_tag_d(sig, p));
                 st_u64((unsigned long long *)&re->lam,
                        (unsigned long long)rl_tag_up(lf, p) | ((unsigned long long)rl_tag_up(mf, p) << 32));
@@ -738,7 +763,7 @@ __device__ __attribute__((always_inline)) static bool rl_finish_expert(const Sta
     const int D = a.D, NCH = D / RL_ROWS, lane = phase_tid() & 63;
     const int ppl = NCH > 64 ? NCH / 64 : 1;
     const unsigned p = rl_par(a, li);
-    const unsigned long long *rec = (const unsigned long long *)(ws_at<DkRec>(a, li, a.o.rec) + (size_t)e * NCH);
+    const unsigned long long *rec = (const unsigned long long *)(ws_at<RlRec>(a, li, a.o.rec) + (size_t)e * NCH);
     const unsigned long long *xsq = ws_at<unsigned long long>(a, li, a.o.xsq);
     // the expert's constants before the wait, so that no round trip follows it
     const double nu = gbl(L.nu)[e];
@@ -946,15 +971,15 @@ __device__ __attribute__((always_inline)) static bool rl_run(const StackArgs &a,
     // prologue: layer 0's records from the launch's input
     if (combine) {
         RlRouter rr;
-        rl_router_rows(a, dk_layer(a, 0), cc, rr);
+        rl_router_rows(a, rl_layer(a, 0), cc, rr);
         if (tid < RL_ROWS) sh.xn_r[tid] = a.x_in[cc * RL_ROWS + tid];
         __syncthreads();
         rl_records(a, 0, cc, rr, sh.xn_r);
         __syncthreads();
     }
     for (int li = 0; li < a.n_layers; li++) {
-        const StackLayer L = dk_layer(a, li);
-        const StackLayer Ln = dk_layer(a, li + 1 < a.n_layers ? li + 1 : li);
+        const StackLayer L = rl_layer(a, li);
+        const StackLayer Ln = rl_layer(a, li + 1 < a.n_layers ? li + 1 : li);
         const int layer = a.first_layer + li;
         const bool routed_on = !(a.flags & GMOE_FLAG_NO_ROUTED) && L.has_routed;
         const long base = (long)li * per_layer;

@@ -20,13 +20,6 @@ __global__ void k_repack_q(const int8_t *__restrict__ raw, uint8_t *__restrict__
         *(u32x4 *)(dst + (size_t)m * dst_stride + u * 16) = v;
         return;
     }
-    if (layout == GM_LAYOUT_ROWGROUPS) {  // unit u = (group, slice, row of the group)
-        const size_t t = u >> 2;
-        const int r = 4 * (int)(t / (size_t)(cols >> 4)) + (int)(u & 3), j = (int)(t % (size_t)(cols >> 4));
-        const u32x4 v = *(const u32x4 *)(raw + (size_t)m * rows * cols + (size_t)r * cols + 16 * (size_t)j);
-        *(u32x4 *)(dst + (size_t)m * dst_stride + u * 16) = v;
-        return;
-    }
     const int lane = (int)(u & 63);
     const size_t pj = u >> 6;
     const int nch = cols >> 6;
@@ -58,6 +51,5 @@ __global__ void k_repack_s(const float *__restrict__ raw, uint8_t *__restrict__ 
     const __half hs = __float2half_rn(s);
     if (inexact && __half2float(hs) != s) atomicAdd(inexact, 1ull);
     __half *out = (__half *)(dst + (size_t)m * dst_stride);
-    out[layout == GM_LAYOUT_SLICES ? gm_ds_offset(r, b, rows)
-        : layout == GM_LAYOUT_ROWGROUPS ? gm_drs_offset(r, b, cols) : gm_s_offset(r, b, cols)] = hs;
+    out[layout == GM_LAYOUT_SLICES ? gm_ds_offset(r, b, rows) : gm_s_offset(r, b, cols)] = hs;
 }

@@ -100,7 +100,7 @@ struct StackLayer {
 // Per-layer workspace: one region of `ws_layer_bytes` per layer of the launch.
 struct StackWs {
     size_t x, xn, dig, dexp, stage, ex_w, ypart;  // byte offsets inside a layer region
-    size_t h, rec, xsq;                           // the row-owner kernel's (decode.h): h digits, router records
+    size_t rec, xsq;                              // relay.h: router records, the chunks' sums of squares
 };
 
 struct StackArgs {
@@ -111,7 +111,6 @@ struct StackArgs {
     int D, F, E, K, flags;
     float eps, routed_scale;
     size_t stride, off_gq, off_uq, off_dq, off_gs, off_us, off_ds;  // down in the column-slice layout
-    size_t off_rq, off_rs;     // down in the row-group layout (k_moe_decode only)
     uint8_t *ws;               // per-layer workspace base
     size_t ws_layer_bytes;
     StackWs o;
@@ -133,7 +132,6 @@ struct StackArgs {
     unsigned long long *trace; // optional: SK_TRACE_STAMPS timestamps per item (see k_moe_stack)
     int n_router;              // router blocks: a power of two, <= min(E, 64)
     int shared_blocks;         // blocks in the shared-expert role
-    int h_words;               // 8-byte words of each layer's h records, zeroed before the launch (decode.h; 0 otherwise)
     unsigned long long *par_dev;  // relay.h: [SK_MAX_LAYERS / 64] words, bit li = the parity of workspace layer li;
                                   // k_stack_reset flips the launch's layers before the kernel reads them
     int rl_cb0;                // relay.h: the routed block that runs combine chunk 0
@@ -217,15 +215,11 @@ struct SkShared {
     unsigned zero;  // 0 for the kernel's life (an always-zero operand of gu_products)
     int xe_local;   // exponent of a routed block's own digits of xn (sk_local_digits)
     unsigned spin_limit;
-    float xr4[4];   // the row-owner kernel's (decode.h): an owner's new rows of x
     float xres[16]; // relay.h: a combine chunk's residual rows
-    unsigned long long hrec[8];  // and an item's h record
     int idx[GM_MAX_K];
     float wk[GM_MAX_K], ws[GM_MAX_K];
     long trace_item;
     unsigned long long *trace;
-    unsigned long long *dk_trace;  // the row-owner kernel's: stamps of the current layer, flushed at its end
-    unsigned long long stamps[SK_TRACE_STAMPS];
 };
 
 __device__ static inline void st_u(unsigned *p, unsigned v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -1115,8 +1109,6 @@ __global__ __launch_bounds__(SK_BLOCK) void k_stack_reset(unsigned *ctr, int n, 
     }
     unsigned long long *stage = ws_at<unsigned long long>(a, li, a.o.stage);
     for (int i = tid; i < SK_STAGE_COPIES * SK_STAGE_COPY_WORDS; i += SK_BLOCK) stage[i] = SK_UNSET;
-    unsigned long long *h = ws_at<unsigned long long>(a, li, a.o.h);
-    for (int i = tid; i < a.h_words; i += SK_BLOCK) h[i] = 0ull;
 }
 
 // Block roles: the first n_router blocks route, and router blocks 1.. then take the shared

@@ -87,6 +87,8 @@ def backend_lib():
         lib.glm_backend_free.restype = None
         lib.glm_backend_try_hip_moe.argtypes = [RP, SP, C.c_int, C.c_int]
         lib.glm_backend_try_hip_moe.restype = C.c_int
+        lib.glm_backend_forward_token.argtypes = [C.c_int, RP, SP, C.c_int, C.c_int, C.c_int]
+        lib.glm_backend_forward_token.restype = C.c_int
         lib._backend_typed = True
     return lib
 
@@ -222,6 +224,10 @@ def forward_lib():
         lib.glm_hip_model_active.restype = C.c_int
         lib.glm_hip_prefill.argtypes = [RP, SP, IP, C.c_int, C.c_int, C.c_int]
         lib.glm_hip_prefill.restype = C.c_int
+        lib.glm_hip_model_read_cache.argtypes = [C.c_int, C.c_int, C.c_int, FP, FP]
+        lib.glm_hip_model_read_cache.restype = C.c_int
+        lib.glm_hip_model_forward.argtypes = [RP, SP, C.c_int, C.c_int, C.c_int, FP, FP, FP]
+        lib.glm_hip_model_forward.restype = C.c_int
         lib._forward_typed = True
     return lib
 
@@ -280,6 +286,16 @@ class Decoder:
             raise RuntimeError(f"glm_hip_prefill failed at positions {pos0}..{pos0 + toks.size - 1}")
         return self.logits()
 
+    def read_cache(self, layer, pos0, n, kv, rope):
+        """Positions pos0..pos0+n-1 of the GPU model's latent cache of attention layer `layer`:
+        (comp [n][kv], pe [n][rope])."""
+        FP = C.POINTER(C.c_float)
+        comp = np.zeros((n, kv), np.float32)
+        pe = np.zeros((n, rope), np.float32)
+        if self.lib.glm_hip_model_read_cache(layer, pos0, n, comp.ctypes.data_as(FP), pe.ctypes.data_as(FP)) != 0:
+            raise RuntimeError("glm_hip_model_read_cache failed")
+        return comp, pe
+
     def on_gpu(self):
         """True when every step of the forward runs on the GPU model (gmoe_model.h)."""
         return self.backend == BACKEND_HIP and bool(self.lib.glm_hip_model_active())
@@ -293,3 +309,18 @@ class Decoder:
             self.backend = BACKEND_CPU
         if self.st.x:
             self.lib.glm_runstate_free(C.byref(self.st))
+
+
+def write_tokenizer(path, vocab_size, bos_id, eos_id):
+    """A `.tokenizer` sidecar in the layout glm.c's loader reads (infer.c:232-285): max token
+    length, bos and eos ids (u32 each), then per token a float score, a u32 length and the
+    bytes. Tokens 33..126 are those single printable ASCII bytes (so a prompt of such bytes
+    encodes to one token per byte, infer.c:1328-1366, with no merges); every other token i is
+    the text "<t{i}>". For glm.c's app on synthetic checkpoints."""
+    import struct
+    toks = [bytes([i]) if 33 <= i < 127 else f"<t{i}>".encode() for i in range(vocab_size)]
+    with open(path, "wb") as f:
+        f.write(struct.pack("<III", max(len(t) for t in toks), bos_id, eos_id))
+        for t in toks:
+            f.write(struct.pack("<fI", 0.0, len(t)))
+            f.write(t)

@@ -57,7 +57,7 @@ class GmoeLayerState(C.Structure):
 # gmoe_profile buckets (GMOE_KERNEL_*): gate_up is k_gate_up (T=1) or k_group_gu (grouped
 # prefill), down is k_down_combine or k_group_down
 KERNEL_NAMES = {0: "k_router_tok", 1: "gate_up", 2: "down", 3: "k_dispatch", 4: "k_moe_stack", 5: "k_act_split",
-                6: "k_token_combine", 7: "k_moe_decode", 8: "k_moe_relay"}
+                6: "k_token_combine", 8: "k_moe_relay"}
 N_KERNEL_IDS = 9
 
 

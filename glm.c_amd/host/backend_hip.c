@@ -224,6 +224,46 @@ static int prepare_model(const Runtime *rt, const RunState *st) {
 
 int glm_hip_model_active(void) { return g_model != NULL; }
 
+
+/* The RunState whose decode history the GPU model's latent cache holds (positions
+ * 0 .. g_model_len-1, in device memory: that state's own host cache is not written), and
+ * its cache buffer, which tells the state from a copy of it. Every other RunState keeps its
+ * history in its host cache, so the model runs a token only for this state, or to start
+ * the first sequence at position 0; other states take glm.c's host steps. */
+static const RunState *g_model_st = NULL;
+static const float *g_model_cache = NULL;
+static int g_model_len = 0;
+
+int glm_hip_model_read_cache(int layer, int pos0, int n, float *comp_out, float *pe_out) {
+    if (!g_model) return -1;
+    if (gmoe_model_read_cache(g_model, layer, pos0, n, comp_out, pe_out, NULL) != GMOE_OK) {
+        fprintf(stderr, "[glm-hip] %s\n", gmoe_last_error());
+        return -1;
+    }
+    return 0;
+}
+
+int glm_hip_model_owns(const RunState *st, int pos) {
+    if (!g_model || !st || pos < 0) return 0;
+    if (!g_model_st) return pos == 0;
+    return st == g_model_st && st->k_cache_comp == g_model_cache && pos <= g_model_len;
+}
+
+static void model_track(const RunState *st, int end) {
+    if (g_model_st != st) g_model_len = 0;
+    g_model_st = st;
+    g_model_cache = st->k_cache_comp;
+    if (end > g_model_len) g_model_len = end;
+}
+
+void glm_hip_model_forget(const RunState *st) {
+    if (st && st == g_model_st) {
+        g_model_st = NULL;
+        g_model_cache = NULL;
+        g_model_len = 0;
+    }
+}
+
 int glm_hip_model_forward(const Runtime *rt, RunState *st, int token, int pos, int keep_state, float *logits,
                           float *attn_ckpt, float *layer_ckpt) {
     (void)rt;
@@ -235,6 +275,19 @@ int glm_hip_model_forward(const Runtime *rt, RunState *st, int token, int pos, i
         fprintf(stderr, "[glm-hip] forward at position %d failed: %s\n", pos, gmoe_last_error());
         return -1;
     }
+    if (!keep_state) model_track(st, pos + 1);
+    return 0;
+}
+
+int glm_hip_model_forward_sums(RunState *st, int token, int pos, float *attn_ckpt, float *layer_ckpt, float *kv_out,
+                               float *concat_out, float *shexp_out, float *moe_out) {
+    if (!g_model || !st) return -1;
+    if (gmoe_model_forward_token_debug(g_model, token, pos, 0, st->logits, st->x, attn_ckpt, layer_ckpt, kv_out,
+                                       concat_out, shexp_out, moe_out, NULL) != GMOE_OK) {
+        fprintf(stderr, "[glm-hip] forward at position %d failed: %s\n", pos, gmoe_last_error());
+        return -1;
+    }
+    model_track(st, pos + 1);
     return 0;
 }
 
@@ -249,6 +302,7 @@ int glm_hip_model_prefill(const Runtime *rt, RunState *st, const int *tokens, in
                     gmoe_last_error());
             return -1;
         }
+        model_track(st, pos0 + i + k);
     }
     return 0;
 }
@@ -291,6 +345,9 @@ int glm_hip_moe_layer(const Runtime *rt, RunState *st, int layer_idx, int debug_
 void glm_hip_free(void) {
     if (g_model) gmoe_model_destroy(g_model);
     g_model = NULL;
+    g_model_st = NULL;
+    g_model_cache = NULL;
+    g_model_len = 0;
     if (g_ctx) gmoe_destroy(g_ctx);
     g_ctx = NULL;
     g_active = 0;

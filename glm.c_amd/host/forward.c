@@ -17,8 +17,9 @@
  * and rel-L2 1e-3 of glm.c's FFN, ~1e-6 relative in practice).
  *
  * glm.c dies on a position past the cache and on allocation failure; these functions
- * print a "[glm-hip]" message and return -1 instead. debug_mode is passed to the MoE
- * layers (their per-layer sums, infer.c:1207-1210); the host steps print nothing.
+ * print a "[glm-hip]" message and return -1 instead. With debug_mode both paths print
+ * glm.c's "[glm-layer-sum]" lines: the MoE layers' two sums at every position
+ * (infer.c:1207-1210) and the per-stage sums at position 0 (infer.c:1811-1895).
  */
 #include <math.h>
 #include <stdio.h>
@@ -77,6 +78,19 @@ static float fw_dot(const float *a, const float *b, int n) {
     float s = 0.0f;
     for (int i = 0; i < n; i++) s += a[i] * b[i];
     return s;
+}
+
+/* infer.c:940-949: the --debug sums, a sequential fp32 sum of a vector. */
+static float fw_sum(const float *x, int n) {
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s += x[i];
+    return s;
+}
+static void fw_print_sum(const char *name, int layer, float v) {
+    if (layer >= 0)
+        fprintf(stderr, "[glm-layer-sum] %s-%d sum=%.6f\n", name, layer, v);
+    else
+        fprintf(stderr, "[glm-layer-sum] %s sum=%.6f\n", name, v);
 }
 
 /* infer.c:912-914 */
@@ -211,11 +225,15 @@ static int fw_forward(const Runtime *rt, RunState *s, int token, int pos, int de
     const int keep_layer = layer_out && layer_stride >= dim && max_layers > 0;
 
     fw_dequant(rt->tok_q + (size_t)token * dim, rt->tok_s + (size_t)token * (dim / gs), s->x, dim, gs);
+    const int sums = debug_mode && pos == 0;  // infer.c:1811-1813, 1831-1859, 1885-1895
+    if (sums) fw_print_sum("embd", -1, fw_sum(s->x, dim));
 
     // the three model forms of infer.c:1817-1881: attention in every layer (then the MoE
     // layers run), attention in layer 0 only, or layer 0's FFN alone
     const int n_run = rt->has_all_attn ? c->n_layers : 1;
     for (int l = 0; l < n_run; l++) {
+        const float before_attn = sums && rt->has_all_attn ? fw_sum(s->x, dim) : 0.0f;
+        float before_ffn = 0.0f;
         if (rt->has_all_attn || rt->has_l0_attn) {
             LayerAttnWeights l0 = {rt->l0_attn_norm, rt->l0_q_a_norm, rt->l0_kv_a_norm, rt->l0_q_a_q, rt->l0_q_a_s,
                                    rt->l0_q_b_q,     rt->l0_q_b_s,    rt->l0_kv_a_q,    rt->l0_kv_a_s, rt->l0_k_b_q,
@@ -228,6 +246,13 @@ static int fw_forward(const Runtime *rt, RunState *s, int token, int pos, int de
                 if (n_attn) *n_attn = l + 1;
             }
         }
+        if (sums && rt->has_all_attn) {
+            fw_print_sum("Vcur", l, fw_sum(s->kv_a, c->kv_lora_rank));
+            fw_print_sum("kqv_out", l, fw_sum(s->att_concat, c->n_heads * c->l0_v_head_dim));
+            fw_print_sum("ffn_inp", l, fw_sum(s->x, dim));
+            fw_print_sum("attn_out", l, fw_sum(s->x, dim) - before_attn);
+            before_ffn = fw_sum(s->x, dim);
+        }
         if (l == 0) {
             fw_dense_ffn(rt, s, gs);
         } else if (fw_moe(rt, s, l, debug_mode) != 0) {
@@ -237,10 +262,78 @@ static int fw_forward(const Runtime *rt, RunState *s, int token, int pos, int de
             memcpy(layer_out + (size_t)l * layer_stride, s->x, (size_t)dim * sizeof(float));
             if (n_layers) *n_layers = l + 1;
         }
+        if (sums) {
+            fw_print_sum("l_out", l, fw_sum(s->x, dim));
+            if (rt->has_all_attn) fw_print_sum("ffn_out", l, fw_sum(s->x, dim) - before_ffn);
+        }
     }
     fw_rmsnorm(s->xn, s->x, rt->output_norm, dim);
+    if (sums) fw_print_sum("result_norm", -1, fw_sum(s->xn, dim));
     fw_matvec(rt->out_q, rt->out_s, s->xn, s->logits, c->vocab_size, dim, gs);
+    if (sums) fw_print_sum("result_output", -1, fw_sum(s->logits, c->vocab_size));
     return 0;
+}
+
+/* The GPU model's forward with glm.c's --debug lines: at every position each MoE layer's
+ * two sums (infer.c:1207-1210), and at position 0 the per-stage sums of infer.c:1811-1895,
+ * from the intermediate vectors the model returns (gmoe_model_forward_token_debug), in
+ * glm.c's order. Advances the model's state as glm_hip_forward_token does. */
+static int fw_forward_device_debug(const Runtime *rt, RunState *s, int token, int pos) {
+    const RuntimeConfig *c = &rt->cfg;
+    const int L = c->n_layers, dim = c->dim, gs = (int)c->group_size, kv = c->kv_lora_rank;
+    const int hv = c->n_heads * c->l0_v_head_dim;
+    const int n_run = rt->has_all_attn ? L : 1;
+    float *attn = (float *)calloc((size_t)L * dim, sizeof(float)), *lay = (float *)calloc((size_t)L * dim, sizeof(float));
+    float *kvb = (float *)calloc((size_t)L * (kv > 0 ? kv : 1), sizeof(float));
+    float *cat = (float *)calloc((size_t)L * (hv > 0 ? hv : 1), sizeof(float));
+    float *sh = (float *)calloc((size_t)L * dim, sizeof(float)), *mo = (float *)calloc((size_t)L * dim, sizeof(float));
+    float *x0 = (float *)calloc((size_t)dim, sizeof(float));
+    int rc = -1;
+    if (!attn || !lay || !kvb || !cat || !sh || !mo || !x0) {
+        fprintf(stderr, "[glm-hip] out of memory for the debug sums\n");
+    } else {
+        if (token < 0 || token >= c->vocab_size) token = 0;
+        rc = glm_hip_model_forward_sums(s, token, pos, attn, lay, kvb, cat, sh, mo);
+    }
+    if (rc == 0) {
+        const int sums = pos == 0;
+        fw_dequant(rt->tok_q + (size_t)token * dim, rt->tok_s + (size_t)token * (dim / gs), x0, dim, gs);
+        if (sums) fw_print_sum("embd", -1, fw_sum(x0, dim));
+        for (int l = 0; l < n_run; l++) {
+            const float *xin = l == 0 ? x0 : lay + (size_t)(l - 1) * dim, *xa = attn + (size_t)l * dim;
+            const float *xl = lay + (size_t)l * dim;
+            float before_ffn = 0.0f;
+            if (sums && rt->has_all_attn) {
+                const float before_attn = fw_sum(xin, dim);
+                fw_print_sum("Vcur", l, fw_sum(kvb + (size_t)l * kv, kv));
+                fw_print_sum("kqv_out", l, fw_sum(cat + (size_t)l * hv, hv));
+                fw_print_sum("ffn_inp", l, fw_sum(xa, dim));
+                fw_print_sum("attn_out", l, fw_sum(xa, dim) - before_attn);
+                before_ffn = fw_sum(xa, dim);
+            }
+            if (l > 0 && rt->has_moe_shared && rt->moe_layers && rt->moe_layers[l].ffn_norm) {
+                fw_print_sum("ffn_moe_out", l, fw_sum(mo + (size_t)l * dim, dim));
+                fw_print_sum("ffn_shexp", l, fw_sum(sh + (size_t)l * dim, dim));
+            }
+            if (sums) {
+                fw_print_sum("l_out", l, fw_sum(xl, dim));
+                if (rt->has_all_attn) fw_print_sum("ffn_out", l, fw_sum(xl, dim) - before_ffn);
+            }
+        }
+        if (sums) {
+            fw_rmsnorm(x0, s->x, rt->output_norm, dim);
+            fw_print_sum("result_norm", -1, fw_sum(x0, dim));
+            fw_print_sum("result_output", -1, fw_sum(s->logits, c->vocab_size));
+        }
+    }
+    free(attn);
+    free(lay);
+    free(kvb);
+    free(cat);
+    free(sh);
+    free(mo);
+    free(x0);
+    return rc;
 }
 
 /* The forward on the GPU model (glm_hip_model_forward), with the per-layer copies of x
@@ -280,8 +373,10 @@ static int fw_forward_device(const Runtime *rt, RunState *s, int token, int pos,
 /* ---- public ----------------------------------------------------------------------- */
 
 int glm_hip_forward_token(const Runtime *rt, RunState *st, int token, int pos, int debug_mode) {
-    if (rt && st && glm_hip_model_active())
+    if (rt && st && glm_hip_model_owns(st, pos)) {
+        if (debug_mode) return fw_forward_device_debug(rt, st, token, pos);
         return fw_forward_device(rt, st, token, pos, 0, NULL, 0, 0, NULL, NULL, 0, 0, NULL);
+    }
     return fw_forward(rt, st, token, pos, debug_mode, NULL, 0, 0, NULL, NULL, 0, 0, NULL);
 }
 
@@ -292,7 +387,8 @@ int glm_hip_prefill(const Runtime *rt, RunState *st, const int *tokens, int n, i
                 st->cache_cap);
         return -1;
     }
-    if (glm_hip_model_active()) return glm_hip_model_prefill(rt, st, tokens, n, pos0);
+    // with debug_mode, token by token: glm.c prints its per-token sums for prompt tokens too
+    if (!debug_mode && glm_hip_model_owns(st, pos0)) return glm_hip_model_prefill(rt, st, tokens, n, pos0);
     for (int i = 0; i < n; i++) {
         int tok = tokens[i];
         if (tok < 0 || tok >= rt->cfg.vocab_size) tok = 0;  // infer.c:2220
@@ -308,7 +404,9 @@ int glm_hip_forward_token_dual_checkpoints(const Runtime *rt, const RunState *sr
     if (!rt || !src || src->cache_cap <= 0) return -1;
     if (attn_layer_out && (attn_layer_stride < rt->cfg.dim || max_attn_layers <= 0)) return -1;
     if (layer_out && (layer_stride < rt->cfg.dim || max_layers <= 0)) return -1;
-    if (glm_hip_model_active())  // the GPU model restores what the token writes: no copy of src needed
+    // src's history on the device (the GPU model restores what the token writes, so no copy
+    // of src is needed); any other state's history is its host cache, on a copy
+    if (glm_hip_model_owns(src, pos))
         return fw_forward_device(rt, (RunState *)src, token, pos, 1, attn_layer_out, attn_layer_stride, max_attn_layers,
                                  written_attn_layers, layer_out, layer_stride, max_layers, written_layers);
     RunState tmp;
@@ -341,6 +439,7 @@ int glm_argmax(const float *x, int n) {
 
 void glm_runstate_free(RunState *s) {
     if (!s) return;
+    glm_hip_model_forget(s);
     void *bufs[] = {s->x,       s->xn,          s->xb,         s->ff_gate,  s->ff_up,      s->logits,     s->k_cache_comp,
                     s->k_cache_pe, s->q_a,      s->q_full,     s->kv_a,     s->q_nope,     s->q_pe,       s->q_abs,
                     s->att_scores, s->att_ctx,  s->att_concat, s->moe_gate, s->moe_up,     s->moe_router, s->moe_out_acc,

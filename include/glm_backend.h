@@ -54,10 +54,27 @@ int glm_hip_moe_layer(const Runtime *rt, RunState *st, int layer_idx, int debug_
 int glm_hip_model_active(void);
 int glm_hip_model_forward(const Runtime *rt, RunState *st, int token, int pos, int keep_state, float *logits,
                           float *attn_ckpt, float *layer_ckpt);
+/* glm_hip_model_forward (not keep_state, logits into st->logits) that also returns, per
+ * layer, the vectors glm.c's --debug sums (gmoe_model_forward_token_debug): x after
+ * attention and FFN, the kv entry, the heads' concat, and for MoE layers the shared and
+ * routed outputs, each [n_layers][..] on the host. 0 ok, -1 error. */
+int glm_hip_model_forward_sums(RunState *st, int token, int pos, float *attn_ckpt, float *layer_ckpt, float *kv_out,
+                               float *concat_out, float *shexp_out, float *moe_out);
 /* n prompt tokens at positions pos0.. through the GPU model in batches of GLM_HIP_PREFILL_BATCH
  * (gmoe_model_prefill): the last token's logits into st->logits and its final x into st->x.
  * 0 ok, -1 error (glm_hip_prefill in glm_forward.h is the form that also works without the model). */
 int glm_hip_model_prefill(const Runtime *rt, RunState *st, const int *tokens, int n, int pos0);
+/* The GPU model's latent cache holds one RunState's history (st->k_cache_* of that state
+ * are not written). 1 when the model can take st's token at pos: st is that state and the
+ * device holds every position below pos, or no state is held yet and pos is 0 (the
+ * forward then takes st on). glm_hip_forward_token, glm_hip_prefill and the checkpoint
+ * forwards run on the host steps otherwise, from st's own cache. */
+int glm_hip_model_owns(const RunState *st, int pos);
+/* Positions pos0.. of the GPU model's latent cache for attention layer `layer` (the held
+ * state's k_cache_comp / k_cache_pe rows, gmoe_model_read_cache). 0 ok, -1 error. */
+int glm_hip_model_read_cache(int layer, int pos0, int n, float *comp_out, float *pe_out);
+/* st's buffers are about to be freed: the model holds no state's history any more. */
+void glm_hip_model_forget(const RunState *st);
 void glm_hip_free(void);
 
 #ifdef __cplusplus

@@ -139,8 +139,7 @@ int gmoe_forward_layers(gmoe_ctx *ctx, int first_layer, int n_layers, int n_toke
  * workspace (every layer's activations, router entries and partial sums, the counters
  * and the error word) in one fixed device array of GMOE_NOALLOC_SCRATCH_BYTES per GPU,
  * which the library holds until the process ends, instead of the context's buffers.
- * At most as many layers per call as fit in that array (at GLM-4.7-Flash's shape 16 on
- * k_moe_stack, 108 on the row-owner kernel of GMOE_DECODE_KERNEL=1):
+ * At most as many layers per call as fit in that array (at GLM-4.7-Flash's shape 16):
  * a longer run is refused with GMOE_ERR_INVALID. Trace and profile recording are
  * skipped. Every call on one GPU shares the array, so calls that overlap on one GPU
  * (other streams, threads or contexts) race; calls in order on one stream do not. A
@@ -178,8 +177,7 @@ int gmoe_get_stats(gmoe_ctx *ctx, gmoe_stats *out);
 #define GMOE_KERNEL_STACK 4      /* persistent decode kernel (T=1, all requested layers) */
 #define GMOE_KERNEL_DIGITS 5     /* prefill: activations to their int8 digit form */
 #define GMOE_KERNEL_COMBINE 6    /* prefill: per-token combine + residual */
-#define GMOE_KERNEL_DECODE 7     /* row-owner persistent decode kernel (T=1, all requested layers), opted into
-                                  * with GMOE_DECODE_KERNEL=1 where the shape fits it */
+/* 7: unused (an earlier persistent decode kernel) */
 #define GMOE_KERNEL_RELAY 8      /* persistent decode kernel whose phases poll each other's tagged results (T=1,
                                   * all requested layers) */
 #define GMOE_KERNEL_COUNT 9

@@ -91,6 +91,16 @@ int gmoe_model_set_moe(gmoe_model *m, gmoe_ctx *moe, const uint8_t *layers, int 
 int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, float *x_out,
                              float *attn_ckpt, float *layer_ckpt, void *stream);
 
+/* gmoe_model_forward_token that also returns what glm.c's --debug sums at position 0
+ * (infer.c:1832-1858, 1207-1210), per layer l, into host buffers (any may be NULL):
+ * kv_out + l*kv_lora_rank the normalised kv entry of the position (glm.c's kv_a),
+ * concat_out + l*n_heads*v_head_dim the heads' attention outputs (att_concat), and for MoE
+ * layers shexp_out + l*dim the shared expert's output (xb) and moe_out + l*dim the routed
+ * combine (moe_out_acc). */
+int gmoe_model_forward_token_debug(gmoe_model *m, int token, int pos, int flags, float *logits, float *x_out,
+                                   float *attn_ckpt, float *layer_ckpt, float *kv_out, float *concat_out,
+                                   float *shexp_out, float *moe_out, void *stream);
+
 /* n tokens at positions pos0 .. pos0+n-1 (n <= max_batch, pos0 + n <= cache_cap) through the
  * model at once, layer by layer, then a synchronisation: the same result as n calls of
  * gmoe_model_forward_token in order (the latent cache gains the n positions), but every
@@ -101,6 +111,12 @@ int gmoe_model_forward_token(gmoe_model *m, int token, int pos, int flags, float
  * after the final layer. The MoE context must take n tokens (gmoe_config.max_tokens >= n). */
 int gmoe_model_prefill(gmoe_model *m, const int32_t *tokens, int n, int pos0, float *logits, float *x_out,
                        void *stream);
+
+/* Positions pos0 .. pos0+n-1 of attention layer `layer`'s latent cache (host buffers, then
+ * a synchronisation): comp_out [n][kv_lora_rank] and pe_out [n][rope_dim] (either may be
+ * NULL), the entries glm.c keeps in RunState.k_cache_comp / k_cache_pe (infer.c:1012-1017,
+ * the rope part rotated). For callers that check or hand over the decode state. */
+int gmoe_model_read_cache(gmoe_model *m, int layer, int pos0, int n, float *comp_out, float *pe_out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -283,3 +283,75 @@ int ref_forward_timed(const char *path, int token, int pos, int cache_cap, int n
     runtime_close(&rt);
     return rc;
 }
+
+/* glm.c's own steps of one token at position pos, each on inputs the caller gives (a child
+ * process, as for ref_ckpt_layout), so that a device forward can be checked stage by stage
+ * on its own intermediate values:
+ *   stage 0  layer `layer`'s attention (apply_mla_attention_layer, infer.c:978-1065) on x_in,
+ *            or for x_in == NULL on the token's embedding row (infer.c:1807-1810), over a
+ *            cache whose positions 0..pos-1 are comp [pos][kv_lora] and pe [pos][rope];
+ *            out = x after it [dim];
+ *   stage 1  layer `layer`'s FFN (apply_l0_dense_ffn for layer 0, else
+ *            apply_moe_shared_ffn_layer, infer.c:1067-1216) on x_in; out = x after it [dim];
+ *   stage 2  the final rmsnorm and the LM head (infer.c:1886-1893) on x_in; out = logits.
+ * 0, or -1. */
+int ref_stage(const char *path, int stage, int layer, int token, int pos, const float *comp, const float *pe,
+              const float *x_in, float *out) {
+    Runtime rt;
+    runtime_open(&rt, path);
+    RunState st;
+    runstate_build(&st, &rt, pos + 1);
+    const RuntimeConfig *c = &rt.cfg;
+    const int dim = c->dim, gs = (int)c->group_size;
+    int rc = 0;
+    if (x_in) {
+        memcpy(st.x, x_in, (size_t)dim * sizeof(float));
+    } else {
+        if (token < 0 || token >= c->vocab_size) token = 0;
+        dequant_row(rt.tok_q + (size_t)token * dim, rt.tok_s + (size_t)token * (dim / gs), st.x, dim, gs);
+    }
+    if (stage == 0) {
+        if (!rt.has_all_attn || layer < 0 || layer >= c->n_layers) {
+            rc = -1;
+        } else {
+            const size_t base = (size_t)layer * (size_t)st.cache_cap;
+            if (pos > 0) {
+                memcpy(st.k_cache_comp + base * c->kv_lora_rank, comp, (size_t)pos * c->kv_lora_rank * sizeof(float));
+                memcpy(st.k_cache_pe + base * c->rope_dim, pe, (size_t)pos * c->rope_dim * sizeof(float));
+            }
+            apply_mla_attention_layer(&rt, &rt.attn_layers[layer], &st, gs, pos, layer, 0);
+            memcpy(out, st.x, (size_t)dim * sizeof(float));
+        }
+    } else if (stage == 1) {
+        if (layer == 0) apply_l0_dense_ffn(&rt, &st, gs, 0);
+        else apply_moe_shared_ffn_layer(&rt, &st, gs, layer, 0, pos);
+        memcpy(out, st.x, (size_t)dim * sizeof(float));
+    } else if (stage == 2) {
+        rmsnorm(st.xn, st.x, rt.output_norm, dim);
+        matvec_rows(rt.out_q, rt.out_s, st.xn, out, c->vocab_size, dim, gs);
+    } else {
+        rc = -1;
+    }
+    runstate_free(&st);
+    runtime_close(&rt);
+    return rc;
+}
+
+/* glm.c's forward of `token` at position pos of a cache of pos + 1 positions as
+ * runstate_build leaves it (zeros below pos; infer.c:827-860): the dual checkpoints
+ * (infer.c:1940-1983) into attn_out and layer_out ([n_layers][dim]) and the logits. A child
+ * process, as above. 0, or -1. */
+int ref_forward_zero_cache(const char *path, int token, int pos, float *attn_out, float *layer_out, float *logits) {
+    Runtime rt;
+    runtime_open(&rt, path);
+    RunState st;
+    runstate_build(&st, &rt, pos + 1);
+    const int L = rt.cfg.n_layers, dim = rt.cfg.dim;
+    int wa = 0, wl = 0;
+    int rc = glm_cpu_forward_token_dual_checkpoints(&rt, &st, token, pos, 0, attn_out, dim, L, &wa, layer_out, dim, L, &wl);
+    if (!rc) rc = glm_cpu_forward_token(&rt, &st, token, pos, 0);
+    if (!rc) memcpy(logits, st.logits, (size_t)rt.cfg.vocab_size * sizeof(float));
+    runstate_free(&st);
+    runtime_close(&rt);
+    return rc;
+}

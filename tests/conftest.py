@@ -35,9 +35,9 @@ def assert_close(got, want, what, max_abs=MAX_ABS, rel_l2=REL_L2):
 
 
 # The persistent T=1 kernels, chosen when a context is created: k_moe_relay (the default,
-# GMOE_DECODE_KERNEL=2 or unset), k_moe_stack (0) and the row-owner k_moe_decode (1).
-DECODE_KERNELS = {"stack": "0", "rows": "1", "relay": "2"}
-DECODE_KERNEL_NAMES = {"stack": "k_moe_stack", "rows": "k_moe_decode", "relay": "k_moe_relay"}
+# GMOE_DECODE_KERNEL=2 or unset) and k_moe_stack (0), its fallback.
+DECODE_KERNELS = {"stack": "0", "relay": "2"}
+DECODE_KERNEL_NAMES = {"stack": "k_moe_stack", "relay": "k_moe_relay"}
 DEFAULT_DECODE_KERNEL = "relay"
 
 

@@ -172,3 +172,48 @@ def test_greedy_decode_picks_glms_tokens(tmp_path, case, mode):
     finally:
         dec.free()
         ck.close()
+
+
+def test_checkpoints_of_a_state_whose_history_the_model_does_not_hold(tmp_path, monkeypatch):
+    """The GPU model's latent cache holds one RunState's history. A second RunState, advanced
+    through other tokens, keeps its history in its host cache, so its tokens and its dual
+    checkpoints take glm.c's host steps from that cache (layer 0 bit for bit with glm.c),
+    and the first state's decode on the GPU model is left as it was."""
+    monkeypatch.delenv("GLM_HIP_HOST_ATTN", raising=False)
+    import ctypes as C
+    sp = small(32, gmoe.SYNTH_SCALES_FP16, n_layers=3, seed=27)
+    toks_a, toks_b = [1, 5, 17, 123], [299, 42, 7]
+    cap = 8
+    path, ck, dec = open_decoder(tmp_path, sp, cap, "gpu")
+    lib = dec.lib
+    other = glm_model.RunState()
+    assert lib.glm_runstate_build(C.byref(other), C.byref(dec.rt), cap) == 0
+    try:
+        ref_a = ref_decode.reference_decode(path, toks_a, cap, dec.L, dec.D, dec.V, tmp_path / "ref_a")
+        ref_b = ref_decode.reference_decode(path, toks_b, cap, dec.L, dec.D, dec.V, tmp_path / "ref_b")
+        for pos in range(3):
+            dec.step(toks_a[pos], pos)
+        for pos in range(2):
+            print(f"[case] second state pos {pos}", flush=True)
+            assert lib.glm_hip_forward_token(C.byref(dec.rt), C.byref(other), toks_b[pos], pos, 0) == 0
+            got = np.ctypeslib.as_array(C.cast(other.logits, C.POINTER(C.c_float)), shape=(dec.V,)).copy()
+            assert_close(got, ref_b["logits"][pos], f"second state pos {pos} logits")
+        attn = np.zeros((dec.L, dec.D), np.float32)
+        layer = np.zeros((dec.L, dec.D), np.float32)
+        na, nl = C.c_int(), C.c_int()
+        FP = C.POINTER(C.c_float)
+        print("[case] dual checkpoints of the second state at pos 2", flush=True)
+        assert lib.glm_hip_forward_token_dual_checkpoints(
+            C.byref(dec.rt), C.byref(other), toks_b[2], 2, 0, attn.ctypes.data_as(FP), dec.D, dec.L, C.byref(na),
+            layer.ctypes.data_as(FP), dec.D, dec.L, C.byref(nl)) == 0
+        for l in range(dec.L):
+            assert_close(attn[l], ref_b["attn"][2][l], f"second state layer {l} attention")
+            assert_close(layer[l], ref_b["layer"][2][l], f"second state layer {l} FFN")
+        assert np.array_equal(bits(attn[0]), bits(ref_b["attn"][2][0])), "host steps: layer 0 attention"
+        print("[case] first state continues on the GPU model at pos 3", flush=True)
+        logits = dec.step(toks_a[3], 3)
+        assert_close(logits, ref_a["logits"][3], "first state pos 3 logits")
+    finally:
+        lib.glm_runstate_free(C.byref(other))
+        dec.free()
+        ck.close()
