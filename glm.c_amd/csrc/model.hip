@@ -31,6 +31,7 @@
 #include "gmoe_model.h"
 #include "common.h"
 #include "dense.h"
+#include "gemm.h"
 
 // gmoe.hip
 void gm_set_err(const char *fmt, ...);
@@ -92,6 +93,11 @@ struct gmoe_model {
           *ctx = nullptr, *concat = nullptr, *ffh = nullptr, *logits = nullptr, *part_ctx = nullptr,
           *part_ml = nullptr, *saved = nullptr;
     int32_t *tokens = nullptr;  // [max_batch] a prefill's token ids
+    // a prefill's GEMM inputs (gemm.h): [max_batch][2][widest input] fp16, their exponents,
+    // and 64 bytes of zeros
+    __half *xs = nullptr;
+    int *xe = nullptr;
+    __half *zeros = nullptr;
     std::vector<void *> allocs;  // every device allocation, freed by gmoe_model_destroy
 };
 
@@ -384,24 +390,97 @@ int dense_ffn(gmoe_model *m, hipStream_t st) {
 // launch for the batch; every token's cache entry is written before any token's scores
 // (token t reads positions up to pos0 + t only), then the attention over the cache runs
 // per token, since its length differs.
+// Whether a batch of n tokens takes the GEMMs of gemm.h for its dense products (a weight
+// panel read once per 64 tokens) rather than k_gemv per token: a batch of a few tokens
+// gains nothing from tiles. Group sizes 16 (glm.c's exporter) and 32 take it.
+bool gemm_batch(const gmoe_model *m, int n) {
+    const int gs = m->c.group_size;
+    return m->xs && n >= QG_GEMM_MIN_TOKENS && (gs == 16 || gs == 32);
+}
+
+// The n tokens' inputs x (ldx apart, cols columns), normalised by norm when given, into
+// the GEMM's split buffer.
+void gemm_inputs(gmoe_model *m, const float *x, int ldx, int cols, const float *norm, int n, hipStream_t st) {
+    hipLaunchKernelGGL(k_norm_split, dim3((unsigned)n), dim3(QG_BLOCK), 0, st, x, ldx, cols, norm, m->xs, m->xe);
+}
+
+// y = q . v for the n tokens' split inputs (gemm_inputs, cols columns): rows of group g
+// (x_rows each) read input columns g * x_stride .. (x_rows = rows: one group); mode
+// QG_PLAIN, QG_RESID (y = resid + dot) or QG_PAIR (y = silu(q . v) * (q2 . v)).
+void gemm_launch(gmoe_model *m, const int8_t *q, const float *s, const int8_t *q2, const float *s2, int rows, int cols,
+                 int x_rows, int x_stride, int xcols, float *y, int ldy, const float *resid, int ldr, int mode, int n,
+                 hipStream_t st) {
+    QgArgs a{};
+    a.q = q;
+    a.s = s;
+    a.q2 = q2;
+    a.s2 = s2;
+    a.xs = m->xs;
+    a.xe = m->xe;
+    a.zeros = m->zeros;
+    a.y = y;
+    a.resid = resid;
+    a.rows = rows;
+    a.cols = cols;
+    a.gs = m->c.group_size;
+    a.n = n;
+    a.xcols = xcols;
+    a.ldy = ldy;
+    a.ldr = ldr;
+    a.x_rows = x_rows;
+    a.x_stride = x_stride;
+    a.bpg = (x_rows + 63) / 64;
+    a.groups = (rows + x_rows - 1) / x_rows;
+    a.tiles = (n + QG_TT - 1) / QG_TT;
+    const int panels = a.bpg * a.groups;
+    const dim3 grid((unsigned)(QG_XCD * ((panels + QG_XCD - 1) / QG_XCD) * a.tiles));
+    const bool k32 = a.gs % 32 == 0 && cols % 32 == 0;
+    if (k32) {
+        if (mode == QG_PAIR) hipLaunchKernelGGL((k_gemm_q8<32, QG_PAIR>), grid, dim3(QG_BLOCK), 0, st, a);
+        else if (mode == QG_RESID) hipLaunchKernelGGL((k_gemm_q8<32, QG_RESID>), grid, dim3(QG_BLOCK), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_q8<32, QG_PLAIN>), grid, dim3(QG_BLOCK), 0, st, a);
+    } else {
+        if (mode == QG_PAIR) hipLaunchKernelGGL((k_gemm_q8<16, QG_PAIR>), grid, dim3(QG_BLOCK), 0, st, a);
+        else if (mode == QG_RESID) hipLaunchKernelGGL((k_gemm_q8<16, QG_RESID>), grid, dim3(QG_BLOCK), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_q8<16, QG_PLAIN>), grid, dim3(QG_BLOCK), 0, st, a);
+    }
+}
+
 int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
     const gmoe_model_config &c = m->c;
     const AttnDev &A = m->attn[l];
     const int gs = c.group_size, H = c.n_heads, kv = c.kv_lora_rank, rope = c.rope_dim, D = c.dim;
     const int ql = c.q_lora_rank, hk = c.head_k_dim, vh = c.v_head_dim;
-    {
+    if (gemm_batch(m, n)) {
+        gemm_inputs(m, m->x, D, D, A.attn_norm, n, st);
+        gemm_launch(m, A.q_a_q, A.q_a_s, nullptr, nullptr, ql, D, ql, 0, D, m->q_a, ql, nullptr, 0, QG_PLAIN, n, st);
+        gemm_launch(m, A.kv_a_q, A.kv_a_s, nullptr, nullptr, kv + rope, D, kv + rope, 0, D, m->kv_a, kv + rope, nullptr,
+                    0, QG_PLAIN, n, st);
+        gemm_inputs(m, m->q_a, ql, ql, A.q_a_norm, n, st);
+        gemm_launch(m, A.q_b_q, A.q_b_s, nullptr, nullptr, H * hk, ql, H * hk, 0, ql, m->q_full, H * hk, nullptr, 0,
+                    QG_PLAIN, n, st);
+    } else {
         GemvArgs qa = batched(gemv(A.q_a_q, A.q_a_s, m->x, A.attn_norm, m->q_a, ql, D, gs), D, ql);
         const GemvArgs kva = batched(gemv(A.kv_a_q, A.kv_a_s, m->x, A.attn_norm, m->kv_a, kv + rope, D, gs), D, kv + rope);
         if (!fuse_second(qa, kva)) launch_gemv(kva, GV_PLAIN, st, n);
         launch_gemv(qa, GV_PLAIN, st, n);
+        launch_gemv(batched(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * hk, ql, gs), ql, H * hk), GV_PLAIN, st, n);
     }
-    launch_gemv(batched(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * hk, ql, gs), ql, H * hk), GV_PLAIN, st, n);
     const AttnArgs aa = attn_args(m, l, pos0);
     GemvArgs kb = batched(gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs), H * hk, H * kv);
     kb.x_rows = kv;
     kb.x_stride = hk;
     launch_query(kb, aa, st, n);  // every token's cache entry before any token's attention
     launch_attn_cache_batch(m, aa, n, st);
+    if (gemm_batch(m, n)) {
+        // per head: concat_h = v_b_h . ctx_h, then x += attn_out . concat
+        gemm_inputs(m, m->ctx, H * kv, H * kv, nullptr, n, st);
+        gemm_launch(m, A.v_b_q, A.v_b_s, nullptr, nullptr, H * vh, kv, vh, kv, H * kv, m->concat, H * vh, nullptr, 0,
+                    QG_PLAIN, n, st);
+        gemm_inputs(m, m->concat, H * vh, H * vh, nullptr, n, st);
+        gemm_launch(m, A.out_q, A.out_s, nullptr, nullptr, D, H * vh, D, 0, H * vh, m->x, D, m->x, D, QG_RESID, n, st);
+        return GMOE_OK;
+    }
     GemvArgs vb = batched(gemv(A.v_b_q, A.v_b_s, m->ctx, nullptr, m->concat, H * vh, kv, gs), H * kv, H * vh);
     vb.x_rows = vh;
     vb.x_stride = kv;
@@ -417,6 +496,14 @@ int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
 int dense_ffn_batch(gmoe_model *m, int n, hipStream_t st) {
     const gmoe_model_config &c = m->c;
     const int D = c.dim, F = c.hidden_dim;
+    if (gemm_batch(m, n)) {
+        gemm_inputs(m, m->x, D, D, m->l0_norm, n, st);
+        gemm_launch(m, m->l0_gate_q, m->l0_gate_s, m->l0_up_q, m->l0_up_s, F, D, F, 0, D, m->ffh, F, nullptr, 0, QG_PAIR, n,
+                    st);
+        gemm_inputs(m, m->ffh, F, F, nullptr, n, st);
+        gemm_launch(m, m->l0_down_q, m->l0_down_s, nullptr, nullptr, D, F, D, 0, F, m->x, D, m->x, D, QG_RESID, n, st);
+        return GMOE_OK;
+    }
     GemvArgs gu = batched(gemv(m->l0_gate_q, m->l0_gate_s, m->x, m->l0_norm, m->ffh, F, D, c.group_size), D, F);
     gu.q2 = m->l0_up_q;
     gu.s2 = m->l0_up_s;
@@ -455,6 +542,14 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
     const size_t ranges = std::max((size_t)attn_ranges(m->n_cu, 1, (int)cap), B * AT_PREFILL_RANGES);
     rc |= mdalloc(m, &m->x, B * c.dim);
     rc |= mdalloc(m, &m->tokens, B);
+    if (B >= QG_GEMM_MIN_TOKENS) {
+        size_t w = (size_t)c.dim;
+        if (c.has_l0_ffn) w = std::max(w, (size_t)c.hidden_dim);
+        if (A > 0) w = std::max({w, (size_t)c.q_lora_rank, H * kv, H * (size_t)c.v_head_dim});
+        rc |= mdalloc(m, &m->xs, B * 2 * w);
+        rc |= mdalloc(m, &m->xe, B);
+        rc |= mdalloc(m, &m->zeros, 64);
+    }
     rc |= mdalloc(m, &m->logits, (size_t)c.vocab_size);
     if (c.has_l0_ffn) rc |= mdalloc(m, &m->ffh, B * c.hidden_dim);
     if (A > 0) {
@@ -491,6 +586,10 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
             gm_set_err("gmoe_model_create: clearing the cache failed");
             rc = GMOE_ERR_HIP;
         }
+    }
+    if (!rc && m->zeros && hipMemset(m->zeros, 0, 64) != hipSuccess) {
+        gm_set_err("gmoe_model_create: clearing the GEMM's zero row failed");
+        rc = GMOE_ERR_HIP;
     }
     if (rc) {
         gmoe_model_destroy(m);
