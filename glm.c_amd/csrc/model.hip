@@ -31,6 +31,7 @@
 #include "gmoe_model.h"
 #include "common.h"
 #include "dense.h"
+#include "attn.h"
 #include "gemm.h"
 
 // gmoe.hip
@@ -165,6 +166,11 @@ int launch_gemv_mode(const GemvArgs &a, hipStream_t st, int nb) {
 template <int LPR, int U>
 void launch_query_lu(const GemvArgs &kb, const AttnArgs &aa, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((k_attn_query<LPR, U>), grid, dim3(DM_BLOCK), 0, st, kb, aa);
+}
+
+// k_attn_query's prep blocks alone (the cache entries and rotated queries of nb tokens).
+void launch_prep(const GemvArgs &kb, const AttnArgs &aa, hipStream_t st, int nb) {
+    launch_query_lu<16, 1>(kb, aa, dim3(1, (unsigned)nb), st);
 }
 
 int launch_query(const GemvArgs &kb, const AttnArgs &aa, hipStream_t st, int nb) {
@@ -344,6 +350,36 @@ void launch_attn_cache_batch(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) 
     hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64, (unsigned)n), dim3(DM_BLOCK), 0, st, aa);
 }
 
+// Whether k_attn_tile takes this model's attention: 16-column groups of the entry and of
+// each part, and an entry that the staging holds.
+bool attn_tile_ok(const gmoe_model_config &c) {
+    return c.kv_lora_rank % 64 == 0 && c.rope_dim % 16 == 0 && c.kv_lora_rank + c.rope_dim <= AQ_KQ_MAX;
+}
+
+// The attention of n tokens at positions aa.pos .. (their cache entries already written) by
+// query tiles: chunks of positions sized so that a token has at most AT_PREFILL_RANGES of
+// them (its partial-result slots), then k_attn_merge over each token's chunks.
+void launch_attn_tile(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) {
+    (void)m;
+    const int P = aa.pos + n;  // positions any token of the batch attends
+    const int per = (P + AT_PREFILL_RANGES - 1) / AT_PREFILL_RANGES;
+    AttnTileArgs g;
+    g.n = n;
+    g.chunk = std::max(AQ_P, (per + AQ_P - 1) / AQ_P * AQ_P);
+    aa.nblk = (P + g.chunk - 1) / g.chunk;
+    g.a = aa;
+    const dim3 grid((unsigned)aa.nblk, (unsigned)((n + AQ_T - 1) / AQ_T), (unsigned)aa.H);
+    switch (aq_rounds(aa.kv + aa.rope)) {
+    case 1: hipLaunchKernelGGL(k_attn_tile<1>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+    case 2: hipLaunchKernelGGL(k_attn_tile<2>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+    case 3: hipLaunchKernelGGL(k_attn_tile<3>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+    case 4: hipLaunchKernelGGL(k_attn_tile<4>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+    default: hipLaunchKernelGGL(k_attn_tile<5>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+    }
+    hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64, (unsigned)n), dim3(DM_BLOCK), 0, st, aa);
+}
+static_assert(aq_rounds(AQ_KQ_MAX) <= 5, "k_attn_tile instances cover the widest entry");
+
 int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
     const gmoe_model_config &c = m->c;
     const AttnDev &A = m->attn[l];
@@ -470,8 +506,20 @@ int attention_batch(gmoe_model *m, int l, int pos0, int n, hipStream_t st) {
     GemvArgs kb = batched(gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs), H * hk, H * kv);
     kb.x_rows = kv;
     kb.x_stride = hk;
-    launch_query(kb, aa, st, n);  // every token's cache entry before any token's attention
-    launch_attn_cache_batch(m, aa, n, st);
+    if (gemm_batch(m, n)) {
+        // the absorbed queries as one GEMM (group h: k_b_h . q_nope_h), then the cache entries
+        // and rotated queries (k_attn_query's last block alone)
+        gemm_inputs(m, m->q_full, H * hk, H * hk, nullptr, n, st);
+        gemm_launch(m, A.k_b_q, A.k_b_s, nullptr, nullptr, H * kv, c.qk_nope_dim, kv, hk, H * hk, m->q_abs, H * kv,
+                    nullptr, 0, QG_PLAIN, n, st);
+        launch_prep(kb, aa, st, n);
+    } else {
+        launch_query(kb, aa, st, n);  // every token's cache entry before any token's attention
+    }
+    if (attn_tile_ok(c))
+        launch_attn_tile(m, aa, n, st);
+    else
+        launch_attn_cache_batch(m, aa, n, st);
     if (gemm_batch(m, n)) {
         // per head: concat_h = v_b_h . ctx_h, then x += attn_out . concat
         gemm_inputs(m, m->ctx, H * kv, H * kv, nullptr, n, st);
@@ -545,7 +593,7 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
     if (B >= QG_GEMM_MIN_TOKENS) {
         size_t w = (size_t)c.dim;
         if (c.has_l0_ffn) w = std::max(w, (size_t)c.hidden_dim);
-        if (A > 0) w = std::max({w, (size_t)c.q_lora_rank, H * kv, H * (size_t)c.v_head_dim});
+        if (A > 0) w = std::max({w, (size_t)c.q_lora_rank, H * kv, H * (size_t)c.v_head_dim, H * (size_t)c.head_k_dim});
         rc |= mdalloc(m, &m->xs, B * 2 * w);
         rc |= mdalloc(m, &m->xe, B);
         rc |= mdalloc(m, &m->zeros, 64);
