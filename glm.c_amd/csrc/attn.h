@@ -16,11 +16,12 @@
 #include "common.h"
 #include "dense.h"
 
-#define AQ_T 32        // query tokens per block (one head): two 16-row MFMA tiles
+#define AQ_T 64        // query tokens per block (one head): four 16-row MFMA tiles
 #define AQ_P 16        // cache positions per staged tile
-#define AQ_BLOCK 512   // eight waves
+#define AQ_BLOCK 1024  // sixteen waves, four per SIMD
 #define AQ_KQ_MAX 576  // widest staged entry (kv + rope)
 #define AQ_STAGES 3    // staged tiles: two in flight while one is used
+#define AQ_SLOTS (AQ_P * (AQ_KQ_MAX / 4 + 1) + 64)  // 16-byte slots of a stage (one wave's DMA past the rows)
 
 typedef float aq_f4 __attribute__((ext_vector_type(4)));
 
@@ -30,10 +31,10 @@ struct AttnTileArgs {
     int chunk;   // positions per chunk
 };
 
-// 16-byte DMA rounds (512 slots each) of a staged tile: AQ_P rows of kq/4 + 1 slots (one
-// slot of padding makes the row stride odd in 16-byte units, so the rows' reads spread
-// over the banks).
-__host__ __device__ constexpr int aq_rounds(int kq) { return (AQ_P * (kq / 4 + 1) + 511) / 512; }
+// 16-byte DMA rounds (AQ_BLOCK slots each) of a staged tile: AQ_P rows of kq/4 + 1 slots
+// (one slot of padding makes the row stride odd in 16-byte units, so the rows' reads
+// spread over the banks).
+__host__ __device__ constexpr int aq_rounds(int kq) { return (AQ_P * (kq / 4 + 1) + AQ_BLOCK - 1) / AQ_BLOCK; }
 
 __device__ static inline aq_f4 aq_mfma(float a, float b, aq_f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -41,17 +42,18 @@ __device__ static inline aq_f4 aq_mfma(float a, float b, aq_f4 c) {
 
 // Block (chunk c, query tile, head h): tokens t0 .. t0 + AQ_T of the batch (at positions
 // pos + t) against positions [c chunk, (c + 1) chunk) that any of them attends. Waves:
-// the scores of a 16-position tile are split by 16-row half (w / 4) and by quarter of the
-// entry's 16-column groups (w % 4), the four quarters summed in shared memory; the
-// weighted sum's 16x16 output blocks (two row halves x kv / 16 column blocks) go round
-// robin over the eight waves. Staging: every thread issues NR 16-byte DMAs per tile, not
-// tracked by the compiler, so each wait is an exact count: the tile before the last is
-// waited for with one tile (NR per thread) still in flight.
+// the scores of a 16-position tile are split by 16-row quarter (w / 4) and by quarter of
+// the entry's 16-column groups (w % 4), the four column quarters summed in shared memory;
+// the weighted sum's 16x16 output blocks (four row quarters x kv / 16 column blocks) go
+// round robin over the sixteen waves. Staging: a tile is NR rounds of 16-byte DMAs (a
+// wave whose slots of the last round lie past the tile's skips it), not tracked by the
+// compiler, so each wait is an exact count per wave: the tile before the last is waited
+// for with one tile's DMAs still in flight.
 template <int NR>
 __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile(AttnTileArgs g) {
-    __shared__ __align__(16) float ks[AQ_STAGES][NR * 512 * 4];
-    __shared__ __align__(16) float sp[4][AQ_T][AQ_P];     // the quarters' partial scores
-    __shared__ __align__(16) float ps[AQ_T][AQ_P + 4];    // exponentials (rows padded: 5 slots)
+    __shared__ __align__(16) float ks[AQ_STAGES][AQ_SLOTS * 4];
+    __shared__ __align__(16) float sp[4][AQ_T][AQ_P + 4];  // the column quarters' partial scores
+    __shared__ __align__(16) float ps[AQ_T][AQ_P + 4];     // exponentials (rows padded: 5 slots)
     __shared__ float run_m[AQ_T], run_l[AQ_T], corr[AQ_T];
     const AttnArgs &a = g.a;
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
@@ -73,36 +75,35 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile(AttnTileArgs g) {
         return;
     }
     const int ksd4 = KQ / 4 + 1;  // 16-byte slots per staged row
+    const int nslot = AQ_P * ksd4;
     const int ntile = (r1 - r0 + AQ_P - 1) / AQ_P;
+    const bool last_round = AQ_BLOCK * (NR - 1) + 64 * w < nslot;  // the wave takes part in round NR - 1
 
-    // the thread's DMA slots: round r writes slot 512 r + 64 w + lane = (row, 16-byte column)
-    const float *src_base[NR];
-    int src_stride[NR], src_row[NR];
+    // the thread's DMA slots: round r writes slot AQ_BLOCK r + 64 w + lane = (row n, 16-byte
+    // column d / 4), packed as n << 20 | (d in the rope part) << 19 | the part's column
+    unsigned src[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
-        const int sl = 512 * r + 64 * w + lane, n = sl / ksd4, d = 4 * (sl % ksd4);
-        src_row[r] = n < AQ_P ? n : 0;  // slots past the tile's rows load row 0 into the tail
-        if (d < kv) {
-            src_base[r] = a.comp + d;
-            src_stride[r] = kv;
-        } else if (d < KQ) {
-            src_base[r] = a.pe + (d - kv);
-            src_stride[r] = rope;
-        } else {  // the padding slot
-            src_base[r] = a.comp;
-            src_stride[r] = kv;
-        }
+        const int sl = AQ_BLOCK * r + 64 * w + lane, n = sl / ksd4, d = 4 * (sl % ksd4);
+        const unsigned row = n < AQ_P ? n : 0;  // slots past the tile's rows load row 0 into the tail
+        src[r] = d < kv ? row << 20 | (unsigned)d : d < KQ ? row << 20 | 1u << 19 | (unsigned)(d - kv) : row << 20;
     }
     auto issue = [&](int stage, int s0) {
 #pragma unroll
         for (int r = 0; r < NR; r++) {
-            const int s = min(s0 + src_row[r], r1 - 1);  // positions past the chunk: any entry (masked)
-            dma16_untracked(gbl((const void *)(src_base[r] + (size_t)s * src_stride[r])),
-                            (lds_void *)&ks[stage][4 * (512 * r + 64 * w)]);
+            if (r + 1 < NR || last_round) {
+                // (opaque here, so that the addresses are formed per request rather than
+                // hoisted out of the tile loop as 64-bit values that do not fit the registers)
+                asm volatile("" : "+v"(src[r]));
+                const int s = min(s0 + (int)(src[r] >> 20), r1 - 1);  // positions past the chunk: any entry (masked)
+                const bool pe = (src[r] >> 19) & 1;
+                const float *p = (pe ? a.pe + (size_t)s * rope : a.comp + (size_t)s * kv) + (src[r] & 0x7ffffu);
+                dma16_untracked(gbl((const void *)p), (lds_void *)&ks[stage][4 * (AQ_BLOCK * r + 64 * w)]);
+            }
         }
     };
 
-    // the lane's query values for the scores: row 16 rb + l16, the quarter's column groups
+    // the lane's query values for the scores: row 16 rb + l16, the column quarter's groups
     const int rb = w >> 2, q = w & 3, nu = KQ / 16;
     const int tq = min(t0 + 16 * rb + l16, g.n - 1);  // rows past the batch: any token (masked)
     constexpr int NQ = (AQ_KQ_MAX / 16 + 3) / 4;
@@ -127,7 +128,6 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile(AttnTileArgs g) {
     issue(0, r0);
     if (ntile > 1) issue(1, r0 + AQ_P);
 
-    const int nbo = 2 * (kv / 16);  // 16x16 output blocks of the weighted sum
     aq_f4 acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = (aq_f4){0.0f, 0.0f, 0.0f, 0.0f};
@@ -135,10 +135,14 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile(AttnTileArgs g) {
     for (int j = 0; j < ntile; j++) {
         const int s0 = r0 + AQ_P * j;
         const float *kt = ks[j % AQ_STAGES];
-        if (j + 1 < ntile)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NR) : "memory");
-        else
+        if (j + 1 < ntile) {
+            if (last_round)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NR) : "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NR - 1) : "memory");
+        } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
         // tile j is in shared memory (every wave's part), and every wave is done with tile
         // j - 1, whose stage the request below refills
         __syncthreads();
@@ -181,32 +185,36 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile(AttnTileArgs g) {
             }
         }
         __syncthreads();
-        // weighted sum: block b = (row half b % 2, columns 16 (b / 2) ..); MFMA k index (lane
-        // group lg) = position 4 lg + e of the tile
+        // weighted sum: the wave's blocks are row quarter w % 4 and column blocks w / 4 + 4 i
+        // (16 columns each); MFMA k index (lane group lg) = position 4 lg + e of the tile
+        {
+            const int rh = w & 3;
+            aq_f4 cr;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int b = w + 8 * i;
-            if (b < nbo) {
-                const int rh = b & 1, cb = b >> 1;
+            for (int r = 0; r < 4; r++) cr[r] = corr[16 * rh + 4 * lg + r];
+            const aq_f4 pa = *(const aq_f4 *)&ps[16 * rh + l16][4 * lg];
+            const float *vr = kt + 4 * ksd4 * (4 * lg) + 16 * (w >> 2) + l16;
 #pragma unroll
-                for (int r = 0; r < 4; r++) acc[i][r] = __fmul_rn(acc[i][r], corr[16 * rh + 4 * lg + r]);
-                const aq_f4 pa = *(const aq_f4 *)&ps[16 * rh + l16][4 * lg];
-                const float *vr = kt + 4 * ksd4 * (4 * lg) + 16 * cb + l16;
-                acc[i] = aq_mfma(pa.x, vr[0], acc[i]);
-                acc[i] = aq_mfma(pa.y, vr[4 * ksd4], acc[i]);
-                acc[i] = aq_mfma(pa.z, vr[8 * ksd4], acc[i]);
-                acc[i] = aq_mfma(pa.w, vr[12 * ksd4], acc[i]);
+            for (int i = 0; i < 8; i++) {
+                if ((w >> 2) + 4 * i < kv / 16) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[i][r] = __fmul_rn(acc[i][r], cr[r]);
+                    const float *v = vr + 64 * i;
+                    acc[i] = aq_mfma(pa.x, v[0], acc[i]);
+                    acc[i] = aq_mfma(pa.y, v[4 * ksd4], acc[i]);
+                    acc[i] = aq_mfma(pa.z, v[8 * ksd4], acc[i]);
+                    acc[i] = aq_mfma(pa.w, v[12 * ksd4], acc[i]);
+                }
             }
         }
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const int b = w + 8 * i;
-        if (b < nbo) {
-            const int rh = b & 1, cb = b >> 1;
+        const int cb = (w >> 2) + 4 * i;
+        if (cb < kv / 16) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int t = t0 + 16 * rh + 4 * lg + r;
+                const int t = t0 + 16 * (w & 3) + 4 * lg + r;
                 if (t < tl) a.part_ctx[slot(t) * kv + 16 * cb + l16] = acc[i][r];
             }
         }

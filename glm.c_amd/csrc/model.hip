@@ -372,13 +372,11 @@ void launch_attn_tile(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) {
     switch (aq_rounds(aa.kv + aa.rope)) {
     case 1: hipLaunchKernelGGL(k_attn_tile<1>, grid, dim3(AQ_BLOCK), 0, st, g); break;
     case 2: hipLaunchKernelGGL(k_attn_tile<2>, grid, dim3(AQ_BLOCK), 0, st, g); break;
-    case 3: hipLaunchKernelGGL(k_attn_tile<3>, grid, dim3(AQ_BLOCK), 0, st, g); break;
-    case 4: hipLaunchKernelGGL(k_attn_tile<4>, grid, dim3(AQ_BLOCK), 0, st, g); break;
-    default: hipLaunchKernelGGL(k_attn_tile<5>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+    default: hipLaunchKernelGGL(k_attn_tile<3>, grid, dim3(AQ_BLOCK), 0, st, g); break;
     }
     hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64, (unsigned)n), dim3(DM_BLOCK), 0, st, aa);
 }
-static_assert(aq_rounds(AQ_KQ_MAX) <= 5, "k_attn_tile instances cover the widest entry");
+static_assert(aq_rounds(AQ_KQ_MAX) <= 3, "k_attn_tile instances cover the widest entry");
 
 int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
     const gmoe_model_config &c = m->c;
