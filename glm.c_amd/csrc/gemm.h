@@ -1,12 +1,12 @@
 // gemm.h -- the dense Q8_0 products of a prefill batch (matvec_q80_rows, infer.c:765-786,
 // for every token of the batch) as MFMA GEMMs: each weight panel is read once per tile of
-// up to 64 tokens instead of once per token.
+// up to QG_TT tokens instead of once per token.
 //
 //   k_norm_split  each token's input row, normalised as glm.c normalises it when the
 //                 product takes rmsnorm(x) * w (infer.c:746-752), in the split form of the
 //                 grouped expert GEMMs (grouped.h): fp16 hi and lo with one exponent per row;
 //   k_gemm_q8     y[t][r] = sum_g s[r][g] * (q[r][g] . x_t[g]) for a tile of 64 rows of the
-//                 matrix (four waves of 16) and up to 64 tokens, with epilogues for glm.c's
+//                 matrix (four waves of 16) and up to QG_TT tokens, with epilogues for glm.c's
 //                 SwiGLU pair (infer.c:1078-1080) and residual add (infer.c:1061, 1083).
 //
 // Weights stay in glm.c's row-major Q8_0 form with fp32 scales, which the decode products
@@ -29,7 +29,8 @@
 #include "common.h"
 
 #define QG_BLOCK 256
-#define QG_TT 64                // tokens per tile (four A tiles of 16)
+#define QG_TT 32                // tokens per tile (two A tiles of 16): twice the blocks of 64-token
+                                // tiles, which leave most CUs idle at a 512-token batch's small matrices
 #define QG_KC 64                // columns per staged chunk
 #define QG_RB (QG_KC * 2)       // bytes of one staged row (one plane of one token)
 #define QG_RG (QG_RB / 16)      // 16-byte groups per staged row
@@ -356,6 +357,6 @@ __global__ __launch_bounds__(QG_BLOCK) void k_gemm_q8(QgArgs a) {
     const int panel = (k / a.tiles) * QG_XCD + xcd, tt = k % a.tiles;
     if (panel >= a.bpg * a.groups) return;
     const int left = a.n - QG_TT * tt;
-    const int na = __builtin_amdgcn_readfirstlane(left >= QG_TT ? 4 : (left + 15) >> 4);
-    qg_with_na<4>(na, [&](auto NA) { qg_tile<decltype(NA)::value, KB, MODE, NM>(a, panel, tt, buf); });
+    const int na = __builtin_amdgcn_readfirstlane(left >= QG_TT ? QG_TT / 16 : (left + 15) >> 4);
+    qg_with_na<QG_TT / 16>(na, [&](auto NA) { qg_tile<decltype(NA)::value, KB, MODE, NM>(a, panel, tt, buf); });
 }

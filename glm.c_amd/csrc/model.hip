@@ -425,7 +425,7 @@ int dense_ffn(gmoe_model *m, hipStream_t st) {
 // (token t reads positions up to pos0 + t only), then the attention over the cache runs
 // per token, since its length differs.
 // Whether a batch of n tokens takes the GEMMs of gemm.h for its dense products (a weight
-// panel read once per 64 tokens) rather than k_gemv per token: a batch of a few tokens
+// panel read once per QG_TT tokens) rather than k_gemv per token: a batch of a few tokens
 // gains nothing from tiles. Group sizes 16 (glm.c's exporter) and 32 take it.
 bool gemm_batch(const gmoe_model *m, int n) {
     const int gs = m->c.group_size;
