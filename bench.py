@@ -41,6 +41,7 @@ for _p in (os.path.join(ROOT, "glm.c_amd"), os.path.join(ROOT, "oracle")):
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 N_MOE_LAYERS = 46
+PREFILL_BATCH = 1024  # prompt tokens per batched prefill step of the end-to-end run
 METRIC = "MoE-stack decode tokens/s (46 GLM-4.7-Flash MoE layers, Q8_0, T=1)"
 
 
@@ -317,6 +318,8 @@ def main():
     ap.add_argument("--e2e", action="store_true",
                     help="only the whole-model decode (a --context-token prompt by batched prefill, then --new tokens)")
     ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--prefill-batch", type=int, default=PREFILL_BATCH,
+                    help="with --e2e: prompt tokens per batched prefill step (the MoE context's max_tokens)")
     ap.add_argument("--new", type=int, default=128)
     ap.add_argument("--e2e-cpu", action="store_true",
                     help="with --e2e: also time glm.c's CPU forward at the same position (writes a ~33 GB checkpoint "
@@ -352,7 +355,7 @@ def main():
     if gmoe.device_count() < 1:
         raise SystemExit("no HIP device visible")
     extras = not args.no_extras
-    max_tokens = 512 if extras else 1
+    max_tokens = PREFILL_BATCH if extras else 1
 
     t0 = time.perf_counter()
     ctx = gmoe.Context(shape, n_layers=L + 1, max_tokens=max_tokens, device=0)
@@ -589,7 +592,7 @@ def e2e_only(args, gmoe, np):
     """--e2e: the whole-model decode alone, on 46 freshly uploaded MoE layers."""
     shape = gmoe.GLM47_FLASH
     t0 = time.perf_counter()
-    ctx = gmoe.Context(shape, n_layers=N_MOE_LAYERS + 1, max_tokens=512, device=0)
+    ctx = gmoe.Context(shape, n_layers=N_MOE_LAYERS + 1, max_tokens=args.prefill_batch, device=0)
     for layer in range(1, N_MOE_LAYERS + 1):
         ctx.upload(layer, gmoe.HostLayer(shape, seed=0, layer=layer))
     log(f"generated and uploaded {N_MOE_LAYERS} layers in {time.perf_counter() - t0:.1f}s")

@@ -357,18 +357,22 @@ bool attn_tile_ok(const gmoe_model_config &c) {
 }
 
 // The attention of n tokens at positions aa.pos .. (their cache entries already written) by
-// query tiles: chunks of positions sized so that a token has at most AT_PREFILL_RANGES of
-// them (its partial-result slots), then k_attn_merge over each token's chunks.
+// query tiles: each token's positions in as few chunks (at most its AT_PREFILL_RANGES
+// partial-result slots) as keep the CUs busy, since every chunk's partial results are
+// written and merged; then k_attn_merge over each token's chunks.
 void launch_attn_tile(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) {
-    (void)m;
     const int P = aa.pos + n;  // positions any token of the batch attends
-    const int per = (P + AT_PREFILL_RANGES - 1) / AT_PREFILL_RANGES;
+    // chunks per token: about AQ_BLOCKS_PER_CU blocks per CU over the tiles and heads
+    const int tiles = (n + AQ_T - 1) / AQ_T;
+    const int want = (AQ_BLOCKS_PER_CU * m->n_cu + tiles * aa.H - 1) / (tiles * aa.H);
+    const int nch = std::min(AT_PREFILL_RANGES, std::max(1, want));
+    const int per = (P + nch - 1) / nch;
     AttnTileArgs g;
     g.n = n;
     g.chunk = std::max(AQ_P, (per + AQ_P - 1) / AQ_P * AQ_P);
     aa.nblk = (P + g.chunk - 1) / g.chunk;
     g.a = aa;
-    const dim3 grid((unsigned)aa.nblk, (unsigned)((n + AQ_T - 1) / AQ_T), (unsigned)aa.H);
+    const dim3 grid((unsigned)aa.nblk, (unsigned)tiles, (unsigned)aa.H);
     switch (aq_rounds(aa.kv + aa.rope)) {
     case 1: hipLaunchKernelGGL(k_attn_tile<1>, grid, dim3(AQ_BLOCK), 0, st, g); break;
     case 2: hipLaunchKernelGGL(k_attn_tile<2>, grid, dim3(AQ_BLOCK), 0, st, g); break;

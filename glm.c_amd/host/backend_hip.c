@@ -15,7 +15,7 @@
  *   GLM_HIP_HOST_ATTN       keep embedding, attention, layer 0 and the LM head on the host
  *                           (glm.c's own arithmetic, forward.c) instead of the GPU model
  *   GLM_HIP_PREFILL_BATCH   most prompt tokens of one batched prefill step (glm_hip_prefill;
- *                           default 512, 1 turns batching off)
+ *                           default 1024, 1 turns batching off)
  *   GLM_HIP_STRICT          exit(1) when a GPU layer fails instead of returning -1
  *   GLM_DISABLE_MOE_ROUTED  skip routed experts, as infer.c:1161-1166 does
  */
@@ -77,7 +77,7 @@ int glm_hip_init(const Runtime *rt, RunState *st) {
     cfg.n_layers = c->n_layers;
     /* the decode loop feeds one token at a time, glm_hip_prefill up to a batch of prompt tokens */
     const char *pb = getenv("GLM_HIP_PREFILL_BATCH");
-    cfg.max_tokens = pb && atoi(pb) > 0 ? atoi(pb) : 512;
+    cfg.max_tokens = pb && atoi(pb) > 0 ? atoi(pb) : 1024;
     cfg.routed_scale = 1.8f; /* infer.c:1171 */
     cfg.norm_eps = 1e-5f;    /* infer.c:750 */
     cfg.q8_form = GMOE_Q8_AUTO; /* tiled at group size 32, glm.c's own layout otherwise */

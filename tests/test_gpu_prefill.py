@@ -8,7 +8,7 @@ The last token's logits and final x are held to the FFN bar (max-abs 1e-2, rel-L
 against glm.c's at that position, with the same argmax. The decode that follows, one token
 at a time on the cache the prefill wrote, must match glm.c's logits at every later
 position, which checks every cache entry the prefill wrote (every attention layer reads all
-of them). Batches of 1, 4 and the default 512 take the prompt whole, in ragged pieces
+of them). Batches of 1, 4 and 512 take the prompt whole, in ragged pieces
 and one token at a time; a 150-token prompt in 64-token batches crosses attention's
 32-position chunks inside a batch, and a 400-token prompt gives ranges of several tiles."""
 import ctypes as C
