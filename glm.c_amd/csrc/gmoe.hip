@@ -16,6 +16,7 @@
 // into the tiled Q8_0 layout of common.h and stay resident.
 #include "gmoe.h"
 
+#include <gnu/libc-version.h>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -168,6 +169,7 @@ struct gmoe_ctx {
 
     long long tokens_routed = 0;
     long long scale_inexact = 0;
+    int expf_libc_match = 0;  // the running glibc is GM_EXPF_LIBC (expf_exact.h's table)
     int last_layer = -1, last_T = 0, last_flags = 0, last_dispatched = 0, stack_launched = 0;
     int stack_last = 0;  // the most recent forward was a persistent launch
     int *stack_error_dev = nullptr;  // the device error word that launch used
@@ -295,6 +297,14 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
 
     gmoe_ctx *c = new gmoe_ctx();
     c->device = device;
+    // the exact router replay reproduces the expf of the glibc its exception table was
+    // measured against (expf_exact.h); glm.c on this host calls this process's glibc
+    c->expf_libc_match = strcmp(gnu_get_libc_version(), GM_EXPF_LIBC) == 0;
+    if (!c->expf_libc_match)
+        fprintf(stderr,
+                "[gmoe] warning: the GPU's expf table was measured against glibc %s but this process runs glibc %s; "
+                "an exact router replay may order near-tied experts unlike this host's libm\n",
+                GM_EXPF_LIBC, gnu_get_libc_version());
     c->cfg = g;
     c->D = g.dim;
     c->F = g.moe_ffn_dim;
@@ -1393,6 +1403,7 @@ extern "C" int gmoe_get_stats(gmoe_ctx *c, gmoe_stats *o) {
     o->routing_exact_path = (int64_t)s[GM_STAT_ROUTE_EXACT];
     o->norm_exact_path = (int64_t)s[GM_STAT_NORM_EXACT];
     o->scale_inexact = c->scale_inexact;
+    o->expf_libc_match = c->expf_libc_match;
     return GMOE_OK;
 }
 

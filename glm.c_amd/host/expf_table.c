@@ -25,10 +25,14 @@
  *   expf_table sweep OUT.bin     measure the table with this host's libm
  *   expf_table inc IN.bin OUT    write it as C initialisers for the device code
  *
- * Table file (little-endian): "GMEXPF01", u32 n, u32 near_log2 (the lookup
- * threshold, as -log2 of fp32 ulps), u32 keys[n] (fp32 bit patterns of x, ascending),
+ * Table file (little-endian): "GMEXPF02", u32 n, u32 near_log2 (the lookup
+ * threshold, as -log2 of fp32 ulps), char libc[16] (gnu_get_libc_version() of the
+ * measuring host, NUL-padded), u32 keys[n] (fp32 bit patterns of x, ascending),
  * u32 up[(n + 31) / 32] (bit i of word i / 32: entry i rounds to the float above).
+ * The generated initialisers carry the version as GM_EXPF_LIBC, which gmoe_create
+ * compares with the running process's C library.
  */
+#include <gnu/libc-version.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -38,6 +42,7 @@
 #define NEAR_LOG2 7          /* the GPU looks up x when exp(x) is within 2^-7 ulp of a midpoint */
 #define HARD_LOG2 20         /* kind (2): within 2^-20 ulp */
 #define MISROUND_MAX_LOG2 9  /* kind (1) must lie within 2^-9 ulp, well inside the lookup zone */
+#define LIBC_LEN 16          /* bytes of the libc version field */
 
 static float u2f(uint32_t u) {
     float f;
@@ -142,9 +147,12 @@ static int sweep(const char *out_path) {
         return 1;
     }
     const uint32_t n32 = (uint32_t)n, near = NEAR_LOG2;
-    fwrite("GMEXPF01", 1, 8, f);
+    char libc[LIBC_LEN] = {0};
+    strncpy(libc, gnu_get_libc_version(), LIBC_LEN - 1);
+    fwrite("GMEXPF02", 1, 8, f);
     fwrite(&n32, 4, 1, f);
     fwrite(&near, 4, 1, f);
+    fwrite(libc, 1, LIBC_LEN, f);
     for (int i = 0; i < NCH; i++) fwrite(ch[i].keys, 4, ch[i].n, f);
     const size_t nw = (n + 31) / 32;
     uint32_t *bits = calloc(nw ? nw : 1, 4);
@@ -171,13 +179,18 @@ static int to_inc(const char *in_path, const char *out_path) {
         perror(in_path);
         return 1;
     }
-    char magic[8];
+    char magic[8], libc[LIBC_LEN];
     uint32_t n, near;
-    if (fread(magic, 1, 8, f) != 8 || memcmp(magic, "GMEXPF01", 8) != 0 || fread(&n, 4, 1, f) != 1 ||
-        fread(&near, 4, 1, f) != 1) {
+    if (fread(magic, 1, 8, f) != 8 || memcmp(magic, "GMEXPF02", 8) != 0 || fread(&n, 4, 1, f) != 1 ||
+        fread(&near, 4, 1, f) != 1 || fread(libc, 1, LIBC_LEN, f) != LIBC_LEN || libc[LIBC_LEN - 1] != 0) {
         fprintf(stderr, "%s: not an expf table\n", in_path);
         return 1;
     }
+    for (const char *c = libc; *c; c++)
+        if (!((*c >= '0' && *c <= '9') || *c == '.')) {
+            fprintf(stderr, "%s: bad libc version field\n", in_path);
+            return 1;
+        }
     const size_t nw = (n + 31) / 32;
     uint32_t *keys = malloc((size_t)n * 4 + 4), *bits = malloc(nw * 4 + 4);
     if (fread(keys, 4, n, f) != n || fread(bits, 4, nw, f) != nw) {
@@ -196,7 +209,7 @@ static int to_inc(const char *in_path, const char *out_path) {
         return 1;
     }
     fprintf(o, "// generated from %s by expf_table inc; do not edit\n", in_path);
-    fprintf(o, "#define GM_EXPF_N %uu\n#define GM_EXPF_NEAR_LOG2 %u\n", n, near);
+    fprintf(o, "#define GM_EXPF_N %uu\n#define GM_EXPF_NEAR_LOG2 %u\n#define GM_EXPF_LIBC \"%s\"\n", n, near, libc);
     fprintf(o, "__device__ const unsigned gm_expf_keys[GM_EXPF_N] = {");
     for (uint32_t i = 0; i < n; i++) fprintf(o, "%s0x%08x", sep(i, 8), keys[i]);
     fprintf(o, "};\n__device__ const unsigned gm_expf_up[%zu] = {", nw);

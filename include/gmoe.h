@@ -112,6 +112,10 @@ typedef struct gmoe_stats {
     int64_t routing_exact_path;  /* routings that needed the exact sequential-fp32 router replay */
     int64_t norm_exact_path;     /* rmsnorms that needed the exact sequential-fp64 sum replay */
     int64_t scale_inexact;       /* weight scales that were not fp16-exact at upload */
+    int64_t expf_libc_match;     /* 1: this process runs the glibc release that the GPU's expf exception
+                                    table was measured against, so an exact router replay reproduces
+                                    its expf bit for bit; 0: near-tied experts may be ordered otherwise
+                                    (gmoe_create warns on stderr) */
 } gmoe_stats;
 
 /* Create a context on HIP device `device` and reserve device memory for

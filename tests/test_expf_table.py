@@ -21,19 +21,29 @@ TOOL = os.path.join(PKG, "_build", "expf_table")
 
 def read_table(path):
     raw = open(path, "rb").read()
-    assert raw[:8] == b"GMEXPF01"
+    assert raw[:8] == b"GMEXPF02"
     n, near = struct.unpack_from("<II", raw, 8)
-    keys = np.frombuffer(raw, "<u4", n, 16)
+    libc = raw[16:32].rstrip(b"\0").decode()
+    keys = np.frombuffer(raw, "<u4", n, 32)
     nw = (n + 31) // 32
-    bits = np.frombuffer(raw, "<u4", nw, 16 + 4 * n)
-    assert len(raw) == 16 + 4 * n + 4 * nw
+    bits = np.frombuffer(raw, "<u4", nw, 32 + 4 * n)
+    assert len(raw) == 32 + 4 * n + 4 * nw
     up = (bits[np.arange(n) // 32] >> (np.arange(n) % 32).astype(np.uint32)) & 1
-    return keys, up.astype(bool), near
+    return keys, up.astype(bool), near, libc
+
+
+def this_libc():
+    import ctypes
+
+    libc = ctypes.CDLL("libc.so.6")
+    libc.gnu_get_libc_version.restype = ctypes.c_char_p
+    return libc.gnu_get_libc_version().decode()
 
 
 def test_table_format_and_premises():
-    keys, up, near = read_table(TABLE)
+    keys, up, near, libc = read_table(TABLE)
     assert near == 7
+    assert libc == this_libc(), "the table records the glibc it was measured against"
     assert keys.size > 100000
     assert np.all(np.diff(keys.astype(np.int64)) > 0), "keys must ascend"
     x = keys.view(np.float32)

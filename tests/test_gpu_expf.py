@@ -47,3 +47,14 @@ def test_exact_expf_equals_libm_on_every_input():
 def test_fast_expf_within_two_ulp_of_libm():
     bad, first_bad = sweep(1, 2)
     assert bad == 0, f"{bad} inputs beyond 2 ulp of libm, the first at bits 0x{first_bad:08x}"
+
+
+def test_context_reports_the_glibc_the_table_was_measured_against():
+    """The exception table records the glibc it was measured against; a context compares it
+    with the running process's glibc and reports the match in its stats (this image's
+    glibc is the one the committed table was measured on)."""
+    ctx = gmoe.Context(gmoe.GLM47_FLASH, n_layers=2, max_tokens=1, device=0)
+    try:
+        assert ctx.stats()["expf_libc_match"] == 1
+    finally:
+        ctx.close()
