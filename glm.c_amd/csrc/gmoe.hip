@@ -1401,6 +1401,7 @@ extern "C" int gmoe_get_stats(gmoe_ctx *c, gmoe_stats *o) {
     HIP_OK(hipMemcpy(s, c->stats_dev, sizeof(s), hipMemcpyDeviceToHost));
     o->tokens_routed = c->tokens_routed;
     o->routing_exact_path = (int64_t)s[GM_STAT_ROUTE_EXACT];
+    o->routing_exact_subset = (int64_t)s[GM_STAT_ROUTE_SUBSET];
     o->norm_exact_path = (int64_t)s[GM_STAT_NORM_EXACT];
     o->scale_inexact = c->scale_inexact;
     o->expf_libc_match = c->expf_libc_match;

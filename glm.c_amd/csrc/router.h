@@ -19,7 +19,7 @@
 #include "common.h"
 #include "expf_exact.h"
 
-enum { GM_STAT_NORM_EXACT = 0, GM_STAT_ROUTE_EXACT = 1, GM_STAT_COUNT = 4 };
+enum { GM_STAT_NORM_EXACT = 0, GM_STAT_ROUTE_EXACT = 1, GM_STAT_ROUTE_SUBSET = 2, GM_STAT_COUNT = 4 };
 
 struct RouterArgs {
     const float *x;            // [T][D]
@@ -107,7 +107,9 @@ __device__ static inline void wave_argmax(double key, int idx, double *bkey, int
 }
 
 #define RT_SEL_C (GM_MAX_E / 64)  // experts per lane in a one-wave selection
-#define RT_XT 128                 // scratch of the exact replay: RT_XT x 64 floats (two 16 KB gate tiles)
+#define RT_BLOCK 256
+#define RT_XT 160                 // scratch of the exact replay: RT_XT x 64 floats (exact_router uses two
+                                  // 16 KB gate tiles; exact_router_subset holds five 2048-column rows at once)
 
 // Certified top-k on one wave, over C chunks of 64 experts whose results are in
 // registers (lane l: experts l + 64c; w0 = fp32 bits of lo | hi << 32, w1 = fp32 bits
@@ -267,6 +269,130 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
     exact_topk(E, K, tid, p, sel, idx, wk_out, stats);
 }
 
+// The exact replay restricted to the experts that can still be chosen: with L the K-th
+// largest lower end of the selection intervals (w0[e] = fp32 bits of lo | hi << 32), at
+// least K experts score at least L, so an expert whose upper end lies below L scores
+// strictly below the K-th best and is never chosen; the others (U, hi >= L: the K
+// best-placed ones and those they overlap) are replayed exactly. Then glm.c's insertion
+// top-k over U's exact scores picks glm.c's experts in glm.c's order, ties to the lower
+// index, and their weights are the exact ones. For |U| <= RT_SUB_MAX the rows of U fit the
+// scratch (RT_XT x 64 floats) in one or two column tiles, every thread forms the products
+// fl(g * xn) in place, and lane u of wave 0 runs expert U[u]'s sequential chain over them:
+// ~2 K dependent adds instead of the full replay's 64 chains fed tile by tile. p keeps
+// the certified probabilities of the experts outside U (they are never chosen). Returns
+// false, before touching any output, when |U| is larger (the caller then runs
+// exact_router); block-uniform.
+#define RT_SUB_MAX 8
+__device__ __attribute__((always_inline)) static bool exact_router_subset(int D, int E, int K, int tid,
+                                                                          const float *gate_inp, const float *bias_p,
+                                                                          const float *xn, float (*prod)[64],
+                                                                          const unsigned long long *w0, float *p, float *sel,
+                                                                          int *idx, float *wk_out, unsigned long long *stats,
+                                                                          int *s_u, int *s_nu) {
+    const int lane = tid & 63, w = tid >> 6;
+    if (w == 0) {
+        const int nch = (E + 63) >> 6;
+        float lo[RT_SEL_C], hi[RT_SEL_C];
+#pragma unroll
+        for (int c = 0; c < RT_SEL_C; c++) {
+            const int e = lane + 64 * c;
+            const bool valid = c < nch && e < E;
+            lo[c] = valid ? __uint_as_float((unsigned)w0[e]) : -INFINITY;
+            hi[c] = valid ? __uint_as_float((unsigned)(w0[e] >> 32)) : -INFINITY;
+            if (lo[c] != lo[c]) lo[c] = -INFINITY;  // never certified, so never the bound
+            if (hi[c] != hi[c]) hi[c] = INFINITY;
+        }
+        // L: the K-th largest lower end (K rounds of a wave maximum, one entry removed each)
+        float rem[RT_SEL_C], L = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < RT_SEL_C; c++) rem[c] = lo[c];
+        for (int k = 0; k < K; k++) {
+            float bm = rem[0];
+#pragma unroll
+            for (int c = 1; c < RT_SEL_C; c++) bm = fmaxf(bm, rem[c]);
+            L = wave_max_dpp_f(bm);
+            int ls = -1, cs = 0;
+#pragma unroll
+            for (int c = 0; c < RT_SEL_C; c++) {
+                const unsigned long long m = __ballot(rem[c] == L);
+                if (ls < 0 && m != 0ull) {
+                    ls = __ffsll(m) - 1;
+                    cs = c;
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < RT_SEL_C; c++)
+                if (lane == ls && c == cs) rem[c] = -INFINITY;
+        }
+        // U in ascending expert order
+        int nu = 0;
+#pragma unroll
+        for (int c = 0; c < RT_SEL_C; c++) {
+            const bool in = c < nch && lane + 64 * c < E && hi[c] >= L;
+            const unsigned long long m = __ballot(in);
+            const int pos = nu + __popcll(m & ((1ull << lane) - 1ull));
+            if (in && pos < RT_SUB_MAX) s_u[pos] = lane + 64 * c;
+            nu += __popcll(m);
+        }
+        if (lane == 0) *s_nu = nu;
+    }
+    __syncthreads();
+    const int nu = *s_nu;
+    if (nu > RT_SUB_MAX) return false;
+    if (tid == 0) atomicAdd(&stats[GM_STAT_ROUTE_SUBSET], 1ull);
+    const GM_GLOBAL float *bias = gbl(bias_p);
+    // rows of U in the scratch, tile by tile: [nu][tc] floats, row u's 16-byte group q at
+    // q ^ (u % 8) so that the chain lanes' reads (one group of each row) miss no bank
+    float *buf = &prod[0][0];
+    const int tc_max = nu * D <= RT_XT * 64 ? D : 1024;  // columns per tile (nu rows of them fit the scratch)
+    float chain = 0.0f;
+    for (int c0 = 0; c0 < D; c0 += tc_max) {
+        const int tc = D - c0 < tc_max ? D - c0 : tc_max, ng = tc >> 2;  // D is a multiple of 256
+        for (int s = tid; s < nu * ng; s += RT_BLOCK) {  // slot s: row s / ng, LDS group s % ng
+            const int u = s / ng, q = s % ng, g = q ^ (u & 7);
+            const int ee = s_u[u];
+            dma16_untracked(gbl(gate_inp + (size_t)ee * D + c0 + 4 * g), (lds_void *)(buf + 4 * (s & ~63)));
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int s = tid; s < nu * ng; s += RT_BLOCK) {  // the products in place (infer.c:922), slot by slot
+            const int u = s / ng, g = (s % ng) ^ (u & 7);
+            float4 *pe = (float4 *)(buf + 4 * s);
+            const float4 v = *pe, xv = *(const float4 *)(xn + c0 + 4 * g);
+            *pe = make_float4(__fmul_rn(v.x, xv.x), __fmul_rn(v.y, xv.y), __fmul_rn(v.z, xv.z), __fmul_rn(v.w, xv.w));
+        }
+        __syncthreads();
+        if (w == 0 && lane < nu) {  // infer.c:916-925: the sequential chain of expert U[lane]
+            const float *row = buf + lane * tc;
+            for (int q0 = 0; q0 < ng; q0 += 16) {  // ng is a multiple of 64
+                // sixteen groups' reads at once, so that the LDS latency is paid once per 64 adds
+                float4 v[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) v[j] = *(const float4 *)(row + 4 * ((q0 + j) ^ (lane & 7)));
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    chain = __fadd_rn(chain, v[j].x);
+                    chain = __fadd_rn(chain, v[j].y);
+                    chain = __fadd_rn(chain, v[j].z);
+                    chain = __fadd_rn(chain, v[j].w);
+                }
+            }
+        }
+        __syncthreads();  // the chains are done with the tile before the next one lands
+    }
+    for (int e = tid; e < E; e += RT_BLOCK) sel[e] = -INFINITY;  // outside U: never chosen
+    __syncthreads();
+    if (w == 0 && lane < nu) {
+        const int e = s_u[lane];
+        const float pr = sigmoid_libm(chain);  // infer.c:1105, libm's expf bits
+        p[e] = pr;
+        sel[e] = __fadd_rn(pr, bias[e]);
+    }
+    __syncthreads();
+    exact_topk(E, K, tid, p, sel, idx, wk_out, stats);
+    return true;
+}
+
 // glm.c's insertion top-k (infer.c:1110-1135) on wave 0 of the block, from every expert's
 // probability p and selection score sel (shared memory): the K largest sel by (value desc,
 // index asc) among values above -inf (NaN is never inserted), by K wave-maximum rounds with
@@ -335,7 +461,6 @@ __device__ __attribute__((always_inline)) static void exact_topk(int E, int K, i
     __syncthreads();
 }
 
-#define RT_BLOCK 256
 #define RT_CPL_MAX (GM_MAX_COLS / 64)  // router columns per lane
 
 // grid (T): the router of one token per block. RMSNorm bit-identical to infer.c:746-752
@@ -364,7 +489,7 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
     __shared__ float s_mean, s_total;
     __shared__ unsigned long long s_w0[GM_MAX_E], s_w1[GM_MAX_E];
     __shared__ float s_p[GM_MAX_E], s_sel[GM_MAX_E], s_wk[GM_MAX_K];
-    __shared__ int s_idx[GM_MAX_K], s_ok;
+    __shared__ int s_idx[GM_MAX_K], s_ok, s_u[RT_SUB_MAX], s_nu;
     __shared__ double s_S[GM_MAX_E];
     __shared__ float s_sp[GM_MAX_E], s_sa[GM_MAX_E];
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -487,7 +612,8 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
             s_wk[tid] = wk;
         }
         __syncthreads();
-    } else {
+    } else if (a.force_exact || !exact_router_subset(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_w0, s_p, s_sel,
+                                                     s_idx, s_wk, a.stats, s_u, &s_nu)) {
         exact_router(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_p, s_sel, s_idx, s_wk, a.stats);
     }
     if (tid < K) {
@@ -633,7 +759,7 @@ __global__ __launch_bounds__(RT_BLOCK) void k_rt_select(RouterArgs a, RtParts p)
     __shared__ float s_total;
     __shared__ unsigned long long s_w0[64], s_w1[64];
     __shared__ float s_p[GM_MAX_E], s_sel[GM_MAX_E], s_wk[GM_MAX_K];
-    __shared__ int s_idx[GM_MAX_K], s_ok;
+    __shared__ int s_idx[GM_MAX_K], s_ok, s_u[RT_SUB_MAX], s_nu;
     const int t = blockIdx.x, tid = threadIdx.x;
     const int D = a.D, E = a.E, K = a.K;
     if (tid < E) {
@@ -687,7 +813,9 @@ __global__ __launch_bounds__(RT_BLOCK) void k_rt_select(RouterArgs a, RtParts p)
     } else {
         for (int i = tid; i < D; i += RT_BLOCK) s_xn[i] = a.xn[(size_t)t * D + i];
         __syncthreads();
-        exact_router(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_p, s_sel, s_idx, s_wk, a.stats);
+        if (a.force_exact || !exact_router_subset(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_w0, s_p, s_sel, s_idx,
+                                                  s_wk, a.stats, s_u, &s_nu))
+            exact_router(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_p, s_sel, s_idx, s_wk, a.stats);
     }
     if (tid < K) {
         const size_t o = (size_t)t * K + tid;

@@ -66,7 +66,8 @@ class GmoeKernelTimes(C.Structure):
 
 
 class GmoeStats(C.Structure):
-    _fields_ = [("tokens_routed", C.c_int64), ("routing_exact_path", C.c_int64), ("norm_exact_path", C.c_int64),
+    _fields_ = [("tokens_routed", C.c_int64), ("routing_exact_path", C.c_int64), ("routing_exact_subset", C.c_int64),
+                ("norm_exact_path", C.c_int64),
                 ("scale_inexact", C.c_int64), ("expf_libc_match", C.c_int64)]
 
 

@@ -136,6 +136,39 @@ def test_cancellation_routing_batch(E):
         assert_close(got, want["x_out"], "batch x_out")
         stats = ctx.stats()
         assert stats["routing_exact_path"] >= T  # no certificate may hold at this cancellation
+        # only the K - 1 certainly selected experts and the pair can still be chosen: the
+        # replay runs on those five, not on every expert
+        assert stats["routing_exact_subset"] >= T
+    finally:
+        ctx.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("E", [64, 128])
+def test_all_experts_tied_batch(E):
+    """Every expert's gate row the same and no bias: all E scores tie exactly, so no
+    certificate holds and no expert can be ruled out. The batch router then replays
+    every expert's chain (more than the subset replay holds), and glm.c's insertion
+    top-k breaks the tie by index: experts 0..K-1, in that order."""
+    shape = gmoe.Shape(dim=2048, moe_ffn_dim=256, n_routed_experts=E, n_experts_used=4)
+    T = 8
+    orc = oracle.Oracle("port")
+    L = gmoe.HostLayer(shape, seed=41, layer=1, norm_mode=gmoe.SYNTH_NORM_RANDOM)
+    L.gate_inp[:] = L.gate_inp[0]
+    L.exp_probs_b[:] = 0.0
+    x = gmoe.activations(41, 7, T, shape.D)
+    ctx = gmoe.Context(shape, n_layers=2, max_tokens=T)
+    try:
+        ctx.upload(1, L)
+        print(f"[case] all experts tied E={E} T={T}", flush=True)
+        want = orc.layer(shape, L, x)
+        got, st = gmoe.forward_host(ctx, 1, x)
+        np.testing.assert_array_equal(st["topk_idx"], want["topk_idx"], err_msg="tied routing")
+        assert np.all(st["topk_idx"] == np.arange(shape.K))
+        assert_close(got, want["x_out"], "tied x_out")
+        stats = ctx.stats()
+        assert stats["routing_exact_path"] >= T
+        assert stats["routing_exact_subset"] == 0
     finally:
         ctx.close()
 
