@@ -14,9 +14,10 @@ own infer.c built from source, OpenMP bound to cores as glm.c's Makefile runs it
 weights). Extra keys time the other workloads on the same resident layers: one MoE
 layer per launch (rotating over the 46), prefill batches of T=512 (near-uniform
 routing) and T=128 (Zipf(1.2)-skewed routing) on the grouped expert GEMMs, the
-glm.c drop-in hook (glm_backend_try_hip_moe on a RunState in host memory), and the whole
-GLM-4.7-Flash-shaped model on the GPU: a 4096-token prompt by batched prefill, then 128
-tokens decoded one at a time.
+glm.c drop-in hook (glm_backend_try_hip_moe on a RunState in host memory), the decode step
+and a T=512 prefill layer on layers in glm.c's exported form (group size 16, fp32 scales),
+and the whole GLM-4.7-Flash-shaped model on the GPU: a 4096-token prompt by batched
+prefill, then 128 tokens decoded one at a time.
 """
 import os
 
@@ -220,6 +221,60 @@ def time_prefill(gmoe, np, ctx, shape, layer_ids, T, x, warmup, steps, profile_s
                          "kernels execute 2x those MACs (hi and lo planes) plus tile padding"},
         "kernels": kernels,
     }
+
+
+def gs16_form(gmoe, np, args, L):
+    """glm.c's exported checkpoint form (group size 16, fp32 scales, glm47_flash_export.py:36,
+    157-169) on the fast path: the same 46-layer decode step and a T=512 prefill layer,
+    seeded layers of that form uploaded to a second context (GMOE_Q8_TILED16)."""
+    shape = gmoe.Shape(group_size=16)
+    ctx = gmoe.Context(shape, n_layers=L + 1, max_tokens=512, device=0)
+    try:
+        t0 = time.perf_counter()
+        for layer in range(1, L + 1):
+            ctx.upload(layer, gmoe.HostLayer(shape, seed=0, layer=layer, scale_mode=gmoe.SYNTH_SCALES_FP32))
+        log(f"gs16: generated and uploaded {L} layers in {time.perf_counter() - t0:.1f}s")
+        x0 = gmoe.activations(0, 0, 1, shape.D)
+        d_in = gmoe.DeviceArray.from_numpy(x0)
+        d_out = gmoe.DeviceArray(x0.nbytes)
+        stream = gmoe.Stream()
+
+        def step():
+            ctx.forward_layers(1, L, 1, d_in.ptr, d_out.ptr, stream=stream.h)
+
+        for _ in range(args.warmup):
+            step()
+        stream.sync()
+        t_begin = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        stream.sync()
+        ms = (time.perf_counter() - t_begin) * 1e3 / args.steps
+        stats = ctx.stats()
+        bpt = 0
+        for layer in range(1, L + 1):
+            idx, _ = ctx.read_topk(layer, 1)
+            bpt += (int(np.sum(idx >= 0)) + 1) * shape.expert_bytes()
+        ctx.profile(True)
+        for _ in range(max(1, args.profile_steps // 5)):
+            step()
+        stream.sync()
+        prof = ctx.profile_read()
+        ctx.profile(False)
+        kern = {k: {"launches": n, "avg_us": round(t * 1e3 / n, 3)} for k, (n, t) in prof.items()}
+        gbs = bpt / (ms * 1e-3) / 1e9
+        out = {"workload": "46 GLM-4.7-Flash MoE layers, T=1, group size 16 with fp32 scales (the exporter's form)",
+               "q8_form": "tiled16" if stats["q8_form"] == gmoe.GMOE_Q8_TILED16 else str(stats["q8_form"]),
+               "decode_tokens_s": round(1e3 / ms, 2), "layer_us": round(ms * 1e3 / L, 3),
+               "expert_bytes_per_token": bpt, "hbm_gbps_expert_bytes": round(gbs, 1),
+               "hbm_frac_expert_bytes": round(gbs / HBM_PEAK_GBS, 4), "kernels": kern}
+        NL = min(args.prefill_layers, L)
+        x512 = gmoe.activations(0, 1, 512, shape.D)
+        out["prefill_t512"] = time_prefill(gmoe, np, ctx, shape, list(range(1, NL + 1)), 512, x512,
+                                           max(2, args.warmup), max(10, args.steps), 10)
+        return out
+    finally:
+        ctx.close()
 
 
 def backend_hook_us(gmoe, np, shape, host_layers, x0, tokens=2):
@@ -486,6 +541,9 @@ def main():
         # the glm.c drop-in hook on host memory (uploads its own copy of the layers)
         extra["backend_hook"] = backend_hook_us(gmoe, np, shape, host_layers, x0)
         log(f"backend hook: {extra['backend_hook']['layer_us']} us/layer")
+        extra["gs16"] = gs16_form(gmoe, np, args, L)
+        log(f"gs16: {extra['gs16']['decode_tokens_s']} tok/s decode, "
+            f"{extra['gs16']['prefill_t512']['layer_us']} us/layer prefill T=512")
         if L == N_MOE_LAYERS:
             extra["e2e_decode"] = e2e_decode(gmoe, np, ctx)
             log(f"e2e: {extra['e2e_decode']['decode_tokens_s']} tok/s decode, "

@@ -80,6 +80,20 @@ __host__ __device__ static inline size_t gm_ds_offset(int r, int b, int rows) {
     return (size_t)b * (size_t)rows + (size_t)r;
 }
 
+// Group size 16 with fp32 scales (the exporter's form), q planes as above. Gate/up scales:
+// panel p (16 rows) holds [cols/64 chunks][16 rows][2 groups][2 blocks] fp32, so that a
+// 64-column chunk's 64 scales are one run, row r's four of them contiguous, ordered (first
+// group of block 0, of block 1, second group of block 0, of block 1). Group g of a row is
+// columns 16g..16g+15: chunk g/4, block (g/2)%2, group g%2 of its block.
+__host__ __device__ static inline size_t gm_s16_offset(int r, int g, int cols) {
+    const int p = r >> 4, m = r & 15, c = g >> 2, hb = (g >> 1) & 1, h = g & 1;
+    return (size_t)p * (size_t)cols + (size_t)((((c * 16 + m) * 2 + h) * 2) + hb);
+}
+// Down scales at group size 16: [F/16 slices][D rows] fp32, one scale per slice row.
+__host__ __device__ static inline size_t gm_ds16_offset(int r, int g, int rows) {
+    return (size_t)g * (size_t)rows + (size_t)r;
+}
+
 // Correctly rounded fp32 square root. The fp32 intrinsic lowers to v_sqrt_f32, which is
 // not always correctly rounded; the fp64 lowering is (Newton-refined), and rounding a
 // correctly rounded fp64 root to fp32 is exact-rounding since 53 >= 2*24 + 2.

@@ -47,14 +47,17 @@ static __device__ __align__(256) unsigned char scratch[GMOE_NOALLOC_SCRATCH_BYTE
 static void *g_scratch_dev[GM_MAX_DEVICES];
 static std::mutex g_scratch_mu;
 
-// The k_moe_relay instance of a shape: D == 2048 or narrower; experts per lane in its selection.
+// The k_moe_relay instance of a shape: D == 2048 or narrower; experts per lane in its
+// selection; group size 32 with fp16 scales or 16 with fp32 scales.
 typedef void (*relay_fn)(StackArgs);
-static relay_fn relay_kernel(int D, int E) {
+template <bool G16>
+static relay_fn relay_kernel_g(int D, int E) {
     const bool full = D == GM_MAX_COLS;
-    if (E <= 64) return full ? k_moe_relay<true, 1> : k_moe_relay<false, 1>;
-    if (E <= 128) return full ? k_moe_relay<true, 2> : k_moe_relay<false, 2>;
-    return full ? k_moe_relay<true, 4> : k_moe_relay<false, 4>;
+    if (E <= 64) return full ? k_moe_relay<true, 1, G16> : k_moe_relay<false, 1, G16>;
+    if (E <= 128) return full ? k_moe_relay<true, 2, G16> : k_moe_relay<false, 2, G16>;
+    return full ? k_moe_relay<true, 4, G16> : k_moe_relay<false, 4, G16>;
 }
+static relay_fn relay_kernel(int D, int E, bool g16) { return g16 ? relay_kernel_g<true>(D, E) : relay_kernel_g<false>(D, E); }
 
 // Router blocks of the persistent kernel: the largest power of two <= min(E, 64), so
 // that every block holds at most GM_MAX_E / 64 experts.
@@ -144,6 +147,7 @@ struct gmoe_ctx {
     int coop = 0;                // the persistent kernels go out as cooperative launches (GMOE_COOPERATIVE=1)
     unsigned long long *sk_par_dev = nullptr;  // k_moe_relay: its workspace layers' parities (StackArgs::par_dev)
     int native = 0;              // GMOE_Q8_NATIVE: checkpoint layout, fp32 scales, native.h kernels
+    int g16 = 0;                 // GMOE_Q8_TILED16: tiled q planes, fp32 scales per 16 columns
     uint8_t *sk_ws = nullptr;    // per-layer workspace, L regions of sk_ws_layer bytes
     size_t sk_ws_layer = 0;
     StackWs sk_o{};
@@ -266,12 +270,20 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
                 g.n_shared_experts);
         return GMOE_ERR_INVALID;
     }
-    if (g.q8_form != GMOE_Q8_AUTO && g.q8_form != GMOE_Q8_TILED && g.q8_form != GMOE_Q8_NATIVE) {
+    if (g.q8_form != GMOE_Q8_AUTO && g.q8_form != GMOE_Q8_TILED && g.q8_form != GMOE_Q8_NATIVE &&
+        g.q8_form != GMOE_Q8_TILED16) {
         set_err("gmoe_create: q8_form %d is not a GMOE_Q8_* value", g.q8_form);
         return GMOE_ERR_INVALID;
     }
-    const bool native = g.q8_form == GMOE_Q8_NATIVE || (g.q8_form == GMOE_Q8_AUTO && g.group_size != GM_QBLOCK);
-    if (!native && g.group_size != GM_QBLOCK) {
+    // group size 16 (the exporter's) goes to the tiled form with fp32 scales where the shape
+    // runs on k_moe_relay (decided below), else to the native form
+    bool g16 = g.q8_form == GMOE_Q8_TILED16 || (g.q8_form == GMOE_Q8_AUTO && g.group_size == 16);
+    bool native = g.q8_form == GMOE_Q8_NATIVE || (g.q8_form == GMOE_Q8_AUTO && g.group_size != GM_QBLOCK && !g16);
+    if (g.q8_form == GMOE_Q8_TILED16 && g.group_size != 16) {
+        set_err("gmoe_create: GMOE_Q8_TILED16 needs group_size 16 (got %d)", g.group_size);
+        return GMOE_ERR_INVALID;
+    }
+    if (!native && !g16 && g.group_size != GM_QBLOCK) {
         set_err("gmoe_create: the tiled form needs group_size %d (got %d); GMOE_Q8_NATIVE takes other sizes",
                 GM_QBLOCK, g.group_size);
         return GMOE_ERR_INVALID;
@@ -322,10 +334,13 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
     c->off_us = 3 * qb + sb;
     c->off_ds = 3 * qb + 2 * sb;
     c->stride = (3 * qb + 3 * sb + 255) & ~(size_t)255;
-    if (native) {
-        // glm.c's layout per expert: gate, up, down int8 rows, then their fp32 scales
+    if (native || g16) {
+        // native: glm.c's layout per expert, gate, up, down int8 rows, then their fp32 scales;
+        // group size 16 tiled: the tiled q planes, then fp32 scales per 16 columns
+        // (gm_s16_offset, gm_ds16_offset), the same sizes
         const size_t sn = qb / (size_t)g.group_size * sizeof(float);
-        c->native = 1;
+        c->native = native;
+        c->g16 = g16;
         c->off_gs = 3 * qb;
         c->off_us = 3 * qb + sn;
         c->off_ds = 3 * qb + 2 * sn;
@@ -411,7 +426,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
             // k_moe_stack
             int per_cu_rl = 0;
             c->relay = c->stack_ok && !(dk_env && dk_env[0] == '0') &&
-                       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rl, relay_kernel(c->D, c->E), SK_BLOCK, 0) ==
+                       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_rl, relay_kernel(c->D, c->E, c->g16), SK_BLOCK, 0) ==
                            hipSuccess &&
                        per_cu_rl >= want && rl_fits(c->stack_grid, c->D, c->F, c->E, c->K);
             int coop_ok = 0;
@@ -420,6 +435,23 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
             // decode step, far more on one-layer launches)
             c->coop = c->stack_ok && co_env && co_env[0] == '1' &&
                       hipDeviceGetAttribute(&coop_ok, hipDeviceAttributeCooperativeLaunch, device) == hipSuccess && coop_ok;
+        }
+    }
+    if (c->g16) {
+        // the group-size-16 tiled form runs on k_moe_relay at T=1 and on the grouped GEMMs
+        // at T>1 only (k_moe_stack and the per-token kernels take fp16 scales per 32 columns)
+        c->grouped_min_t = 2;
+        if (!c->relay) {
+            if (g.q8_form == GMOE_Q8_TILED16) {
+                set_err("gmoe_create: GMOE_Q8_TILED16 runs on k_moe_relay, which this shape or GMOE_DECODE_KERNEL=0 / "
+                        "GMOE_STACK_KERNEL=0 rules out; GMOE_Q8_NATIVE takes it");
+                free_ctx(c);
+                return GMOE_ERR_INVALID;
+            }
+            c->g16 = 0;  // same offsets and sizes as the native form at group size 16
+            c->native = 1;
+            c->stack_ok = 0;
+            c->coop = 0;
         }
     }
     {
@@ -499,6 +531,12 @@ static void repack_staged(gmoe_ctx *c, int n_mat, int rows, int cols, uint8_t *d
     const size_t units = qbytes / 16;
     hipLaunchKernelGGL(k_repack_q, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, 0,
                        (const int8_t *)c->staging, dst + off_q, dst_stride, rows, cols, n_mat, layout);
+    if (c->g16) {
+        const size_t ns = (size_t)n_mat * rows * (cols / 16);
+        hipLaunchKernelGGL(k_repack_s16, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, 0,
+                           (const float *)(c->staging + qbytes), dst + off_s, dst_stride, rows, cols, n_mat, layout);
+        return;
+    }
     const size_t ns = (size_t)n_mat * rows * (cols / GM_QBLOCK);
     hipLaunchKernelGGL(k_repack_s, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, 0,
                        (const float *)(c->staging + qbytes), dst + off_s, dst_stride, rows, cols, n_mat, layout,
@@ -510,7 +548,7 @@ static void repack_staged(gmoe_ctx *c, int n_mat, int rows, int cols, uint8_t *d
 static int upload_matrices(gmoe_ctx *c, const int8_t *q, const float *s, int n_mat, int rows, int cols, uint8_t *dst,
                            size_t dst_stride, size_t off_q, size_t off_s, int layout, unsigned long long *inexact_dev) {
     const size_t qbytes = (size_t)n_mat * rows * cols;
-    const size_t sbytes = (size_t)n_mat * rows * (cols / GM_QBLOCK) * sizeof(float);
+    const size_t sbytes = (size_t)n_mat * rows * (cols / (c->g16 ? 16 : GM_QBLOCK)) * sizeof(float);
     if (qbytes + sbytes > c->staging_bytes) {
         dev_free(c->staging);
         c->staging = nullptr;
@@ -855,7 +893,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
     ProfRecord *pr = space ? nullptr
                            : prof_begin(c, st, c->relay ? GMOE_KERNEL_RELAY : GMOE_KERNEL_STACK);
     {
-        const void *fn = c->relay ? (const void *)relay_kernel(c->D, c->E) : (const void *)k_moe_stack;
+        const void *fn = c->relay ? (const void *)relay_kernel(c->D, c->E, c->g16) : (const void *)k_moe_stack;
         // Every block waits on others' results, so the grid must be resident at once: a
         // cooperative launch has the runtime guarantee it (or refuse the launch), where an
         // ordinary one relies on the GPU being otherwise idle and the bounded waits turn a
@@ -867,7 +905,7 @@ static int launch_stack(gmoe_ctx *c, int first, int n, const float *x_in, float 
             HIP_OK(hipLaunchCooperativeKernel(fn, dim3(c->stack_grid), dim3(SK_BLOCK), args, 0, st));
         } else {
             if (c->relay)
-                hipLaunchKernelGGL(relay_kernel(c->D, c->E), dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
+                hipLaunchKernelGGL(relay_kernel(c->D, c->E, c->g16), dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
             else
                 hipLaunchKernelGGL(k_moe_stack, dim3(c->stack_grid), dim3(SK_BLOCK), 0, st, a);
         }
@@ -1099,7 +1137,8 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
         ga.out = c->hbuf;
         const int max_tiles = (routed_on ? E + (T * K + GP_TOK - 1) / GP_TOK : 0) + (T + GP_TOK - 1) / GP_TOK;
         pr = prof_begin(c, st, GMOE_KERNEL_GATE_UP);
-        hipLaunchKernelGGL(k_group_gu, dim3(F / 64, max_tiles), dim3(GP_BLOCK), 0, st, ga);
+        if (c->g16) hipLaunchKernelGGL(k_group_gu<true>, dim3(F / 64, max_tiles), dim3(GP_BLOCK), 0, st, ga);
+        else hipLaunchKernelGGL(k_group_gu<false>, dim3(F / 64, max_tiles), dim3(GP_BLOCK), 0, st, ga);
         prof_end(pr, st);
         // routed rows [0, offsets[E]) and the shared rows [TK, TK + T)
         pr = prof_begin(c, st, GMOE_KERNEL_DIGITS);
@@ -1113,7 +1152,8 @@ extern "C" int gmoe_forward(gmoe_ctx *c, int layer, int T, const float *x_in, fl
         ga.aexp = c->hexp;
         ga.out = c->ybuf;
         pr = prof_begin(c, st, GMOE_KERNEL_DOWN);
-        hipLaunchKernelGGL(k_group_down, dim3(D / 64, max_tiles), dim3(GP_BLOCK), 0, st, ga);
+        if (c->g16) hipLaunchKernelGGL(k_group_down<true>, dim3(D / 64, max_tiles), dim3(GP_BLOCK), 0, st, ga);
+        else hipLaunchKernelGGL(k_group_down<false>, dim3(D / 64, max_tiles), dim3(GP_BLOCK), 0, st, ga);
         prof_end(pr, st);
         TokenCombineArgs ta;
         ta.topk_idx = c->topk_idx;
@@ -1405,6 +1445,7 @@ extern "C" int gmoe_get_stats(gmoe_ctx *c, gmoe_stats *o) {
     o->norm_exact_path = (int64_t)s[GM_STAT_NORM_EXACT];
     o->scale_inexact = c->scale_inexact;
     o->expf_libc_match = c->expf_libc_match;
+    o->q8_form = c->g16 ? GMOE_Q8_TILED16 : c->native ? GMOE_Q8_NATIVE : GMOE_Q8_TILED;
     return GMOE_OK;
 }
 

@@ -220,14 +220,33 @@ typedef uint8_t gp_abuf3_t[3][GP_TOK * 2 * GP_RB];  // k_group_gu: two chunks in
 // k_group_gu: grid (F/64, max tiles). Wave w computes rows 64 p + 16 w .. +16 of F, gate
 // and up, for the tile's inputs, and from them h = silu(g) * u.
 typedef unsigned gp_sw __attribute__((ext_vector_type(GP_NB / 2)));  // a chunk's GP_NB fp16 block scales
+typedef float gp_s4 __attribute__((ext_vector_type(4)));
+template <bool G16>
 struct GuRegs {
     u32x4 q[2][GP_NB / 2];  // gate, up: the chunk's 64-column pieces
     gp_sw s[2];             // gate, up: the chunk's block scales
 };
+template <>
+struct GuRegs<true> {       // group size 16: fp32 scales
+    u32x4 q[2][GP_NB / 2];
+    gp_s4 s[2][GP_NB / 2];  // gate, up: per 64-column piece, the row's four (gm_s16_offset order)
+};
 // loads per chunk and thread
-__host__ __device__ constexpr int gp_gu_loads(int na) { return 2 * (GP_NB / 2) + 2 + gp_stage_iters(na); }
+__host__ __device__ constexpr int gp_gu_loads(int na, bool g16) {
+    return 2 * (GP_NB / 2) + (g16 ? 2 * (GP_NB / 2) : 2) + gp_stage_iters(na);
+}
 
-template <int NA>
+// The B operand of one block split by its 16-column groups: lanes 0..31 hold k 0..15 (the
+// first group), lanes 32..63 k 16..31; each half keeps its own lanes and zeros elsewhere,
+// so that two MFMAs give the two groups' dots apart.
+__device__ static inline void gp_split16(gp_h8 B, gp_h8 &B0, gp_h8 &B1) {
+    const bool first = (threadIdx.x & 63) < 32;
+    const gp_h8 z = {};
+    B0 = first ? B : z;
+    B1 = first ? z : B;
+}
+
+template <int NA, bool G16>
 __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const GroupArgs &a, const GpTile &tl, gp_abuf3_t &abuf) {
     const int p = blockIdx.x;
     const int D = a.D, F = a.F, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -237,9 +256,12 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
     const GM_GLOBAL u32x4 *qg = gbl((const u32x4 *)(base + a.off_gq + (size_t)P * nchunks * GM_CHUNK_BYTES)) + lane;
     const GM_GLOBAL u32x4 *qu = gbl((const u32x4 *)(base + a.off_uq + (size_t)P * nchunks * GM_CHUNK_BYTES)) + lane;
     const int row = 16 * P + (lane & 15);
-    // the row's fp16 scales, one chunk's blocks per load
+    // the row's fp16 scales, one chunk's blocks per load; at group size 16 the row's four
+    // fp32 scales of each 64-column piece (gm_s16_offset: piece c at 16 c + row % 16)
     const GM_GLOBAL gp_sw *sg = gbl((const gp_sw *)(base + a.off_gs + (size_t)row * nblocks * 2));
     const GM_GLOBAL gp_sw *su = gbl((const gp_sw *)(base + a.off_us + (size_t)row * nblocks * 2));
+    const GM_GLOBAL gp_s4 *sg16 = gbl((const gp_s4 *)(base + a.off_gs + (size_t)P * D * 4)) + (lane & 15);
+    const GM_GLOBAL gp_s4 *su16 = gbl((const gp_s4 *)(base + a.off_us + (size_t)P * D * 4)) + (lane & 15);
     auto src_row = [&](int i) { return gp_token(a, tl.row + (i < tl.count ? i : 0)); };
     const GpStage<NA> stg = gp_stage_init<NA>(a.aspl, D, src_row);
     const int nkc = D / GP_KC;  // K chunks
@@ -249,17 +271,25 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
     for (int i = 0; i < NA; i++)
 #pragma unroll
         for (int k = 0; k < 4; k++) ag[i][k] = au[i][k] = 0.0f;
-    auto issue = [&](GuRegs &r, int kc) {  // gp_gu_loads(NA) loads
+    auto issue = [&](GuRegs<G16> &r, int kc) {  // gp_gu_loads(NA, G16) loads
 #pragma unroll
         for (int u = 0; u < GP_NB / 2; u++) {
             r.q[0][u] = qg[(size_t)((GP_NB / 2) * kc + u) * 64];
             r.q[1][u] = qu[(size_t)((GP_NB / 2) * kc + u) * 64];
         }
-        r.s[0] = sg[kc];
-        r.s[1] = su[kc];
+        if constexpr (G16) {
+#pragma unroll
+            for (int u = 0; u < GP_NB / 2; u++) {
+                r.s[0][u] = sg16[(size_t)((GP_NB / 2) * kc + u) * 16];
+                r.s[1][u] = su16[(size_t)((GP_NB / 2) * kc + u) * 16];
+            }
+        } else {
+            r.s[0] = sg[kc];
+            r.s[1] = su[kc];
+        }
         gp_stage<NA>(stg, abuf[kc % 3], kc * GP_KC);
     };
-    auto compute = [&](const GuRegs &r, int kc) {
+    auto compute = [&](const GuRegs<G16> &r, int kc) {
         const uint8_t *buf = abuf[kc % 3];
 #pragma unroll
         for (int b = 0; b < GP_NB; b++) {
@@ -267,21 +297,30 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
             for (int m = 0; m < 2; m++) {
                 const u32x4 c = r.q[m][b >> 1];
                 const gp_h8 B = (b & 1) ? gp_i8_to_h8(c.z, c.w) : gp_i8_to_h8(c.x, c.y);
-                const unsigned s2 = r.s[m][b >> 1];
-                const float sc = __half2float(__ushort_as_half((unsigned short)((b & 1) ? s2 >> 16 : s2 & 0xffffu)));
-                gp_block<NA>(buf, b, B, sc, m ? au : ag);
+                if constexpr (G16) {
+                    // the block's first group scales lanes 0..31's half of B, its second 32..63's
+                    const gp_s4 s4 = r.s[m][b >> 1];
+                    gp_h8 B0, B1;
+                    gp_split16(B, B0, B1);
+                    gp_block<NA>(buf, b, B0, (b & 1) ? s4.y : s4.x, m ? au : ag);
+                    gp_block<NA>(buf, b, B1, (b & 1) ? s4.w : s4.z, m ? au : ag);
+                } else {
+                    const unsigned s2 = r.s[m][b >> 1];
+                    const float sc = __half2float(__ushort_as_half((unsigned short)((b & 1) ? s2 >> 16 : s2 & 0xffffu)));
+                    gp_block<NA>(buf, b, B, sc, m ? au : ag);
+                }
             }
         }
     };
     // one step: chunk kc's data is in (r, buffer kc % 3); chunk kc + 2's is requested into rn
     // (into the registers and buffer chunk kc - 1 used), so that two chunks are in flight
     // while one is multiplied; the wait leaves the later chunks' loads outstanding
-    auto step = [&](GuRegs &r, GuRegs &rn, int kc) {
+    auto step = [&](GuRegs<G16> &r, GuRegs<G16> &rn, int kc) {
         if (kc + 2 < nkc) {
             issue(rn, kc + 2);
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * gp_gu_loads(NA)) : "memory");
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * gp_gu_loads(NA, G16)) : "memory");
         } else if (kc + 1 < nkc) {
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gp_gu_loads(NA)) : "memory");
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gp_gu_loads(NA, G16)) : "memory");
         } else {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
@@ -289,7 +328,7 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
         compute(r, kc);
         gp_barrier();  // every wave is done with buffer kc % 3 before it is refilled
     };
-    GuRegs r0, r1, r2;
+    GuRegs<G16> r0, r1, r2;
     issue(r0, 0);
     if (nkc > 1) issue(r1, 1);
     for (int kc = 0; kc < nkc; kc += 3) {
@@ -312,24 +351,31 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
         }
 }
 
+template <bool G16>
 __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
     __shared__ __align__(16) gp_abuf3_t abuf;
     if ((int)blockIdx.y >= *a.n_tiles) return;
     const GpTile tl = a.tiles[blockIdx.y];
     gp_with_na<GP_NA_MAX>(__builtin_amdgcn_readfirstlane((tl.count + 15) >> 4),
-                          [&](auto NA) { gp_gu_tile<decltype(NA)::value>(a, tl, abuf); });
+                          [&](auto NA) { gp_gu_tile<decltype(NA)::value, G16>(a, tl, abuf); });
 }
 
 // k_group_down: grid (D/64, max tiles). Wave w computes D rows 64 p + 16 w .. +16 for the
 // tile's inputs (list rows), from h's split form; down is in the column-slice layout.
+template <bool G16>
 struct DnRegs {
     unsigned long long q[GP_NB];  // the chunk's blocks: 8 bytes of the row each
     unsigned short s[GP_NB];
 };
+template <>
+struct DnRegs<true> {             // group size 16: the row's fp32 scales of both groups of each block
+    unsigned long long q[GP_NB];
+    float s[GP_NB][2];
+};
 // loads per chunk and thread
-__host__ __device__ constexpr int gp_dn_loads(int na) { return 2 * GP_NB + gp_stage_iters(na); }
+__host__ __device__ constexpr int gp_dn_loads(int na, bool g16) { return (g16 ? 3 : 2) * GP_NB + gp_stage_iters(na); }
 
-template <int NA>
+template <int NA, bool G16>
 __device__ __attribute__((always_inline)) static inline void gp_down_tile(const GroupArgs &a, const GpTile &tl, gp_abuf_t &abuf) {
     const int p = blockIdx.x;
     const int D = a.D, F = a.F, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -338,6 +384,7 @@ __device__ __attribute__((always_inline)) static inline void gp_down_tile(const 
     // B operand of block b (F columns 32b + 8 qh .. +8): slice 2b + qh/2, half qh % 2
     const GM_GLOBAL uint8_t *qd = gbl(base + a.off_dq) + (size_t)row * 16 + 8 * (qh & 1);
     const GM_GLOBAL unsigned short *sd = gbl((const unsigned short *)(base + a.off_ds)) + row;
+    const GM_GLOBAL float *sd16 = gbl((const float *)(base + a.off_ds)) + row;  // gm_ds16_offset: [F/16][D]
     auto src_row = [&](int i) { return tl.row + (i < tl.count ? i : 0); };
     const GpStage<NA> stg = gp_stage_init<NA>(a.aspl, F, src_row);
     const int nkc = F / GP_KC;
@@ -346,35 +393,48 @@ __device__ __attribute__((always_inline)) static inline void gp_down_tile(const 
     for (int i = 0; i < NA; i++)
 #pragma unroll
         for (int k = 0; k < 4; k++) acc[i][k] = 0.0f;
-    auto issue = [&](DnRegs &r, int kc) {  // gp_dn_loads(NA) loads
+    auto issue = [&](DnRegs<G16> &r, int kc) {  // gp_dn_loads(NA, G16) loads
 #pragma unroll
         for (int b = 0; b < GP_NB; b++) {
             const int blk = GP_NB * kc + b;
             r.q[b] = *(const GM_GLOBAL unsigned long long *)(qd + ((size_t)(2 * blk + (qh >> 1)) * D) * 16);
-            r.s[b] = sd[(size_t)blk * D];
+            if constexpr (G16) {
+                r.s[b][0] = sd16[(size_t)(2 * blk) * D];
+                r.s[b][1] = sd16[(size_t)(2 * blk + 1) * D];
+            } else {
+                r.s[b] = sd[(size_t)blk * D];
+            }
         }
         gp_stage<NA>(stg, abuf[kc & 1], kc * GP_KC);
     };
-    auto compute = [&](const DnRegs &r, int kc) {
+    auto compute = [&](const DnRegs<G16> &r, int kc) {
         const uint8_t *buf = abuf[kc & 1];
 #pragma unroll
-        for (int b = 0; b < GP_NB; b++)
-            gp_block<NA>(buf, b, gp_i8_to_h8((unsigned)r.q[b], (unsigned)(r.q[b] >> 32)), __half2float(__ushort_as_half(r.s[b])),
-                         acc);
+        for (int b = 0; b < GP_NB; b++) {
+            const gp_h8 B = gp_i8_to_h8((unsigned)r.q[b], (unsigned)(r.q[b] >> 32));
+            if constexpr (G16) {
+                gp_h8 B0, B1;
+                gp_split16(B, B0, B1);
+                gp_block<NA>(buf, b, B0, r.s[b][0], acc);
+                gp_block<NA>(buf, b, B1, r.s[b][1], acc);
+            } else {
+                gp_block<NA>(buf, b, B, __half2float(__ushort_as_half(r.s[b])), acc);
+            }
+        }
     };
-    auto step = [&](DnRegs &r, DnRegs &rn, int kc) {
+    auto step = [&](DnRegs<G16> &r, DnRegs<G16> &rn, int kc) {
         issue(rn, kc + 1);
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gp_dn_loads(NA)) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(gp_dn_loads(NA, G16)) : "memory");
         gp_barrier();
         compute(r, kc);
         gp_barrier();
     };
-    auto last = [&](DnRegs &r, int kc) {
+    auto last = [&](DnRegs<G16> &r, int kc) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         gp_barrier();
         compute(r, kc);
     };
-    DnRegs r0, r1;
+    DnRegs<G16> r0, r1;
     issue(r0, 0);
     int kc = 0;
     for (; kc + 2 < nkc; kc += 2) {
@@ -399,12 +459,13 @@ __device__ __attribute__((always_inline)) static inline void gp_down_tile(const 
         }
 }
 
+template <bool G16>
 __global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_down(GroupArgs a) {
     __shared__ __align__(16) gp_abuf_t abuf;
     if ((int)blockIdx.y >= *a.n_tiles) return;
     const GpTile tl = a.tiles[blockIdx.y];
     gp_with_na<GP_NA_MAX>(__builtin_amdgcn_readfirstlane((tl.count + 15) >> 4),
-                          [&](auto NA) { gp_down_tile<decltype(NA)::value>(a, tl, abuf); });
+                          [&](auto NA) { gp_down_tile<decltype(NA)::value, G16>(a, tl, abuf); });
 }
 
 struct TokenCombineArgs {

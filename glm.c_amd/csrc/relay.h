@@ -455,7 +455,7 @@ struct RlItem {
     u32x4 g0, g1, u0, u1;  // D == 2048: row (lane & 15)'s gate/up scales of the wave's blocks
 };
 
-template <bool FULL>
+template <bool FULL, bool G16>
 __device__ __attribute__((always_inline)) static void rl_item_request(const StackArgs &a, const StackLayer &L, int e,
                                                                       int j, RlItem &it, SkShared &sh) {
     const int D = FULL ? GM_MAX_COLS : a.D, tid = phase_tid(), lane = tid & 63, w = tid >> 6, wave0 = tid & ~63;
@@ -463,7 +463,31 @@ __device__ __attribute__((always_inline)) static void rl_item_request(const Stac
     const GM_GLOBAL u32x4 *qs = gbl((const u32x4 *)(base + a.off_dq)) + (size_t)j * D + tid;
     const int o = 1024 * w + 16 * lane;
     const int c = D / SK_BLOCK;
-    if (FULL) {
+    if (G16) {
+        // group size 16: the slice's D fp32 down scales (4 KB per 16 bytes a thread), then the
+        // wave's own run of each gate/up scale panel (D bytes: its chunks' 64 scales each),
+        // then the down slice, all by DMA that the compiler does not count; last the gate/up
+        // chunks to registers (FULL: all of them, branch-free, so that the compiler waits for
+        // each chunk by itself)
+        const uint8_t *ds = base + a.off_ds + (size_t)j * D * 4;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            if (o + 4096 * h < 4 * D) dma16_untracked(gbl(ds + o + 4096 * h), (lds_void *)((uint8_t *)sh.sc16_d + 4096 * h + 1024 * w));
+        const size_t pw = (size_t)j * D * 4 + (size_t)w * D;  // bytes: panel j, then the wave's run
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                if (64 * i + lane < D / 16)
+                    dma16_untracked(gbl(base + (mt ? a.off_us : a.off_gs) + pw + 16 * (64 * i + lane)),
+                                    (lds_void *)((uint8_t *)sh.sc16_gu + (2 * w + mt) * D + 1024 * i));
+#pragma unroll
+        for (int i = 0; i < SK_PER_MAX; i++)
+            if (FULL || i < c) dma16_untracked(qs + (size_t)i * SK_BLOCK, (lds_void *)(sh.dslice + i * SK_BLOCK + wave0));
+        __builtin_amdgcn_sched_barrier(0);
+        if (FULL) panel_load_q_all<2, EX_NB_MAX>(it.pr, base + a.off_gq, base + a.off_uq, j, D);
+        else panel_load_q<2, EX_NB_MAX>(it.pr, base + a.off_gq, base + a.off_uq, j, D);
+    } else if (FULL) {
         const int m = lane & 15, j0 = w * EX_NB_MAX;
         dma16_untracked(gbl(base + a.off_ds + (size_t)(j >> 1) * D * 2 + o), (lds_void *)((uint8_t *)sh.sc_d + 1024 * w));
 #pragma unroll
@@ -497,7 +521,7 @@ __device__ __attribute__((always_inline)) static void rl_item_request(const Stac
 // sh.xn_r, h = silu(g) * u (:1188, :1202), and the partial y = down[:, 16j..16j+16) . h
 // over all D rows (:1190, :1205), stored tagged at piece (j, slot) of every combine chunk:
 // chunk r/16 holds [F/16][K+1][16] floats, so each 16 lanes store one 64-byte piece.
-template <bool FULL>
+template <bool FULL, bool G16>
 __device__ __attribute__((always_inline)) static void rl_item_compute(const StackArgs &a, int li, int slot, int j, int e,
                                                                       const RlItem &it, SkShared &sh) {
     const int D = FULL ? GM_MAX_COLS : a.D, NPF = a.F >> 4, NS = a.K + 1, tid = phase_tid(), lane = tid & 63, w = tid >> 6;
@@ -514,7 +538,17 @@ __device__ __attribute__((always_inline)) static void rl_item_compute(const Stac
         return;
     }
     float gu[2];
-    if (FULL) {
+    if (G16) {
+        // the wave's scale runs (issued before its 16 chunk loads) have landed: every load but
+        // the chunks is done
+        if (FULL) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * EX_NB_MAX) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const float *sg16 = sh.sc16_gu + (2 * w) * (D / 4), *su16 = sh.sc16_gu + (2 * w + 1) * (D / 4);
+        gu_products16<EX_NB_MAX>(it.pr, D, FULL ? EX_NB_MAX : D >> 8, (const int8_t *)sh.xn_r, sg16, su16, gu);
+        // the down slice and scales (not counted by the compiler) are in shared memory before
+        // the barrier below
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (FULL) {
         const int m = lane & 15, j0 = w * EX_NB_MAX;
         const int8_t *drow = (const int8_t *)sh.xn_r + (m < 3 ? m : 0) * D + 64 * j0 + 8 * (lane >> 4);
         long A[EX_NB_MAX][2];
@@ -561,11 +595,11 @@ __device__ __attribute__((always_inline)) static void rl_item_compute(const Stac
     for (int q = 0; q < 12; q++) h4[q] = sh.u.g.hd[q];
     const int hexp = sh.u.g.hexp;
     u32x4 dqs[SK_PER_MAX];
-    unsigned scs[SK_PER_MAX];
+    unsigned scs[SK_PER_MAX];  // the rows' fp16 scales, or (G16) their fp32 scales' bits
 #pragma unroll
     for (int i = 0; i < SK_PER_MAX; i++) {
         dqs[i] = sh.dslice[i * SK_BLOCK + tid];
-        scs[i] = sh.sc_d[i * SK_BLOCK + tid];
+        scs[i] = G16 ? __float_as_uint(sh.sc16_d[i * SK_BLOCK + tid]) : (unsigned)sh.sc_d[i * SK_BLOCK + tid];
     }
 #pragma unroll
     for (int i = 0; i < SK_PER_MAX; i++) asm volatile("" ::"v"(dqs[i]), "v"(scs[i]));
@@ -582,8 +616,8 @@ __device__ __attribute__((always_inline)) static void rl_item_compute(const Stac
                 for (int q = 0; q < 4; q++) s = __builtin_amdgcn_sdot4(wq[q], h4[4 * d + q], s, false);
                 acc[d] = s;
             }
-            const float f = digits_to_float(acc[0], acc[1], acc[2]) *
-                            ldexpf(__half2float(__ushort_as_half((unsigned short)scs[i])), hexp);
+            const float sd = G16 ? __uint_as_float(scs[i]) : __half2float(__ushort_as_half((unsigned short)scs[i]));
+            const float f = digits_to_float(acc[0], acc[1], acc[2]) * ldexpf(sd, hexp);
             __hip_atomic_store((unsigned *)(yp + (size_t)i * (SK_BLOCK / RL_ROWS) * ychunk), rl_tag(f, p), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -949,7 +983,7 @@ __host__ __device__ static inline bool rl_fits(int G, int D, int F, int E, int K
            (K + 1) * (RL_ROWS / 2) <= SK_BLOCK;
 }
 
-template <bool FULL, int C>
+template <bool FULL, int C, bool G16>
 __device__ __attribute__((always_inline)) static bool rl_run(const StackArgs &a, SkShared &sh) {
     const int G = (int)gridDim.x, b = blockIdx.x, K = a.K, NPF = a.F >> 4, D = FULL ? GM_MAX_COLS : a.D, per = D / SK_BLOCK;
     const RlRoles R = rl_roles(G, D, a.F, a.E, K);
@@ -995,10 +1029,10 @@ __device__ __attribute__((always_inline)) static bool rl_run(const StackArgs &a,
                 // the norm rows have arrived (requested before the wait): the count of the loads
                 // the compiler waits on below must not include the item's DMA
                 __builtin_amdgcn_s_waitcnt(GM_WAIT_VM0);
-                rl_item_request<FULL>(a, L, a.E, jp, it, sh);
+                rl_item_request<FULL, G16>(a, L, a.E, jp, it, sh);
                 rl_xn<FULL>(a, nw, xv, true, sh);
                 sk_stamp(sh, 11);
-                rl_item_compute<FULL>(a, li, K, jp, a.E, it, sh);
+                rl_item_compute<FULL, G16>(a, li, K, jp, a.E, it, sh);
             } else {
                 rl_xn<FULL>(a, nw, xv, true, sh);
                 sk_stamp(sh, 11);
@@ -1009,8 +1043,8 @@ __device__ __attribute__((always_inline)) static bool rl_run(const StackArgs &a,
                     e = sh.idx[slot];
                 }
                 if (!routed_on) e = -1;
-                if (e >= 0) rl_item_request<FULL>(a, L, e, jp, it, sh);
-                rl_item_compute<FULL>(a, li, slot, jp, e, it, sh);
+                if (e >= 0) rl_item_request<FULL, G16>(a, L, e, jp, it, sh);
+                rl_item_compute<FULL, G16>(a, li, slot, jp, e, it, sh);
             }
             if (a.trace && tid == 0) trace_put(a.trace, SK_TRACE_STAMPS * sh.trace_item + 2);
             __syncthreads();
@@ -1037,8 +1071,8 @@ __device__ __attribute__((always_inline)) static bool rl_run(const StackArgs &a,
 }
 
 // FULL: D == 2048 (a row of xn fills the item's registers exactly); C: chunks of 64 experts
-// per lane in the selection (E <= 64 C).
-template <bool FULL, int C>
+// per lane in the selection (E <= 64 C); G16: experts at group size 16 with fp32 scales.
+template <bool FULL, int C, bool G16>
 __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_relay(StackArgs a) {
     __shared__ SkShared sh;
     if (threadIdx.x == 0) {
@@ -1050,7 +1084,7 @@ __global__ __launch_bounds__(SK_BLOCK, 2) void k_moe_relay(StackArgs a) {
     }
     if (threadIdx.x < SK_MAX_LAYERS / 64) rl_par_sh[threadIdx.x] = a.par_dev[threadIdx.x];
     __syncthreads();
-    if (!rl_run<FULL, C>(a, sh) && threadIdx.x == 0)
+    if (!rl_run<FULL, C, G16>(a, sh) && threadIdx.x == 0)
         __hip_atomic_store(a.error_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 

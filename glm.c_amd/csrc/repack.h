@@ -53,3 +53,18 @@ __global__ void k_repack_s(const float *__restrict__ raw, uint8_t *__restrict__ 
     __half *out = (__half *)(dst + (size_t)m * dst_stride);
     out[layout == GM_LAYOUT_SLICES ? gm_ds_offset(r, b, rows) : gm_s_offset(r, b, cols)] = hs;
 }
+
+// Group size 16: one thread per fp32 scale (raw [rows][cols/16], glm.c's order), copied as
+// it is into gm_s16_offset's panel runs or (GM_LAYOUT_SLICES) gm_ds16_offset's slice rows.
+__global__ void k_repack_s16(const float *__restrict__ raw, uint8_t *__restrict__ dst, size_t dst_stride, int rows,
+                             int cols, int n_mat, int layout) {
+    const int ng = cols >> 4;
+    const size_t per = (size_t)rows * ng;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= per * (size_t)n_mat) return;
+    const int m = (int)(gid / per);
+    const size_t i = gid % per;
+    const int r = (int)(i / ng), g = (int)(i % ng);
+    float *out = (float *)(dst + (size_t)m * dst_stride);
+    out[layout == GM_LAYOUT_SLICES ? gm_ds16_offset(r, g, rows) : gm_s16_offset(r, g, cols)] = raw[gid];
+}

@@ -183,7 +183,22 @@ __device__ static inline void trace_put(unsigned long long *t, long idx) {
     *(GM_GLOBAL unsigned long long *)(t + idx) = wall_clock64();
 }
 
+// The small fields first and the scale buffers last: shared-memory instructions reach 64 KB
+// past their base register, and the block holds ~71 KB.
 struct SkShared {
+    double red[4];
+    float mxw[4];  // per-wave max |xn|
+    float mean, total;
+    unsigned old;
+    int ok, sel_ok;
+    unsigned zero;  // 0 for the kernel's life (an always-zero operand of gu_products)
+    int xe_local;   // exponent of a routed block's own digits of xn (sk_local_digits)
+    unsigned spin_limit;
+    float xres[16]; // relay.h: a combine chunk's residual rows
+    int idx[GM_MAX_K];
+    float wk[GM_MAX_K], ws[GM_MAX_K];
+    long trace_item;
+    unsigned long long *trace;
     union {
         struct {  // router item
             double wv[4][SK_RX_MAX][3];  // per wave: segment total, sum |S_k|, sum |p|
@@ -203,23 +218,19 @@ struct SkShared {
             float y[GM_MAX_K + 1][SK_CROWS];
         } c;
     } u;
-    u32x4 dslice[GM_MAX_COLS];  // an expert item's down columns, D rows x 16 bytes
     float xn_r[GM_MAX_COLS];    // a router item's xn (kept through the top-k and its replay)
-    __attribute__((aligned(16))) unsigned short sc_gu[2 * GM_MAX_COLS / 2];  // its gate and up panel scales, [2][16][D/32]
-    unsigned short sc_d[GM_MAX_COLS];           // its down scales, one per row
-    double red[4];
-    float mxw[4];  // per-wave max |xn|
-    float mean, total;
-    unsigned old;
-    int ok, sel_ok;
-    unsigned zero;  // 0 for the kernel's life (an always-zero operand of gu_products)
-    int xe_local;   // exponent of a routed block's own digits of xn (sk_local_digits)
-    unsigned spin_limit;
-    float xres[16]; // relay.h: a combine chunk's residual rows
-    int idx[GM_MAX_K];
-    float wk[GM_MAX_K], ws[GM_MAX_K];
-    long trace_item;
-    unsigned long long *trace;
+    u32x4 dslice[GM_MAX_COLS];  // an expert item's down columns, D rows x 16 bytes
+    union {
+        struct {
+            __attribute__((aligned(16))) unsigned short sc_gu[2 * GM_MAX_COLS / 2];  // its gate and up panel scales, [2][16][D/32]
+            unsigned short sc_d[GM_MAX_COLS];  // its down scales, one per row
+        };
+        struct {  // group size 16 (k_moe_relay only): fp32 scales
+            // per wave, gate then up: the wave's chunks of the panel's scale runs (gm_s16_offset)
+            __attribute__((aligned(16))) float sc16_gu[2 * 16 * GM_MAX_COLS / 16];
+            float sc16_d[GM_MAX_COLS];  // the item's down scales, one per row
+        };
+    };
 };
 
 __device__ static inline void st_u(unsigned *p, unsigned v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
@@ -829,6 +840,51 @@ __device__ static inline void gu_products(const PanelRegs<2, NB> &r, int cols, c
         su[u] = *(on ? pu + u : zero);
     }
     gu_products_r<NB>(r, A, sg, su, out);
+}
+
+// gu_products at group size 16 with fp32 scales: the two 16-column groups of every
+// 32-column block get their own scale. A's rows 0..2 hold the digits of the block's first
+// 16 columns (zeros in its last 16) and rows 4..6 those of its last 16 (zeros in its first),
+// so the one MFMA per block and matrix leaves the first group's three digit dots on lanes
+// 0..15 and the second group's on lanes 16..31 (rows 4..6 of the product), each lane
+// scaling by its own group's scale; lanes 0..15 end with the sum of both. Rows 3 and 7..15
+// of the product are never read. sg16 / su16: the wave's scale runs in shared memory,
+// [cpw chunks][16 rows][2 groups][2 blocks] each; chunks past cpw read chunk 0 and add zero.
+template <int NB>
+__device__ static inline void gu_products16(const PanelRegs<2, NB> &r, int cols, int cpw, const int8_t *dig,
+                                            const float *sg16, const float *su16, float out[2]) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, m = lane & 15, kq = lane >> 4;
+    const int j0 = w * cpw;
+    const int dr = (m & 3) < 3 ? (m & 3) : 0;      // the digit row of A row m (rows 3, 7: any)
+    const bool on = (m < 4) == (kq < 2);           // rows 0..3 take k 0..15, rows 4..7 k 16..31
+    const int8_t *drow = dig + dr * cols + 64 * j0 + 8 * kq;
+    const int so = 2 * (2 * m + (kq & 1));         // the lane's (row, group) pair in a chunk's run
+    float ag = 0.0f, au = 0.0f;
+    u32x4 qg = r.q[0][0], qu = r.q[1][0];
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const bool in = u < cpw;
+        const int uu = in ? u : 0;
+        const long a0 = *(const long *)(drow + 64 * uu), a1 = *(const long *)(drow + 64 * uu + 32);
+        const float2 sgv = *(const float2 *)(sg16 + 64 * uu + so), suv = *(const float2 *)(su16 + 64 * uu + so);
+        const long A0 = on ? a0 : 0, A1 = on ? a1 : 0;
+        const float sg0 = in ? sgv.x : 0.0f, sg1 = in ? sgv.y : 0.0f, su0 = in ? suv.x : 0.0f, su1 = in ? suv.y : 0.0f;
+        const v4i g0 = mfma_digits(A0, chunk_half(qg, 0));
+        const v4i g1 = mfma_digits(A1, chunk_half(qg, 1));
+        const v4i u0 = mfma_digits(A0, chunk_half(qu, 0));
+        const v4i u1 = mfma_digits(A1, chunk_half(qu, 1));
+        ag = fmaf(digits_to_float(g0[0], g0[1], g0[2]), sg0, ag);
+        ag = fmaf(digits_to_float(g1[0], g1[1], g1[2]), sg1, ag);
+        au = fmaf(digits_to_float(u0[0], u0[1], u0[2]), su0, au);
+        au = fmaf(digits_to_float(u1[0], u1[1], u1[2]), su1, au);
+        if (u + 1 < NB) {
+            qg = r.q[0][u + 1];
+            qu = r.q[1][u + 1];
+        }
+        asm volatile("" : "+v"(ag), "+v"(au), "+v"(qg), "+v"(qu));
+    }
+    out[0] = ag + __shfl_xor(ag, 16, 64);
+    out[1] = au + __shfl_xor(au, 16, 64);
 }
 
 // Rows [16j, 16j+16) of F for expert e in `slot` (-1: idle slot, nothing to compute):

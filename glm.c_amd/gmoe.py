@@ -21,7 +21,7 @@ LIBHOST = os.path.join(HERE, "libglm_hip.so")
 GMOE_FLAG_NO_ROUTED = 1
 GMOE_FLAG_EXACT_ROUTER = 2
 # gmoe_config.q8_form: device form of the expert matrices
-GMOE_Q8_AUTO, GMOE_Q8_TILED, GMOE_Q8_NATIVE = 0, 1, 2
+GMOE_Q8_AUTO, GMOE_Q8_TILED, GMOE_Q8_NATIVE, GMOE_Q8_TILED16 = 0, 1, 2, 3
 SYNTH_NORM_ONES, SYNTH_NORM_RANDOM = 0, 1
 SYNTH_BIAS_NORMAL, SYNTH_BIAS_ZIPF = 0, 1
 SYNTH_SCALES_FP16, SYNTH_SCALES_FP32 = 0, 1
@@ -68,7 +68,7 @@ class GmoeKernelTimes(C.Structure):
 class GmoeStats(C.Structure):
     _fields_ = [("tokens_routed", C.c_int64), ("routing_exact_path", C.c_int64), ("routing_exact_subset", C.c_int64),
                 ("norm_exact_path", C.c_int64),
-                ("scale_inexact", C.c_int64), ("expf_libc_match", C.c_int64)]
+                ("scale_inexact", C.c_int64), ("expf_libc_match", C.c_int64), ("q8_form", C.c_int64)]
 
 
 class SynthSpec(C.Structure):
@@ -160,8 +160,11 @@ class Shape:
         self.D, self.F, self.E, self.K, self.gs = dim, moe_ffn_dim, n_routed_experts, n_experts_used, group_size
 
     def expert_bytes(self):
-        """Algorithmic Q8_0 bytes of one expert (three matrices, 34 bytes per 32 weights)."""
-        return 3 * self.F * self.D * 34 // 32
+        """Algorithmic Q8_0 bytes of one expert as the device keeps it: three matrices of int8
+        weights plus one scale per group, fp16 at group size 32 (34 bytes per 32 weights), fp32
+        otherwise (20 bytes per 16 weights at the exporter's group size 16)."""
+        sb = 2 if self.gs == 32 else 4
+        return 3 * self.F * self.D * (self.gs + sb) // self.gs
 
 
 GLM47_FLASH = Shape()

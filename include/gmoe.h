@@ -49,8 +49,9 @@ typedef struct gmoe_config {
     int32_t n_routed_experts;  /* E (model.h:21); 1..256 */
     int32_t n_experts_used;    /* K (model.h:22); 1..8 */
     int32_t n_shared_experts;  /* S (model.h:23); 0 or 1 */
-    int32_t group_size;        /* quantisation group (model.h:26): 32 for the tiled form, a multiple of 16
-                                * dividing dim and moe_ffn_dim for the native form */
+    int32_t group_size;        /* quantisation group (model.h:26): 32 for the tiled form, 16 for the
+                                * tiled form with fp32 scales, a multiple of 16 dividing dim and
+                                * moe_ffn_dim for the native form */
     int32_t n_layers;          /* total layers; MoE layers are 1..n_layers-1 (infer.c:1844-1845) */
     int32_t max_tokens;        /* largest n_tokens passed to the forward calls */
     float routed_scale;        /* routed expert scale, hard-coded 1.8f at infer.c:1171 */
@@ -66,10 +67,16 @@ typedef struct gmoe_config {
  *   multiple of 16 and divides dim and moe_ffn_dim (the exporter writes group size 16 and
  *   scales max|w|/127, glm47_flash_export.py:36,157-169). Every T runs the native
  *   kernels: one wave per matrix row, each group's sum scaled by its own fp32 scale.
- * AUTO (0): TILED when group_size is 32, NATIVE otherwise. */
+ * TILED16: the exporter's form on the fast path: group size 16, fp32 scales kept exactly
+ *   as they are, q planes tiled as in TILED. T=1 runs the persistent relay decode kernel
+ *   (k_moe_relay), T>1 the grouped prefill GEMMs; gmoe_create refuses it where the shape
+ *   (or GMOE_DECODE_KERNEL=0, GMOE_STACK_KERNEL=0) rules the relay kernel out.
+ * AUTO (0): TILED when group_size is 32; TILED16 when it is 16 and the relay kernel runs
+ *   the shape, NATIVE otherwise. */
 #define GMOE_Q8_AUTO 0
 #define GMOE_Q8_TILED 1
 #define GMOE_Q8_NATIVE 2
+#define GMOE_Q8_TILED16 3
 
 /* Host-side weights of one MoE layer in glm.c's checkpoint layout:
  * LayerMoeShared (model.h:65-75) followed by LayerMoeRouted (model.h:77-84).
@@ -117,6 +124,8 @@ typedef struct gmoe_stats {
                                     table was measured against, so an exact router replay reproduces
                                     its expf bit for bit; 0: near-tied experts may be ordered otherwise
                                     (gmoe_create warns on stderr) */
+    int64_t q8_form;             /* the device form the context keeps its experts in (GMOE_Q8_TILED,
+                                    GMOE_Q8_NATIVE or GMOE_Q8_TILED16; what GMOE_Q8_AUTO resolved to) */
 } gmoe_stats;
 
 /* Create a context on HIP device `device` and reserve device memory for
@@ -125,7 +134,7 @@ int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg);
 
 /* Upload and repack one MoE layer (1 <= layer < n_layers) from host memory into
  * the device form (q8_form). In the tiled form scales must be fp16-representable (checked;
- * GMOE_ERR_SCALE); the native form keeps them as they are. */
+ * GMOE_ERR_SCALE); the tiled form at group size 16 and the native form keep them as they are. */
 int gmoe_upload_layer(gmoe_ctx *ctx, int layer, const gmoe_layer_weights *w);
 
 /* One MoE layer for n_tokens tokens: x_out = x_in + shared + routed.

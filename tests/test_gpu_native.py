@@ -1,9 +1,12 @@
-"""Checkpoints in glm.c's own Q8_0 form on the GPU (GMOE_Q8_NATIVE): group size 16 as the
-exporter writes it (glm47_flash_export.py:36), fp32 scales that fp16 cannot hold
-(max|w|/127 there, glm47_flash_export.py:157-169; random fp32 here), and other group sizes
-(infer.c:380-385, 646 take any). Each case runs against the oracle, which follows
-infer.c:765-786 for any group size. Bar as elsewhere: top-k exact, xn bit for bit, router
-probabilities and weights within 1e-5, outputs within max-abs 1e-2 and rel-L2 1e-3."""
+"""Checkpoints in glm.c's own Q8_0 form on the GPU: group size 16 as the exporter writes
+it (glm47_flash_export.py:36), fp32 scales that fp16 cannot hold (max|w|/127 there,
+glm47_flash_export.py:157-169; random fp32 here), and other group sizes (infer.c:380-385,
+646 take any). Group size 16 runs in two device forms: GMOE_Q8_TILED16 (what AUTO picks:
+the tiled q planes with the fp32 scales kept as they are, on the relay decode kernel and
+the grouped GEMMs) and GMOE_Q8_NATIVE (glm.c's layout, native kernels); the tests name the
+kernels that ran. Each case runs against the oracle, which follows infer.c:765-786 for any
+group size. Bar as elsewhere: top-k exact, xn bit for bit, router probabilities and
+weights within 1e-5, outputs within max-abs 1e-2 and rel-L2 1e-3."""
 import numpy as np
 import pytest
 
@@ -28,6 +31,23 @@ def check(want, got, st, what):
     assert_close(got, want["x_out"], f"{what}: x_out")
 
 
+GS16_FORMS = [pytest.param(gmoe.GMOE_Q8_AUTO, id="tiled16"), pytest.param(gmoe.GMOE_Q8_NATIVE, id="native")]
+
+
+def expect_kernels(ctx, q8_form, T):
+    """The form AUTO resolved to at group size 16, and the kernels the profiled calls ran."""
+    ran = ctx.profile_read()
+    if q8_form == gmoe.GMOE_Q8_NATIVE:
+        assert ctx.stats()["q8_form"] == gmoe.GMOE_Q8_NATIVE
+        assert "k_moe_relay" not in ran and "k_act_split" not in ran, ran
+    else:
+        assert ctx.stats()["q8_form"] == gmoe.GMOE_Q8_TILED16
+        if T == 1:
+            assert "k_moe_relay" in ran and "gate_up" not in ran, ran
+        else:
+            assert "k_act_split" in ran and "gate_up" in ran and "k_moe_relay" not in ran, ran  # k_group_gu
+
+
 def run(shape, seed, T, q8_form=gmoe.GMOE_Q8_AUTO, flags=0, n_layers=1):
     layers = [gmoe.HostLayer(shape, seed=seed, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM,
                              scale_mode=gmoe.SYNTH_SCALES_FP32) for l in range(1, n_layers + 1)]
@@ -36,32 +56,42 @@ def run(shape, seed, T, q8_form=gmoe.GMOE_Q8_AUTO, flags=0, n_layers=1):
     try:
         for l, hl in enumerate(layers, start=1):
             ctx.upload(l, hl)
+        ctx.profile(True)
         x = gmoe.activations(seed, 7, T, shape.D)
         for l, hl in enumerate(layers, start=1):
-            print(f"[case] native gs={shape.gs} D={shape.D} E={shape.E} T={T} layer {l} flags={flags}", flush=True)
+            print(f"[case] gs={shape.gs} form={q8_form} D={shape.D} E={shape.E} T={T} layer {l} flags={flags}", flush=True)
             want = orc.layer(shape, hl, x, disable_routed=bool(flags & gmoe.GMOE_FLAG_NO_ROUTED))
             got, st = gmoe.forward_host(ctx, l, x, flags=flags)
             check(want, got, st, f"gs={shape.gs} T={T} layer {l}")
             x = got
+        return ctx.profile_read(), ctx.stats()
     finally:
         ctx.close()
 
 
-def test_gs16_fp32_scales_decode():
-    run(GLM16, seed=41, T=1, n_layers=3)
+@pytest.mark.parametrize("q8_form", GS16_FORMS)
+def test_gs16_fp32_scales_decode(q8_form):
+    ran, stats = run(GLM16, seed=41, T=1, n_layers=3, q8_form=q8_form)
+    if q8_form == gmoe.GMOE_Q8_AUTO:
+        assert stats["q8_form"] == gmoe.GMOE_Q8_TILED16 and ran["k_moe_relay"][0] == 3, (stats, ran)
+    else:
+        assert stats["q8_form"] == gmoe.GMOE_Q8_NATIVE and "k_moe_relay" not in ran, (stats, ran)
 
 
-def test_gs16_fp32_scales_batch_and_lists():
+@pytest.mark.parametrize("q8_form", GS16_FORMS)
+def test_gs16_fp32_scales_batch_and_lists(q8_form):
     shape, T = GLM16, 6
     hl = gmoe.HostLayer(shape, seed=42, layer=1, scale_mode=gmoe.SYNTH_SCALES_FP32)
-    ctx = gmoe.Context(shape, n_layers=2, max_tokens=T)
+    ctx = gmoe.Context(shape, n_layers=2, max_tokens=T, q8_form=q8_form)
     try:
         ctx.upload(1, hl)
+        ctx.profile(True)
         x = gmoe.activations(42, 1, T, shape.D)
-        print(f"[case] native gs=16 T={T} with per-expert lists", flush=True)
+        print(f"[case] gs=16 form={q8_form} T={T} with per-expert lists", flush=True)
         want = oracle.Oracle("port").layer(shape, hl, x)
         got, st = gmoe.forward_host(ctx, 1, x)
         check(want, got, st, "gs=16 batch")
+        expect_kernels(ctx, q8_form, T)
         # per-expert lists: the ascending tokens of each expert, a brute-force grouping
         offs, toks = [0], []
         for e in range(shape.E):
@@ -75,6 +105,70 @@ def test_gs16_fp32_scales_batch_and_lists():
 
 def test_gs16_routed_experts_off():
     run(GLM16, seed=43, T=2, flags=gmoe.GMOE_FLAG_NO_ROUTED)
+    run(GLM16, seed=43, T=1, flags=gmoe.GMOE_FLAG_NO_ROUTED)
+
+
+@pytest.mark.parametrize("T", [128, 37])
+def test_gs16_prefill_batch(T):
+    """A prefill-sized batch at group size 16 (every expert's list several tiles long at
+    T=128; ragged tiles at T=37) on the grouped GEMMs, against the oracle."""
+    shape = GLM16
+    hl = gmoe.HostLayer(shape, seed=47, layer=1, norm_mode=gmoe.SYNTH_NORM_RANDOM, scale_mode=gmoe.SYNTH_SCALES_FP32)
+    ctx = gmoe.Context(shape, n_layers=2, max_tokens=T)
+    try:
+        ctx.upload(1, hl)
+        ctx.profile(True)
+        x = gmoe.activations(47, 1, T, shape.D)
+        print(f"[case] gs=16 tiled16 prefill T={T}", flush=True)
+        want = oracle.Oracle("port").layer(shape, hl, x)
+        got, st = gmoe.forward_host(ctx, 1, x)
+        check(want, got, st, f"gs=16 prefill T={T}")
+        expect_kernels(ctx, gmoe.GMOE_Q8_AUTO, T)
+    finally:
+        ctx.close()
+
+
+def test_gs16_layers_in_one_launch():
+    """Three gs=16 layers in one k_moe_relay launch (gmoe_forward_layers), against the
+    oracle layer by layer, and the same as three one-layer launches bit for bit."""
+    shape, n = GLM16, 3
+    layers = [gmoe.HostLayer(shape, seed=48, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM,
+                             scale_mode=gmoe.SYNTH_SCALES_FP32) for l in range(1, n + 1)]
+    ctx = gmoe.Context(shape, n_layers=n + 1, max_tokens=1)
+    orc = oracle.Oracle("port")
+    try:
+        for l, hl in enumerate(layers, start=1):
+            ctx.upload(l, hl)
+        assert ctx.stats()["q8_form"] == gmoe.GMOE_Q8_TILED16
+        x = gmoe.activations(48, 3, 1, shape.D)
+        want = x
+        for l, hl in enumerate(layers, start=1):
+            want = orc.layer(shape, hl, want)["x_out"]
+        print("[case] gs=16 tiled16, 3 layers in one launch", flush=True)
+        d_in = gmoe.DeviceArray.from_numpy(x)
+        d_out = gmoe.DeviceArray(x.nbytes)
+        ctx.forward_layers(1, n, 1, d_in.ptr, d_out.ptr)
+        got = d_out.download((1, shape.D), np.float32)
+        assert_close(got, want, "3-layer x_out")
+        one = x
+        for l in range(1, n + 1):
+            one, _ = gmoe.forward_host(ctx, l, one)
+        assert np.array_equal(got.view(np.uint32), one.view(np.uint32)), "one launch vs per-layer launches"
+    finally:
+        ctx.close()
+
+
+def test_tiled16_refused_where_the_relay_kernel_cannot_run(monkeypatch):
+    """GMOE_Q8_TILED16 runs on k_moe_relay only: with it switched off the context is
+    refused with a message; AUTO then keeps group size 16 in the native form."""
+    monkeypatch.setenv("GMOE_DECODE_KERNEL", "0")
+    with pytest.raises(RuntimeError, match="TILED16"):
+        gmoe.Context(GLM16, n_layers=2, max_tokens=1, q8_form=gmoe.GMOE_Q8_TILED16)
+    ctx = gmoe.Context(GLM16, n_layers=2, max_tokens=1)
+    try:
+        assert ctx.stats()["q8_form"] == gmoe.GMOE_Q8_NATIVE
+    finally:
+        ctx.close()
 
 
 def test_gs64_small_shape():
