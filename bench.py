@@ -370,6 +370,8 @@ def main():
                     help="instead of decode, time one MoE layer over T tokens (the grouped expert GEMM path)")
     ap.add_argument("--zipf", action="store_true", help="with --prefill: Zipf(1.2)-skewed router bias")
     ap.add_argument("--prefill-layers", type=int, default=8, help="seeded layers the prefill timings rotate through")
+    ap.add_argument("--group-size", type=int, default=32, choices=(16, 32),
+                    help="with --prefill: expert group size (16: fp32 scales, the exporter's form)")
     ap.add_argument("--e2e", action="store_true",
                     help="only the whole-model decode (a --context-token prompt by batched prefill, then --new tokens)")
     ap.add_argument("--context", type=int, default=4096)
@@ -683,14 +685,15 @@ def e2e_only(args, gmoe, np):
 def prefill_only(args, gmoe, np):
     """--prefill T: one MoE layer over T tokens (T=512 with N(0, 0.01) router bias, or
     T=128 with the Zipf(1.2) bias), the workload of the prefill profiles."""
-    shape = gmoe.GLM47_FLASH
+    shape = gmoe.Shape(group_size=args.group_size)
     T, NL = args.prefill, args.prefill_layers
     bias = gmoe.SYNTH_BIAS_ZIPF if args.zipf else gmoe.SYNTH_BIAS_NORMAL
+    scales = gmoe.SYNTH_SCALES_FP16 if args.group_size == 32 else gmoe.SYNTH_SCALES_FP32
     t0 = time.perf_counter()
     ctx = gmoe.Context(shape, n_layers=NL + 1, max_tokens=T, device=0)
     first = None
     for layer in range(1, NL + 1):
-        hl = gmoe.HostLayer(shape, seed=0, layer=layer, bias_mode=bias)
+        hl = gmoe.HostLayer(shape, seed=0, layer=layer, bias_mode=bias, scale_mode=scales)
         ctx.upload(layer, hl)
         if layer == 1:
             first = hl
@@ -699,7 +702,8 @@ def prefill_only(args, gmoe, np):
     res = time_prefill(gmoe, np, ctx, shape, list(range(1, NL + 1)), T, x0, args.warmup, args.steps,
                        args.profile_steps)
     cpu = None if args.no_cpu else cpu_prefill_baseline(shape, first, x0)
-    name = f"T={T}" + (" Zipf(1.2) routing" if args.zipf else "")
+    name = f"T={T}" + (" Zipf(1.2) routing" if args.zipf else "") + ("" if args.group_size == 32 else
+                                                                    f", group size {args.group_size} fp32 scales")
     out = {
         "metric": f"MoE-layer prefill tokens/s ({name}, GLM-4.7-Flash shape, Q8_0, grouped expert GEMM)",
         "value": res["tokens_s"],

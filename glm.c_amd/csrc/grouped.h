@@ -352,7 +352,7 @@ __device__ __attribute__((always_inline)) static inline void gp_gu_tile(const Gr
 }
 
 template <bool G16>
-__global__ __launch_bounds__(GP_BLOCK, GP_OCC) void k_group_gu(GroupArgs a) {
+__global__ __launch_bounds__(GP_BLOCK, G16 ? 2 : GP_OCC) void k_group_gu(GroupArgs a) {
     __shared__ __align__(16) gp_abuf3_t abuf;
     if ((int)blockIdx.y >= *a.n_tiles) return;
     const GpTile tl = a.tiles[blockIdx.y];

@@ -62,7 +62,7 @@ def odd_heads(seed=26):
     return sp
 
 
-CASES = {"gs16_native": lambda: small(16, gmoe.SYNTH_SCALES_FP32), "gs32_tiled": lambda: small(32, gmoe.SYNTH_SCALES_FP16),
+CASES = {"gs16": lambda: small(16, gmoe.SYNTH_SCALES_FP32), "gs32_tiled": lambda: small(32, gmoe.SYNTH_SCALES_FP16),
          "glm_dims": glm_dims, "glm_heads": glm_heads, "odd_heads": odd_heads}
 TOKENS = [1, 5, 17, 299, 42, 0, 17, 123, 7, 250]
 MODES = ["gpu", "host_attn"]

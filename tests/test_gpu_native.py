@@ -218,7 +218,7 @@ def test_backend_takes_exporter_checkpoints(shape):
 
 
 @pytest.mark.parametrize("gs,scale_mode", [(16, gmoe.SYNTH_SCALES_FP32), (32, gmoe.SYNTH_SCALES_FP16)],
-                         ids=["gs16_native", "gs32_tiled"])
+                         ids=["gs16", "gs32_tiled"])
 def test_backend_runs_a_checkpoint_file(tmp_path, gs, scale_mode):
     """A v4 .bin written by glm_ckpt_write_synth and mapped by glm_ckpt_open (the Runtime
     glm.c's runtime_open would fill) goes to glm_backend_init(BACKEND_HIP); each MoE layer

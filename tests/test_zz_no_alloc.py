@@ -65,3 +65,27 @@ def test_noalloc_refuses_a_run_longer_than_its_workspace(ctx):
     m = re.search(r"at most (\d+) layers", msg)
     assert m, msg
     assert N_UPLOADED <= int(m.group(1)) < 400, msg
+
+
+def test_noalloc_at_group_size_16():
+    """The exporter's form (group size 16, fp32 scales) on the same entry point: two calls in
+    a row, the second over fewer layers, each equal to gmoe_forward_layers bit for bit."""
+    s16 = gmoe.Shape(group_size=16)
+    c = gmoe.Context(s16, n_layers=4, max_tokens=1)
+    try:
+        for l in range(1, 4):
+            c.upload(l, gmoe.HostLayer(s16, seed=32, layer=l, norm_mode=gmoe.SYNTH_NORM_RANDOM,
+                                       scale_mode=gmoe.SYNTH_SCALES_FP32))
+        assert c.stats()["q8_form"] == gmoe.GMOE_Q8_TILED16
+        for first, n in [(1, 3), (2, 1)]:
+            x0 = gmoe.activations(32, first, 1, s16.D)
+            d_in = gmoe.DeviceArray.from_numpy(x0)
+            d_out = gmoe.DeviceArray(x0.nbytes)
+            print(f"[case] noalloc gs=16 layers {first}..{first + n - 1}", flush=True)
+            assert noalloc(c, first, n, d_in, d_out) == 0, gmoe.last_error()
+            got = d_out.download((1, s16.D), np.float32)
+            c.forward_layers(first, n, 1, d_in.ptr, d_out.ptr)
+            want = d_out.download((1, s16.D), np.float32)
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"gs=16 layers {first}+{n}"
+    finally:
+        c.close()
