@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <deque>
 #include <vector>
 #include <stdlib.h>
 #include <string.h>
@@ -114,7 +115,7 @@ struct gmoe_ctx {
     int device = 0;
     int prof_on = 0;
     size_t prof_used = 0;
-    std::vector<ProfRecord> prof;
+    std::deque<ProfRecord> prof;  // a deque: records stay where they are while later ones are added
     gmoe_config cfg{};
     int D = 0, F = 0, E = 0, K = 0, S = 0, L = 0, Tmax = 0;
     size_t stride = 0, off_gq = 0, off_uq = 0, off_dq = 0, off_gs = 0, off_us = 0, off_ds = 0;

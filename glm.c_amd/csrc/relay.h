@@ -938,7 +938,21 @@ __device__ __attribute__((always_inline)) static bool rl_route(const StackArgs &
             for (int i = tid; i < a.D; i += SK_BLOCK) st_f(a.xn + i, sh.xn_r[i]);
     }
     if (!sh.sel_ok) {
-        sk_exact_select(a, L, sh);
+        // glm.c's router replayed on the experts that can still be chosen, from the intervals
+        // rl_select_c left in the slice buffer (the whole replay when forced, when more than
+        // RT_SUB_MAX experts overlap the K-th, and above 128 experts, where the inlined subset
+        // code pushes this kernel into hundreds of bytes of scratch)
+        const unsigned long long *ent0 = (const unsigned long long *)((const int *)sh.dslice + 4 * GM_MAX_E);
+        constexpr int RL_SUB_NV = 4;  // the chains' reads in flight: few registers in this kernel
+        if (C <= 2 && !(a.flags & GMOE_FLAG_EXACT_ROUTER) &&
+            exact_router_subset<RL_SUB_NV>(a.D, a.E, a.K, tid, L.gate_inp, L.bias, sh.xn_r, (float(*)[64])sh.dslice, ent0,
+                                sh.u.s.p, sh.u.s.sel, sh.idx, sh.wk, a.stats, sh.u.s.su, &sh.u.s.nu,
+                                (int)(sizeof(sh.dslice) / sizeof(float)))) {
+            if (tid < a.K) sh.ws[tid] = __fmul_rn(sh.wk[tid], a.routed_scale);
+            __syncthreads();
+        } else {
+            sk_exact_select(a, L, sh);
+        }
         if (tid < SK_SEL_WORDS) {
             unsigned long long word = 0;
             for (int q = 0; q < 4; q++) {

@@ -276,19 +276,22 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
 // best-placed ones and those they overlap) are replayed exactly. Then glm.c's insertion
 // top-k over U's exact scores picks glm.c's experts in glm.c's order, ties to the lower
 // index, and their weights are the exact ones. For |U| <= RT_SUB_MAX the rows of U fit the
-// scratch (RT_XT x 64 floats) in one or two column tiles, every thread forms the products
+// scratch `prod` (cap floats, at least RT_SUB_MAX x 1024) in one or two column tiles, the
+// intervals w0 (read before the scratch is written, so they may lie in it) are no longer
+// needed, every thread forms the products
 // fl(g * xn) in place, and lane u of wave 0 runs expert U[u]'s sequential chain over them:
 // ~2 K dependent adds instead of the full replay's 64 chains fed tile by tile. p keeps
 // the certified probabilities of the experts outside U (they are never chosen). Returns
 // false, before touching any output, when |U| is larger (the caller then runs
 // exact_router); block-uniform.
 #define RT_SUB_MAX 8
+template <int NV>  // 16-byte groups a chain lane reads at once (a multiple of 4 that divides 64)
 __device__ __attribute__((always_inline)) static bool exact_router_subset(int D, int E, int K, int tid,
                                                                           const float *gate_inp, const float *bias_p,
                                                                           const float *xn, float (*prod)[64],
                                                                           const unsigned long long *w0, float *p, float *sel,
                                                                           int *idx, float *wk_out, unsigned long long *stats,
-                                                                          int *s_u, int *s_nu) {
+                                                                          int *s_u, int *s_nu, int cap) {
     const int lane = tid & 63, w = tid >> 6;
     if (w == 0) {
         const int nch = (E + 63) >> 6;
@@ -344,7 +347,7 @@ __device__ __attribute__((always_inline)) static bool exact_router_subset(int D,
     // rows of U in the scratch, tile by tile: [nu][tc] floats, row u's 16-byte group q at
     // q ^ (u % 8) so that the chain lanes' reads (one group of each row) miss no bank
     float *buf = &prod[0][0];
-    const int tc_max = nu * D <= RT_XT * 64 ? D : 1024;  // columns per tile (nu rows of them fit the scratch)
+    const int tc_max = nu * D <= cap ? D : 1024;  // columns per tile (nu rows of them fit the scratch)
     float chain = 0.0f;
     for (int c0 = 0; c0 < D; c0 += tc_max) {
         const int tc = D - c0 < tc_max ? D - c0 : tc_max, ng = tc >> 2;  // D is a multiple of 256
@@ -364,13 +367,13 @@ __device__ __attribute__((always_inline)) static bool exact_router_subset(int D,
         __syncthreads();
         if (w == 0 && lane < nu) {  // infer.c:916-925: the sequential chain of expert U[lane]
             const float *row = buf + lane * tc;
-            for (int q0 = 0; q0 < ng; q0 += 16) {  // ng is a multiple of 64
-                // sixteen groups' reads at once, so that the LDS latency is paid once per 64 adds
-                float4 v[16];
+            for (int q0 = 0; q0 < ng; q0 += NV) {  // ng is a multiple of 64
+                // NV groups' reads at once, so that the LDS latency is paid once per 4 NV adds
+                float4 v[NV];
 #pragma unroll
-                for (int j = 0; j < 16; j++) v[j] = *(const float4 *)(row + 4 * ((q0 + j) ^ (lane & 7)));
+                for (int j = 0; j < NV; j++) v[j] = *(const float4 *)(row + 4 * ((q0 + j) ^ (lane & 7)));
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
+                for (int j = 0; j < NV; j++) {
                     chain = __fadd_rn(chain, v[j].x);
                     chain = __fadd_rn(chain, v[j].y);
                     chain = __fadd_rn(chain, v[j].z);
@@ -612,8 +615,8 @@ __global__ __launch_bounds__(RT_BLOCK) void k_router_tok(RouterArgs a) {
             s_wk[tid] = wk;
         }
         __syncthreads();
-    } else if (a.force_exact || !exact_router_subset(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_w0, s_p, s_sel,
-                                                     s_idx, s_wk, a.stats, s_u, &s_nu)) {
+    } else if (a.force_exact || !exact_router_subset<16>(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_w0, s_p, s_sel,
+                                                     s_idx, s_wk, a.stats, s_u, &s_nu, RT_XT * 64)) {
         exact_router(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_p, s_sel, s_idx, s_wk, a.stats);
     }
     if (tid < K) {
@@ -813,8 +816,8 @@ __global__ __launch_bounds__(RT_BLOCK) void k_rt_select(RouterArgs a, RtParts p)
     } else {
         for (int i = tid; i < D; i += RT_BLOCK) s_xn[i] = a.xn[(size_t)t * D + i];
         __syncthreads();
-        if (a.force_exact || !exact_router_subset(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_w0, s_p, s_sel, s_idx,
-                                                  s_wk, a.stats, s_u, &s_nu))
+        if (a.force_exact || !exact_router_subset<16>(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_w0, s_p, s_sel, s_idx,
+                                                  s_wk, a.stats, s_u, &s_nu, RT_XT * 64))
             exact_router(D, E, K, tid, a.gate_inp, a.bias, s_xn, s_prod, s_p, s_sel, s_idx, s_wk, a.stats);
     }
     if (tid < K) {

@@ -205,6 +205,7 @@ struct SkShared {
         } r;
         struct {  // top-k selection and its exact replay
             float p[GM_MAX_E], sel[GM_MAX_E];
+            int su[RT_SUB_MAX], nu;  // the subset replay's experts (k_moe_relay)
         } s;
         struct {  // expert item
             int8_t dig[3 * GM_MAX_COLS];

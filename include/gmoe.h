@@ -117,7 +117,7 @@ typedef struct gmoe_layer_state {
 typedef struct gmoe_stats {
     int64_t tokens_routed;       /* token-layer routings performed */
     int64_t routing_exact_path;  /* routings that needed the exact sequential-fp32 router replay */
-    int64_t routing_exact_subset; /* of those, batch routings replayed on the few experts that could still be chosen */
+    int64_t routing_exact_subset; /* of those, routings replayed on the few experts that could still be chosen */
     int64_t norm_exact_path;     /* rmsnorms that needed the exact sequential-fp64 sum replay */
     int64_t scale_inexact;       /* weight scales that were not fp16-exact at upload */
     int64_t expf_libc_match;     /* 1: this process runs the glibc release that the GPU's expf exception

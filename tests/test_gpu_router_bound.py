@@ -114,6 +114,34 @@ def test_cancellation_routing_against_oracle(seed):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("E", [64, 128])
+def test_cancellation_routing_relay(E):
+    """The cancellation at T=1 on k_moe_relay (moe_ffn_dim 512: enough expert items for its
+    combine chunks): no certificate holds, and the replay runs on the few experts that can
+    still be chosen (the K - 1 certainly selected ones and the pair)."""
+    shape = gmoe.Shape(dim=2048, moe_ffn_dim=512, n_routed_experts=E, n_experts_used=4)
+    rng = np.random.default_rng(41 + E)
+    orc = oracle.Oracle("port")
+    L = gmoe.HostLayer(shape, seed=41, layer=1, norm_mode=gmoe.SYNTH_NORM_RANDOM)
+    x = gmoe.activations(41, 7, 1, shape.D)
+    make_adversarial(L, orc.layer(shape, L, x)["xn"][0], rng, shape)
+    ctx = gmoe.Context(shape, n_layers=2, max_tokens=1)
+    try:
+        ctx.upload(1, L)
+        ctx.profile(True)
+        print(f"[case] cancellation on k_moe_relay E={E}", flush=True)
+        want = orc.layer(shape, L, x)
+        got, st = gmoe.forward_host(ctx, 1, x)
+        np.testing.assert_array_equal(st["topk_idx"], want["topk_idx"], err_msg="relay routing")
+        assert_close(got, want["x_out"], "relay x_out")
+        assert "k_moe_relay" in ctx.profile_read()
+        stats = ctx.stats()
+        assert stats["routing_exact_path"] >= 1 and stats["routing_exact_subset"] >= 1, stats
+    finally:
+        ctx.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("E", [64, 128])
 def test_cancellation_routing_batch(E):
     """The batch router's certificates under the same cancellation: with 64 experts the
     four-quarter partial sums and their joined bound, with 128 the one-block-per-token
@@ -144,14 +172,15 @@ def test_cancellation_routing_batch(E):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("E", [64, 128])
-def test_all_experts_tied_batch(E):
+@pytest.mark.parametrize("E,T", [(64, 8), (128, 8), (64, 1), (128, 1)])
+def test_all_experts_tied_batch(E, T):
     """Every expert's gate row the same and no bias: all E scores tie exactly, so no
-    certificate holds and no expert can be ruled out. The batch router then replays
-    every expert's chain (more than the subset replay holds), and glm.c's insertion
-    top-k breaks the tie by index: experts 0..K-1, in that order."""
-    shape = gmoe.Shape(dim=2048, moe_ffn_dim=256, n_routed_experts=E, n_experts_used=4)
-    T = 8
+    certificate holds and no expert can be ruled out. The router (the batch routers at
+    T=8, the decode kernel at T=1) then replays every expert's chain (more than the subset
+    replay holds), and glm.c's insertion top-k breaks the tie by index: experts 0..K-1, in
+    that order."""
+    # at T=1, moe_ffn_dim 512 so that the shape runs on k_moe_relay
+    shape = gmoe.Shape(dim=2048, moe_ffn_dim=512 if T == 1 else 256, n_routed_experts=E, n_experts_used=4)
     orc = oracle.Oracle("port")
     L = gmoe.HostLayer(shape, seed=41, layer=1, norm_mode=gmoe.SYNTH_NORM_RANDOM)
     L.gate_inp[:] = L.gate_inp[0]
