@@ -277,6 +277,30 @@ def gs16_form(gmoe, np, args, L):
         ctx.close()
 
 
+def gs16_only(args, gmoe, np):
+    """--group-size 16 without --prefill: the exporter's form alone (gs16_form), one JSON line."""
+    if gmoe.device_count() < 1:
+        raise SystemExit("no HIP device visible")
+    res = gs16_form(gmoe, np, args, args.layers)
+    out = {
+        "metric": "MoE-stack decode tokens/s (46 GLM-4.7-Flash MoE layers, Q8_0 at group size 16 with fp32 scales, T=1)",
+        "value": res["decode_tokens_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 / res["decode_tokens_s"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xint8->int32 + fp32",
+        "data": "synthetic (seeded random-init Q8_0 weights, fp32 scales, N(0,1) input)",
+        "config": {"workload": res["workload"], "layers": args.layers},
+        **{k: v for k, v in res.items() if k not in ("workload", "decode_tokens_s")},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def backend_hook_us(gmoe, np, shape, host_layers, x0, tokens=2):
     """glm.c's drop-in path: glm_backend_init(BACKEND_HIP) uploads the layers, then
     glm_backend_try_hip_moe runs each MoE layer on a RunState in host memory (an H2D copy of
@@ -371,7 +395,8 @@ def main():
     ap.add_argument("--zipf", action="store_true", help="with --prefill: Zipf(1.2)-skewed router bias")
     ap.add_argument("--prefill-layers", type=int, default=8, help="seeded layers the prefill timings rotate through")
     ap.add_argument("--group-size", type=int, default=32, choices=(16, 32),
-                    help="with --prefill: expert group size (16: fp32 scales, the exporter's form)")
+                    help="16: the exporter's form (fp32 scales); with --prefill that prefill workload, alone the "
+                         "46-layer decode step and a T=512 prefill layer")
     ap.add_argument("--e2e", action="store_true",
                     help="only the whole-model decode (a --context-token prompt by batched prefill, then --new tokens)")
     ap.add_argument("--context", type=int, default=4096)
@@ -406,6 +431,8 @@ def main():
         return prefill_only(args, gmoe, np)
     if args.e2e:
         return e2e_only(args, gmoe, np)
+    if args.group_size == 16:
+        return gs16_only(args, gmoe, np)
 
     shape = gmoe.GLM47_FLASH
     L = args.layers
