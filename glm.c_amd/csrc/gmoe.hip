@@ -161,6 +161,7 @@ struct gmoe_ctx {
     // input and all of its outputs with one copy each way.
     uint8_t *obs = nullptr, *obs_host = nullptr;
     size_t obs_bytes = 0;
+    float *obs_pack = nullptr;  // a T-token call's parts of obs back to back, and the launch's error word
     int *sk_error_host_dev = nullptr;  // its device address
     unsigned sk_spin_limit = SK_SPIN_LIMIT;
     StackLayer *sk_layers = nullptr;  // [L], device
@@ -234,7 +235,7 @@ static void free_ctx(gmoe_ctx *c) {
         }
         delete[] c->layers;
     }
-    void *bufs[] = {c->obs, c->topk_ws, c->h, c->y,
+    void *bufs[] = {c->obs, c->obs_pack, c->topk_ws, c->h, c->y,
                     c->stage, c->tok_counter, c->panel_counter, c->offsets, c->tokens, c->slots, c->hist_idx, c->hist_w,
                     c->stats_dev, c->staging, c->sk_ws, c->sk_ctr, c->sk_error, c->sk_par_dev,
                     c->sk_layers, c->sk_trace, c->xspl, c->hspl, c->xexp, c->hexp, c->pair_row, c->n_tiles,
@@ -356,6 +357,7 @@ extern "C" int gmoe_create(gmoe_ctx **out, int device, const gmoe_config *cfg) {
         // topk_idx [T][K] -- 4-byte elements, in this order (obs_slice)
         c->obs_bytes = (4 * T * D + T * E + 2 * T * K + 1) * sizeof(float);
         rc |= dev_alloc(&c->obs, c->obs_bytes);
+        rc |= dev_alloc(&c->obs_pack, c->obs_bytes / sizeof(float));
         if (!rc && hipHostMalloc((void **)&c->obs_host, c->obs_bytes, hipHostMallocDefault) != hipSuccess) {
             c->obs_host = nullptr;
             set_err("hipHostMalloc of %zu bytes failed", c->obs_bytes);
@@ -1314,6 +1316,30 @@ static int copy_out(void *dst, const void *src, size_t bytes) {
 
 extern "C" int gmoe_read_layer_state(gmoe_ctx *c, gmoe_layer_state *o, void *stream);
 
+// The first T rows of obs's seven arrays (x, xn, shared_out, routed_out [T][D]; router_prob
+// [T][E]; topk_w, topk_idx [T][K]) back to back into pack, then the persistent launch's error
+// word (0 without one): a T-token call's observables leave the device in one copy.
+__global__ __launch_bounds__(256) void k_obs_pack(const float *__restrict__ obs, float *__restrict__ pack, int T, int TM,
+                                                  int D, int E, int K, const int *__restrict__ err) {
+    const size_t TD = (size_t)T * D, n = 4 * TD + (size_t)T * E + 2 * (size_t)T * K;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i <= n; i += (size_t)gridDim.x * 256) {
+        if (i == n) {
+            pack[n] = __int_as_float(err ? *err : 0);
+            continue;
+        }
+        size_t src;
+        if (i < 4 * TD) {
+            src = (i / TD) * (size_t)TM * D + i % TD;  // array i / TD, row-major [T][D] prefix
+        } else {
+            const size_t j = i - 4 * TD, TE = (size_t)T * E, TK = (size_t)T * K;
+            const size_t base = 4 * (size_t)TM * D;
+            src = j < TE ? base + j : j < TE + TK ? base + (size_t)TM * E + (j - TE)
+                                                   : base + (size_t)TM * E + (size_t)TM * K + (j - TE - TK);
+        }
+        pack[i] = obs[src];
+    }
+}
+
 extern "C" int gmoe_forward_host(gmoe_ctx *c, int layer, int T, const float *x_in, float *x_out, int flags,
                                  gmoe_layer_state *state) {
     if (!c || !x_in || !x_out) {
@@ -1333,37 +1359,33 @@ extern "C" int gmoe_forward_host(gmoe_ctx *c, int layer, int T, const float *x_i
     HIP_OK(hipMemcpyAsync(c->x_host_io, h, bytes, hipMemcpyHostToDevice, nullptr));
     int rc = gmoe_forward(c, layer, T, c->x_host_io, c->x_host_io, flags, nullptr);
     if (rc) return rc;
-    // out: x and the observables in one copy of the block (its used parts when T < max_tokens),
-    // and the launch's device error word, then one synchronisation
-    int *err_h = (int *)(c->obs_host + c->obs_bytes - sizeof(int));
-    *err_h = 0;
-    if (T_ == TM) {
-        HIP_OK(hipMemcpyAsync(c->obs_host, c->obs, c->obs_bytes - sizeof(int), hipMemcpyDeviceToHost, nullptr));
-    } else {
-        const size_t parts[][2] = {{0, T_ * D}, {TM * D, T_ * D}, {2 * TM * D, T_ * D}, {3 * TM * D, T_ * D},
-                                   {4 * TM * D, T_ * E}, {4 * TM * D + TM * E, T_ * K}, {4 * TM * D + TM * E + TM * K, T_ * K}};
-        for (const auto &pt : parts)
-            HIP_OK(hipMemcpyAsync(c->obs_host + pt[0] * 4, c->obs + pt[0] * 4, pt[1] * 4, hipMemcpyDeviceToHost, nullptr));
-    }
-    if (c->stack_launched && c->stack_last)
-        HIP_OK(hipMemcpyAsync(err_h, c->stack_error_dev, sizeof(int), hipMemcpyDeviceToHost, nullptr));
+    // out: x, the observables and the launch's error word packed on the device, one copy, one
+    // synchronisation
+    const size_t TD = T_ * D, n = 4 * TD + T_ * E + 2 * T_ * K;
+    const int *err_dev = c->stack_launched && c->stack_last ? c->stack_error_dev : nullptr;
+    hipLaunchKernelGGL(k_obs_pack, dim3((unsigned)std::min<size_t>((n + 256) / 256, 1024)), dim3(256), 0, nullptr,
+                       (const float *)c->obs, c->obs_pack, T, (int)TM, (int)D, (int)E, (int)K, err_dev);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipMemcpyAsync(c->obs_host, c->obs_pack, (n + 1) * sizeof(float), hipMemcpyDeviceToHost, nullptr));
     HIP_OK(hipStreamSynchronize(nullptr));
+    const float *ho = (const float *)c->obs_host;
     // a timed-out launch leaves x_out untouched, so a caller may rerun the layer from it
     const int launch_rc = take_launch_error(c);
-    if (launch_rc || *err_h) {
+    int err_word = 0;
+    memcpy(&err_word, ho + n, sizeof(int));
+    if (launch_rc || err_word) {
         if (!launch_rc) relay_reset(c);
         set_err("%s", k_timeout_msg);
         return GMOE_ERR_HIP;
     }
-    memcpy(x_out, h, bytes);
+    memcpy(x_out, ho, bytes);
     if (!state) return GMOE_OK;
-    const float *ho = (const float *)c->obs_host;
-    if (state->xn) memcpy(state->xn, ho + TM * D, bytes);
-    if (state->shared_out) memcpy(state->shared_out, ho + 2 * TM * D, bytes);
-    if (state->routed_out) memcpy(state->routed_out, ho + 3 * TM * D, bytes);
-    if (state->router_prob) memcpy(state->router_prob, ho + 4 * TM * D, T_ * E * sizeof(float));
-    if (state->topk_w) memcpy(state->topk_w, ho + 4 * TM * D + TM * E, T_ * K * sizeof(float));
-    if (state->topk_idx) memcpy(state->topk_idx, ho + 4 * TM * D + TM * E + TM * K, T_ * K * sizeof(int));
+    if (state->xn) memcpy(state->xn, ho + TD, bytes);
+    if (state->shared_out) memcpy(state->shared_out, ho + 2 * TD, bytes);
+    if (state->routed_out) memcpy(state->routed_out, ho + 3 * TD, bytes);
+    if (state->router_prob) memcpy(state->router_prob, ho + 4 * TD, T_ * E * sizeof(float));
+    if (state->topk_w) memcpy(state->topk_w, ho + 4 * TD + T_ * E, T_ * K * sizeof(float));
+    if (state->topk_idx) memcpy(state->topk_idx, ho + 4 * TD + T_ * E + T_ * K, T_ * K * sizeof(int));
     if (state->expert_offsets || state->expert_tokens) {
         // the per-expert lists (dispatched on demand at T=1) take the general read-back
         gmoe_layer_state lists;
