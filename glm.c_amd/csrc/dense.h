@@ -583,3 +583,46 @@ __global__ __launch_bounds__(DM_BLOCK) void k_attn_merge(AttnArgs a) {
         a.ctx[(size_t)h * a.kv + d] = __fmul_rn(t, __fdiv_rn(1.0f, l));
     }
 }
+
+// k_attn_merge for at most AM_SMALL ranges per token (the batch attention's position chunks,
+// attn.h): one wave per (token, head), lane l taking columns l + 64 j, with the same operations
+// in the same order as k_attn_merge (a range per lane for the maximum and the sum; per column
+// the ranges w and w + 4 of "wave" w, then (s0 + s1) + (s2 + s3)), so its results are
+// bit-identical, in one wave instead of a block of four per 64 columns and three barriers.
+#define AM_SMALL 8
+__global__ __launch_bounds__(DM_BLOCK) void k_attn_merge_small(AttnArgs a0, int n) {
+    const int lane = threadIdx.x & 63, pair = blockIdx.x * (DM_BLOCK / 64) + (threadIdx.x >> 6);
+    if (pair >= n * a0.H) return;
+    const int t = pair / a0.H, h = pair % a0.H;
+    AttnArgs a = a0;
+    attn_token(a, t);
+    const int nc = min(a.nblk, a.pos + 1);  // <= AM_SMALL (the caller's guarantee)
+    const float raw = lane < nc ? a.part_ml[((size_t)lane * a.H + h) * 2] : -INFINITY;
+    const float m = wave_max_dpp_f(fmaxf(-INFINITY, raw));
+    float e = 0.0f, lp = 0.0f;
+    if (lane < nc) {
+        e = expf(__fsub_rn(raw, m));
+        lp = fmaf(a.part_ml[((size_t)lane * a.H + h) * 2 + 1], e, 0.0f);
+    }
+    const float l = __fadd_rn(__fadd_rn(gv_reduce<64>(lp), 0.0f), __fadd_rn(0.0f, 0.0f));
+    float wgt[AM_SMALL];
+#pragma unroll
+    for (int c = 0; c < AM_SMALL; c++) wgt[c] = readlane_f(e, c);
+    const float inv = __fdiv_rn(1.0f, l);
+    const size_t cs = (size_t)a.H * a.kv;  // one range's stride
+    const float *pc = a.part_ctx + (size_t)h * a.kv;
+    for (int d = lane; d < a.kv; d += 64) {
+        float v[AM_SMALL];
+#pragma unroll
+        for (int c = 0; c < AM_SMALL; c++) v[c] = c < nc ? pc[(size_t)c * cs + d] : 0.0f;
+        float sw[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            float sv = 0.0f;
+            if (w < nc) sv = fmaf(wgt[w], v[w], sv);
+            if (w + 4 < nc) sv = fmaf(wgt[w + 4], v[w + 4], sv);
+            sw[w] = sv;
+        }
+        a.ctx[(size_t)h * a.kv + d] = __fmul_rn(__fadd_rn(__fadd_rn(sw[0], sw[1]), __fadd_rn(sw[2], sw[3])), inv);
+    }
+}

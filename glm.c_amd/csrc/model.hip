@@ -343,11 +343,24 @@ void launch_attn_cache(gmoe_model *m, AttnArgs aa, hipStream_t st) {
 // cache entries already written): one launch of ranges for the whole batch (grid z = token,
 // up to AT_PREFILL_RANGES ranges each, so that the tokens' blocks share the CUs), then one
 // merge.
+// The merge of n tokens' ranges: a wave per (token, head) where at most AM_SMALL ranges
+// were written (GMOE_ATTN_MERGE_WIDE=1 forces k_attn_merge's block per 64 columns, a
+// diagnostic: the two give the same bits).
+void launch_attn_merge(const AttnArgs &aa, int n, hipStream_t st) {
+    const char *env = getenv("GMOE_ATTN_MERGE_WIDE");
+    const bool wide = env && env[0] == '1';
+    if (aa.nblk <= AM_SMALL && !wide)
+        hipLaunchKernelGGL(k_attn_merge_small, dim3((unsigned)((n * aa.H + DM_BLOCK / 64 - 1) / (DM_BLOCK / 64))),
+                           dim3(DM_BLOCK), 0, st, aa, n);
+    else
+        hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64, (unsigned)n), dim3(DM_BLOCK), 0, st, aa);
+}
+
 void launch_attn_cache_batch(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) {
     const int groups = (aa.H + aa.hg - 1) / aa.hg;
     aa.nblk = std::min(AT_PREFILL_RANGES, std::max(1, m->n_cu / groups));
     hipLaunchKernelGGL(k_attn_chunk, dim3(aa.nblk, groups, (unsigned)n), dim3(AT_BLOCK), 0, st, aa);
-    hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64, (unsigned)n), dim3(DM_BLOCK), 0, st, aa);
+    launch_attn_merge(aa, n, st);
 }
 
 // Whether k_attn_tile takes this model's attention: 16-column groups of the entry and of
@@ -378,7 +391,7 @@ void launch_attn_tile(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) {
     case 2: hipLaunchKernelGGL(k_attn_tile<2>, grid, dim3(AQ_BLOCK), 0, st, g); break;
     default: hipLaunchKernelGGL(k_attn_tile<3>, grid, dim3(AQ_BLOCK), 0, st, g); break;
     }
-    hipLaunchKernelGGL(k_attn_merge, dim3(aa.H, aa.kv / 64, (unsigned)n), dim3(DM_BLOCK), 0, st, aa);
+    launch_attn_merge(aa, n, st);
 }
 static_assert(aq_rounds(AQ_KQ_MAX) <= 3, "k_attn_tile instances cover the widest entry");
 

@@ -112,3 +112,29 @@ def test_prefill_at_an_offset_and_past_the_cache(tmp_path, monkeypatch):
     finally:
         dec.free()
         ck.close()
+
+
+def test_merge_paths_agree_bit_for_bit(tmp_path, monkeypatch):
+    """The batch attention's merge by one wave per (token, head) and k_attn_merge's block per
+    64 columns (GMOE_ATTN_MERGE_WIDE=1) give the same bits: the prefill's logits and final x
+    over a 400-token prompt in one batch (eight position chunks per token)."""
+    monkeypatch.setenv("GLM_HIP_PREFILL_BATCH", "512")
+    monkeypatch.delenv("GLM_HIP_HOST_ATTN", raising=False)
+    sp = small(32, gmoe.SYNTH_SCALES_FP16, n_layers=3, seed=28, seq_len=512)
+    rng = np.random.default_rng(28)
+    tokens = [1] + [int(t) for t in rng.integers(3, sp.vocab_size, 399)]
+    out = {}
+    for wide in ("0", "1"):
+        monkeypatch.setenv("GMOE_ATTN_MERGE_WIDE", wide)
+        d = tmp_path / f"wide{wide}"
+        d.mkdir()
+        _, ck, dec = open_decoder(d, sp, len(tokens) + 1)
+        try:
+            print(f"[case] merge paths: GMOE_ATTN_MERGE_WIDE={wide}", flush=True)
+            logits = dec.prefill(tokens)
+            out[wide] = (logits.copy(), final_x(dec))
+        finally:
+            dec.free()
+            ck.close()
+    assert np.array_equal(out["0"][0].view(np.uint32), out["1"][0].view(np.uint32)), "prefill logits"
+    assert np.array_equal(out["0"][1].view(np.uint32), out["1"][1].view(np.uint32)), "final x"
