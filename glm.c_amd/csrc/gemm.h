@@ -65,6 +65,7 @@ typedef unsigned qg_u2 __attribute__((ext_vector_type(2)));
 // mean, 1 / sqrtf of mean + 1e-5, then (x * inv) * w), else v = x; then
 // sp[t][0][:] = fp16(v 2^-e), sp[t][1][:] = fp16(v 2^-e - hi), ex[t] = e, with e from
 // max |v| so that the row's largest value sits near 2^14.
+#define QG_SPLIT_MAX 40  // row values a thread holds: rows of up to 40 x QG_BLOCK = 10240 columns
 __global__ __launch_bounds__(QG_BLOCK) void k_norm_split(const float *__restrict__ x, int ldx, int n,
                                                          const float *__restrict__ norm, __half *__restrict__ sp,
                                                          int *__restrict__ ex) {
@@ -72,20 +73,33 @@ __global__ __launch_bounds__(QG_BLOCK) void k_norm_split(const float *__restrict
     __shared__ float red_f[QG_BLOCK / 64];
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const float *src = x + (size_t)t * ldx;
+    // the row read once: thread tid holds columns tid + QG_BLOCK k
+    float v[QG_SPLIT_MAX], nw[QG_SPLIT_MAX];
+#pragma unroll
+    for (int k = 0; k < QG_SPLIT_MAX; k++) {
+        const int i = tid + QG_BLOCK * k;
+        v[k] = i < n ? src[i] : 0.0f;
+        nw[k] = norm && i < n ? norm[i] : 0.0f;
+    }
     float inv = 1.0f;
     if (norm) {
         double ss = 0.0;
-        for (int i = tid; i < n; i += QG_BLOCK) ss += (double)src[i] * (double)src[i];
+#pragma unroll
+        for (int k = 0; k < QG_SPLIT_MAX; k++)
+            if (tid + QG_BLOCK * k < n) ss += (double)v[k] * (double)v[k];
         ss = wave_sum_dpp(ss);
         if (lane == 0) red_d[w] = ss;
         __syncthreads();
         ss = (red_d[0] + red_d[1]) + (red_d[2] + red_d[3]);
         const float mean = (float)(ss / (double)n);
         inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, 1e-5f)));
+#pragma unroll
+        for (int k = 0; k < QG_SPLIT_MAX; k++) v[k] = __fmul_rn(__fmul_rn(v[k], inv), nw[k]);
     }
-    auto val = [&](int i) { return norm ? __fmul_rn(__fmul_rn(src[i], inv), norm[i]) : src[i]; };
     float mx = 0.0f;
-    for (int i = tid; i < n; i += QG_BLOCK) mx = fmaxf(mx, fabsf(val(i)));
+#pragma unroll
+    for (int k = 0; k < QG_SPLIT_MAX; k++)
+        if (tid + QG_BLOCK * k < n) mx = fmaxf(mx, fabsf(v[k]));
     mx = wave_max_f(mx);
     if (lane == 0) red_f[w] = mx;
     __syncthreads();
@@ -98,18 +112,15 @@ __global__ __launch_bounds__(QG_BLOCK) void k_norm_split(const float *__restrict
     }
     if (tid == 0) ex[t] = e;
     __half *hi = sp + (size_t)t * 2 * n, *lo = hi + n;
-    for (int i = tid * 8; i < n; i += QG_BLOCK * 8) {
-        unsigned hw[4], lw[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float x0 = ldexpf(val(i + 2 * k), -e), x1 = ldexpf(val(i + 2 * k + 1), -e);
-            const __half h0 = __float2half_rn(x0), h1 = __float2half_rn(x1);
-            const __half l0 = __float2half_rn(x0 - __half2float(h0)), l1 = __float2half_rn(x1 - __half2float(h1));
-            hw[k] = (unsigned)__half_as_ushort(h0) | ((unsigned)__half_as_ushort(h1) << 16);
-            lw[k] = (unsigned)__half_as_ushort(l0) | ((unsigned)__half_as_ushort(l1) << 16);
+    for (int k = 0; k < QG_SPLIT_MAX; k++) {
+        const int i = tid + QG_BLOCK * k;
+        if (i < n) {
+            const float xs = ldexpf(v[k], -e);
+            const __half h = __float2half_rn(xs);
+            hi[i] = h;
+            lo[i] = __float2half_rn(xs - __half2float(h));
         }
-        *(uint4 *)(hi + i) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        *(uint4 *)(lo + i) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
 }
 

@@ -251,6 +251,7 @@ bool fuse_second(GemvArgs &a, const GemvArgs &b) {
 }
 
 constexpr int kMaxCols = 16 * 64 * 10;  // the widest k_gemv instance
+static_assert(kMaxCols <= QG_SPLIT_MAX * QG_BLOCK, "k_norm_split holds a whole row");
 
 int check_config(const gmoe_model_config &c) {
     const int gs = c.group_size;
