@@ -253,3 +253,21 @@ def test_backend_runs_a_checkpoint_file(tmp_path, gs, scale_mode):
     finally:
         model.free()
         ck.close()
+
+
+@pytest.mark.parametrize("shape", [
+    gmoe.Shape(dim=1024, moe_ffn_dim=512, n_routed_experts=64, n_experts_used=4, group_size=16),
+    gmoe.Shape(dim=2048, moe_ffn_dim=512, n_routed_experts=128, n_experts_used=6, group_size=16),
+    gmoe.Shape(dim=512, moe_ffn_dim=512, n_routed_experts=256, n_experts_used=8, group_size=16),
+], ids=["d1024_e64", "d2048_e128", "d512_e256"])
+@pytest.mark.parametrize("T", [1, 9])
+def test_gs16_tiled_other_shapes(shape, T):
+    """The group-size-16 tiled form beyond the GLM shape: narrower rows (the relay kernel's
+    shared-memory scale path), 128 and 256 experts (its wider selections), on the relay
+    kernel at T=1 and the grouped GEMMs at T=9."""
+    ran, stats = run(shape, seed=49, T=T, n_layers=2)
+    assert stats["q8_form"] == gmoe.GMOE_Q8_TILED16, stats
+    if T == 1:
+        assert "k_moe_relay" in ran, ran
+    else:
+        assert "k_act_split" in ran and "gate_up" in ran, ran
