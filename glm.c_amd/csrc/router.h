@@ -703,15 +703,19 @@ __global__ __launch_bounds__(RT_BLOCK) void k_rt_norm(RouterArgs a, int T) {
 // 64 columns, [64 experts][16 four-column groups] with group g of row e at slot
 // g ^ (e % 16) (so that the 64 lanes' reads of one group spread over the banks), two
 // tiles in flight; xn's quarter of the block's tokens is staged once.
+#define RT_DOT_STAGES 3  // router-row tiles in shared memory: two in flight while one is used
 __global__ __launch_bounds__(RT_BLOCK) void k_rt_dots(RouterArgs a, RtParts p, int T) {
-    __shared__ __align__(16) float4 gt[2][64 * 16];
-    __shared__ __align__(16) float xs[4][RT_QMAX];
+    __shared__ __align__(16) float4 gt[RT_DOT_STAGES][64 * 16];
+    __shared__ __align__(16) float xs[4 * RT_QMAX];  // the block's 4 tokens' quarters, Lq floats apart
     const int tg = blockIdx.x, q = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int D = a.D, E = a.E, Lq = D / 4, c0 = q * Lq, ntile = Lq / 64;
     const int t = 4 * tg + w;
-    for (int i = tid; i < 4 * Lq; i += RT_BLOCK) {
-        const int tw = i / Lq, k = i - tw * Lq, tt = 4 * tg + tw;
-        xs[tw][k] = tt < T ? a.xn[(size_t)tt * D + c0 + k] : 0.0f;
+    // The quarters by DMA too, issued first: Lq pieces of 16 bytes (Lq / 4 a row), 64 to a
+    // wave's DMA, dealt round the waves. A token past T reads token T - 1 (its sums are not stored).
+    for (int s = w; s < Lq / 64; s += 4) {
+        const int piece = 64 * s + lane, tw = piece / (Lq / 4), k = 4 * (piece - tw * (Lq / 4));
+        const int tt = min(4 * tg + tw, T - 1);
+        dma16_untracked(gbl(a.xn + (size_t)tt * D + c0 + k), (lds_void *)(xs + 256 * s));
     }
     auto stage = [&](int j, int buf) {  // 1024 pieces of 16 bytes: four per lane
 #pragma unroll
@@ -721,15 +725,23 @@ __global__ __launch_bounds__(RT_BLOCK) void k_rt_dots(RouterArgs a, RtParts p, i
             dma16_untracked(gbl(a.gate_inp + (size_t)ee * D + c0 + 64 * j + 4 * g), (lds_void *)(gt[buf] + (4 * w + i) * 64));
         }
     };
+    // tiles of 64 columns, two ahead. Each stage() is four DMAs a thread; the waits below
+    // count them in order, so vmcnt(4) after stage(1) also covers the quarters' DMAs.
+    // The barriers are s_barrier in inline assembly after an exact wait (with the shared-memory
+    // stores and reads done): __syncthreads() would also wait for the DMAs still in flight.
     stage(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    if (ntile > 1) {
+        stage(1, 1);
+        asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
     double acc = 0.0, sp = 0.0;
     float sa = 0.0f;
     for (int j = 0; j < ntile; j++) {
-        if (j + 1 < ntile) stage(j + 1, (j + 1) & 1);
-        const float4 *gb = gt[j & 1] + lane * 16;
-        const float *xw = xs[w] + 64 * j;
+        if (j + 2 < ntile) stage(j + 2, (j + 2) % RT_DOT_STAGES);
+        const float4 *gb = gt[j % RT_DOT_STAGES] + lane * 16;
+        const float *xw = xs + w * Lq + 64 * j;
 #pragma unroll
         for (int g = 0; g < 16; g++) {
             const float4 gv = gb[g ^ (lane & 15)];
@@ -742,8 +754,12 @@ __global__ __launch_bounds__(RT_BLOCK) void k_rt_dots(RouterArgs a, RtParts p, i
                 sa = fmaf(fabsf(gg[c]), fabsf(xx[c]), sa);
             }
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the next tile is in shared memory
-        __syncthreads();                                    // and every wave is done with this one
+        // tile j + 1 is in shared memory (tile j + 2's DMAs may still be in flight), and after
+        // the barrier every wave is done with tile j, whose buffer tile j + 3 refills
+        if (j + 2 < ntile)
+            asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
     if (t < T && lane < E) {
         const size_t o = ((size_t)t * 4 + q) * E + lane;
