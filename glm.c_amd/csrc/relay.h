@@ -13,8 +13,10 @@
 // word of the layers it runs, so before the store lands a word still holds the other
 // parity. A reader re-reads until every word it needs carries the current parity, then
 // clears the bit.
-// (x is rounded toward zero to an even significand at every layer boundary, so its value
-// does not depend on the tag.) The stage entries keep stack.h's reset-to-unset form.
+// (x and the items' partial sums are rounded to an even significand, with no direction on
+// average (rl_even), at every layer, so their values do not depend on the tag; the launch's
+// final x is rounded the same way, so one launch of n layers gives the bits of n launches
+// of one.) The stage entries keep stack.h's reset-to-unset form.
 //
 // Roles (G blocks, two per CU: blocks b and b + G/2 share a CU):
 //  * routed items, blocks 0 .. K*F/16-1: poll x, compute xn and its digit form themselves
@@ -88,10 +90,18 @@ __device__ static inline unsigned rl_par(const StackArgs &a, int li) {
     const int q = a.par_base + li;
     return (unsigned)(rl_par_sh[q >> 6] >> (q & 63)) & 1u;
 }
-__device__ static inline unsigned rl_tag(float v, unsigned p) { return (__float_as_uint(v) & ~1u) | p; }
+// v rounded to an even significand, the value a tagged word carries: an odd significand
+// goes to the neighbour whose bit 1 is clear (round half to even one bit up), so the
+// rounding has no direction on average (|error| <= 1 ulp, mean 0). In bits, odd b becomes
+// (b + 1) with its two lowest bits cleared (b + 1 when bit 1 was set, b - 1 when it was
+// not) and even b stays: four integer operations, no branch. (Like any rounding up, the
+// largest finite value can become infinity; x and the partial sums stay far below it.)
+__device__ static inline float rl_even(float v) {
+    const unsigned b = __float_as_uint(v), m = b & 1u;
+    return __uint_as_float((b + m) & ~(m | (m << 1)));
+}
+__device__ static inline unsigned rl_tag(float v, unsigned p) { return __float_as_uint(rl_even(v)) | p; }
 __device__ static inline float rl_untag(unsigned b) { return __uint_as_float(b & ~1u); }
-// v rounded toward zero to an even significand: the value a tagged word carries
-__device__ static inline float rl_even(float v) { return __uint_as_float(__float_as_uint(v) & ~1u); }
 __device__ static inline unsigned long long rl_tag_d(double v, unsigned p) {
     return ((unsigned long long)__double_as_longlong(v) & ~1ull) | p;
 }
@@ -764,6 +774,7 @@ __device__ __attribute__((always_inline)) static bool rl_combine(const StackArgs
                 if (k < K && sh.idx[k] >= 0) acc = __fadd_rn(acc, __fmul_rn(sh.ws[k], sh.u.c.y[k][tid]));
         }
         const float shv = sh.u.c.y[K][tid];
+        // the launch's output too, so that one launch of n layers equals n launches of one
         const float xo = rl_even(__fadd_rn(xr, __fadd_rn(shv, acc)));
         if (last) {
             st_f(a.x_out + r, xo);
