@@ -955,6 +955,7 @@ __device__ __attribute__((always_inline)) static bool rl_route(const StackArgs &
         // code pushes this kernel into hundreds of bytes of scratch)
         const unsigned long long *ent0 = (const unsigned long long *)((const int *)sh.dslice + 4 * GM_MAX_E);
         constexpr int RL_SUB_NV = 4;  // the chains' reads in flight: few registers in this kernel
+        static_assert(sizeof(sh.dslice) / sizeof(float) >= RT_SUB_MAX * 260, "the replay's rows fit the slice buffer");
         if (C <= 2 && !(a.flags & GMOE_FLAG_EXACT_ROUTER) &&
             exact_router_subset<RL_SUB_NV>(a.D, a.E, a.K, tid, L.gate_inp, L.bias, sh.xn_r, (float(*)[64])sh.dslice, ent0,
                                 sh.u.s.p, sh.u.s.sel, sh.idx, sh.wk, a.stats, sh.u.s.su, &sh.u.s.nu,

@@ -276,7 +276,7 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
 // best-placed ones and those they overlap) are replayed exactly. Then glm.c's insertion
 // top-k over U's exact scores picks glm.c's experts in glm.c's order, ties to the lower
 // index, and their weights are the exact ones. For |U| <= RT_SUB_MAX the rows of U fit the
-// scratch `prod` (cap floats, at least RT_SUB_MAX x 1024) in one or two column tiles, the
+// scratch `prod` (cap floats, at least RT_SUB_MAX x 260) in column tiles, the
 // intervals w0 (read before the scratch is written, so they may lie in it) are no longer
 // needed, every thread forms the products
 // fl(g * xn) in place, and lane u of wave 0 runs expert U[u]'s sequential chain over them:
@@ -285,6 +285,7 @@ __device__ __attribute__((always_inline)) static void exact_router(int D, int E,
 // false, before touching any output, when |U| is larger (the caller then runs
 // exact_router); block-uniform.
 #define RT_SUB_MAX 8
+static_assert(RT_XT * 64 >= RT_SUB_MAX * 260, "the batch routers' replay scratch holds RT_SUB_MAX padded 256-column rows");
 template <int NV>  // 16-byte groups a chain lane reads at once (a multiple of 4 that divides 64)
 __device__ __attribute__((always_inline)) static bool exact_router_subset(int D, int E, int K, int tid,
                                                                           const float *gate_inp, const float *bias_p,
@@ -344,34 +345,42 @@ __device__ __attribute__((always_inline)) static bool exact_router_subset(int D,
     if (nu > RT_SUB_MAX) return false;
     if (tid == 0) atomicAdd(&stats[GM_STAT_ROUTE_SUBSET], 1ull);
     const GM_GLOBAL float *bias = gbl(bias_p);
-    // rows of U in the scratch, tile by tile: [nu][tc] floats, row u's 16-byte group q at
-    // q ^ (u % 8) so that the chain lanes' reads (one group of each row) miss no bank
+    // rows of U in the scratch, tile by tile: [nu][tc + 4] floats, the 4 floats of padding
+    // putting row u's groups 16 u bytes further round the banks, so that the chain lanes'
+    // reads (one group of each row, at the same column) miss no bank with no address
+    // arithmetic beyond an add (an XOR swizzle of the groups instead took the chain from
+    // ~7.7 to ~10.6 cycles an add, its address work issuing between the dependent adds)
     float *buf = &prod[0][0];
-    const int tc_max = nu * D <= cap ? D : 1024;  // columns per tile (nu rows of them fit the scratch)
+    // columns per tile: the widest of D, 1024, 512, 256 whose nu padded rows fit the scratch
+    // (a multiple of 256, as D is, so that every tile's groups fill whole 64-lane DMAs)
+    int tc_max = D;
+    if (nu * (tc_max + 4) > cap) tc_max = D < 1024 ? D : 1024;
+    if (nu * (tc_max + 4) > cap) tc_max = D < 512 ? D : 512;
+    if (nu * (tc_max + 4) > cap) tc_max = 256;
     float chain = 0.0f;
     for (int c0 = 0; c0 < D; c0 += tc_max) {
-        const int tc = D - c0 < tc_max ? D - c0 : tc_max, ng = tc >> 2;  // D is a multiple of 256
-        for (int s = tid; s < nu * ng; s += RT_BLOCK) {  // slot s: row s / ng, LDS group s % ng
-            const int u = s / ng, q = s % ng, g = q ^ (u & 7);
+        const int tc = D - c0 < tc_max ? D - c0 : tc_max, ng = tc >> 2, rs = tc + 4;  // D is a multiple of 256
+        for (int s = tid; s < nu * ng; s += RT_BLOCK) {  // slot s: row s / ng, group s % ng (64 of one row a wave)
+            const int u = s / ng, q = s % ng;
             const int ee = s_u[u];
-            dma16_untracked(gbl(gate_inp + (size_t)ee * D + c0 + 4 * g), (lds_void *)(buf + 4 * (s & ~63)));
+            dma16_untracked(gbl(gate_inp + (size_t)ee * D + c0 + 4 * q), (lds_void *)(buf + (size_t)u * rs + 4 * (q & ~63)));
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         for (int s = tid; s < nu * ng; s += RT_BLOCK) {  // the products in place (infer.c:922), slot by slot
-            const int u = s / ng, g = (s % ng) ^ (u & 7);
-            float4 *pe = (float4 *)(buf + 4 * s);
-            const float4 v = *pe, xv = *(const float4 *)(xn + c0 + 4 * g);
+            const int u = s / ng, q = s % ng;
+            float4 *pe = (float4 *)(buf + (size_t)u * rs + 4 * q);
+            const float4 v = *pe, xv = *(const float4 *)(xn + c0 + 4 * q);
             *pe = make_float4(__fmul_rn(v.x, xv.x), __fmul_rn(v.y, xv.y), __fmul_rn(v.z, xv.z), __fmul_rn(v.w, xv.w));
         }
         __syncthreads();
         if (w == 0 && lane < nu) {  // infer.c:916-925: the sequential chain of expert U[lane]
-            const float *row = buf + lane * tc;
+            const float *row = buf + (size_t)lane * rs;
             for (int q0 = 0; q0 < ng; q0 += NV) {  // ng is a multiple of 64
                 // NV groups' reads at once, so that the LDS latency is paid once per 4 NV adds
                 float4 v[NV];
 #pragma unroll
-                for (int j = 0; j < NV; j++) v[j] = *(const float4 *)(row + 4 * ((q0 + j) ^ (lane & 7)));
+                for (int j = 0; j < NV; j++) v[j] = *(const float4 *)(row + 4 * (q0 + j));
 #pragma unroll
                 for (int j = 0; j < NV; j++) {
                     chain = __fadd_rn(chain, v[j].x);
