@@ -32,6 +32,7 @@
 #include "common.h"
 #include "dense.h"
 #include "attn.h"
+#include "attn16.h"
 #include "gemm.h"
 
 // gmoe.hip
@@ -387,10 +388,17 @@ void launch_attn_tile(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) {
     aa.nblk = (P + g.chunk - 1) / g.chunk;
     g.a = aa;
     const dim3 grid((unsigned)aa.nblk, (unsigned)tiles, (unsigned)aa.H);
-    switch (aq_rounds(aa.kv + aa.rope)) {
-    case 1: hipLaunchKernelGGL(k_attn_tile<1>, grid, dim3(AQ_BLOCK), 0, st, g); break;
-    case 2: hipLaunchKernelGGL(k_attn_tile<2>, grid, dim3(AQ_BLOCK), 0, st, g); break;
-    default: hipLaunchKernelGGL(k_attn_tile<3>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+    // fp16 matrix cores on split operands (attn16.h); GMOE_ATTN_TILE_FP32=1 keeps the fp32
+    // MFMA kernel (a diagnostic and the tests' reference for the split form)
+    const char *env = getenv("GMOE_ATTN_TILE_FP32");
+    if (!(env && env[0] == '1') && aa.kv <= AT_KV_MAX) {
+        hipLaunchKernelGGL(k_attn_tile16, grid, dim3(AQ_BLOCK), 0, st, g);
+    } else {
+        switch (aq_rounds(aa.kv + aa.rope)) {
+        case 1: hipLaunchKernelGGL(k_attn_tile<1>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+        case 2: hipLaunchKernelGGL(k_attn_tile<2>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+        default: hipLaunchKernelGGL(k_attn_tile<3>, grid, dim3(AQ_BLOCK), 0, st, g); break;
+        }
     }
     launch_attn_merge(aa, n, st);
 }
