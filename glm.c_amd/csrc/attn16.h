@@ -7,64 +7,65 @@
 // ~2^-22 of it). fp32 MFMA runs at 157 TFLOP/s on MI355X, fp16 at 2.5 PFLOP/s, so the three
 // fp16 products cost about a fifth of one fp32 product.
 //
-// fp16's range needs exponents: each token's query row is scaled by 2^-eq (max below
-// 2^15) and each staged cache row by 2^-ek (kv and rope parts together, for the scores);
-// a score is the MFMA's sum times 2^(eq + ek). For the weighted sum the compressed part
-// of row p is scaled by its own 2^-ev[p], and the tile's exponentials by 2^(ev[p] - eV),
-// eV the tile's largest ev (so the weights stay <= 1); the tile's sum starts from zero on
-// the matrix cores and joins the running fp32 sum as acc = acc * corr + sum * 2^eV.
+// The cache entries come in the split form attn_prep_run writes once per position (dense.h:
+// ksp rows scaled by 2^-e[p], vsp blocks of the compressed part transposed), so the 16 query
+// tiles x heads that read a position do not each convert it: a tile's rows and its
+// transposed block land in shared memory by DMA, two tiles in flight. Each token's query
+// row is split once per block, scaled by 2^-eq; a score is the MFMA's sum times 2^(eq + e[p]).
+// For the weighted sum the tile's exponentials are scaled by 2^(e[p] - eT), eT the tile's
+// largest e over the positions it attends (so the weights stay <= 1); the tile's sum starts
+// from zero on the matrix cores and joins the running fp32 sum as acc = acc * corr + sum * 2^eT.
 //
-// A tile's rows are loaded to registers (one row a wave, requested while the tile before
-// is used), converted to the split planes in shared memory (kp: [position][column] for the
-// scores' B operand; vp: [column][position] for the weighted sum's), then: the
-// scores (waves by 16-row quarter and quarter of the 32-column steps, summed in shared
-// memory), the softmax step as in k_attn_tile, and the weighted sum (16x16 output blocks
-// round robin over the waves).
+// A tile: the scores (waves by 16-row quarter and quarter of the 32-column steps, summed in
+// shared memory), the softmax step as in k_attn_tile, and the weighted sum (16x16 output
+// blocks round robin over the waves).
 #pragma once
 
 #include "attn.h"
 
-#define A16_KQS 584    // halves a kp row: 576 + 8, an odd count of 16-byte units (the 16 rows' reads miss no bank)
-#define A16_VS 20      // halves a vp row: 16 positions + 4, an odd count of 8-byte units
-#define A16_PS 20      // halves a pp row (the same)
 #define A16_NKS (AQ_KQ_MAX / 32)  // 32-column steps of the widest entry
 #define A16_NQS ((A16_NKS + 3) / 4)  // steps a wave's quarter holds at most
-#define A16_NJ (AQ_KQ_MAX / 64)   // a row's 64-column groups (one per lane and load)
-#define A16_EMPTY (-1000)         // exponent of an all-zero row
-// A timing point (k: 0 start, 1 queries ready, then per tile 2 converted, 3 scores, 4 softmax,
+#define A16_PS 20                  // halves a row of the exponentials' planes: 16 + 4, an odd count of 8-byte units
+#define A16_KB (AQ_P * SPL_KROW * 2)             // bytes of a stage's rows
+#define A16_VB (2 * AT_KV_MAX * 16 * 2)          // bytes of a stage's transposed block at the widest kv
+#define A16_STAGE (A16_KB + A16_VB)
+// A timing point (k: 0 start, 1 queries ready, then per tile 2 landed, 3 scores, 4 softmax,
 // 5 weighted sum); empty unless a timing build defines it.
 #ifndef A16_STAMP
 #define A16_STAMP(k, j)
 #endif
-static_assert(AQ_P == 16, "one wave per staged row, and a 16-position K dimension for the weighted sum");
+static_assert(AQ_P == 16, "one ksp row a wave's share of the DMA, and a 16-position K dimension for the weighted sum");
 static_assert(AQ_BLOCK == 1024 && AQ_T == 64, "16 waves: four 16-row quarters by four column quarters");
+static_assert(AQ_KQ_MAX == SPL_KCOLS, "the split rows hold the widest entry");
+static_assert(A16_KB % 16 == 0 && A16_STAGE % 16 == 0, "16-byte DMA slots");
 
 typedef _Float16 a16_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 a16_h4 __attribute__((ext_vector_type(4)));
 
-// The exponent e with |x| 2^-e < 2^15 for every |x| <= mx (A16_EMPTY when mx is 0).
-__device__ static inline int a16_exp(float mx) {
-    if (!(mx > 0.0f)) return A16_EMPTY;
-    int k;
-    (void)frexpf(mx, &k);  // mx < 2^k
-    return k - 15;
-}
-
-// x = hi + lo: hi the nearest fp16, lo the nearest fp16 to the (exact) remainder.
-__device__ static inline void a16_split(float x, _Float16 &hi, _Float16 &lo) {
-    hi = (_Float16)x;
-    lo = (_Float16)(x - (float)hi);
+// Save (restore 0) or restore (1) position pos's split entries of every layer (a block each):
+// the ksp row and the position's slot of each vsp plane column.
+__global__ __launch_bounds__(DM_BLOCK) void k_spl_keep(_Float16 *ksp, _Float16 *vsp, _Float16 *saved, size_t cap16,
+                                                      int kv, int pos, int restore) {
+    const int l = blockIdx.x;
+    _Float16 *kr = ksp + ((size_t)l * cap16 + pos) * SPL_KROW;
+    _Float16 *vb = vsp + (size_t)l * cap16 * 2 * kv + (size_t)(pos >> 4) * 2 * kv * 16 + (pos & 15);
+    _Float16 *sv = saved + (size_t)l * (SPL_KROW + 2 * kv);
+    for (int i = threadIdx.x; i < SPL_KROW + 2 * kv; i += DM_BLOCK) {
+        _Float16 *g = i < SPL_KROW ? kr + i : vb + (size_t)(i - SPL_KROW) * 16;
+        if (restore)
+            *g = sv[i];
+        else
+            sv[i] = *g;
+    }
 }
 
 __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
-    // each pair of planes in one array (lo at a fixed offset from hi), so that every read of
-    // a product takes one base address and immediate offsets
-    __shared__ __align__(16) _Float16 kp[2][AQ_P * A16_KQS];
-    __shared__ __align__(16) _Float16 vp[2][AT_KV_MAX * A16_VS];
-    __shared__ __align__(16) _Float16 pp[2][AQ_T * A16_PS];
-    __shared__ __align__(16) float sp[4][AQ_T][AQ_P + 4];  // the column quarters' partial scores
+    __shared__ __align__(16) uint8_t stg[2][A16_STAGE];        // tiles j and j + 1: rows, then the block
+    __shared__ __align__(16) float sp[4][AQ_T][AQ_P];         // the column quarters' partial scores
     __shared__ float run_m[AQ_T], run_l[AQ_T], corr[AQ_T];
-    __shared__ int ek_s[AQ_P], ev_s[AQ_P], eq_s[AQ_T], ev_tile;
+    __shared__ int eq_s[AQ_T], et_s;
+    _Float16(*pp)[AQ_T * A16_PS] = reinterpret_cast<_Float16(*)[AQ_T * A16_PS]>(&sp[0][0][0]);  // after the scores are read
+    static_assert(2 * AQ_T * A16_PS * 2 <= sizeof(sp), "the exponentials' planes fit the scores' buffer");
     const AttnArgs &a = g.a;
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -83,8 +84,7 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
         return;
     }
     A16_STAMP(0, 0);
-    const int nks = (KQ + 31) / 32;   // 32-column steps (columns past KQ are zeros)
-    const int ncol = 32 * nks;        // columns of the kp planes that the steps read
+    const int nks = (KQ + 31) / 32;   // 32-column steps (ksp holds zeros past KQ)
     const int ntile = (r1 - r0 + AQ_P - 1) / AQ_P;
 
     // the queries: the lane's operand columns (row 16 rb + l16, steps q + 4 i, columns 32 s +
@@ -110,8 +110,7 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
 #pragma unroll
             for (int k = 0; k < 2; k++)
                 mx = fmaxf(mx, fmaxf(fmaxf(fabsf(qv[i][k].x), fabsf(qv[i][k].y)), fmaxf(fabsf(qv[i][k].z), fabsf(qv[i][k].w))));
-        // the row's maximum over its columns: four lane groups in each of four waves
-        sp[q][16 * rb + l16][lg] = mx;
+        sp[q][16 * rb + l16][lg] = mx;  // the row's maximum over its columns: four lane groups in each of four waves
     }
     if (tid < AQ_T) {
         run_m[tid] = -INFINITY;
@@ -124,7 +123,7 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
         for (int qq = 0; qq < 4; qq++)
 #pragma unroll
             for (int g4 = 0; g4 < 4; g4++) mx = fmaxf(mx, sp[qq][tid][g4]);
-        eq_s[tid] = a16_exp(mx);
+        eq_s[tid] = spl_exp(mx);
     }
     __syncthreads();
     a16_h8 qh[A16_NQS], ql[A16_NQS];
@@ -136,7 +135,7 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 _Float16 hi, lo;
-                a16_split(ldexpf(xs[k], -e), hi, lo);
+                spl_split(ldexpf(xs[k], -e), hi, lo);
                 qh[i][k] = hi;
                 ql[i][k] = lo;
             }
@@ -145,27 +144,32 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
     int eqd[4];  // the exponents of the score rows the lane holds: tokens 16 rb + 4 lg + r
 #pragma unroll
     for (int r = 0; r < 4; r++) eqd[r] = eq_s[16 * rb + 4 * lg + r];
+    A16_STAMP(1, 0);
 
-    // a tile's rows: wave w loads position s0 + w, lane columns lane + 64 j (zeros past the
-    // chunk and past KQ)
-    // (the lane index passes through an opaque copy per call, so that its 64-bit addresses
-    // are formed per request rather than hoisted out of the tile loop, where they would not
-    // fit the registers)
-    float xr[A16_NJ];
-    auto load = [&](int s0) {
-        const int pos = s0 + w;
-        const bool ok = pos < r1;
+    // a tile by DMA into stage st: its 16 ksp rows (contiguous), then its vsp block (4 kv
+    // 16-byte slots); 64 slots per wave and round, the last round's lanes past the data idle.
+    // The wave's count of DMA instructions is the same for every tile (nd below).
+    constexpr int NKS = A16_KB / 16;
+    const int nvs = 4 * kv;
+    const int nd = 2 + (2048 + 64 * w < NKS ? 1 : 0) + (64 * w < nvs ? 1 : 0) + (1024 + 64 * w < nvs ? 1 : 0);
+    auto issue = [&](int s0, int st) {
+        const uint8_t *ks = reinterpret_cast<const uint8_t *>(a.ksp + (size_t)s0 * SPL_KROW);
+        const uint8_t *vs = reinterpret_cast<const uint8_t *>(a.vsp + (size_t)(s0 >> 4) * 2 * kv * 16);
         int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const float *cr = a.comp + (size_t)pos * kv + ln, *pr = a.pe + (size_t)pos * rope + (ln - kv);
+        asm volatile("" : "+v"(ln));  // (addresses formed per request, not hoisted out of the loop)
 #pragma unroll
-        for (int j = 0; j < A16_NJ; j++) {
-            const int col = ln + 64 * j;
-            xr[j] = ok && col < KQ ? (col < kv ? cr[64 * j] : pr[64 * j]) : 0.0f;
+        for (int r = 0; r < 3; r++) {
+            const int b0 = 1024 * r + 64 * w;
+            if (b0 < NKS && b0 + ln < NKS) dma16_untracked(gbl((const void *)(ks + 16 * (b0 + ln))), (lds_void *)(stg[st] + 16 * b0));
+        }
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int b0 = 1024 * r + 64 * w;
+            if (b0 < nvs) dma16_untracked(gbl((const void *)(vs + 16 * (b0 + ln))), (lds_void *)(stg[st] + A16_KB + 16 * b0));
         }
     };
-    load(r0);
-    A16_STAMP(1, 0);
+    issue(r0, 0);
+    if (ntile > 1) issue(r0 + AQ_P, 1);
 
     aq_f4 acc[8];
 #pragma unroll
@@ -173,61 +177,37 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
 
     for (int j = 0; j < ntile; j++) {
         const int s0 = r0 + AQ_P * j;
-        {
-            // the row of position s0 + w into the planes: kp scaled by its exponent over the
-            // whole row, vp (the kv part) by its exponent over that part
-            float mk = 0.0f, mv = 0.0f;
-#pragma unroll
-            for (int jj = 0; jj < A16_NJ; jj++) {
-                const int col = lane + 64 * jj;
-                mk = fmaxf(mk, fabsf(xr[jj]));
-                if (col < kv) mv = fmaxf(mv, fabsf(xr[jj]));
+        const uint8_t *sb = stg[j & 1];
+        const _Float16 *K = reinterpret_cast<const _Float16 *>(sb), *V = reinterpret_cast<const _Float16 *>(sb + A16_KB);
+        // tile j has landed (this wave's DMAs of tile j + 1, issued after, may still be in flight)
+        if (j + 1 < ntile) {
+            switch (nd) {
+            case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+            case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+            case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+            default: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
             }
-            const int ek = a16_exp(wave_max_dpp_f(mk)), ev = a16_exp(wave_max_dpp_f(mv));
-            if (lane == 0) {
-                ek_s[w] = ek;
-                ev_s[w] = ev;
-            }
-            int ln = lane;
-            asm volatile("" : "+v"(ln));
-            _Float16 *khr = &kp[0][w * A16_KQS + ln], *klr = &kp[1][w * A16_KQS + ln];
-            _Float16 *vhr = &vp[0][ln * A16_VS + w], *vlr = &vp[1][ln * A16_VS + w];
-#pragma unroll
-            for (int jj = 0; jj < A16_NJ; jj++) {
-                const int col = ln + 64 * jj;
-                if (col < ncol) {
-                    _Float16 hi, lo;
-                    a16_split(ldexpf(xr[jj], -ek), hi, lo);
-                    khr[64 * jj] = hi;
-                    klr[64 * jj] = lo;
-                }
-                if (col < kv) {
-                    _Float16 hi, lo;
-                    a16_split(ldexpf(xr[jj], -ev), hi, lo);
-                    vhr[64 * A16_VS * jj] = hi;
-                    vlr[64 * A16_VS * jj] = lo;
-                }
-            }
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
-        if (j + 1 < ntile) load(s0 + AQ_P);  // in flight while this tile is used
-        at_barrier();  // (shared memory only: __syncthreads() would wait for that load)
+        at_barrier();  // every wave's part of tile j (shared memory only: the next tile's DMA stays in flight)
         A16_STAMP(2, j);
         {
             // partial scores: lane holds rows 16 rb + 4 lg + r, position l16
             aq_f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
-            const _Float16 *kr = &kp[0][l16 * A16_KQS + 8 * lg + 32 * q];  // step q + 4 i at + 128 i
+            const _Float16 *kr = K + l16 * SPL_KROW + 8 * lg + 32 * q;  // step q + 4 i at + 128 i, lo at + SPL_KCOLS
 #pragma unroll
             for (int i = 0; i < A16_NQS; i++) {
                 const int s = q + 4 * i;
                 if (s < nks) {
                     const a16_h8 bh = *(const a16_h8 *)(kr + 128 * i);
-                    const a16_h8 bl = *(const a16_h8 *)(kr + 128 * i + AQ_P * A16_KQS);
+                    const a16_h8 bl = *(const a16_h8 *)(kr + 128 * i + SPL_KCOLS);
                     d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[i], bh, d, 0, 0, 0);
                     d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[i], bl, d, 0, 0, 0);
                     d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[i], bh, d, 0, 0, 0);
                 }
             }
-            const int ekp = ek_s[l16];
+            const int ekp = *(const int *)(K + l16 * SPL_KROW + SPL_KEXP);
 #pragma unroll
             for (int r = 0; r < 4; r++) sp[q][16 * rb + 4 * lg + r][l16] = ldexpf(d[r], eqd[r] + ekp);
         }
@@ -237,15 +217,17 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
             // softmax step: thread = (row tid / 16, position tid % 16), a 16-lane DPP row per row
             const int row = tid >> 4, p = tid & 15, t = t0 + row, s = s0 + p;
             float v = (sp[0][row][p] + sp[1][row][p]) + (sp[2][row][p] + sp[3][row][p]);
+            at_barrier();  // every score read: the exponentials' planes below reuse the buffer
             v = __fmul_rn(v, a.kq_scale);
-            if (t >= tl || s >= r1 || s > a.pos + t) v = -INFINITY;  // causal, and past the chunk
+            const bool in = s < r1;
+            if (t >= tl || !in || s > a.pos + t) v = -INFINITY;  // causal, and past the chunk
             const float mo = run_m[row], mn = fmaxf(mo, row_max_dpp_f(v));
             const float e = mn == -INFINITY ? 0.0f : expf(__fsub_rn(v, mn));
             const float l = row_sum_dpp_f(e);
-            const int evp = ev_s[p];
-            const int eV = (int)row_max_dpp_f((float)evp);  // the tile's largest (the same in every row)
+            const int ep = *(const int *)(K + p * SPL_KROW + SPL_KEXP);
+            const int eT = (int)row_max_dpp_f((float)(in ? ep : SPL_EMPTY));  // the same in every row
             _Float16 hi, lo;
-            a16_split(ldexpf(e, evp - eV), hi, lo);
+            spl_split(ldexpf(e, ep - eT), hi, lo);
             pp[0][row * A16_PS + p] = hi;
             pp[1][row * A16_PS + p] = lo;
             if (p == 0) {
@@ -253,7 +235,7 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
                 run_m[row] = mn;
                 run_l[row] = fmaf(run_l[row], cr, l);
                 corr[row] = cr;
-                if (row == 0) ev_tile = eV;
+                if (row == 0) et_s = eT;
             }
         }
         at_barrier();
@@ -264,16 +246,16 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
             aq_f4 cr;
 #pragma unroll
             for (int r = 0; r < 4; r++) cr[r] = corr[16 * rh + 4 * lg + r];
-            const float sv = ldexpf(1.0f, ev_tile);
+            const float sv = ldexpf(1.0f, et_s);
             const a16_h4 ah = *(const a16_h4 *)&pp[0][(16 * rh + l16) * A16_PS + 4 * lg];
             const a16_h4 al = *(const a16_h4 *)&pp[1][(16 * rh + l16) * A16_PS + 4 * lg];
-            const _Float16 *vr = &vp[0][(16 * (w >> 2) + l16) * A16_VS + 4 * lg];  // block i at + 64 A16_VS i
+            const _Float16 *vh = V + (16 * (w >> 2) + l16) * 16 + 4 * lg;  // block i at + 1024 i
+            const _Float16 *vl = vh + kv * 16;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int cb = (w >> 2) + 4 * i;
                 if (cb < kv / 16) {
-                    const a16_h4 bh = *(const a16_h4 *)(vr + 64 * A16_VS * i);
-                    const a16_h4 bl = *(const a16_h4 *)(vr + 64 * A16_VS * i + AT_KV_MAX * A16_VS);
+                    const a16_h4 bh = *(const a16_h4 *)(vh + 1024 * i), bl = *(const a16_h4 *)(vl + 1024 * i);
                     aq_f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
                     d = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, d, 0, 0, 0);
                     d = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, d, 0, 0, 0);
@@ -283,8 +265,9 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
                 }
             }
         }
-        at_barrier();  // the next tile overwrites the planes, the scores and the exponents
+        at_barrier();  // every wave is done with stage j % 2, the scores' buffer and the exponents
         A16_STAMP(5, j);
+        if (j + 2 < ntile) issue(s0 + 2 * AQ_P, j & 1);
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) {

@@ -240,7 +240,38 @@ struct AttnArgs {
     int hg;                // heads per block of k_attn_chunk (<= AT_HG)
     int nblk;              // position ranges of k_attn_chunk (blocks per head group), <= AT_MAX_PARTS
     float kq_scale;
+    // this layer's cache entries in split fp16 form for the batch attention on matrix cores
+    // (null: not kept): ksp [cap16][SPL_KROW] halves, a row per position (see below); vsp
+    // [cap16 / 16][2][kv][16] halves, the compressed part transposed in blocks of 16 positions
+    _Float16 *ksp, *vsp;
 };
+
+// The split form of a cache entry (the matrix cores' operands, written once per position
+// by attn_prep_run): x = hi + lo, fp16 each, of the entry scaled by 2^-e, e the exponent with
+// max |entry| 2^-e < 2^15 (SPL_EMPTY for a zero entry). A ksp row is the kv + rope columns'
+// hi (SPL_KCOLS halves, zeros past kv + rope), then their lo, then e (an int), then
+// padding to SPL_KROW halves, an odd count of 16-byte units so that rows read together fall
+// in distinct banks. vsp holds the compressed part's hi and lo planes transposed by blocks
+// of 16 positions: block b, plane, column c, position slot s at ((b * 2 + plane) * kv + c) * 16 + s.
+#define SPL_KCOLS 576
+#define SPL_KEXP (2 * SPL_KCOLS)   // half index of the exponent in a ksp row
+#define SPL_KROW (2 * SPL_KCOLS + 8)
+#define SPL_EMPTY (-1000)
+static_assert((SPL_KROW * 2 / 16) % 2 == 1, "a ksp row is an odd count of 16-byte units");
+
+// The exponent e with |x| 2^-e < 2^15 for every |x| <= mx (SPL_EMPTY when mx is 0).
+__device__ static inline int spl_exp(float mx) {
+    if (!(mx > 0.0f)) return SPL_EMPTY;
+    int k;
+    (void)frexpf(mx, &k);  // mx < 2^k
+    return k - 15;
+}
+
+// x = hi + lo: hi the nearest fp16, lo the nearest fp16 to the (exact) remainder.
+__device__ static inline void spl_split(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
 
 // The position's cache entry and the heads' rotated queries (infer.c:1000-1016): the
 // compressed kv normalised (rmsnorm over kv values), the rope part of kv_a and of every
@@ -248,6 +279,8 @@ struct AttnArgs {
 // position pos + t (its kv_a, q_full and q_pe t token strides on).
 __device__ __attribute__((always_inline)) static void attn_prep_run(AttnArgs a, int t) {
     __shared__ double red[DM_BLOCK / 64];
+    __shared__ float row[SPL_KCOLS];  // the entry, for its split form
+    __shared__ float rmax[DM_BLOCK / 64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     {
         a.kv_a += (size_t)t * (a.kv + a.rope);
@@ -264,7 +297,11 @@ __device__ __attribute__((always_inline)) static void attn_prep_run(AttnArgs a, 
     const float mean = (float)(ss / (double)a.kv);
     const float inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, 1e-5f)));
     float *comp = a.comp + (size_t)a.pos * a.kv, *pe = a.pe + (size_t)a.pos * a.rope;
-    for (int i = tid; i < a.kv; i += DM_BLOCK) comp[i] = __fmul_rn(__fmul_rn(a.kv_a[i], inv), a.kv_norm[i]);
+    for (int i = tid; i < a.kv; i += DM_BLOCK) {
+        const float v = __fmul_rn(__fmul_rn(a.kv_a[i], inv), a.kv_norm[i]);
+        comp[i] = v;
+        if (i < SPL_KCOLS) row[i] = v;
+    }
     const float *cs = a.rope_cs + (size_t)a.pos * a.rope;  // rope/2 pairs of (cos, sin)
     const int half = a.rope >> 1;
     // infer.c:964-976 on kv_a's rope part (pair 0 .. half-1) and each head's (pairs half ..)
@@ -273,9 +310,37 @@ __device__ __attribute__((always_inline)) static void attn_prep_run(AttnArgs a, 
         const float *src = h < 0 ? a.kv_a + a.kv : a.q_full + (size_t)h * a.head_k + a.nope;
         float *dst = h < 0 ? pe : a.q_pe + (size_t)h * a.rope;
         const float c = cs[2 * i], s = cs[2 * i + 1], x0 = src[2 * i], x1 = src[2 * i + 1];
-        dst[2 * i] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
-        dst[2 * i + 1] = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+        const float y0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s)), y1 = __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+        dst[2 * i] = y0;
+        dst[2 * i + 1] = y1;
+        if (h < 0 && a.kv + 2 * i + 1 < SPL_KCOLS) {
+            row[a.kv + 2 * i] = y0;
+            row[a.kv + 2 * i + 1] = y1;
+        }
     }
+    if (!a.ksp) return;
+    // the entry's split form (kv + rope <= SPL_KCOLS, kv <= the vsp planes' width: the host's checks)
+    __syncthreads();
+    const int KQ = a.kv + a.rope;
+    float mx = 0.0f;
+    for (int i = tid; i < KQ; i += DM_BLOCK) mx = fmaxf(mx, fabsf(row[i]));
+    mx = wave_max_dpp_f(mx);
+    if (lane == 0) rmax[w] = mx;
+    __syncthreads();
+    const int e = spl_exp(fmaxf(fmaxf(rmax[0], rmax[1]), fmaxf(rmax[2], rmax[3])));
+    _Float16 *kr = a.ksp + (size_t)a.pos * SPL_KROW;
+    _Float16 *vb = a.vsp + (size_t)(a.pos >> 4) * 2 * a.kv * 16 + (a.pos & 15);
+    for (int i = tid; i < SPL_KCOLS; i += DM_BLOCK) {
+        _Float16 hi = (_Float16)0.0f, lo = (_Float16)0.0f;
+        if (i < KQ) spl_split(ldexpf(row[i], -e), hi, lo);
+        kr[i] = hi;
+        kr[SPL_KCOLS + i] = lo;
+        if (i < a.kv) {
+            vb[(size_t)i * 16] = hi;
+            vb[((size_t)a.kv + i) * 16] = lo;
+        }
+    }
+    if (tid < (SPL_KROW - SPL_KEXP) / 2) ((int *)(kr + SPL_KEXP))[tid] = tid == 0 ? e : 0;
 }
 
 // The query side of a token's attention in one launch: the absorbed queries q_abs = k_b_h .

@@ -94,6 +94,10 @@ struct gmoe_model {
     float *x = nullptr, *q_a = nullptr, *q_full = nullptr, *kv_a = nullptr, *q_pe = nullptr, *q_abs = nullptr,
           *ctx = nullptr, *concat = nullptr, *ffh = nullptr, *logits = nullptr, *part_ctx = nullptr,
           *part_ml = nullptr, *saved = nullptr;
+    // the caches' split fp16 form for the batch attention (dense.h: ksp rows, vsp blocks; null
+    // where the shape does not take it), cap rounded up to 16 positions, and a token's saved entries
+    _Float16 *ksp = nullptr, *vsp = nullptr, *ksaved = nullptr;
+    size_t cap16 = 0;
     int32_t *tokens = nullptr;  // [max_batch] a prefill's token ids
     // a prefill's GEMM inputs (gemm.h): [max_batch][2][widest input] fp16, their exponents,
     // and 64 bytes of zeros
@@ -313,6 +317,8 @@ AttnArgs attn_args(gmoe_model *m, int l, int pos) {
     aa.part_ctx = m->part_ctx;
     aa.part_ml = m->part_ml;
     aa.ctx = m->ctx;
+    aa.ksp = m->ksp ? m->ksp + (size_t)l * m->cap16 * SPL_KROW : nullptr;
+    aa.vsp = m->vsp ? m->vsp + (size_t)l * m->cap16 * 2 * kv : nullptr;
     aa.H = H;
     aa.kv = kv;
     aa.rope = rope;
@@ -388,10 +394,11 @@ void launch_attn_tile(gmoe_model *m, AttnArgs aa, int n, hipStream_t st) {
     aa.nblk = (P + g.chunk - 1) / g.chunk;
     g.a = aa;
     const dim3 grid((unsigned)aa.nblk, (unsigned)tiles, (unsigned)aa.H);
-    // fp16 matrix cores on split operands (attn16.h); GMOE_ATTN_TILE_FP32=1 keeps the fp32
-    // MFMA kernel (a diagnostic and the tests' reference for the split form)
+    // fp16 matrix cores on the cache's split form (attn16.h; the model keeps it where the shape
+    // fits); GMOE_ATTN_TILE_FP32=1 keeps the fp32 MFMA kernel (a diagnostic and the tests'
+    // reference for the split form)
     const char *env = getenv("GMOE_ATTN_TILE_FP32");
-    if (!(env && env[0] == '1') && aa.kv <= AT_KV_MAX) {
+    if (!(env && env[0] == '1') && aa.ksp) {
         hipLaunchKernelGGL(k_attn_tile16, grid, dim3(AQ_BLOCK), 0, st, g);
     } else {
         switch (aq_rounds(aa.kv + aa.rope)) {
@@ -638,6 +645,12 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
         rc |= mdalloc(m, &m->part_ctx, ranges * H * kv);
         rc |= mdalloc(m, &m->part_ml, ranges * H * 2);
         rc |= mdalloc(m, &m->saved, A * (kv + rope));
+        if (attn_tile_ok(c) && kv <= AT_KV_MAX) {
+            m->cap16 = (cap + 15) / 16 * 16;
+            rc |= mdalloc(m, &m->ksp, A * m->cap16 * SPL_KROW);
+            rc |= mdalloc(m, &m->vsp, A * m->cap16 * 2 * kv);
+            rc |= mdalloc(m, &m->ksaved, A * (SPL_KROW + 2 * kv));
+        }
     }
     if (!rc && A > 0) {
         // glm.c's angles (infer.c:964-976): pair i of position p turns by p * 1e6^(-2i / rope)
@@ -654,7 +667,9 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
             rc = GMOE_ERR_HIP;
         }
         if (!rc && (hipMemset(m->comp, 0, A * cap * kv * sizeof(float)) != hipSuccess ||
-                    hipMemset(m->pe, 0, A * cap * rope * sizeof(float)) != hipSuccess)) {
+                    hipMemset(m->pe, 0, A * cap * rope * sizeof(float)) != hipSuccess ||
+                    (m->ksp && hipMemset(m->ksp, 0, A * m->cap16 * SPL_KROW * sizeof(_Float16)) != hipSuccess) ||
+                    (m->vsp && hipMemset(m->vsp, 0, A * m->cap16 * 2 * kv * sizeof(_Float16)) != hipSuccess))) {
             gm_set_err("gmoe_model_create: clearing the cache failed");
             rc = GMOE_ERR_HIP;
         }
@@ -806,6 +821,9 @@ int forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, f
                                kv * sizeof(float), A, hipMemcpyDeviceToDevice, st));
         MH_OK(hipMemcpy2DAsync(m->saved + A * kv, rope * sizeof(float), m->pe + pos * rope, cap * rope * sizeof(float),
                                rope * sizeof(float), A, hipMemcpyDeviceToDevice, st));
+        if (m->ksp)
+            hipLaunchKernelGGL(k_spl_keep, dim3((unsigned)A), dim3(DM_BLOCK), 0, st, m->ksp, m->vsp, m->ksaved, m->cap16,
+                               (int)kv, pos, 0);
     }
     hipLaunchKernelGGL(k_embed, dim3((unsigned)((D + DM_BLOCK - 1) / DM_BLOCK)), dim3(DM_BLOCK), 0, st, m->tok_q, m->tok_s,
                        token, c.dim, c.group_size, m->x);
@@ -866,6 +884,9 @@ int forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, f
                                kv * sizeof(float), A, hipMemcpyDeviceToDevice, st));
         MH_OK(hipMemcpy2DAsync(m->pe + pos * rope, cap * rope * sizeof(float), m->saved + A * kv, rope * sizeof(float),
                                rope * sizeof(float), A, hipMemcpyDeviceToDevice, st));
+        if (m->ksp)
+            hipLaunchKernelGGL(k_spl_keep, dim3((unsigned)A), dim3(DM_BLOCK), 0, st, m->ksp, m->vsp, m->ksaved, m->cap16,
+                               (int)kv, pos, 1);
     }
     MH_OK(hipStreamSynchronize(st));
     if (m->moe && gm_take_launch_error(m->moe)) return GMOE_ERR_HIP;

@@ -10,7 +10,11 @@ test_gpu_prefill.py and test_gpu_config5.py apply to the default kernel), with t
 argmax. Shapes: a small one (kv 64 + rope 16 = 80 columns: the last 32-column step is
 padded with zeros) and glm.c's attention ranks (kv 512 + rope 64), 4 and 20 heads. Prompts:
 300 tokens in one batch (five 64-token query tiles, several position chunks), then 200 more
-at position 300 over that cache (chunks that span both batches, causal masks inside)."""
+at position 300 over that cache (chunks that span both batches, causal masks inside); then
+a decode token with GMOE_MODEL_KEEP_CACHE at position 250 (its entries written, then
+restored: the split form must be restored with the fp32 one, or the split kernel would read
+the overwritten entry), three tokens decoded one at a time (their split entries written by
+the decode's cache step) and 8 more tokens in a batch over all of them."""
 import os
 
 import numpy as np
@@ -20,6 +24,8 @@ import gmoe
 from conftest import assert_close
 
 pytestmark = pytest.mark.gpu
+
+KEEP_CACHE = 1  # GMOE_MODEL_KEEP_CACHE, include/gmoe_model.h
 
 
 def small():
@@ -64,12 +70,21 @@ def test_split_fp16_attention_matches_fp32(name):
         rng = np.random.default_rng(5)
         first = rng.integers(0, cfg["vocab_size"], 300).astype(np.int32)
         second = rng.integers(0, cfg["vocab_size"], 200).astype(np.int32)
-        for what, toks, pos0 in (("300 tokens at 0", first, 0), ("200 tokens at 300", second, 300)):
+        def check(what, toks, pos0):
             print(f"[case] {name}: {what}", flush=True)
             want = run(model, toks, pos0, fp32=True)
             got = run(model, toks, pos0, fp32=False)
             assert np.isfinite(got).all()
             assert_close(got, want, f"{name} {what}: logits", max_abs=2e-4, rel_l2=2e-5)
             assert int(np.argmax(got)) == int(np.argmax(want)), f"{name} {what}: argmax"
+
+        check("300 tokens at 0", first, 0)
+        check("200 tokens at 300", second, 300)
+        # a kept decode token overwrites position 250's entries and restores them (the split form
+        # with the fp32 one); tokens decoded one at a time write theirs; a batch then reads both
+        model.forward_token(7, 250, flags=KEEP_CACHE)
+        for pos in range(500, 503):
+            model.forward_token(int(rng.integers(0, cfg["vocab_size"])), pos)
+        check("8 tokens at 503 after kept and decoded tokens", rng.integers(0, cfg["vocab_size"], 8).astype(np.int32), 503)
     finally:
         model.close()
