@@ -42,23 +42,6 @@ static_assert(A16_KB % 16 == 0 && A16_STAGE % 16 == 0, "16-byte DMA slots");
 typedef _Float16 a16_h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 a16_h4 __attribute__((ext_vector_type(4)));
 
-// Save (restore 0) or restore (1) position pos's split entries of every layer (a block each):
-// the ksp row and the position's slot of each vsp plane column.
-__global__ __launch_bounds__(DM_BLOCK) void k_spl_keep(_Float16 *ksp, _Float16 *vsp, _Float16 *saved, size_t cap16,
-                                                      int kv, int pos, int restore) {
-    const int l = blockIdx.x;
-    _Float16 *kr = ksp + ((size_t)l * cap16 + pos) * SPL_KROW;
-    _Float16 *vb = vsp + (size_t)l * cap16 * 2 * kv + (size_t)(pos >> 4) * 2 * kv * 16 + (pos & 15);
-    _Float16 *sv = saved + (size_t)l * (SPL_KROW + 2 * kv);
-    for (int i = threadIdx.x; i < SPL_KROW + 2 * kv; i += DM_BLOCK) {
-        _Float16 *g = i < SPL_KROW ? kr + i : vb + (size_t)(i - SPL_KROW) * 16;
-        if (restore)
-            *g = sv[i];
-        else
-            sv[i] = *g;
-    }
-}
-
 __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
     __shared__ __align__(16) uint8_t stg[2][A16_STAGE];        // tiles j and j + 1: rows, then the block
     __shared__ __align__(16) float sp[4][AQ_T][AQ_P];         // the column quarters' partial scores

@@ -273,6 +273,32 @@ __device__ static inline void spl_split(float x, _Float16 &hi, _Float16 &lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
+// The split form of the entry row[0 .. kv + rope) (the block's shared memory, written before
+// a barrier) into ksp row kr and vsp slot vb (kv + rope <= SPL_KCOLS, kv <= the vsp planes'
+// width: the host's checks); rmax: DM_BLOCK / 64 floats of shared memory.
+__device__ __attribute__((always_inline)) static void spl_store(const float *row, int kv, int rope, _Float16 *kr,
+                                                                _Float16 *vb, float *rmax) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, KQ = kv + rope;
+    float mx = 0.0f;
+    for (int i = tid; i < KQ; i += DM_BLOCK) mx = fmaxf(mx, fabsf(row[i]));
+    mx = wave_max_dpp_f(mx);
+    if (lane == 0) rmax[w] = mx;
+    __syncthreads();
+    const int e = spl_exp(fmaxf(fmaxf(rmax[0], rmax[1]), fmaxf(rmax[2], rmax[3])));
+    for (int i = tid; i < SPL_KCOLS; i += DM_BLOCK) {
+        _Float16 hi = (_Float16)0.0f, lo = (_Float16)0.0f;
+        if (i < KQ) spl_split(ldexpf(row[i], -e), hi, lo);
+        kr[i] = hi;
+        kr[SPL_KCOLS + i] = lo;
+        if (i < kv) {
+            vb[(size_t)i * 16] = hi;
+            vb[((size_t)kv + i) * 16] = lo;
+        }
+    }
+    if (tid < (SPL_KROW - SPL_KEXP) / 2) ((int *)(kr + SPL_KEXP))[tid] = tid == 0 ? e : 0;
+}
+static_assert(DM_BLOCK == 256, "spl_store joins four waves' maxima");
+
 // The position's cache entry and the heads' rotated queries (infer.c:1000-1016): the
 // compressed kv normalised (rmsnorm over kv values), the rope part of kv_a and of every
 // head's query rotated by the position's angles. One block for token t of a batch, at
@@ -318,29 +344,24 @@ __device__ __attribute__((always_inline)) static void attn_prep_run(AttnArgs a, 
             row[a.kv + 2 * i + 1] = y1;
         }
     }
-    if (!a.ksp) return;
-    // the entry's split form (kv + rope <= SPL_KCOLS, kv <= the vsp planes' width: the host's checks)
+    if (!a.ksp) return;  // a decode step: the host marks the position for k_spl_fill
     __syncthreads();
-    const int KQ = a.kv + a.rope;
-    float mx = 0.0f;
-    for (int i = tid; i < KQ; i += DM_BLOCK) mx = fmaxf(mx, fabsf(row[i]));
-    mx = wave_max_dpp_f(mx);
-    if (lane == 0) rmax[w] = mx;
+    spl_store(row, a.kv, a.rope, a.ksp + (size_t)a.pos * SPL_KROW, a.vsp + (size_t)(a.pos >> 4) * 2 * a.kv * 16 + (a.pos & 15),
+              rmax);
+}
+
+// Positions p0 + blockIdx.x of attention layer blockIdx.y: the split form from the fp32
+// entry (the same values attn_prep_run splits), for positions a decode step wrote without it.
+__global__ __launch_bounds__(DM_BLOCK) void k_spl_fill(const float *comp, const float *pe, _Float16 *ksp, _Float16 *vsp,
+                                                      size_t cap, size_t capt, int kv, int rope, int p0) {
+    __shared__ float row[SPL_KCOLS];
+    __shared__ float rmax[DM_BLOCK / 64];
+    const int p = p0 + blockIdx.x, l = blockIdx.y;
+    const float *ce = comp + ((size_t)l * cap + p) * kv, *re = pe + ((size_t)l * cap + p) * rope;
+    for (int i = threadIdx.x; i < kv + rope; i += DM_BLOCK) row[i] = i < kv ? ce[i] : re[i - kv];
     __syncthreads();
-    const int e = spl_exp(fmaxf(fmaxf(rmax[0], rmax[1]), fmaxf(rmax[2], rmax[3])));
-    _Float16 *kr = a.ksp + (size_t)a.pos * SPL_KROW;
-    _Float16 *vb = a.vsp + (size_t)(a.pos >> 4) * 2 * a.kv * 16 + (a.pos & 15);
-    for (int i = tid; i < SPL_KCOLS; i += DM_BLOCK) {
-        _Float16 hi = (_Float16)0.0f, lo = (_Float16)0.0f;
-        if (i < KQ) spl_split(ldexpf(row[i], -e), hi, lo);
-        kr[i] = hi;
-        kr[SPL_KCOLS + i] = lo;
-        if (i < a.kv) {
-            vb[(size_t)i * 16] = hi;
-            vb[((size_t)a.kv + i) * 16] = lo;
-        }
-    }
-    if (tid < (SPL_KROW - SPL_KEXP) / 2) ((int *)(kr + SPL_KEXP))[tid] = tid == 0 ? e : 0;
+    spl_store(row, kv, rope, ksp + ((size_t)l * capt + p) * SPL_KROW,
+              vsp + (size_t)l * capt * 2 * kv + (size_t)(p >> 4) * 2 * kv * 16 + (p & 15), rmax);
 }
 
 // The query side of a token's attention in one launch: the absorbed queries q_abs = k_b_h .

@@ -95,9 +95,12 @@ struct gmoe_model {
           *ctx = nullptr, *concat = nullptr, *ffh = nullptr, *logits = nullptr, *part_ctx = nullptr,
           *part_ml = nullptr, *saved = nullptr;
     // the caches' split fp16 form for the batch attention (dense.h: ksp rows, vsp blocks; null
-    // where the shape does not take it), cap rounded up to 16 positions, and a token's saved entries
-    _Float16 *ksp = nullptr, *vsp = nullptr, *ksaved = nullptr;
+    // where the shape does not take it), cap rounded up to 16 positions
+    _Float16 *ksp = nullptr, *vsp = nullptr;
     size_t cap16 = 0;
+    // positions stale_lo .. stale_hi - 1 hold fp32 entries a decode step wrote without their
+    // split form (decode reads only the fp32 cache); a prefill converts them first
+    int stale_lo = 0, stale_hi = 0;
     int32_t *tokens = nullptr;  // [max_batch] a prefill's token ids
     // a prefill's GEMM inputs (gemm.h): [max_batch][2][widest input] fp16, their exponents,
     // and 64 bytes of zeros
@@ -422,7 +425,8 @@ int attention(gmoe_model *m, int l, int pos, hipStream_t st) {
         launch_gemv(qa, GV_PLAIN, st);
     }
     launch_gemv(gemv(A.q_b_q, A.q_b_s, m->q_a, A.q_a_norm, m->q_full, H * c.head_k_dim, c.q_lora_rank, gs), GV_PLAIN, st);
-    const AttnArgs aa = attn_args(m, l, pos);
+    AttnArgs aa = attn_args(m, l, pos);
+    aa.ksp = aa.vsp = nullptr;  // the split form waits for the next prefill (k_spl_fill)
     // the query absorbed into the latent space, per head: k_b_h [kv][nope] . q_nope_h, with
     // the cache entry and the rotated queries in the same launch
     GemvArgs kb = gemv(A.k_b_q, A.k_b_s, m->q_full, nullptr, m->q_abs, H * kv, c.qk_nope_dim, gs);
@@ -649,7 +653,6 @@ extern "C" int gmoe_model_create(gmoe_model **out, int device, const gmoe_model_
             m->cap16 = (cap + 15) / 16 * 16;
             rc |= mdalloc(m, &m->ksp, A * m->cap16 * SPL_KROW);
             rc |= mdalloc(m, &m->vsp, A * m->cap16 * 2 * kv);
-            rc |= mdalloc(m, &m->ksaved, A * (SPL_KROW + 2 * kv));
         }
     }
     if (!rc && A > 0) {
@@ -815,15 +818,16 @@ int forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, f
     const size_t D = (size_t)c.dim, kv = (size_t)c.kv_lora_rank, rope = (size_t)c.rope_dim, cap = (size_t)c.cache_cap;
     const size_t A = (size_t)c.attn_layers;
     const bool keep = (flags & GMOE_MODEL_KEEP_CACHE) && A > 0;
+    if (m->ksp && !keep) {
+        m->stale_lo = m->stale_hi > m->stale_lo ? std::min(m->stale_lo, pos) : pos;
+        m->stale_hi = std::max(m->stale_hi, pos + 1);
+    }
     if (keep) {
         // the entries this position is about to overwrite, one per attention layer
         MH_OK(hipMemcpy2DAsync(m->saved, kv * sizeof(float), m->comp + pos * kv, cap * kv * sizeof(float),
                                kv * sizeof(float), A, hipMemcpyDeviceToDevice, st));
         MH_OK(hipMemcpy2DAsync(m->saved + A * kv, rope * sizeof(float), m->pe + pos * rope, cap * rope * sizeof(float),
                                rope * sizeof(float), A, hipMemcpyDeviceToDevice, st));
-        if (m->ksp)
-            hipLaunchKernelGGL(k_spl_keep, dim3((unsigned)A), dim3(DM_BLOCK), 0, st, m->ksp, m->vsp, m->ksaved, m->cap16,
-                               (int)kv, pos, 0);
     }
     hipLaunchKernelGGL(k_embed, dim3((unsigned)((D + DM_BLOCK - 1) / DM_BLOCK)), dim3(DM_BLOCK), 0, st, m->tok_q, m->tok_s,
                        token, c.dim, c.group_size, m->x);
@@ -884,9 +888,6 @@ int forward_token(gmoe_model *m, int token, int pos, int flags, float *logits, f
                                kv * sizeof(float), A, hipMemcpyDeviceToDevice, st));
         MH_OK(hipMemcpy2DAsync(m->pe + pos * rope, cap * rope * sizeof(float), m->saved + A * kv, rope * sizeof(float),
                                rope * sizeof(float), A, hipMemcpyDeviceToDevice, st));
-        if (m->ksp)
-            hipLaunchKernelGGL(k_spl_keep, dim3((unsigned)A), dim3(DM_BLOCK), 0, st, m->ksp, m->vsp, m->ksaved, m->cap16,
-                               (int)kv, pos, 1);
     }
     MH_OK(hipStreamSynchronize(st));
     if (m->moe && gm_take_launch_error(m->moe)) return GMOE_ERR_HIP;
@@ -922,6 +923,14 @@ extern "C" int gmoe_model_prefill(gmoe_model *m, const int32_t *tokens, int n, i
     MH_OK(hipSetDevice(m->device));
     hipStream_t st = (hipStream_t)stream;
     const size_t D = (size_t)c.dim;
+    if (m->ksp && m->stale_hi > m->stale_lo) {
+        // the entries decode steps wrote without their split form, before any attention of
+        // this batch reads them
+        hipLaunchKernelGGL(k_spl_fill, dim3((unsigned)(m->stale_hi - m->stale_lo), (unsigned)c.attn_layers), dim3(DM_BLOCK),
+                           0, st, m->comp, m->pe, m->ksp, m->vsp, (size_t)c.cache_cap, m->cap16, c.kv_lora_rank, c.rope_dim,
+                           m->stale_lo);
+        m->stale_lo = m->stale_hi = 0;
+    }
     MH_OK(hipMemcpyAsync(m->tokens, tokens, (size_t)n * sizeof(int32_t), hipMemcpyHostToDevice, st));
     hipLaunchKernelGGL(k_embed_batch, dim3((unsigned)((D + DM_BLOCK - 1) / DM_BLOCK), (unsigned)n), dim3(DM_BLOCK), 0, st,
                        m->tok_q, m->tok_s, m->tokens, c.vocab_size, c.dim, c.group_size, m->x);

@@ -11,10 +11,10 @@ argmax. Shapes: a small one (kv 64 + rope 16 = 80 columns: the last 32-column st
 padded with zeros) and glm.c's attention ranks (kv 512 + rope 64), 4 and 20 heads. Prompts:
 300 tokens in one batch (five 64-token query tiles, several position chunks), then 200 more
 at position 300 over that cache (chunks that span both batches, causal masks inside); then
-a decode token with GMOE_MODEL_KEEP_CACHE at position 250 (its entries written, then
-restored: the split form must be restored with the fp32 one, or the split kernel would read
-the overwritten entry), three tokens decoded one at a time (their split entries written by
-the decode's cache step) and 8 more tokens in a batch over all of them."""
+a decode token with GMOE_MODEL_KEEP_CACHE at position 250 (its fp32 entries written, then
+restored; the split form, which decode steps do not write, must be left as the prefill
+wrote it), three tokens decoded one at a time (fp32 entries only: the next prefill converts
+them with k_spl_fill before its attention) and 8 more tokens in a batch over all of them."""
 import os
 
 import numpy as np
@@ -80,8 +80,8 @@ def test_split_fp16_attention_matches_fp32(name):
 
         check("300 tokens at 0", first, 0)
         check("200 tokens at 300", second, 300)
-        # a kept decode token overwrites position 250's entries and restores them (the split form
-        # with the fp32 one); tokens decoded one at a time write theirs; a batch then reads both
+        # a kept decode token overwrites position 250's fp32 entries and restores them; tokens
+        # decoded one at a time write fp32 entries only; a batch then reads both in split form
         model.forward_token(7, 250, flags=KEEP_CACHE)
         for pos in range(500, 503):
             model.forward_token(int(rng.integers(0, cfg["vocab_size"])), pos)
