@@ -45,10 +45,9 @@ typedef _Float16 a16_h4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
     __shared__ __align__(16) uint8_t stg[2][A16_STAGE];        // tiles j and j + 1: rows, then the block
     __shared__ __align__(16) float sp[4][AQ_T][AQ_P];         // the column quarters' partial scores
+    __shared__ __align__(16) _Float16 pp[2][AQ_T * A16_PS];   // the exponentials' hi and lo planes
     __shared__ float run_m[AQ_T], run_l[AQ_T], corr[AQ_T];
     __shared__ int eq_s[AQ_T], et_s;
-    _Float16(*pp)[AQ_T * A16_PS] = reinterpret_cast<_Float16(*)[AQ_T * A16_PS]>(&sp[0][0][0]);  // after the scores are read
-    static_assert(2 * AQ_T * A16_PS * 2 <= sizeof(sp), "the exponentials' planes fit the scores' buffer");
     const AttnArgs &a = g.a;
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -200,7 +199,6 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
             // softmax step: thread = (row tid / 16, position tid % 16), a 16-lane DPP row per row
             const int row = tid >> 4, p = tid & 15, t = t0 + row, s = s0 + p;
             float v = (sp[0][row][p] + sp[1][row][p]) + (sp[2][row][p] + sp[3][row][p]);
-            at_barrier();  // every score read: the exponentials' planes below reuse the buffer
             v = __fmul_rn(v, a.kq_scale);
             const bool in = s < r1;
             if (t >= tl || !in || s > a.pos + t) v = -INFINITY;  // causal, and past the chunk
@@ -248,7 +246,7 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
                 }
             }
         }
-        at_barrier();  // every wave is done with stage j % 2, the scores' buffer and the exponents
+        at_barrier();  // every wave is done with stage j % 2 and the exponentials' planes
         A16_STAMP(5, j);
         if (j + 2 < ntile) issue(s0 + 2 * AQ_P, j & 1);
     }
