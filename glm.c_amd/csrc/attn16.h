@@ -69,6 +69,31 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
     const int nks = (KQ + 31) / 32;   // 32-column steps (ksp holds zeros past KQ)
     const int ntile = (r1 - r0 + AQ_P - 1) / AQ_P;
 
+    // a tile by DMA into stage st: its 16 ksp rows (contiguous), then its vsp block (4 kv
+    // 16-byte slots); 64 slots per wave and round, the last round's lanes past the data idle.
+    // The wave's count of DMA instructions is the same for every tile (nd below).
+    constexpr int NKS = A16_KB / 16;
+    const int nvs = 4 * kv;
+    const int nd = 2 + (2048 + 64 * w < NKS ? 1 : 0) + (64 * w < nvs ? 1 : 0) + (1024 + 64 * w < nvs ? 1 : 0);
+    auto issue = [&](int s0, int st) {
+        const uint8_t *ks = reinterpret_cast<const uint8_t *>(a.ksp + (size_t)s0 * SPL_KROW);
+        const uint8_t *vs = reinterpret_cast<const uint8_t *>(a.vsp + (size_t)(s0 >> 4) * 2 * kv * 16);
+        int ln = lane;
+        asm volatile("" : "+v"(ln));  // (addresses formed per request, not hoisted out of the loop)
+#pragma unroll
+        for (int r = 0; r < 3; r++) {
+            const int b0 = 1024 * r + 64 * w;
+            if (b0 < NKS && b0 + ln < NKS) dma16_untracked(gbl((const void *)(ks + 16 * (b0 + ln))), (lds_void *)(stg[st] + 16 * b0));
+        }
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int b0 = 1024 * r + 64 * w;
+            if (b0 < nvs) dma16_untracked(gbl((const void *)(vs + 16 * (b0 + ln))), (lds_void *)(stg[st] + A16_KB + 16 * b0));
+        }
+    };
+    issue(r0, 0);  // before the queries' loads: the two share a round trip
+    if (ntile > 1) issue(r0 + AQ_P, 1);
+
     // the queries: the lane's operand columns (row 16 rb + l16, steps q + 4 i, columns 32 s +
     // 8 lg .. + 7, each 8-column group inside one part since kv and KQ are multiples of 16)
     // as float4 pairs, all requested at once; the row's exponent from the four waves that
@@ -128,30 +153,6 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
     for (int r = 0; r < 4; r++) eqd[r] = eq_s[16 * rb + 4 * lg + r];
     A16_STAMP(1, 0);
 
-    // a tile by DMA into stage st: its 16 ksp rows (contiguous), then its vsp block (4 kv
-    // 16-byte slots); 64 slots per wave and round, the last round's lanes past the data idle.
-    // The wave's count of DMA instructions is the same for every tile (nd below).
-    constexpr int NKS = A16_KB / 16;
-    const int nvs = 4 * kv;
-    const int nd = 2 + (2048 + 64 * w < NKS ? 1 : 0) + (64 * w < nvs ? 1 : 0) + (1024 + 64 * w < nvs ? 1 : 0);
-    auto issue = [&](int s0, int st) {
-        const uint8_t *ks = reinterpret_cast<const uint8_t *>(a.ksp + (size_t)s0 * SPL_KROW);
-        const uint8_t *vs = reinterpret_cast<const uint8_t *>(a.vsp + (size_t)(s0 >> 4) * 2 * kv * 16);
-        int ln = lane;
-        asm volatile("" : "+v"(ln));  // (addresses formed per request, not hoisted out of the loop)
-#pragma unroll
-        for (int r = 0; r < 3; r++) {
-            const int b0 = 1024 * r + 64 * w;
-            if (b0 < NKS && b0 + ln < NKS) dma16_untracked(gbl((const void *)(ks + 16 * (b0 + ln))), (lds_void *)(stg[st] + 16 * b0));
-        }
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int b0 = 1024 * r + 64 * w;
-            if (b0 < nvs) dma16_untracked(gbl((const void *)(vs + 16 * (b0 + ln))), (lds_void *)(stg[st] + A16_KB + 16 * b0));
-        }
-    };
-    issue(r0, 0);
-    if (ntile > 1) issue(r0 + AQ_P, 1);
 
     aq_f4 acc[8];
 #pragma unroll
