@@ -66,6 +66,10 @@ typedef unsigned qg_u2 __attribute__((ext_vector_type(2)));
 // sp[t][0][:] = fp16(v 2^-e), sp[t][1][:] = fp16(v 2^-e - hi), ex[t] = e, with e from
 // max |v| so that the row's largest value sits near 2^14.
 #define QG_SPLIT_MAX 40  // row values a thread holds: rows of up to 40 x QG_BLOCK = 10240 columns
+// NK: the values a thread holds (n <= NK x QG_BLOCK; the launch takes the fewest of 2, 8,
+// 20, 40 that hold the row, so a 2048-column row issues 8 loads a thread, not 40; the
+// values past n add nothing, so every NK gives the same bits)
+template <int NK>
 __global__ __launch_bounds__(QG_BLOCK) void k_norm_split(const float *__restrict__ x, int ldx, int n,
                                                          const float *__restrict__ norm, __half *__restrict__ sp,
                                                          int *__restrict__ ex) {
@@ -74,9 +78,9 @@ __global__ __launch_bounds__(QG_BLOCK) void k_norm_split(const float *__restrict
     const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const float *src = x + (size_t)t * ldx;
     // the row read once: thread tid holds columns tid + QG_BLOCK k
-    float v[QG_SPLIT_MAX], nw[QG_SPLIT_MAX];
+    float v[NK], nw[NK];
 #pragma unroll
-    for (int k = 0; k < QG_SPLIT_MAX; k++) {
+    for (int k = 0; k < NK; k++) {
         const int i = tid + QG_BLOCK * k;
         v[k] = i < n ? src[i] : 0.0f;
         nw[k] = norm && i < n ? norm[i] : 0.0f;
@@ -85,7 +89,7 @@ __global__ __launch_bounds__(QG_BLOCK) void k_norm_split(const float *__restrict
     if (norm) {
         double ss = 0.0;
 #pragma unroll
-        for (int k = 0; k < QG_SPLIT_MAX; k++)
+        for (int k = 0; k < NK; k++)
             if (tid + QG_BLOCK * k < n) ss += (double)v[k] * (double)v[k];
         ss = wave_sum_dpp(ss);
         if (lane == 0) red_d[w] = ss;
@@ -94,11 +98,11 @@ __global__ __launch_bounds__(QG_BLOCK) void k_norm_split(const float *__restrict
         const float mean = (float)(ss / (double)n);
         inv = __fdiv_rn(1.0f, sqrt_rn_f32(__fadd_rn(mean, 1e-5f)));
 #pragma unroll
-        for (int k = 0; k < QG_SPLIT_MAX; k++) v[k] = __fmul_rn(__fmul_rn(v[k], inv), nw[k]);
+        for (int k = 0; k < NK; k++) v[k] = __fmul_rn(__fmul_rn(v[k], inv), nw[k]);
     }
     float mx = 0.0f;
 #pragma unroll
-    for (int k = 0; k < QG_SPLIT_MAX; k++)
+    for (int k = 0; k < NK; k++)
         if (tid + QG_BLOCK * k < n) mx = fmaxf(mx, fabsf(v[k]));
     mx = wave_max_f(mx);
     if (lane == 0) red_f[w] = mx;
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(QG_BLOCK) void k_norm_split(const float *__restrict
     if (tid == 0) ex[t] = e;
     __half *hi = sp + (size_t)t * 2 * n, *lo = hi + n;
 #pragma unroll
-    for (int k = 0; k < QG_SPLIT_MAX; k++) {
+    for (int k = 0; k < NK; k++) {
         const int i = tid + QG_BLOCK * k;
         if (i < n) {
             const float xs = ldexpf(v[k], -e);

@@ -472,7 +472,11 @@ bool gemm_batch(const gmoe_model *m, int n) {
 // The n tokens' inputs x (ldx apart, cols columns), normalised by norm when given, into
 // the GEMM's split buffer.
 void gemm_inputs(gmoe_model *m, const float *x, int ldx, int cols, const float *norm, int n, hipStream_t st) {
-    hipLaunchKernelGGL(k_norm_split, dim3((unsigned)n), dim3(QG_BLOCK), 0, st, x, ldx, cols, norm, m->xs, m->xe);
+    const dim3 grid((unsigned)n), block(QG_BLOCK);
+    if (cols <= 2 * QG_BLOCK) hipLaunchKernelGGL(k_norm_split<2>, grid, block, 0, st, x, ldx, cols, norm, m->xs, m->xe);
+    else if (cols <= 8 * QG_BLOCK) hipLaunchKernelGGL(k_norm_split<8>, grid, block, 0, st, x, ldx, cols, norm, m->xs, m->xe);
+    else if (cols <= 20 * QG_BLOCK) hipLaunchKernelGGL(k_norm_split<20>, grid, block, 0, st, x, ldx, cols, norm, m->xs, m->xe);
+    else hipLaunchKernelGGL(k_norm_split<QG_SPLIT_MAX>, grid, block, 0, st, x, ldx, cols, norm, m->xs, m->xe);
 }
 
 // y = q . v for the n tokens' split inputs (gemm_inputs, cols columns): rows of group g
