@@ -51,7 +51,11 @@ __global__ __launch_bounds__(AQ_BLOCK) void k_attn_tile16(AttnTileArgs g) {
     const AttnArgs &a = g.a;
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int c = blockIdx.x, t0 = AQ_T * blockIdx.y, h = blockIdx.z;
+    // blocks dispatched longest first, so that short ones fill the CUs at the end: chunk by
+    // chunk (the earlier chunks are the full ones), and in a chunk the later token tiles
+    // (which attend more of its positions) first, the heads of a tile in a row
+    const int L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), per = gridDim.y * gridDim.z;
+    const int c = L / per, t0 = AQ_T * (gridDim.y - 1 - (L % per) / gridDim.z), h = (L % per) % gridDim.z;
     const int kv = a.kv, rope = a.rope, KQ = kv + rope, H = a.H, nch = a.nblk;
     const int tl = min(g.n, t0 + AQ_T);    // the tile's tokens t0 .. tl - 1
     const int r0 = c * g.chunk;
